@@ -1,0 +1,289 @@
+// The C ABI of libayaka_hip (declared in include/ayaka_hip.h): argument
+// checks, geometry, and the launches. No entry point allocates, frees or
+// synchronises; all work is queued on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "ayaka_hip.h"
+#include "ayaka_hip_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return AYK_OK;
+}
+
+int launched(hipError_t err, const char* what) {
+  if (err != hipSuccess) return fail(AYK_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(err));
+  return ok();
+}
+
+int log2_exact(int32_t v) {
+  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return s;
+}
+
+// Split a group of query heads into equal chunks of at most 8 heads (one workgroup each).
+int head_chunks_for(int group) {
+  for (int n = 1; n <= group; ++n)
+    if (group % n == 0 && group / n <= 8) return n;
+  return group;
+}
+
+struct AttnCall {
+  void* out;
+  const void* q;
+  const void* k_cache;
+  const void* v_cache;
+  const int32_t* block_table;
+  int64_t table_stride;
+  const int32_t* kv_lengths;
+  const int32_t* request_of_row;
+  const int32_t* positions;
+  int32_t n_rows, num_heads, num_kv_heads, head_dim, num_blocks, block_size, max_blocks, layout,
+      dtype;
+  float scale;
+};
+
+// Check a call and fill the launch record; returns AYK_OK or an error code.
+int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_per_chunk) {
+  if (c.n_rows < 0) return fail(AYK_ERR_ARGUMENT, "%s: n_rows is negative (%d)", op, c.n_rows);
+  if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: head_dim %d is not one of 64, 128, 256", op, c.head_dim);
+  if (c.dtype != AYK_DTYPE_FP16 && c.dtype != AYK_DTYPE_BF16)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: dtype %d is not fp16 (0) or bf16 (1)", op, c.dtype);
+  if (c.layout != AYK_LAYOUT_NHD && c.layout != AYK_LAYOUT_HND)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: layout %d is not NHD (0) or HND (1)", op, c.layout);
+  if (c.num_kv_heads <= 0 || c.num_heads <= 0 || c.num_heads % c.num_kv_heads != 0)
+    return fail(AYK_ERR_ARGUMENT,
+                "%s: %d query heads is not a positive multiple of %d key/value heads", op,
+                c.num_heads, c.num_kv_heads);
+  const int shift = log2_exact(c.block_size);
+  if (shift < 0 || shift > 16)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: block_size %d is not a power of two up to 65536", op,
+                c.block_size);
+  if (c.num_blocks <= 0 || c.max_blocks < 0 || c.table_stride < c.max_blocks)
+    return fail(AYK_ERR_ARGUMENT, "%s: num_blocks %d, max_blocks %d, table_stride %lld", op,
+                c.num_blocks, c.max_blocks, (long long)c.table_stride);
+  if ((c.request_of_row == nullptr) != (c.positions == nullptr))
+    return fail(AYK_ERR_ARGUMENT, "%s: request_of_row and positions are given together or not at all",
+                op);
+  if (c.n_rows > 0 && (!c.out || !c.q || !c.k_cache || !c.v_cache || !c.block_table ||
+                       !c.kv_lengths))
+    return fail(AYK_ERR_ARGUMENT, "%s: a required pointer is null", op);
+  const int group = c.num_heads / c.num_kv_heads;
+  const int chunks = head_chunks_for(group);
+  if ((int64_t)c.num_kv_heads * chunks > 65535)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: %d key/value heads x %d head chunks exceed the grid", op,
+                c.num_kv_heads, chunks);
+  heads_per_chunk = group / chunks;
+  p = ayk::AttnParams{};
+  p.out = c.out;
+  p.q = static_cast<const uint16_t*>(c.q);
+  p.k_cache = static_cast<const uint16_t*>(c.k_cache);
+  p.v_cache = static_cast<const uint16_t*>(c.v_cache);
+  p.block_table = c.block_table;
+  p.kv_lengths = c.kv_lengths;
+  p.request_of_row = c.request_of_row;
+  p.positions = c.positions;
+  p.table_stride = c.table_stride;
+  const int64_t D = c.head_dim, H = c.num_kv_heads, B = c.block_size;
+  if (c.layout == AYK_LAYOUT_NHD) {
+    p.block_stride = B * H * D;
+    p.token_stride = H * D;
+    p.head_stride = D;
+  } else {
+    p.block_stride = H * B * D;
+    p.token_stride = D;
+    p.head_stride = B * D;
+  }
+  p.n_rows = c.n_rows;
+  p.num_heads = c.num_heads;
+  p.group = group;
+  p.head_chunks = chunks;
+  p.num_blocks = c.num_blocks;
+  p.bs_shift = shift;
+  const int64_t table_len = (int64_t)c.max_blocks << shift;
+  p.max_len = (int32_t)std::min<int64_t>(table_len, INT32_MAX);
+  p.scale_log2 = c.scale * 1.4426950408889634f;
+  p.partition_size = INT32_MAX;
+  p.max_partitions = 1;
+  return AYK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ayk_abi_version(void) { return 1; }
+
+const char* ayk_last_error(void) { return g_last_error.c_str(); }
+
+int ayk_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
+                          const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t layout,
+                          int32_t elem_bytes, void* stream) {
+  const char* op = "ayk_reshape_and_cache";
+  if (n_rows < 0) return fail(AYK_ERR_ARGUMENT, "%s: n_rows is negative", op);
+  if (num_kv_heads <= 0 || head_dim <= 0 || num_blocks <= 0 || block_size <= 0)
+    return fail(AYK_ERR_ARGUMENT, "%s: num_kv_heads %d, head_dim %d, num_blocks %d, block_size %d",
+                op, num_kv_heads, head_dim, num_blocks, block_size);
+  if (elem_bytes != 2 && elem_bytes != 4)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: elem_bytes %d is not 2 or 4", op, elem_bytes);
+  if (layout != AYK_LAYOUT_NHD && layout != AYK_LAYOUT_HND)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: layout %d is not NHD (0) or HND (1)", op, layout);
+  if (n_rows == 0) return ok();
+  if (!k || !v || !k_cache || !v_cache || !slot_mapping)
+    return fail(AYK_ERR_ARGUMENT, "%s: a required pointer is null", op);
+  return launched(ayk::launch_reshape_and_cache(k, v, k_cache, v_cache, slot_mapping, n_rows,
+                                                num_kv_heads, head_dim, num_blocks, block_size,
+                                                layout == AYK_LAYOUT_HND, elem_bytes,
+                                                static_cast<hipStream_t>(stream)),
+                  op);
+}
+
+int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,
+                           const int32_t* block_table, int64_t table_stride,
+                           const int32_t* kv_lengths, const int32_t* request_of_row,
+                           const int32_t* positions, int32_t n_rows, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                           int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
+                           float scale, void* stream) {
+  const char* op = "ayk_paged_attention_v1";
+  AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
+             kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
+             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, scale};
+  ayk::AttnParams p;
+  int gc = 0;
+  const int rc = prepare(op, c, p, gc);
+  if (rc != AYK_OK) return rc;
+  if (n_rows == 0) return ok();
+  return launched(ayk::launch_paged_attention(p, head_dim, gc, dtype == AYK_DTYPE_BF16, false,
+                                              static_cast<hipStream_t>(stream)),
+                  op);
+}
+
+size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads, int32_t head_dim,
+                                              int32_t max_partitions) {
+  if (n_rows <= 0 || num_heads <= 0 || head_dim <= 0 || max_partitions <= 0) return 0;
+  const size_t parts = (size_t)n_rows * num_heads * max_partitions;
+  // partial outputs first (16-byte aligned rows), then the (m, l) pairs
+  return parts * (size_t)head_dim * sizeof(float) + parts * 2 * sizeof(float);
+}
+
+int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const void* v_cache,
+                           const int32_t* block_table, int64_t table_stride,
+                           const int32_t* kv_lengths, const int32_t* request_of_row,
+                           const int32_t* positions, int32_t n_rows, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                           int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
+                           float scale, int32_t partition_size, int32_t max_partitions,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  const char* op = "ayk_paged_attention_v2";
+  AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
+             kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
+             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, scale};
+  ayk::AttnParams p;
+  int gc = 0;
+  const int rc = prepare(op, c, p, gc);
+  if (rc != AYK_OK) return rc;
+  if (partition_size <= 0 || partition_size % 64 != 0)
+    return fail(AYK_ERR_ARGUMENT, "%s: partition_size %d is not a positive multiple of 64", op,
+                partition_size);
+  if (max_partitions <= 0 || max_partitions > 65535)
+    return fail(AYK_ERR_ARGUMENT, "%s: max_partitions %d is not in [1, 65535]", op, max_partitions);
+  if (n_rows == 0) return ok();
+  const size_t need =
+      ayk_paged_attention_v2_workspace_bytes(n_rows, num_heads, head_dim, max_partitions);
+  if (!workspace || workspace_bytes < need)
+    return fail(AYK_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", op, workspace_bytes,
+                need);
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return fail(AYK_ERR_ARGUMENT, "%s: workspace is not 16-byte aligned", op);
+  const size_t parts = (size_t)n_rows * num_heads * max_partitions;
+  p.part_o = static_cast<float*>(workspace);
+  p.part_ml = p.part_o + parts * head_dim;
+  p.partition_size = partition_size;
+  p.max_partitions = max_partitions;
+  p.max_len = (int32_t)std::min<int64_t>(p.max_len, (int64_t)partition_size * max_partitions);
+  return launched(ayk::launch_paged_attention(p, head_dim, gc, dtype == AYK_DTYPE_BF16, true,
+                                              static_cast<hipStream_t>(stream)),
+                  op);
+}
+
+static int block_op_checks(const char* op, int64_t n, int32_t num_blocks, int64_t block_bytes) {
+  if (n < 0 || num_blocks <= 0 || block_bytes <= 0 || block_bytes % 2 != 0)
+    return fail(AYK_ERR_ARGUMENT, "%s: n %lld, num_blocks %d, block_bytes %lld", op, (long long)n,
+                num_blocks, (long long)block_bytes);
+  if (n > INT32_MAX) return fail(AYK_ERR_ARGUMENT, "%s: too many blocks (%lld)", op, (long long)n);
+  return AYK_OK;
+}
+
+int ayk_gather_blocks(const void* k_cache, const void* v_cache, void* out_k, void* out_v,
+                      const void* block_ids, int32_t ids_are_64bit, int64_t n, int32_t num_blocks,
+                      int64_t block_bytes, void* stream) {
+  const char* op = "ayk_gather_blocks";
+  const int rc = block_op_checks(op, n, num_blocks, block_bytes);
+  if (rc != AYK_OK) return rc;
+  if (n == 0) return ok();
+  if (!k_cache || !v_cache || !out_k || !out_v || !block_ids)
+    return fail(AYK_ERR_ARGUMENT, "%s: a required pointer is null", op);
+  return launched(ayk::launch_block_op(0, k_cache, v_cache, out_k, out_v, block_ids, nullptr,
+                                       ids_are_64bit != 0, n, num_blocks, block_bytes,
+                                       static_cast<hipStream_t>(stream)),
+                  op);
+}
+
+int ayk_copy_blocks(void* k_cache, void* v_cache, const void* src, const void* dst,
+                    int32_t ids_are_64bit, int64_t n, int32_t num_blocks, int64_t block_bytes,
+                    void* stream) {
+  const char* op = "ayk_copy_blocks";
+  const int rc = block_op_checks(op, n, num_blocks, block_bytes);
+  if (rc != AYK_OK) return rc;
+  if (n == 0) return ok();
+  if (!k_cache || !v_cache || !src || !dst)
+    return fail(AYK_ERR_ARGUMENT, "%s: a required pointer is null", op);
+  return launched(ayk::launch_block_op(1, k_cache, v_cache, k_cache, v_cache, src, dst,
+                                       ids_are_64bit != 0, n, num_blocks, block_bytes,
+                                       static_cast<hipStream_t>(stream)),
+                  op);
+}
+
+int ayk_zero_blocks(void* k_cache, void* v_cache, const void* block_ids, int32_t ids_are_64bit,
+                    int64_t n, int32_t num_blocks, int64_t block_bytes, void* stream) {
+  const char* op = "ayk_zero_blocks";
+  const int rc = block_op_checks(op, n, num_blocks, block_bytes);
+  if (rc != AYK_OK) return rc;
+  if (n == 0) return ok();
+  if (!k_cache || !v_cache || !block_ids)
+    return fail(AYK_ERR_ARGUMENT, "%s: a required pointer is null", op);
+  return launched(ayk::launch_block_op(2, nullptr, nullptr, k_cache, v_cache, block_ids, nullptr,
+                                       ids_are_64bit != 0, n, num_blocks, block_bytes,
+                                       static_cast<hipStream_t>(stream)),
+                  op);
+}
+
+}  // extern "C"

@@ -1,0 +1,51 @@
+// Kernel parameter records and launchers shared by the HIP sources of libayaka_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace ayk {
+
+// Everything one paged-attention launch reads. Strides are in elements.
+struct AttnParams {
+  void* out;
+  const uint16_t* q;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  const int32_t* block_table;
+  const int32_t* kv_lengths;
+  const int32_t* request_of_row;  // nullptr: row n is request n
+  const int32_t* positions;       // nullptr: row n attends to its whole context
+  float* part_o;                  // v2 only: [n_rows, num_heads, max_partitions, head_dim]
+  float* part_ml;                 // v2 only: [n_rows, num_heads, max_partitions, 2] = (m, l)
+  int64_t table_stride;
+  int64_t block_stride;
+  int64_t token_stride;
+  int64_t head_stride;
+  int32_t n_rows;
+  int32_t num_heads;
+  int32_t group;        // query heads per key/value head
+  int32_t head_chunks;  // workgroups that split one group's heads (group / head_chunks each)
+  int32_t num_blocks;
+  int32_t bs_shift;     // log2(block_size)
+  int32_t max_len;      // no row reads positions at or past this
+  int32_t partition_size;
+  int32_t max_partitions;
+  float scale_log2;     // scale * log2(e): scores live in the log2 domain
+};
+
+hipError_t launch_paged_attention(const AttnParams& p, int head_dim, int heads_per_chunk, bool bf16,
+                                  bool split, hipStream_t stream);
+
+hipError_t launch_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
+                                    const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t num_blocks, int32_t block_size,
+                                    bool hnd, int32_t elem_bytes, hipStream_t stream);
+
+// mode: 0 = gather (dst index i), 1 = copy (dst ids), 2 = zero (no source)
+hipError_t launch_block_op(int mode, const void* src_k, const void* src_v, void* dst_k, void* dst_v,
+                           const void* src_ids, const void* dst_ids, bool ids64, int64_t n,
+                           int32_t num_blocks, int64_t block_bytes, hipStream_t stream);
+
+}  // namespace ayk

@@ -1,0 +1,461 @@
+// Paged-attention decode kernels for MI355X (gfx950, CDNA4, wave64).
+//
+// Semantics follow the reference's decode attention
+// (python/ayaka/ops/backends/torch/attention.py:237-271) and its row
+// convention (python/ayaka/ops/attention.py:12-30): row n attends to
+// positions [0, len_n) of its request, with scores scale * q.k, softmax and the
+// value sum in fp32, and the result rounded once to the output dtype.
+//
+// Design (bandwidth-bound GEMV over the cache, so VALU rather than MFMA):
+//  * One workgroup of 4 waves per (row, key/value head[, partition]). The G
+//    query heads that share a key/value head are served from the same K/V
+//    loads, so every cache byte is read once per row.
+//  * A token's head_dim slice (128 or 256 contiguous bytes in either layout)
+//    is read by LPT = head_dim/8 lanes with one 128-bit load each, so one load
+//    instruction covers TPL = 64/LPT tokens and a 16-lane group reads 256
+//    contiguous bytes.
+//  * q.k uses v_dot2 (bf16/fp16 pairs, fp32 accumulate) and a DPP butterfly
+//    inside the LPT-lane group; no LDS on the hot path except the block table.
+//  * Online softmax per lane group (running max m and sum l in the log2
+//    domain); the groups of a wave are merged with cross-lane shuffles and the
+//    4 waves through LDS at the end.
+//  * K of the next chunk is loaded while the current chunk is computed.
+//  * The v2 ("split") variant covers partition z of each row and writes the
+//    normalised partial output plus (m, l) to scratch; a reduce kernel merges
+//    the partitions with the log-sum-exp identity.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "ayaka_hip_internal.h"
+
+namespace ayk {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWave * kWaves;
+// Block-table entries staged in LDS per segment of a row's context.
+constexpr int kTableCap = 512;
+
+template <bool BF16>
+struct Elem;
+
+template <>
+struct Elem<true> {
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, b), c, false);
+  }
+  // Round to nearest even, NaN kept quiet (what torch's float -> bfloat16 does).
+  static __device__ __forceinline__ uint32_t round(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+  }
+};
+
+template <>
+struct Elem<false> {
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
+                                  false);
+  }
+  static __device__ __forceinline__ uint32_t round(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of LPT lanes (8, 16 or 32); every lane gets its group's sum.
+template <int LPT>
+__device__ __forceinline__ float group_sum(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+  x += dpp<0x141>(x);  // row_half_mirror: the other quad of the 8
+  if constexpr (LPT >= 16) x += dpp<0x140>(x);  // row_mirror: the other 8 of the 16
+  if constexpr (LPT >= 32) x += __shfl_xor(x, 16);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Length of row `row`'s context and its request, clamped so no read leaves the table.
+__device__ __forceinline__ void row_context(const AttnParams& p, int row, int& req, int& len) {
+  req = p.request_of_row ? p.request_of_row[row] : row;
+  len = p.kv_lengths[req];
+  if (len > 0 && p.positions) len = min(len, p.positions[row] + 1);
+  len = max(0, min(len, p.max_len));
+}
+
+template <int D, int GC, int NLD, bool BF16, bool SPLIT>
+__global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnParams p) {
+  using E = Elem<BF16>;
+  constexpr int LPT = D / 8;         // lanes per token (8 elements = 16 bytes each)
+  constexpr int TPL = kWave / LPT;   // tokens per load instruction
+  constexpr int CH = TPL * NLD;      // tokens per chunk (one chunk per wave per step)
+
+  __shared__ int s_tbl[kTableCap];
+  __shared__ float s_o[kWaves][GC][D];
+  __shared__ float s_m[kWaves][GC];
+  __shared__ float s_l[kWaves][GC];
+
+  const int row = blockIdx.x;
+  const int kvh = blockIdx.y / p.head_chunks;
+  const int h0 = kvh * p.group + (blockIdx.y % p.head_chunks) * GC;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int r = lane / LPT;
+  const int c = lane % LPT;
+
+  int req, len;
+  row_context(p, row, req, len);
+  int t_begin = 0, t_end = len;
+  if constexpr (SPLIT) {
+    t_begin = blockIdx.z * p.partition_size;
+    t_end = min(len, t_begin + p.partition_size);
+    if (t_begin >= t_end) return;  // the reduce kernel reads only partitions that hold tokens
+  } else if (len == 0) {
+    // Padding row: zeros, and nothing of the cache is read.
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+    for (int it = tid; it < GC * LPT; it += kThreads) {
+      const int g = it / LPT, cc = it % LPT;
+      *reinterpret_cast<u32x4*>(out + ((int64_t)row * p.num_heads + h0 + g) * D + cc * 8) =
+          u32x4{0u, 0u, 0u, 0u};
+    }
+    return;
+  }
+
+  // This lane's 8 elements of each of the GC query heads, kept packed for v_dot2.
+  uint32_t qw[GC][4];
+#pragma unroll
+  for (int g = 0; g < GC; ++g) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(p.q + ((int64_t)row * p.num_heads + h0 + g) * D +
+                                                    c * 8);
+    qw[g][0] = v.x; qw[g][1] = v.y; qw[g][2] = v.z; qw[g][3] = v.w;
+  }
+
+  float m[GC], l[GC], o[GC][8];
+#pragma unroll
+  for (int g = 0; g < GC; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+  }
+
+  const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
+  const int shift = p.bs_shift;
+  const int bs_mask = (1 << shift) - 1;
+  const int seg_len = (((kTableCap - 1) << shift) / CH) * CH;
+  const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + c * 8;
+  const uint16_t* vbase = p.v_cache + (int64_t)kvh * p.head_stride + c * 8;
+
+  for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
+    const int s1 = min(t_end, s0 + seg_len);
+    const int b0 = s0 >> shift;
+    const int nb = ((s1 - 1) >> shift) - b0 + 1;
+    __syncthreads();  // the previous segment is done with s_tbl
+    for (int i = tid; i < nb; i += kThreads) {
+      const int b = tbl[b0 + i];
+      s_tbl[i] = ((unsigned)b < (unsigned)p.num_blocks) ? b : 0;
+    }
+    __syncthreads();
+
+    const int nch = (s1 - s0 + CH - 1) / CH;
+    int64_t offs[NLD];
+    u32x4 kc[NLD];
+    auto token_offsets = [&](int ci, int64_t* dst) {
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) {
+        const int t = min(s0 + ci * CH + j * TPL + r, s1 - 1);
+        const int blk = s_tbl[(t >> shift) - b0];
+        dst[j] = (int64_t)blk * p.block_stride + (int64_t)(t & bs_mask) * p.token_stride;
+      }
+    };
+
+    int ci = wave;
+    if (ci < nch) {
+      token_offsets(ci, offs);
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) kc[j] = *reinterpret_cast<const u32x4*>(kbase + offs[j]);
+    }
+    while (ci < nch) {
+      u32x4 vc[NLD];
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) vc[j] = *reinterpret_cast<const u32x4*>(vbase + offs[j]);
+      const int cn = ci + kWaves;
+      int64_t noffs[NLD];
+      u32x4 kn[NLD];
+      if (cn < nch) {
+        token_offsets(cn, noffs);
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) kn[j] = *reinterpret_cast<const u32x4*>(kbase + noffs[j]);
+      }
+
+      const int tb = s0 + ci * CH;
+      const bool tail = tb + CH > s1;
+      float s[NLD][GC];
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) {
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+          float a = E::dot2(qw[g][0], kc[j].x, 0.f);
+          a = E::dot2(qw[g][1], kc[j].y, a);
+          a = E::dot2(qw[g][2], kc[j].z, a);
+          a = E::dot2(qw[g][3], kc[j].w, a);
+          s[j][g] = group_sum<LPT>(a) * p.scale_log2;
+        }
+      }
+      if (tail) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j)
+          if (tb + j * TPL + r >= s1) {
+#pragma unroll
+            for (int g = 0; g < GC; ++g) s[j][g] = -INFINITY;
+          }
+      }
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        float mx = s[0][g];
+#pragma unroll
+        for (int j = 1; j < NLD; ++j) mx = fmaxf(mx, s[j][g]);
+        const float mn = fmaxf(m[g], mx);
+        const float mr = (mn == -INFINITY) ? 0.f : mn;
+        const float alpha = fast_exp2(m[g] - mr);
+        float sum = 0.f;
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+          s[j][g] = fast_exp2(s[j][g] - mr);
+          sum += s[j][g];
+        }
+        l[g] = l[g] * alpha + sum;
+        m[g] = mn;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+      }
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) {
+        float vf[8];
+        vf[0] = E::lo(vc[j].x); vf[1] = E::hi(vc[j].x);
+        vf[2] = E::lo(vc[j].y); vf[3] = E::hi(vc[j].y);
+        vf[4] = E::lo(vc[j].z); vf[5] = E::hi(vc[j].z);
+        vf[6] = E::lo(vc[j].w); vf[7] = E::hi(vc[j].w);
+        if (tail && tb + j * TPL + r >= s1) {
+          // A slot past the context may hold anything, NaN included, and 0 * NaN is NaN.
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vf[e] = 0.f;
+        }
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[g][e] = fmaf(s[j][g], vf[e], o[g][e]);
+        }
+      }
+
+      ci = cn;
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) {
+        offs[j] = noffs[j];
+        kc[j] = kn[j];
+      }
+    }
+  }
+
+  // Merge the TPL lane groups of this wave (butterfly: every group ends with the merged state).
+#pragma unroll
+  for (int st = LPT; st < kWave; st <<= 1) {
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      const float m2 = __shfl_xor(m[g], st);
+      const float l2 = __shfl_xor(l[g], st);
+      const float mn = fmaxf(m[g], m2);
+      const float mr = (mn == -INFINITY) ? 0.f : mn;
+      const float a = fast_exp2(m[g] - mr);
+      const float b = fast_exp2(m2 - mr);
+      l[g] = l[g] * a + l2 * b;
+      m[g] = mn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] = o[g][e] * a + __shfl_xor(o[g][e], st) * b;
+    }
+  }
+  if (r == 0) {
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_o[wave][g][c * 8 + e] = o[g][e];
+      if (c == 0) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Merge the 4 waves and write: one thread per (head, 8 elements).
+  for (int it = tid; it < GC * LPT; it += kThreads) {
+    const int g = it / LPT, cc = it % LPT;
+    float mn = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) mn = fmaxf(mn, s_m[w][g]);
+    const float mr = (mn == -INFINITY) ? 0.f : mn;
+    float wt[kWaves];
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      wt[w] = fast_exp2(s_m[w][g] - mr);
+      L += s_l[w][g] * wt[w];
+    }
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float a = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) a = fmaf(wt[w], s_o[w][g][cc * 8 + e], a);
+      acc[e] = a;
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    const int64_t head_row = (int64_t)row * p.num_heads + h0 + g;
+    if constexpr (SPLIT) {
+      float* po = p.part_o + (head_row * p.max_partitions + blockIdx.z) * D + cc * 8;
+      typedef float f32x4 __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<f32x4*>(po) = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+      *reinterpret_cast<f32x4*>(po + 4) =
+          f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
+      if (cc == 0) {
+        float* pml = p.part_ml + (head_row * p.max_partitions + blockIdx.z) * 2;
+        pml[0] = mn;
+        pml[1] = L;
+      }
+    } else {
+      uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D + cc * 8;
+      u32x4 w;
+      w.x = E::round(acc[0] * inv) | (E::round(acc[1] * inv) << 16);
+      w.y = E::round(acc[2] * inv) | (E::round(acc[3] * inv) << 16);
+      w.z = E::round(acc[4] * inv) | (E::round(acc[5] * inv) << 16);
+      w.w = E::round(acc[6] * inv) | (E::round(acc[7] * inv) << 16);
+      *reinterpret_cast<u32x4*>(out) = w;
+    }
+  }
+}
+
+// Merge the partitions of one (row, head): o = sum_p w_p o_p / sum_p w_p with
+// w_p = l_p * 2^(m_p - max m). A row with one partition copies it, so v2 with a
+// single partition rounds exactly the value v1 rounds.
+template <int D, bool BF16>
+__global__ __launch_bounds__(kWave) void partition_reduce_kernel(const AttnParams p) {
+  using E = Elem<BF16>;
+  constexpr int EPL = D / kWave;  // 1, 2 or 4 elements per lane
+  const int h = blockIdx.x;
+  const int row = blockIdx.y;
+  const int lane = threadIdx.x;
+  int req, len;
+  row_context(p, row, req, len);
+  const int64_t head_row = (int64_t)row * p.num_heads + h;
+  uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D + lane * EPL;
+
+  float res[EPL];
+  const int np = (len + p.partition_size - 1) / p.partition_size;
+  const float* ml = p.part_ml + head_row * p.max_partitions * 2;
+  const float* po = p.part_o + head_row * p.max_partitions * D + lane * EPL;
+  if (np == 0) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) res[e] = 0.f;
+  } else if (np == 1) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) res[e] = po[e];
+  } else {
+    float mx = -INFINITY;
+    for (int i = lane; i < np; i += kWave) mx = fmaxf(mx, ml[2 * i]);
+#pragma unroll
+    for (int st = 1; st < kWave; st <<= 1) mx = fmaxf(mx, __shfl_xor(mx, st));
+    const float mr = (mx == -INFINITY) ? 0.f : mx;
+    float acc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
+    float L = 0.f;
+#pragma unroll 4
+    for (int i = 0; i < np; ++i) {
+      const float w = ml[2 * i + 1] * fast_exp2(ml[2 * i] - mr);
+      L += w;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) acc[e] = fmaf(w, po[(int64_t)i * D + e], acc[e]);
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) res[e] = acc[e] * inv;
+  }
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) out[e] = (uint16_t)E::round(res[e]);
+}
+
+// ---------------------------------------------------------------------------
+// Host-side dispatch.
+
+template <int D, int GC, bool BF16>
+static hipError_t launch_typed(const AttnParams& p, bool split, hipStream_t stream) {
+  constexpr int NLD = (D == 64) ? 2 : 4;
+  const dim3 block(kThreads);
+  const int hy = (p.num_heads / p.group) * p.head_chunks;
+  if (!split) {
+    hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, BF16, false>), dim3(p.n_rows, hy, 1),
+                       block, 0, stream, p);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, BF16, true>),
+                     dim3(p.n_rows, hy, p.max_partitions), block, 0, stream, p);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL((partition_reduce_kernel<D, BF16>), dim3(p.num_heads, p.n_rows, 1),
+                     dim3(kWave), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int D, bool BF16>
+static hipError_t launch_gc(const AttnParams& p, int gc, bool split, hipStream_t stream) {
+  switch (gc) {
+    case 1: return launch_typed<D, 1, BF16>(p, split, stream);
+    case 2: return launch_typed<D, 2, BF16>(p, split, stream);
+    case 3: return launch_typed<D, 3, BF16>(p, split, stream);
+    case 4: return launch_typed<D, 4, BF16>(p, split, stream);
+    case 5: return launch_typed<D, 5, BF16>(p, split, stream);
+    case 6: return launch_typed<D, 6, BF16>(p, split, stream);
+    case 7: return launch_typed<D, 7, BF16>(p, split, stream);
+    case 8: return launch_typed<D, 8, BF16>(p, split, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_paged_attention(const AttnParams& p, int head_dim, int gc, bool bf16, bool split,
+                                  hipStream_t stream) {
+  switch (head_dim) {
+    case 64: return bf16 ? launch_gc<64, true>(p, gc, split, stream)
+                         : launch_gc<64, false>(p, gc, split, stream);
+    case 128: return bf16 ? launch_gc<128, true>(p, gc, split, stream)
+                          : launch_gc<128, false>(p, gc, split, stream);
+    case 256: return bf16 ? launch_gc<256, true>(p, gc, split, stream)
+                          : launch_gc<256, false>(p, gc, split, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ayk

@@ -1,0 +1,120 @@
+"""Argument checks of the hip ops.
+
+The messages follow the reference's (``python/ayaka/ops/backends/torch/_checks.py:21-59``,
+``kvcache.py:39-62``) so that callers and tests read the same refusals. The
+hip backend computes in fp16 and bf16 only, on HIP devices, for head widths of
+64, 128 and 256 and power-of-two block sizes.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Sequence
+
+import torch
+
+from ayaka_amd.enums import KVLayoutKind
+from ayaka_amd.errors import BackendError
+from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+
+__all__ = [
+    "HEAD_DIMS",
+    "capturing",
+    "dtype_name",
+    "require_buffers",
+    "require_device",
+    "require_index_tensor",
+    "require_like",
+]
+
+HEAD_DIMS = frozenset({64, 128, 256})
+_DTYPES = (torch.float16, torch.bfloat16)
+_NAMES = {
+    torch.float16: "float16",
+    torch.bfloat16: "bfloat16",
+    torch.float32: "float32",
+    torch.float64: "float64",
+    torch.int32: "int32",
+    torch.int64: "int64",
+}
+
+
+def dtype_name(dtype: torch.dtype) -> str:
+    return _NAMES.get(dtype, str(dtype).removeprefix("torch."))
+
+
+def capturing(tensor: torch.Tensor) -> bool:
+    """Whether ``tensor``'s device is capturing a graph on the current stream."""
+    return tensor.is_cuda and torch.cuda.is_current_stream_capturing()
+
+
+def require_like(
+    op: str, name: str, tensor: torch.Tensor, shape: Sequence[int], dtype: torch.dtype
+) -> None:
+    if tuple(tensor.shape) != tuple(shape) or tensor.dtype != dtype:
+        raise BackendError(
+            f"{op}: {name} must be {dtype_name(dtype)} {list(shape)}, "
+            f"got {dtype_name(tensor.dtype)} {list(tensor.shape)}",
+            context={"op": op, "argument": name},
+        )
+    if not tensor.is_contiguous():
+        raise BackendError(f"{op}: {name} must be contiguous", context={"op": op, "argument": name})
+
+
+def require_index_tensor(op: str, name: str, tensor: torch.Tensor, *, ndim: int) -> None:
+    if tensor.dtype not in (torch.int32, torch.int64) or tensor.ndim != ndim:
+        raise BackendError(
+            f"{op}: {name} must be an int32 or int64 tensor with {ndim} dimension(s), "
+            f"got {dtype_name(tensor.dtype)} {list(tensor.shape)}",
+            context={"op": op, "argument": name},
+        )
+
+
+def require_device(op: str, name: str, tensor: torch.Tensor, device: torch.device) -> None:
+    if tensor.device != device:
+        raise BackendError(
+            f"{op}: {name} is on {tensor.device}, the cache is on {device}",
+            context={"op": op, "argument": name},
+        )
+
+
+def require_buffers(op: str, buffers: KVBuffers) -> None:
+    """Refuse a cache these kernels cannot read: layout, codec, shape, dtype, device, strides."""
+    if buffers.layout not in (KVLayoutKind.NHD, KVLayoutKind.HND):
+        raise BackendError(
+            f"{op}: the hip backend serves the NHD and HND layouts, not {buffers.layout}",
+            context={"op": op, "argument": "buffers"},
+        )
+    if buffers.codec != RAW_CODEC:
+        raise BackendError(
+            f"{op}: the hip backend stores the {RAW_CODEC!r} codec, not {buffers.codec!r}",
+            context={"op": op, "argument": "buffers"},
+        )
+    k = buffers.k
+    if k.dtype not in _DTYPES:
+        raise BackendError(
+            f"{op}: buffers.k is {dtype_name(k.dtype)}; the hip backend computes in "
+            "float16, bfloat16",
+            context={"op": op, "argument": "buffers.k"},
+        )
+    if k.ndim != 4:
+        raise BackendError(
+            f"{op}: buffers.k must have four dimensions, got {list(k.shape)}",
+            context={"op": op, "argument": "buffers"},
+        )
+    if tuple(buffers.v.shape) != tuple(k.shape) or buffers.v.dtype != k.dtype:
+        raise BackendError(
+            f"{op}: buffers.v must be {dtype_name(k.dtype)} {list(k.shape)}, "
+            f"got {dtype_name(buffers.v.dtype)} {list(buffers.v.shape)}",
+            context={"op": op, "argument": "buffers.v"},
+        )
+    if not (k.is_contiguous() and buffers.v.is_contiguous()):
+        raise BackendError(
+            f"{op}: buffers.k and buffers.v must be contiguous",
+            context={"op": op, "argument": "buffers"},
+        )
+    if not k.is_cuda or buffers.v.device != k.device:
+        raise BackendError(
+            f"{op}: the hip backend runs on a HIP device; buffers are on {k.device} "
+            f"and {buffers.v.device}",
+            context={"op": op, "argument": "buffers"},
+        )

@@ -1,0 +1,468 @@
+"""Attention over the paged cache with the MI355X kernels; implements the ``AttentionOps`` contract.
+
+``plan`` runs on the host once per step. It checks the step and derives
+positions, slots and lengths by the reference's rules
+(``python/ayaka/ops/backends/torch/attention.py:64-164``) and records the host
+facts ``attend`` needs to pick a launch without reading the device.
+
+``attend`` launches one of two kernels through ``libayaka_hip.so``:
+
+* v1 (``ayk_paged_attention_v1``): one workgroup per (row, key/value head)
+  streams the row's whole context once;
+* v2 (``ayk_paged_attention_v2``): one workgroup per (row, key/value head,
+  partition of :data:`PARTITION_SIZE` positions), then a log-sum-exp merge.
+
+:func:`choose_partitions` picks between them from the step's shape only, so a
+step computes the same thing eagerly and when replayed from a graph. Decode rows
+(one per request) and multi-row steps (prefill chunks, verify windows) use the
+same kernels: a multi-row step passes each row's request and position, and row
+``j`` attends to positions ``0 .. position_j`` (the reference's causal rule,
+``attention.py:209-234``).
+
+``graph_metadata`` / ``update_graph_metadata`` follow the reference's
+fixed-address record (``attention.py:274-374``): device tensors allocated once,
+host staging pinned, asynchronous copies on the current stream. ``attend`` on
+graph metadata reads nothing on the host that changes between replays: the
+launch shape comes from the bucket's table width.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from ayaka_amd.enums import ForwardMode, KVLayoutKind
+from ayaka_amd.attention import AttentionMetadata
+from ayaka_amd.errors import BackendError
+from ayaka_amd.hip import _lib
+from ayaka_amd.hip._checks import (
+    HEAD_DIMS,
+    capturing,
+    require_buffers,
+    require_device,
+    require_index_tensor,
+    require_like,
+)
+from ayaka_amd.kvcache import KVBuffers
+
+__all__ = [
+    "PARTITION_SIZE",
+    "HipAttentionPlan",
+    "HipGraphPlan",
+    "attend",
+    "attend_with",
+    "choose_partitions",
+    "graph_metadata",
+    "plan",
+    "update_graph_metadata",
+]
+
+#: Positions per v2 partition (a multiple of 64).
+PARTITION_SIZE = 512
+#: Compute units of one MI355X; the split heuristic aims to keep all of them busy.
+COMPUTE_UNITS = 256
+
+_LAYOUT_CODES = {KVLayoutKind.NHD: 0, KVLayoutKind.HND: 1}
+_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+
+
+@dataclass(frozen=True, slots=True)
+class HipAttentionPlan:
+    """Host facts of an eagerly planned step.
+
+    ``rows`` / ``kv_lengths`` are the per-request lists ``plan`` read;
+    ``max_length`` is the longest context any row attends to.
+    """
+
+    rows: tuple[int, ...]
+    kv_lengths: tuple[int, ...]
+    max_length: int
+
+
+@dataclass(frozen=True, slots=True, eq=False)
+class HipGraphPlan:
+    """Pinned host staging of a graph bucket, and its fixed table width."""
+
+    positions: torch.Tensor
+    slot_mapping: torch.Tensor
+    kv_lengths: torch.Tensor
+    block_table: torch.Tensor
+    max_blocks: int
+
+
+def _host_ints(tensor: torch.Tensor) -> tuple[int, ...]:
+    return tuple(int(x) for x in tensor.tolist())
+
+
+def plan(
+    mode: ForwardMode,
+    rows_per_request: torch.Tensor,
+    kv_lengths: torch.Tensor,
+    block_rows: torch.Tensor,
+    block_size: int,
+) -> AttentionMetadata:
+    """Check one step and build its metadata (reference ``torch/attention.py:64-110``)."""
+    op = "attention.plan"
+    require_index_tensor(op, "rows_per_request", rows_per_request, ndim=1)
+    require_index_tensor(op, "kv_lengths", kv_lengths, ndim=1)
+    require_index_tensor(op, "block_rows", block_rows, ndim=2)
+    batch = rows_per_request.shape[0]
+    if kv_lengths.shape[0] != batch or block_rows.shape[0] != batch:
+        raise BackendError(
+            f"{op}: rows_per_request, kv_lengths and block_rows must all describe the same "
+            f"requests, got {batch}, {kv_lengths.shape[0]} and {block_rows.shape[0]}",
+            context={"op": op},
+        )
+    if block_size < 1:
+        raise BackendError(f"{op}: block_size must be positive, got {block_size}", context={"op": op})
+    rows, lengths = _host_ints(rows_per_request), _host_ints(kv_lengths)
+    for index, (count, length) in enumerate(zip(rows, lengths)):
+        if count < 0 or length < 0:
+            raise BackendError(
+                f"{op}: request {index} has {count} rows and {length} tokens; neither can be "
+                "negative",
+                context={"op": op, "request": index},
+            )
+        if length and count > length:
+            raise BackendError(
+                f"{op}: request {index} has {count} query rows but only {length} tokens with "
+                "keys after this step; kv_lengths counts this step's rows",
+                context={"op": op, "request": index},
+            )
+        if mode == ForwardMode.DECODE and count != 1:
+            raise BackendError(
+                f"{op}: a DECODE step has one row per request, request {index} has {count}",
+                context={"op": op, "request": index},
+            )
+    total = sum(rows)
+    if mode == ForwardMode.IDLE and total:
+        raise BackendError(f"{op}: an IDLE step has no rows, got {total}", context={"op": op})
+
+    # The table: long enough for every request, and no padding block inside a used range.
+    table_host = block_rows.to(device="cpu", dtype=torch.int64)
+    max_blocks = table_host.shape[1]
+    needed = [-(-length // block_size) for length in lengths]
+    longest = max(needed, default=0)
+    if longest > max_blocks or (total > 0 and max_blocks == 0):
+        raise BackendError(
+            f"{op}: block_rows has {max_blocks} column(s) but the longest request needs "
+            f"{longest} blocks of {block_size}",
+            context={"op": op, "argument": "block_rows"},
+        )
+    if batch and max_blocks:
+        used = torch.arange(max_blocks)[None, :] < torch.tensor(needed, dtype=torch.int64)[:, None]
+        if bool((used & (table_host == 0)).any()):
+            raise BackendError(
+                f"{op}: block_rows has the padding block 0 inside a request's blocks",
+                context={"op": op, "argument": "block_rows"},
+            )
+
+    request_of_row: list[int] = []
+    positions: list[int] = []
+    slots: list[int] = []
+    table_list = table_host.tolist()
+    for request, (count, length) in enumerate(zip(rows, lengths)):
+        for j in range(count):
+            request_of_row.append(request)
+            if length == 0:
+                positions.append(0)
+                slots.append(0)
+            else:
+                position = length - count + j
+                positions.append(position)
+                slots.append(
+                    table_list[request][position // block_size] * block_size
+                    + position % block_size
+                )
+
+    device = rows_per_request.device
+    return AttentionMetadata(
+        mode=mode,
+        block_size=block_size,
+        rows_per_request=torch.tensor(rows, dtype=torch.int32, device=device),
+        request_of_row=torch.tensor(request_of_row, dtype=torch.int32, device=device),
+        positions=torch.tensor(positions, dtype=torch.int32, device=device),
+        slot_mapping=torch.tensor(slots, dtype=torch.int64, device=device),
+        kv_lengths=torch.tensor(lengths, dtype=torch.int32, device=device),
+        block_table=block_rows.to(device=device, dtype=torch.int32).contiguous(),
+        plan=HipAttentionPlan(rows, lengths, max(lengths, default=0)),
+    )
+
+
+def head_chunks(group: int) -> int:
+    """Workgroups that share one key/value head's query heads (at most 8 heads each)."""
+    for chunks in range(1, group + 1):
+        if group % chunks == 0 and group // chunks <= 8:
+            return chunks
+    return group
+
+
+def choose_partitions(n_rows: int, num_kv_heads: int, group: int, max_length: int) -> int:
+    """Partitions per row for v2, or 0 to run v1.
+
+    v1 gives one workgroup per (row, key/value head). When that is too few
+    workgroups to keep the 256 compute units streaming, or a context is long
+    enough that one workgroup's serial walk dominates, the context is split into
+    :data:`PARTITION_SIZE` pieces. Depends only on the step's shape.
+    """
+    if max_length <= PARTITION_SIZE:
+        return 0
+    workgroups = n_rows * num_kv_heads * head_chunks(group)
+    partitions = -(-max_length // PARTITION_SIZE)
+    if workgroups >= 8 * COMPUTE_UNITS and partitions <= 2:
+        return 0
+    return partitions
+
+
+_workspaces: dict[torch.device, torch.Tensor] = {}
+# Buffers a larger one replaced: a captured graph may still point at them, so they are never freed.
+_retired: list[torch.Tensor] = []
+
+
+def _workspace(op: str, device: torch.device, nbytes: int, capture: bool) -> torch.Tensor:
+    found = _workspaces.get(device)
+    if found is not None and found.numel() >= nbytes:
+        return found
+    if capture:
+        raise BackendError(
+            f"{op}: the v2 scratch for this step ({nbytes} bytes) is larger than the one "
+            "allocated so far; run the step once eagerly before capturing it",
+            context={"op": op},
+        )
+    size = max(nbytes, 2 * found.numel() if found is not None else 0, 1 << 20)
+    with torch.inference_mode(False):
+        fresh = torch.empty(size, dtype=torch.uint8, device=device)
+    if found is not None:
+        _retired.append(found)
+    _workspaces[device] = fresh
+    return fresh
+
+
+def attend(
+    q: torch.Tensor,
+    buffers: KVBuffers,
+    meta: AttentionMetadata,
+    out: torch.Tensor,
+    *,
+    scale: float,
+) -> None:
+    """Write every query row's attention output into ``out`` (reference ``attention.py:167-234``)."""
+    attend_with(q, buffers, meta, out, scale=scale, partitions=None)
+
+
+def attend_with(
+    q: torch.Tensor,
+    buffers: KVBuffers,
+    meta: AttentionMetadata,
+    out: torch.Tensor,
+    *,
+    scale: float,
+    partitions: int | None,
+) -> None:
+    """:func:`attend` with the launch chosen by the caller.
+
+    ``partitions`` 0 runs v1, a positive count runs v2 over that many partitions
+    (it must cover the step's longest context), ``None`` lets
+    :func:`choose_partitions` decide. Benchmarks and tests use it to time and
+    check both kernels on one step.
+    """
+    op = "attention.attend"
+    require_buffers(op, buffers)
+    step = meta.plan
+    table = meta.block_table
+    if not isinstance(step, (HipAttentionPlan, HipGraphPlan)) or not isinstance(table, torch.Tensor):
+        raise BackendError(
+            f"{op}: this step was planned by another backend; plan it with the same ops",
+            context={"op": op, "argument": "meta"},
+        )
+    if meta.block_size != buffers.block_size:
+        raise BackendError(
+            f"{op}: the step was planned for blocks of {meta.block_size} positions "
+            f"but the cache has blocks of {buffers.block_size}",
+            context={"op": op, "argument": "meta"},
+        )
+    heads = q.shape[1] if q.ndim == 3 else 0
+    n_rows = meta.request_of_row.shape[0]
+    require_like(op, "q", q, (n_rows, heads, buffers.head_dim), buffers.k.dtype)
+    require_like(op, "out", out, q.shape, q.dtype)
+    kv_heads = buffers.num_kv_heads
+    if heads == 0 or heads % kv_heads:
+        raise BackendError(
+            f"{op}: q has {heads} heads, which is not a positive multiple of the cache's "
+            f"{kv_heads} key/value heads",
+            context={"op": op, "argument": "q"},
+        )
+    if buffers.head_dim not in HEAD_DIMS:
+        raise BackendError(
+            f"{op}: the hip kernels are built for head widths {sorted(HEAD_DIMS)}, "
+            f"not {buffers.head_dim}",
+            context={"op": op, "argument": "buffers"},
+        )
+    block_size = buffers.block_size
+    if block_size & (block_size - 1):
+        raise BackendError(
+            f"{op}: the hip kernels need a power-of-two block size, not {block_size}",
+            context={"op": op, "argument": "buffers"},
+        )
+    device = buffers.k.device
+    for name, tensor in (
+        ("q", q),
+        ("out", out),
+        ("meta.kv_lengths", meta.kv_lengths),
+        ("meta.block_table", table),
+        ("meta.request_of_row", meta.request_of_row),
+        ("meta.positions", meta.positions),
+    ):
+        require_device(op, name, tensor, device)
+    decode = meta.mode == ForwardMode.DECODE
+    if isinstance(step, HipGraphPlan):
+        if not decode:
+            raise BackendError(f"{op}: graph metadata must be a DECODE step", context={"op": op})
+        max_length = step.max_blocks * block_size
+    else:
+        max_length = step.max_length
+    if n_rows == 0:
+        return
+    if table.dtype != torch.int32 or not table.is_contiguous() or table.ndim != 2:
+        raise BackendError(f"{op}: meta.block_table must be a contiguous int32 [B, max_blocks] tensor")
+
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    # Decode rows need no per-row indirection: row n is request n and sees its whole context.
+    row_request = 0 if decode else meta.request_of_row.data_ptr()
+    row_position = 0 if decode else meta.positions.data_ptr()
+    group = heads // kv_heads
+    common = (
+        out.data_ptr(),
+        q.data_ptr(),
+        buffers.k.data_ptr(),
+        buffers.v.data_ptr(),
+        table.data_ptr(),
+        table.stride(0),
+        meta.kv_lengths.data_ptr(),
+        row_request,
+        row_position,
+        n_rows,
+        heads,
+        kv_heads,
+        buffers.head_dim,
+        buffers.num_blocks,
+        block_size,
+        table.shape[1],
+        _LAYOUT_CODES[KVLayoutKind(buffers.layout)],
+        _DTYPE_CODES[q.dtype],
+        float(scale),
+    )
+    if partitions is None:
+        partitions = choose_partitions(n_rows, kv_heads, group, max_length)
+    elif partitions and partitions * PARTITION_SIZE < max_length:
+        raise BackendError(
+            f"{op}: {partitions} partitions of {PARTITION_SIZE} do not cover {max_length} positions",
+            context={"op": op},
+        )
+    if partitions == 0:
+        _lib.check(op, lib.ayk_paged_attention_v1(*common, stream))
+        return
+    nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, partitions)
+    scratch = _workspace(op, device, nbytes, capturing(q))
+    _lib.check(
+        op,
+        lib.ayk_paged_attention_v2(
+            *common, PARTITION_SIZE, partitions, scratch.data_ptr(), scratch.numel(), stream
+        ),
+    )
+
+
+def graph_metadata(
+    num_requests: int, max_blocks: int, block_size: int, device: torch.device
+) -> AttentionMetadata:
+    """Allocate the fixed metadata of a decode bucket (reference ``attention.py:274-305``)."""
+    if num_requests < 1 or max_blocks < 1 or block_size < 1:
+        raise BackendError(
+            "attention.graph_metadata: num_requests, max_blocks and block_size must be "
+            f"positive, got {num_requests}, {max_blocks} and {block_size}",
+            context={"op": "attention.graph_metadata"},
+        )
+    target = torch.device(device)
+    pinned = target.type == "cuda"
+
+    def host(shape: tuple[int, ...], dtype: torch.dtype) -> torch.Tensor:
+        return torch.zeros(shape, dtype=dtype, pin_memory=pinned)
+
+    staging = HipGraphPlan(
+        positions=host((num_requests,), torch.int32),
+        slot_mapping=host((num_requests,), torch.int64),
+        kv_lengths=host((num_requests,), torch.int32),
+        block_table=host((num_requests, max_blocks), torch.int32),
+        max_blocks=max_blocks,
+    )
+    return AttentionMetadata(
+        mode=ForwardMode.DECODE,
+        block_size=block_size,
+        rows_per_request=torch.ones(num_requests, dtype=torch.int32, device=target),
+        request_of_row=torch.arange(num_requests, dtype=torch.int32, device=target),
+        positions=torch.zeros(num_requests, dtype=torch.int32, device=target),
+        slot_mapping=torch.zeros(num_requests, dtype=torch.int64, device=target),
+        kv_lengths=torch.zeros(num_requests, dtype=torch.int32, device=target),
+        block_table=torch.zeros((num_requests, max_blocks), dtype=torch.int32, device=target),
+        plan=staging,
+    )
+
+
+def update_graph_metadata(
+    meta: AttentionMetadata, kv_lengths: torch.Tensor, block_rows: torch.Tensor
+) -> None:
+    """Write the next decode step into ``meta`` without waiting on the device.
+
+    Reference ``attention.py:308-374``: checks the host inputs, derives positions
+    and slots on the host, fills the pinned staging and queues asynchronous
+    copies on the current stream.
+    """
+    op = "attention.update_graph_metadata"
+    staging = meta.plan
+    table = meta.block_table
+    if not isinstance(staging, HipGraphPlan) or not isinstance(table, torch.Tensor):
+        raise BackendError(
+            f"{op}: meta was not made by this backend's graph_metadata",
+            context={"op": op, "argument": "meta"},
+        )
+    requests, max_blocks = staging.block_table.shape
+    for name, tensor, shape in (
+        ("kv_lengths", kv_lengths, (requests,)),
+        ("block_rows", block_rows, (requests, max_blocks)),
+    ):
+        if (
+            tuple(tensor.shape) != shape
+            or tensor.dtype != torch.int32
+            or tensor.device.type != "cpu"
+        ):
+            raise BackendError(
+                f"{op}: {name} must be an int32 CPU tensor of shape {list(shape)}, got "
+                f"{tensor.dtype} {list(tensor.shape)} on {tensor.device}",
+                context={"op": op, "argument": name},
+            )
+    block_size = meta.block_size
+    lengths = kv_lengths.long()
+    if bool((lengths < 0).any()) or bool((lengths > max_blocks * block_size).any()):
+        raise BackendError(
+            f"{op}: every length must be in [0, {max_blocks * block_size}] for a table of "
+            f"{max_blocks} blocks of {block_size}",
+            context={"op": op, "argument": "kv_lengths"},
+        )
+    real = lengths > 0
+    positions = torch.where(real, lengths - 1, 0)
+    block = block_rows.long().gather(1, (positions // block_size)[:, None])[:, 0]
+    staging.positions.copy_(positions)
+    staging.slot_mapping.copy_(torch.where(real, block * block_size + positions % block_size, 0))
+    staging.kv_lengths.copy_(kv_lengths)
+    staging.block_table.copy_(block_rows)
+    for device_tensor, host_tensor in (
+        (meta.positions, staging.positions),
+        (meta.slot_mapping, staging.slot_mapping),
+        (meta.kv_lengths, staging.kv_lengths),
+        (table, staging.block_table),
+    ):
+        device_tensor.copy_(host_tensor, non_blocking=True)
+
+

@@ -1,0 +1,195 @@
+"""Decode-attention benchmark on one MI355X: µs per call, KV bytes/s and the HBM roofline fraction.
+
+The workload is the headline configuration: Llama-3-8B-shape decode attention
+(32 query heads, 8 key/value heads, head_dim 128, bf16, block 16), batch 64 at
+4096 context, random block permutation over a 40000-block pool, synthetic
+N(0,1) data. A step is one ``attend`` call over the batch, with every input
+already resident in HBM. ``value`` is algorithmic bytes per call / time per call.
+
+Also reported, in the same JSON line: v1 and v2 timed separately, the
+roofline record of the dominant kernel, and the reference CPU algorithm
+(the oracle's restatement of ``_attend_decode``) timed on a bounded sample of
+the same workload on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=3, help="benchmark configuration 1-5 (3 = headline)")
+    ap.add_argument("--only", choices=["auto", "v1", "v2"], default=None,
+                    help="time only this launch (for profiler runs)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=8, help="rows of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def time_calls(fn, steps: int, warmup: int) -> dict:
+    """Per-call HIP-event times on the current stream, plus the whole timed region."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn()
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [s.elapsed_time(e) * 1000.0 for s, e in zip(starts, ends)]  # µs
+    return {"median_us": statistics.median(per), "mean_us": statistics.fmean(per), "min_us": min(per),
+            "wall_ms_per_step": wall * 1000.0 / steps}
+
+
+def cpu_baseline(step, cfg, rows: int) -> dict:
+    """The oracle's restatement of the reference CPU decode, timed on a sample of the batch."""
+    import numpy as np
+
+    from ayaka_amd import workloads
+    from oracle import paged
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    rows = min(rows, cfg.batch)
+    sample = workloads.sample_rows(step, list(range(rows)))
+    runs = []
+    for _ in range(6):  # 1 warm-up + 5 timed
+        t0 = time.perf_counter()
+        paged.attention(sample["q"], sample["k"], sample["v"], sample["table"], sample["lengths"],
+                        scale=cfg.scale, precision=np.float32)
+        runs.append(time.perf_counter() - t0)
+    seconds = statistics.median(runs[1:]) * cfg.batch / rows  # scaled to the whole batch
+    return {
+        "value": workloads.algorithmic_bytes(cfg) / seconds / 1e9,
+        "unit": "GB/s",
+        "us_per_call": seconds * 1e6,
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{rows} of {cfg.batch} rows of the same step, fp32 gather-then-softmax (numpy), "
+                  f"median of 5 runs after 1 warm-up, scaled by {cfg.batch}/{rows} to one call",
+    }
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(decode attention needs no collective; see the sharding note in DESIGN.md)", file=sys.stderr)
+        return 2
+    import torch
+
+    from ayaka_amd import workloads
+    from ayaka_amd.enums import ForwardMode, KVLayoutKind
+    from ayaka_amd.hip import _lib
+    from ayaka_amd.hip import attention as hip_attention
+    from ayaka_amd.hip import kvcache as hip_kvcache
+    from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    cfg = workloads.config(args.config)
+    step = workloads.build(cfg, dev, poison=False)
+    buffers = KVBuffers(step.k_cache, step.v_cache, KVLayoutKind.NHD, RAW_CODEC)
+    write = hip_attention.plan(ForwardMode.MIXED, step.rows_per_request, step.lengths, step.table, cfg.block_size)
+    hip_kvcache.store(step.k_new, step.v_new, buffers, write)
+    meta = hip_attention.plan(ForwardMode.DECODE, torch.ones(cfg.batch, dtype=torch.int32, device=dev),
+                              step.lengths, step.table, cfg.block_size)
+    out = torch.empty_like(step.q)
+    nbytes = workloads.algorithmic_bytes(cfg)
+    max_len = max(cfg.lengths)
+    auto_parts = hip_attention.choose_partitions(cfg.batch, cfg.kv_heads, cfg.heads // cfg.kv_heads, max_len)
+    launches = {
+        "auto": auto_parts,
+        "v1": 0,
+        "v2": -(-max_len // hip_attention.PARTITION_SIZE),
+    }
+    if args.only:
+        launches = {args.only: launches[args.only]}
+
+    results = {}
+    for name, parts in launches.items():
+        def call(parts=parts):
+            hip_attention.attend_with(step.q, buffers, meta, out, scale=cfg.scale, partitions=parts)
+        results[name] = time_calls(call, args.steps, args.warmup)
+        results[name]["partitions"] = parts
+        results[name]["gbs"] = nbytes / (results[name]["median_us"] * 1e-6) / 1e9
+        print(f"[bench] {cfg.name} {name}: {results[name]['median_us']:.1f} us/call "
+              f"{results[name]['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+
+    head = results.get("auto") or next(iter(results.values()))
+    store_us = time_calls(lambda: hip_kvcache.store(step.k_new, step.v_new, buffers, write), 50, 5)["median_us"]
+    kernel = "paged_attention_kernel (v1)" if head["partitions"] == 0 else \
+        "paged_attention_kernel (v2 split) + partition_reduce_kernel"
+    line = {
+        "metric": "decode-attention µs/call + achieved HBM GB/s (% of peak) at 1 MI355X",
+        "value": round(head["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["wall_ms_per_step"], 4),
+        "us_per_call": round(head["median_us"], 2),
+        "hbm_fraction": round(head["gbs"] / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg.dtype_label,
+        "data": "synthetic (seeded N(0,1) K/V/Q, random block permutation)",
+        "config": {
+            "workload": f"C{cfg.index} {cfg.name} decode attention: Hq {cfg.heads}, Hkv {cfg.kv_heads}, "
+                        f"D {cfg.head_dim}, {cfg.dtype_label}, block {cfg.block_size}, batch {cfg.batch}, "
+                        f"context {min(cfg.lengths)}-{max(cfg.lengths)} (sum {sum(cfg.lengths)}), "
+                        f"pool {cfg.num_blocks} blocks",
+            "algorithmic_bytes_per_call": nbytes,
+            "launch": "v1" if head["partitions"] == 0 else f"v2 x{head['partitions']} partitions of "
+                                                          f"{hip_attention.PARTITION_SIZE}",
+        },
+        "kernels": {k: {"us_per_call": round(v["median_us"], 2), "gbs": round(v["gbs"], 1),
+                        "partitions": v["partitions"]} for k, v in results.items()},
+        "kv_write": {"us_per_call": round(store_us, 2), "rows": int(step.k_new.shape[0]),
+                     "bytes": workloads.store_bytes(cfg)},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": kernel,
+            "achieved": round(head["gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(head["gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(step, cfg, args.cpu_rows)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

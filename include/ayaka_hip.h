@@ -1,0 +1,135 @@
+/*
+ * ayaka_hip.h -- C ABI of the MI355X (gfx950) paged-attention decode path.
+ *
+ * Every entry point is a plain C function over raw device pointers, sizes and a
+ * hipStream_t passed as `void*`. None of them allocates, frees or synchronises:
+ * the caller owns every buffer (the v2 scratch included) and the work is queued
+ * asynchronously on `stream`. Each returns AYK_OK (0) or an AYK_ERR_* code; the
+ * message of the last failure on the calling thread is ayk_last_error().
+ *
+ * The layouts are the ones Ayaka's ops contract defines
+ * (reference python/ayaka/ops/kvcache.py:8-38):
+ *   NHD cache: [num_blocks, block_size, num_kv_heads, head_dim], contiguous
+ *   HND cache: [num_blocks, num_kv_heads, block_size, head_dim], contiguous
+ *   slot = block_id * block_size + offset; block 0 is the padding block.
+ *   q / out:   [n_rows, num_heads, head_dim], contiguous
+ *   block table: int32 [n_requests, table_stride], row b lists request b's blocks.
+ * Query head h reads key/value head h / (num_heads / num_kv_heads).
+ *
+ * Ids are not range-checked against the caller's intent (reference
+ * python/ayaka/ops/kvcache.py:97-100), but nothing here reads or writes out of
+ * bounds on bad metadata: block ids are clamped into [0, num_blocks), lengths
+ * into the table width, and store drops rows whose slot is outside the pool.
+ */
+#ifndef AYAKA_HIP_H
+#define AYAKA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  AYK_OK = 0,
+  AYK_ERR_ARGUMENT = 1,    /* a size, pointer or combination the call cannot serve */
+  AYK_ERR_UNSUPPORTED = 2, /* a head width / dtype / layout no kernel is built for */
+  AYK_ERR_LAUNCH = 3,      /* the HIP runtime refused the launch */
+  AYK_ERR_WORKSPACE = 4    /* the v2 workspace is smaller than ayk_paged_attention_v2_workspace_bytes */
+};
+
+enum { AYK_DTYPE_FP16 = 0, AYK_DTYPE_BF16 = 1 };
+enum { AYK_LAYOUT_NHD = 0, AYK_LAYOUT_HND = 1 };
+
+/* Version of this ABI; bumped on any signature change. */
+int ayk_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* ayk_last_error(void);
+
+/*
+ * KV write ("reshape_and_cache"): row i of k and v ([n_rows, num_kv_heads,
+ * head_dim], contiguous, elem_bytes per element) is copied bit for bit into
+ * slot slot_mapping[i] of k_cache and v_cache. Replaces the reference's
+ * KVCacheOps.store, python/ayaka/ops/backends/torch/kvcache.py:65-80
+ * (an index_put by slot). Padding rows carry slot 0 and all land in block 0.
+ */
+int ayk_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
+                          const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t num_blocks, int32_t block_size,
+                          int32_t layout, int32_t elem_bytes, void* stream);
+
+/*
+ * Paged attention, single pass ("v1"): one workgroup per (row, key/value head)
+ * streams every page of that row's context once and serves the query heads of
+ * the group from it. Replaces the reference's decode attention,
+ * python/ayaka/ops/backends/torch/attention.py:237-271 (_attend_decode), and
+ * the row-causal multi-row path of the same file, :209-234.
+ *
+ * Rows: with request_of_row == NULL and positions == NULL, row i is request i
+ * and attends to positions [0, kv_lengths[i]) (a decode step). Otherwise row i
+ * belongs to request request_of_row[i] and attends to [0, positions[i] + 1)
+ * (reference python/ayaka/ops/attention.py:12-30). A row whose request has
+ * kv_lengths 0 is a padding row and gets zeros. Scores are scale * q.k in fp32,
+ * the softmax and the value sum are fp32, and out is rounded once.
+ * head_dim must be 64, 128 or 256 and block_size a power of two.
+ */
+int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,
+                           const int32_t* block_table, int64_t table_stride,
+                           const int32_t* kv_lengths, const int32_t* request_of_row,
+                           const int32_t* positions, int32_t n_rows, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                           int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
+                           float scale, void* stream);
+
+/* Bytes of scratch ayk_paged_attention_v2 needs for these sizes. */
+size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads, int32_t head_dim,
+                                              int32_t max_partitions);
+
+/*
+ * Paged attention, split context ("v2"): one workgroup per (row, key/value
+ * head, partition of partition_size positions) writes a partial result and its
+ * log-sum-exp state into `workspace`, then a reduce kernel merges the
+ * partitions of each (row, head) and rounds once. Same arguments and semantics
+ * as v1, plus the partition size (a positive multiple of 64) and the number of
+ * partitions the grid covers: every row's length must be at most
+ * max_partitions * partition_size (positions beyond it are not read). The math
+ * the reference delegates to flashinfer's split-KV decode
+ * (python/ayaka/ops/backends/flashinfer/attention.py:240-251, :326).
+ */
+int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const void* v_cache,
+                           const int32_t* block_table, int64_t table_stride,
+                           const int32_t* kv_lengths, const int32_t* request_of_row,
+                           const int32_t* positions, int32_t n_rows, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                           int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
+                           float scale, int32_t partition_size, int32_t max_partitions,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Whole-block copies of both caches; block_bytes is the size of one block of
+ * one cache (block_size * num_kv_heads * head_dim * elem_bytes), the same in
+ * either layout. Ids are int64 when ids_are_64bit, else int32.
+ *
+ * ayk_gather_blocks: out_k[i] = k_cache[block_ids[i]] (and v), for i < n.
+ *   Replaces python/ayaka/ops/backends/torch/kvcache.py:83-93 (gather).
+ * ayk_copy_blocks: block dst[i] = block src[i] in both caches.
+ *   Replaces python/ayaka/ops/backends/torch/kvcache.py:96-107 (copy_blocks).
+ * ayk_zero_blocks: every byte of the listed blocks set to zero.
+ *   Replaces python/ayaka/ops/backends/torch/kvcache.py:110-115 (zero_blocks).
+ */
+int ayk_gather_blocks(const void* k_cache, const void* v_cache, void* out_k, void* out_v,
+                      const void* block_ids, int32_t ids_are_64bit, int64_t n, int32_t num_blocks,
+                      int64_t block_bytes, void* stream);
+int ayk_copy_blocks(void* k_cache, void* v_cache, const void* src, const void* dst,
+                    int32_t ids_are_64bit, int64_t n, int32_t num_blocks, int64_t block_bytes,
+                    void* stream);
+int ayk_zero_blocks(void* k_cache, void* v_cache, const void* block_ids, int32_t ids_are_64bit,
+                    int64_t n, int32_t num_blocks, int64_t block_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AYAKA_HIP_H */

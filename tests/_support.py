@@ -1,0 +1,157 @@
+"""Builders shared by the tests: small paged scenarios with NaN-poisoned caches.
+
+Modelled on the reference's test builder (``tests/ops/test_attention_contract.py:72-141``):
+each request gets random keys/values at its positions, its blocks are drawn
+from a seeded permutation of the pool (never block 0), and every slot nobody
+wrote holds NaN, so reading block 0, an unused block or the unwritten tail of a
+block shows up as NaN. Values are drawn in float32 and rounded to the cache
+dtype, and kept both as raw 16-bit words (for the device) and widened back to
+float32 (for the oracle), so both sides see identical inputs.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from oracle import paged
+from oracle.numerics import bits_to_f32, f32_to_bits
+
+NAN_BITS = {"bf16": 0x7FC0, "fp16": 0x7E00}
+
+
+@dataclass
+class Scenario:
+    dtype: str
+    layout: str
+    block_size: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    rows: list[int]
+    lengths: list[int]
+    mode: str
+    table: np.ndarray  # [B, max_blocks] int64
+    q_bits: np.ndarray  # [N, H, D] uint16
+    k_bits: np.ndarray  # cache words in the scenario's layout
+    v_bits: np.ndarray
+    plan: dict[str, np.ndarray]
+    scale: float
+
+    @property
+    def q(self) -> np.ndarray:
+        return bits_to_f32(self.q_bits, self.dtype)
+
+    @property
+    def k(self) -> np.ndarray:
+        return bits_to_f32(self.k_bits, self.dtype)
+
+    @property
+    def v(self) -> np.ndarray:
+        return bits_to_f32(self.v_bits, self.dtype)
+
+    def expected(self, precision: type = np.float64) -> np.ndarray:
+        decode = self.mode == "decode"
+        return paged.attention(
+            self.q,
+            self.k,
+            self.v,
+            self.table,
+            np.asarray(self.lengths),
+            scale=self.scale,
+            layout=self.layout,
+            request_of_row=None if decode else self.plan["request_of_row"],
+            positions=None if decode else self.plan["positions"],
+            precision=precision,
+        )
+
+
+def build_scenario(
+    steps: list[tuple[int, int]],
+    *,
+    dtype: str = "bf16",
+    layout: str = "nhd",
+    heads: int = 4,
+    kv_heads: int = 2,
+    head_dim: int = 64,
+    block_size: int = 4,
+    mode: str = "mixed",
+    seed: int = 0,
+    spare_blocks: int = 3,
+    scale: float | None = None,
+) -> Scenario:
+    """A paged cache holding each request's context; ``steps`` is ``[(rows, length), ...]``."""
+    rng = np.random.default_rng(seed)
+    needed = [-(-length // block_size) for _, length in steps]
+    num_blocks = 1 + sum(needed) + spare_blocks
+    nhd_shape = (num_blocks, block_size, kv_heads, head_dim)
+    k_nhd = np.full(nhd_shape, NAN_BITS[dtype], dtype=np.uint16)
+    v_nhd = np.full(nhd_shape, NAN_BITS[dtype], dtype=np.uint16)
+    free = list(rng.permutation(np.arange(1, num_blocks)))
+    table = np.zeros((len(steps), max(needed, default=0) or 1), dtype=np.int64)
+    for b, ((_, length), n) in enumerate(zip(steps, needed)):
+        blocks = [int(free.pop()) for _ in range(n)]
+        table[b, :n] = blocks
+        ctx_k = f32_to_bits(rng.standard_normal((length, kv_heads, head_dim)).astype(np.float32), dtype)
+        ctx_v = f32_to_bits(rng.standard_normal((length, kv_heads, head_dim)).astype(np.float32), dtype)
+        for pos in range(length):
+            k_nhd[blocks[pos // block_size], pos % block_size] = ctx_k[pos]
+            v_nhd[blocks[pos // block_size], pos % block_size] = ctx_v[pos]
+    rows = [r for r, _ in steps]
+    lengths = [n for _, n in steps]
+    q_bits = f32_to_bits(
+        rng.standard_normal((sum(rows), heads, head_dim)).astype(np.float32), dtype
+    )
+    if layout == "hnd":
+        k_bits = np.ascontiguousarray(k_nhd.transpose(0, 2, 1, 3))
+        v_bits = np.ascontiguousarray(v_nhd.transpose(0, 2, 1, 3))
+    else:
+        k_bits, v_bits = k_nhd, v_nhd
+    return Scenario(
+        dtype=dtype,
+        layout=layout,
+        block_size=block_size,
+        heads=heads,
+        kv_heads=kv_heads,
+        head_dim=head_dim,
+        rows=rows,
+        lengths=lengths,
+        mode=mode,
+        table=table,
+        q_bits=q_bits,
+        k_bits=k_bits,
+        v_bits=v_bits,
+        plan=paged.plan(mode, rows, lengths, table, block_size),
+        scale=head_dim**-0.5 if scale is None else scale,
+    )
+
+
+def brute_force(s: Scenario) -> np.ndarray:
+    """Pure-Python float64 attention, one row, head and position at a time (tiny inputs only)."""
+    q, k, v = s.q.astype(np.float64), paged.nhd(s.k, s.layout), paged.nhd(s.v, s.layout)
+    group = s.heads // s.kv_heads
+    out = np.zeros(q.shape)
+    row = 0
+    for b, (count, length) in enumerate(zip(s.rows, s.lengths)):
+        for j in range(count):
+            if length:
+                visible = length - count + j + 1
+                for h in range(s.heads):
+                    kvh = h // group
+                    scores = []
+                    for pos in range(visible):
+                        blk, off = s.table[b, pos // s.block_size], pos % s.block_size
+                        dot = 0.0
+                        for d in range(s.head_dim):
+                            dot += q[row, h, d] * float(k[blk, off, kvh, d])
+                        scores.append(dot * s.scale)
+                    top = max(scores)
+                    weights = [np.exp(x - top) for x in scores]
+                    total = sum(weights)
+                    for pos in range(visible):
+                        blk, off = s.table[b, pos // s.block_size], pos % s.block_size
+                        for d in range(s.head_dim):
+                            out[row, h, d] += weights[pos] / total * float(v[blk, off, kvh, d])
+            row += 1
+    return out

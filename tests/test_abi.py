@@ -1,0 +1,74 @@
+"""The C ABI library: it loads, exports every function ``include/ayaka_hip.h`` declares,
+and refuses bad arguments on the host (no kernel is launched here)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from ayaka_amd.hip import _lib
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "ayaka_hip.h"
+
+
+def declared() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return re.findall(r"\b(ayk_\w+)\s*\(", text)
+
+
+def test_every_declared_function_is_exported_and_bound() -> None:
+    names = declared()
+    assert len(names) == 9
+    lib = _lib.lib()
+    for name in names:
+        assert hasattr(lib, name), name
+    assert sorted(names) == sorted(_lib.EXPORTS)
+    assert lib.ayk_abi_version() == _lib.ABI_VERSION
+
+
+def test_workspace_size() -> None:
+    lib = _lib.lib()
+    assert lib.ayk_paged_attention_v2_workspace_bytes(64, 32, 128, 8) == 64 * 32 * 8 * (128 + 2) * 4
+    assert lib.ayk_paged_attention_v2_workspace_bytes(0, 32, 128, 8) == 0
+
+
+def _v1(lib: ctypes.CDLL, **kw: object) -> int:
+    args = dict(out=1, q=1, k=1, v=1, table=1, stride=4, lengths=1, ror=None, pos=None, n_rows=1,
+                heads=8, kv_heads=2, head_dim=128, num_blocks=10, block_size=16, max_blocks=4,
+                layout=0, dtype=1, scale=ctypes.c_float(1.0), stream=None)
+    args.update(kw)
+    return lib.ayk_paged_attention_v1(*args.values())
+
+
+@pytest.mark.parametrize(
+    "changes,code,message",
+    [
+        ({"head_dim": 96}, 2, b"head_dim 96"),
+        ({"dtype": 5}, 2, b"dtype 5"),
+        ({"layout": 3}, 2, b"layout 3"),
+        ({"heads": 6, "kv_heads": 4}, 1, b"not a positive multiple"),
+        ({"block_size": 12}, 2, b"power of two"),
+        ({"ror": 1}, 1, b"together"),
+        ({"q": None}, 1, b"null"),
+        ({"stride": 2}, 1, b"table_stride"),
+    ],
+)
+def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, message: bytes) -> None:
+    lib = _lib.lib()
+    assert _v1(lib, **changes) == code
+    assert message in lib.ayk_last_error()
+
+
+def test_v2_and_store_refusals() -> None:
+    lib = _lib.lib()
+    base = [1, 1, 1, 1, 1, 4, 1, None, None, 1, 8, 2, 128, 10, 16, 4, 0, 1, ctypes.c_float(1.0)]
+    assert lib.ayk_paged_attention_v2(*base, 100, 4, 1, 1 << 20, None) == 1
+    assert b"multiple of 64" in lib.ayk_last_error()
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, 1, 16, None) == 4
+    assert b"workspace" in lib.ayk_last_error()
+    assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 3, None) == 2
+    assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 0, 2, 64, 10, 16, 0, 2, None) == 0
+    assert lib.ayk_zero_blocks(1, 1, 1, 0, 2, 0, 64, None) == 1

@@ -1,0 +1,404 @@
+"""Parity of the HIP path with the oracle, on a HIP device (MI355X).
+
+Every call goes through the C ABI of ``libayaka_hip.so`` (via the ``hip``
+backend's ops, and once directly with ctypes). Bars:
+
+* KV write and block ops: bit-exact.
+* Attention: against the float64 oracle, ``max_abs_excess`` (error beyond half
+  an output ulp) <= 2e-3 and ``rel_l2`` (against the oracle rounded once to the
+  output dtype) <= 1e-3; plus the reference tests' own bound
+  ``|out - exact| <= 4 eps max|y|`` (``tests/ops/test_parity.py:196-201``).
+  The oracle's own rounded fp32 result is held to the same metrics and reported.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from ayaka_amd import workloads
+from ayaka_amd.enums import ForwardMode, KVLayoutKind
+from ayaka_amd.errors import BackendError
+from ayaka_amd.hip import _lib
+from ayaka_amd.hip import attention as hip_attention
+from ayaka_amd.hip import kvcache as hip_kvcache
+from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+from oracle import paged
+from oracle.numerics import bits_to_f32, f32_to_bits, parity_report
+from tests._support import Scenario, build_scenario
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+TORCH_DTYPES = {"bf16": torch.bfloat16, "fp16": torch.float16}
+EPS = {"bf16": 2.0**-7, "fp16": 2.0**-10}
+DEV = torch.device("cuda:0")
+
+
+def to_device(bits: np.ndarray, dtype: str) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(TORCH_DTYPES[dtype]).to(DEV)
+
+
+def to_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def assert_parity(out: torch.Tensor, expected: np.ndarray, dtype: str, label: str = "") -> dict:
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all(), f"{label}: non-finite output"
+    rep = parity_report(got, expected, dtype)
+    ref = parity_report(bits_to_f32(f32_to_bits(expected.astype(np.float32), dtype), dtype), expected, dtype)
+    bound = 4 * EPS[dtype] * float(np.abs(expected).max(initial=0.0))
+    worst = float(np.abs(got - expected).max(initial=0.0))
+    assert rep["max_abs_excess"] <= 2e-3, f"{label}: {rep} (reference rounding: {ref})"
+    assert rep["rel_l2"] <= 1e-3, f"{label}: {rep} (reference rounding: {ref})"
+    assert worst <= max(bound, 1e-6), f"{label}: {worst} > 4 eps max|y| = {bound}"
+    return rep
+
+
+def scenario_buffers(s: Scenario) -> KVBuffers:
+    layout = KVLayoutKind.NHD if s.layout == "nhd" else KVLayoutKind.HND
+    return KVBuffers(to_device(s.k_bits, s.dtype), to_device(s.v_bits, s.dtype), layout, RAW_CODEC)
+
+
+def plan_scenario(s: Scenario):
+    mode = ForwardMode(s.mode)
+    return hip_attention.plan(
+        mode,
+        torch.tensor(s.rows, dtype=torch.int32, device=DEV),
+        torch.tensor(s.lengths, dtype=torch.int32, device=DEV),
+        torch.from_numpy(s.table).to(DEV),
+        s.block_size,
+    )
+
+
+def run_attention(s: Scenario, partitions: int | None = None) -> torch.Tensor:
+    buffers = scenario_buffers(s)
+    meta = plan_scenario(s)
+    q = to_device(s.q_bits, s.dtype)
+    out = torch.full_like(q, 7.0)
+    hip_attention.attend_with(q, buffers, meta, out, scale=s.scale, partitions=partitions)
+    torch.cuda.synchronize()
+    return out
+
+
+# --- KV write --------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+@pytest.mark.parametrize("head_dim", [64, 128, 8, 12])
+def test_store_is_bit_exact(dtype: str, layout: str, head_dim: int) -> None:
+    s = build_scenario([(3, 9), (1, 2), (2, 0), (5, 40)], dtype=dtype, layout=layout, head_dim=head_dim,
+                       block_size=4, seed=21)
+    rng = np.random.default_rng(5)
+    n = sum(s.rows)
+    k_new = f32_to_bits(rng.standard_normal((n, s.kv_heads, head_dim)).astype(np.float32), dtype)
+    v_new = f32_to_bits(rng.standard_normal((n, s.kv_heads, head_dim)).astype(np.float32), dtype)
+    buffers = scenario_buffers(s)
+    meta = plan_scenario(s)
+    assert meta.slot_mapping.cpu().tolist() == s.plan["slot_mapping"].tolist()
+    hip_kvcache.store(to_device(k_new, dtype), to_device(v_new, dtype), buffers, meta)
+    torch.cuda.synchronize()
+    want_k, want_v = s.k_bits.copy(), s.v_bits.copy()
+    paged.store(want_k, want_v, k_new, v_new, s.plan["slot_mapping"], layout)
+    got_k, got_v = to_bits(buffers.k), to_bits(buffers.v)
+    # block 0 receives the padding rows in an unspecified order; every other block is exact
+    assert np.array_equal(got_k[1:], want_k[1:])
+    assert np.array_equal(got_v[1:], want_v[1:])
+
+
+def test_store_of_an_empty_step_is_a_no_op() -> None:
+    s = build_scenario([(1, 3)], mode="decode", seed=2)
+    buffers = scenario_buffers(s)
+    meta = hip_attention.plan(
+        ForwardMode.IDLE,
+        torch.zeros(0, dtype=torch.int32, device=DEV),
+        torch.zeros(0, dtype=torch.int32, device=DEV),
+        torch.zeros((0, 1), dtype=torch.int32, device=DEV),
+        s.block_size,
+    )
+    empty = torch.empty((0, s.kv_heads, s.head_dim), dtype=torch.bfloat16, device=DEV)
+    hip_kvcache.store(empty, empty, buffers, meta)
+    out = torch.empty((0, s.heads, s.head_dim), dtype=torch.bfloat16, device=DEV)
+    hip_attention.attend(out, buffers, meta, out.clone(), scale=1.0)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_bits(buffers.k), s.k_bits)
+
+
+# --- attention: the reference's contract cases ---------------------------------------------
+
+CASES = [
+    ("one-block", [(1, 16), (1, 16)], "decode"),
+    ("block-multiples", [(1, 32), (1, 48)], "decode"),
+    ("ends-inside-blocks", [(1, 1), (1, 15), (1, 17), (1, 31), (1, 33)], "decode"),
+    ("padding-requests", [(1, 6), (1, 0), (1, 70), (1, 0)], "decode"),
+    ("parity-lengths", [(1, 1), (1, 16), (1, 17), (1, 70)], "decode"),
+    ("prefill-chunks", [(16, 16), (5, 5), (3, 11), (4, 12), (1 + 3, 9)], "mixed"),
+    ("mixed-batch", [(7, 7), (1, 9), (4, 16), (2, 2), (1, 1), (3, 6), (2, 0)], "mixed"),
+]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+@pytest.mark.parametrize("name,steps,mode", CASES, ids=[c[0] for c in CASES])
+def test_attention_contract_cases(dtype: str, layout: str, name: str, steps: list, mode: str) -> None:
+    s = build_scenario(steps, dtype=dtype, layout=layout, heads=8, kv_heads=2, head_dim=64,
+                       block_size=16, mode=mode, seed=31)
+    expected = s.expected(np.float64)
+    for partitions in (0, 1):
+        out = run_attention(s, partitions)
+        assert_parity(out, expected, dtype, f"{name}/{partitions}")
+        padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
+        if padding_rows:
+            assert torch.count_nonzero(out[padding_rows]) == 0
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(4, 4), (4, 2), (6, 1), (8, 4), (8, 1), (12, 4), (9, 3), (64, 8), (16, 1)])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_grouped_query_heads(heads: int, kv_heads: int, head_dim: int) -> None:
+    s = build_scenario([(1, 37), (1, 200), (3, 10)], heads=heads, kv_heads=kv_heads, head_dim=head_dim,
+                       block_size=16, seed=41)
+    assert_parity(run_attention(s), s.expected(np.float64), "bf16", f"{heads}/{kv_heads}/{head_dim}")
+
+
+@pytest.mark.parametrize("block_size", [1, 4, 8, 16, 32, 64])
+def test_block_sizes(block_size: int) -> None:
+    s = build_scenario([(1, 1), (1, 63), (1, 130), (2, 70)], block_size=block_size, head_dim=128,
+                       heads=8, kv_heads=2, seed=43)
+    assert_parity(run_attention(s), s.expected(np.float64), "bf16", f"bs{block_size}")
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_split_partitions_agree_with_the_oracle_and_v1(dtype: str, head_dim: int) -> None:
+    # contexts across several 512-position partitions, one ending inside a block and a partition
+    s = build_scenario([(1, 1500), (1, 513), (1, 512), (1, 2048), (1, 7), (1, 0)], dtype=dtype,
+                       head_dim=head_dim, heads=8, kv_heads=2, block_size=16, mode="decode", seed=47)
+    expected = s.expected(np.float64)
+    v1 = run_attention(s, 0)
+    v2 = run_attention(s, 4)
+    assert_parity(v1, expected, dtype, "v1")
+    assert_parity(v2, expected, dtype, "v2")
+    auto = run_attention(s, None)
+    assert_parity(auto, expected, dtype, "auto")
+
+
+def test_one_partition_reproduces_v1_bit_for_bit() -> None:
+    s = build_scenario([(1, 300), (1, 17), (1, 512)], heads=8, kv_heads=2, head_dim=128, block_size=16,
+                       mode="decode", seed=53)
+    v1 = run_attention(s, 0)
+    v2 = run_attention(s, 1)
+    assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
+
+
+def test_one_visible_key_returns_its_value_exactly() -> None:
+    s = build_scenario([(1, 1), (1, 1)], heads=4, kv_heads=2, head_dim=64, block_size=16, mode="decode", seed=3)
+    out = run_attention(s)
+    v = paged.nhd(s.v_bits, s.layout)
+    for b in range(2):
+        want = np.repeat(v[s.table[b, 0], 0], 2, axis=0)
+        assert np.array_equal(to_bits(out[b]), want)
+
+
+def test_scale_zero_averages_the_visible_values() -> None:
+    s = build_scenario([(2, 600)], heads=4, kv_heads=2, head_dim=64, block_size=16, seed=5, scale=0.0)
+    assert_parity(run_attention(s), s.expected(np.float64), "bf16", "scale0")
+
+
+def test_the_cache_is_only_read() -> None:
+    s = build_scenario([(3, 90), (1, 700)], heads=4, kv_heads=2, head_dim=64, block_size=16, seed=6)
+    buffers = scenario_buffers(s)
+    meta = plan_scenario(s)
+    q = to_device(s.q_bits, s.dtype)
+    out = torch.empty_like(q)
+    hip_attention.attend(q, buffers, meta, out, scale=s.scale)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_bits(buffers.k), s.k_bits) and np.array_equal(to_bits(buffers.v), s.v_bits)
+
+
+def test_golden_fixture() -> None:
+    data = np.load(GOLDEN / "smollm2_small.npz")
+    buffers = KVBuffers(to_device(data["k_cache_before"], "fp16"), to_device(data["v_cache_before"], "fp16"),
+                        KVLayoutKind.NHD, RAW_CODEC)
+    table = torch.from_numpy(data["table"]).to(DEV)
+    lengths = torch.from_numpy(data["lengths"]).to(DEV)
+    write = hip_attention.plan(ForwardMode.MIXED, torch.from_numpy(data["rows_per_request"]).to(DEV), lengths,
+                               table, 16)
+    assert write.slot_mapping.cpu().numpy().tolist() == data["slot_mapping"].tolist()
+    hip_kvcache.store(to_device(data["k_new"], "fp16"), to_device(data["v_new"], "fp16"), buffers, write)
+    decode = hip_attention.plan(ForwardMode.DECODE, torch.ones(4, dtype=torch.int32, device=DEV), lengths, table, 16)
+    q = to_device(data["q"], "fp16")
+    out = torch.empty_like(q)
+    hip_attention.attend(q, buffers, decode, out, scale=float(data["scale"]))
+    torch.cuda.synchronize()
+    assert np.array_equal(to_bits(buffers.k), data["k_cache"])
+    assert np.array_equal(to_bits(buffers.v), data["v_cache"])
+    assert_parity(out, data["expected"], "fp16", "golden")
+
+
+# --- benchmark configurations at full size --------------------------------------------------
+
+SAMPLES = {1: [0, 1, 2, 3], 2: list(range(32)), 3: [0, 21, 42, 63], 4: [0, 3, 7], 5: None}
+
+
+@pytest.mark.parametrize("index", [1, 2, 3, 4, 5])
+def test_benchmark_configuration(index: int) -> None:
+    cfg = workloads.config(index)
+    print(f"config {index} {cfg.name}", flush=True)
+    step = workloads.build(cfg, DEV)
+    layout = KVLayoutKind.NHD
+    buffers = KVBuffers(step.k_cache, step.v_cache, layout, RAW_CODEC)
+    write = hip_attention.plan(ForwardMode.MIXED, step.rows_per_request, step.lengths, step.table, cfg.block_size)
+    hip_kvcache.store(step.k_new, step.v_new, buffers, write)
+    # the write is bit-exact: read the slots back
+    slots = write.slot_mapping
+    got_k = step.k_cache.view(-1, cfg.kv_heads, cfg.head_dim)[slots]
+    got_v = step.v_cache.view(-1, cfg.kv_heads, cfg.head_dim)[slots]
+    assert torch.equal(got_k.view(torch.int16), step.k_new.view(torch.int16))
+    assert torch.equal(got_v.view(torch.int16), step.v_new.view(torch.int16))
+
+    decode = hip_attention.plan(ForwardMode.DECODE, torch.ones(cfg.batch, dtype=torch.int32, device=DEV),
+                                step.lengths, step.table, cfg.block_size)
+    outs = {}
+    for name, parts in (("v1", 0), ("v2", -(-max(cfg.lengths) // hip_attention.PARTITION_SIZE)), ("auto", None)):
+        out = torch.empty_like(step.q)
+        hip_attention.attend_with(step.q, buffers, decode, out, scale=cfg.scale, partitions=parts)
+        outs[name] = out
+    torch.cuda.synchronize()
+    rows = SAMPLES[index]
+    if rows is None:  # the shortest, the longest and a spread between
+        order = np.argsort(cfg.lengths)
+        rows = sorted({int(order[0]), int(order[-1]), *[int(order[i]) for i in range(0, cfg.batch, 37)]})
+    sample = workloads.sample_rows(step, rows)
+    expected = paged.attention(sample["q"], sample["k"], sample["v"], sample["table"], sample["lengths"],
+                               scale=cfg.scale, precision=np.float64)
+    for name, out in outs.items():
+        assert_parity(out[rows], expected, cfg.dtype_label, f"config {index} {name}")
+    # size-independent: v1 and v2 agree on every row, and every row is finite
+    for out in outs.values():
+        assert torch.isfinite(out.float()).all()
+    diff = (outs["v1"].float() - outs["v2"].float()).abs().max().item()
+    assert diff <= 4 * EPS[cfg.dtype_label] * outs["v1"].float().abs().max().item() + 1e-6
+
+
+# --- graph metadata and capture ---------------------------------------------------------------
+
+
+def test_graph_metadata_replays_match_eager_steps() -> None:
+    rng = np.random.default_rng(61)
+    heads, kv_heads, dim, bs, max_blocks, bucket = 8, 2, 128, 16, 80, 4
+    num_blocks = 1 + bucket * max_blocks
+    k_cache = (torch.randn((num_blocks, bs, kv_heads, dim), device=DEV)).to(torch.bfloat16)
+    v_cache = (torch.randn((num_blocks, bs, kv_heads, dim), device=DEV)).to(torch.bfloat16)
+    buffers = KVBuffers(k_cache, v_cache, KVLayoutKind.NHD, RAW_CODEC)
+    perm = rng.permutation(np.arange(1, num_blocks)).reshape(bucket, max_blocks).astype(np.int32)
+    meta = hip_attention.graph_metadata(bucket, max_blocks, bs, DEV)
+    q = torch.zeros((bucket, heads, dim), dtype=torch.bfloat16, device=DEV)
+    k_new = torch.zeros((bucket, kv_heads, dim), dtype=torch.bfloat16, device=DEV)
+    v_new = torch.zeros_like(k_new)
+    out = torch.zeros_like(q)
+
+    def step() -> None:
+        hip_kvcache.store(k_new, v_new, buffers, meta)
+        hip_attention.attend(q, buffers, meta, out, scale=dim**-0.5)
+
+    # one eager step sizes the scratch, then capture
+    lengths0 = torch.tensor([1, 1, 1, 1], dtype=torch.int32)
+    hip_attention.update_graph_metadata(meta, lengths0, torch.from_numpy(perm))
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        step()
+    torch.cuda.current_stream().wait_stream(stream)
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for trial, lens in enumerate([[5, 0, 1000, 17], [1280, 640, 0, 0], [33, 1, 2, 900]]):
+        lengths = torch.tensor(lens, dtype=torch.int32)
+        table = torch.from_numpy(perm.copy())
+        q.copy_(torch.randn(q.shape, device=DEV).to(torch.bfloat16))
+        k_new.copy_(torch.randn(k_new.shape, device=DEV).to(torch.bfloat16))
+        v_new.copy_(torch.randn(v_new.shape, device=DEV).to(torch.bfloat16))
+        hip_attention.update_graph_metadata(meta, lengths, table)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        # the same step planned eagerly, on a copy of the cache after the replay's write
+        eager_meta = hip_attention.plan(ForwardMode.DECODE, torch.ones(bucket, dtype=torch.int32, device=DEV),
+                                        lengths.to(DEV), table.to(DEV), bs)
+        eager_out = torch.empty_like(out)
+        hip_attention.attend(q, buffers, eager_meta, eager_out, scale=dim**-0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(replayed.view(torch.int16), eager_out.view(torch.int16)), f"replay {trial}"
+        assert torch.count_nonzero(replayed[[i for i, n in enumerate(lens) if n == 0]]) == 0
+
+
+# --- block ops ------------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+@pytest.mark.parametrize("ids_dtype", [torch.int32, torch.int64])
+def test_block_ops_are_bit_exact(layout: str, ids_dtype: torch.dtype) -> None:
+    s = build_scenario([(1, 40), (1, 9)], layout=layout, head_dim=128, block_size=16, spare_blocks=6, seed=7)
+    buffers = scenario_buffers(s)
+    k0, v0 = s.k_bits.copy(), s.v_bits.copy()
+    ids = torch.tensor([5, 1, 5, 3], dtype=ids_dtype, device=DEV)
+    out_k = torch.empty((4, *buffers.k.shape[1:]), dtype=buffers.k.dtype, device=DEV)
+    out_v = torch.empty_like(out_k)
+    hip_kvcache.gather(buffers, ids, out_k, out_v)
+    hip_kvcache.copy_blocks(buffers, torch.tensor([1, 2], dtype=ids_dtype, device=DEV),
+                            torch.tensor([6, 7], dtype=ids_dtype, device=DEV))
+    torch.cuda.synchronize()
+    assert np.array_equal(to_bits(out_k), k0[[5, 1, 5, 3]]) and np.array_equal(to_bits(out_v), v0[[5, 1, 5, 3]])
+    want_k, want_v = k0.copy(), v0.copy()
+    paged.copy_blocks(want_k, want_v, np.array([1, 2]), np.array([6, 7]))
+    assert np.array_equal(to_bits(buffers.k), want_k) and np.array_equal(to_bits(buffers.v), want_v)
+    hip_kvcache.zero_blocks(buffers, torch.tensor([2, 4], dtype=ids_dtype, device=DEV))
+    torch.cuda.synchronize()
+    paged.zero_blocks(want_k, want_v, np.array([2, 4]))
+    assert np.array_equal(to_bits(buffers.k), want_k) and np.array_equal(to_bits(buffers.v), want_v)
+
+
+# --- the C ABI called directly ----------------------------------------------------------------
+
+
+def test_c_abi_direct_call() -> None:
+    s = build_scenario([(1, 100), (1, 1), (1, 0)], heads=8, kv_heads=2, head_dim=128, block_size=16,
+                       mode="decode", seed=71)
+    k, v, q = to_device(s.k_bits, "bf16"), to_device(s.v_bits, "bf16"), to_device(s.q_bits, "bf16")
+    table = torch.from_numpy(s.table.astype(np.int32)).to(DEV)
+    lengths = torch.tensor(s.lengths, dtype=torch.int32, device=DEV)
+    out = torch.empty_like(q)
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.ayk_paged_attention_v1(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
+                                    table.shape[1], lengths.data_ptr(), None, None, 3, 8, 2, 128,
+                                    k.shape[0], 16, table.shape[1], 0, 1, ctypes.c_float(s.scale), stream)
+    assert rc == 0, lib.ayk_last_error()
+    torch.cuda.synchronize()
+    assert_parity(out, s.expected(np.float64), "bf16", "abi")
+    rc = lib.ayk_paged_attention_v1(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
+                                    table.shape[1], lengths.data_ptr(), None, None, 3, 8, 2, 96,
+                                    k.shape[0], 16, table.shape[1], 0, 1, ctypes.c_float(1.0), stream)
+    assert rc == 2 and b"head_dim 96" in lib.ayk_last_error()
+
+
+def test_unsupported_shapes_are_refused_before_launch() -> None:
+    s = build_scenario([(1, 10)], head_dim=64, block_size=16, mode="decode")
+    buffers = scenario_buffers(s)
+    meta = plan_scenario(s)
+    q = to_device(s.q_bits, s.dtype)
+    with pytest.raises(BackendError, match="not a positive multiple"):
+        hip_attention.attend(q[:, :3], buffers, meta, torch.empty_like(q[:, :3]), scale=1.0)
+    odd = build_scenario([(1, 10)], head_dim=96, block_size=16, mode="decode")
+    with pytest.raises(BackendError, match="head widths"):
+        q96 = to_device(odd.q_bits, odd.dtype)
+        hip_attention.attend(q96, scenario_buffers(odd), plan_scenario(odd), torch.empty_like(q96), scale=1.0)

@@ -1,0 +1,173 @@
+"""Host logic of the hip backend, on the CPU: plan, graph metadata, checks and the registry.
+
+``plan`` and ``update_graph_metadata`` run on the host, so they are checked here
+against the known answers of the reference's tests
+(``tests/ops/test_attention_contract.py:393-467``,
+``tests/ops/test_attention_graph.py:56-143``) and against the oracle's plan.
+"""
+
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from ayaka_amd import backend as registry
+from ayaka_amd.enums import DType, ForwardMode, KVLayoutKind
+from ayaka_amd.errors import BackendError, CapabilityError, ConfigError
+from ayaka_amd.hip import attention as hip_attention
+from ayaka_amd.hip import kvcache as hip_kvcache
+from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+from oracle import paged
+
+KNOWN = json.loads((Path(__file__).resolve().parent / "golden" / "known_answers.json").read_text())
+
+
+def _ints(*values: int) -> torch.Tensor:
+    return torch.tensor(values, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("case", KNOWN["plan"], ids=lambda c: c["mode"])
+def test_plan_known_answers(case: dict) -> None:
+    meta = hip_attention.plan(
+        ForwardMode(case["mode"]), _ints(*case["rows"]), _ints(*case["lengths"]),
+        torch.tensor(case["table"]), case["block_size"],
+    )
+    assert meta.request_of_row.tolist() == case["request_of_row"]
+    assert meta.positions.tolist() == case["positions"]
+    assert meta.slot_mapping.tolist() == case["slot_mapping"]
+    assert meta.slot_mapping.dtype == torch.int64 and meta.rows_per_request.dtype == torch.int32
+    assert meta.kv_lengths.tolist() == case["lengths"] and meta.block_size == case["block_size"]
+
+
+@pytest.mark.parametrize("case", KNOWN["plan_refusals"], ids=lambda c: c["message"])
+def test_plan_refusals(case: dict) -> None:
+    with pytest.raises(BackendError, match=case["message"]):
+        hip_attention.plan(ForwardMode(case["mode"]), torch.tensor(case["rows"]),
+                           torch.tensor(case["lengths"]), torch.tensor(case["table"]), 4)
+
+
+def test_plan_matches_the_oracle_on_random_steps() -> None:
+    rng = np.random.default_rng(0)
+    for _ in range(40):
+        batch, bs = int(rng.integers(1, 7)), int(rng.choice([1, 4, 16, 32]))
+        lengths = [int(x) for x in rng.integers(0, 100, size=batch)]
+        rows = [int(rng.integers(1, n + 1)) if n else int(rng.integers(0, 3)) for n in lengths]
+        width = max(max(-(-n // bs) for n in lengths), 1)
+        table = rng.integers(1, 999, size=(batch, width))
+        meta = hip_attention.plan(ForwardMode.MIXED, _ints(*rows), _ints(*lengths), torch.from_numpy(table), bs)
+        want = paged.plan("mixed", rows, lengths, table, bs)
+        for key in ("request_of_row", "positions", "slot_mapping"):
+            assert getattr(meta, key).tolist() == want[key].tolist()
+        assert meta.plan.max_length == max(lengths)
+
+
+def test_plan_rejects_mismatched_batches_and_bad_types() -> None:
+    with pytest.raises(BackendError, match=r"same requests, got 2, 1 and 2"):
+        hip_attention.plan(ForwardMode.MIXED, _ints(1, 1), _ints(2), torch.tensor([[1], [2]]), 4)
+    with pytest.raises(BackendError, match="rows_per_request must be an int32 or int64"):
+        hip_attention.plan(ForwardMode.MIXED, torch.ones(1), _ints(2), torch.tensor([[1]]), 4)
+    with pytest.raises(BackendError, match="block_size must be positive"):
+        hip_attention.plan(ForwardMode.MIXED, _ints(1), _ints(1), torch.tensor([[1]]), 0)
+
+
+def test_metadata_is_a_frozen_snapshot() -> None:
+    meta = hip_attention.plan(ForwardMode.DECODE, _ints(1), _ints(3), torch.tensor([[1]]), 4)
+    with pytest.raises(AttributeError):
+        meta.mode = ForwardMode.PREFILL  # type: ignore[misc]
+
+
+def test_graph_metadata_starts_as_padding_and_updates_in_place() -> None:
+    meta = hip_attention.graph_metadata(3, 4, 4, torch.device("cpu"))
+    assert meta.mode == ForwardMode.DECODE and meta.kv_lengths.tolist() == [0, 0, 0]
+    addresses = [t.data_ptr() for t in (meta.positions, meta.slot_mapping, meta.kv_lengths, meta.block_table)]
+    table = torch.tensor([[3, 1, 0, 0], [0, 0, 0, 0], [2, 4, 5, 0]], dtype=torch.int32)
+    hip_attention.update_graph_metadata(meta, _ints(5, 0, 10), table)
+    planned = hip_attention.plan(ForwardMode.DECODE, _ints(1, 1, 1), _ints(5, 0, 10), table, 4)
+    for key in ("positions", "slot_mapping", "kv_lengths"):
+        assert getattr(meta, key).tolist() == getattr(planned, key).tolist()
+    assert meta.block_table.tolist() == table.tolist()
+    assert addresses == [t.data_ptr() for t in (meta.positions, meta.slot_mapping, meta.kv_lengths, meta.block_table)]
+
+
+def test_graph_metadata_update_refusals() -> None:
+    meta = hip_attention.graph_metadata(2, 2, 4, torch.device("cpu"))
+    with pytest.raises(BackendError, match=r"must be in \[0, 8\]"):
+        hip_attention.update_graph_metadata(meta, _ints(9, 0), torch.zeros((2, 2), dtype=torch.int32))
+    with pytest.raises(BackendError, match="int32 CPU tensor of shape"):
+        hip_attention.update_graph_metadata(meta, torch.tensor([1, 0]), torch.zeros((2, 2), dtype=torch.int32))
+    planned = hip_attention.plan(ForwardMode.DECODE, _ints(1), _ints(3), torch.tensor([[1]]), 4)
+    with pytest.raises(BackendError, match="not made by this backend's graph_metadata"):
+        hip_attention.update_graph_metadata(planned, _ints(1), torch.zeros((1, 1), dtype=torch.int32))
+    with pytest.raises(BackendError, match="must be positive"):
+        hip_attention.graph_metadata(0, 2, 4, torch.device("cpu"))
+
+
+def test_the_split_heuristic_depends_only_on_the_shape() -> None:
+    assert hip_attention.choose_partitions(64, 8, 4, 512) == 0
+    assert hip_attention.choose_partitions(8, 8, 4, 32768) == 64
+    assert hip_attention.head_chunks(4) == 1 and hip_attention.head_chunks(12) == 2
+    assert hip_attention.head_chunks(16) == 2 and hip_attention.head_chunks(11) == 11
+
+
+def _cpu_buffers(**changes: object) -> KVBuffers:
+    k = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16)
+    buffers = KVBuffers(k, k.clone(), KVLayoutKind.NHD, RAW_CODEC)
+    return buffers._replace(**changes)
+
+
+def test_ops_refuse_caches_they_cannot_serve() -> None:
+    meta = hip_attention.plan(ForwardMode.DECODE, _ints(1), _ints(3), torch.tensor([[1]]), 16)
+    q = torch.zeros(1, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(BackendError, match="serves the NHD and HND layouts"):
+        hip_attention.attend(q, _cpu_buffers(layout=KVLayoutKind.NLD), meta, q.clone(), scale=1.0)
+    with pytest.raises(BackendError, match="stores the 'raw' codec, not 'fp8'"):
+        hip_kvcache.store(q[:, :2], q[:, :2], _cpu_buffers(codec="fp8"), meta)
+    fp32 = torch.zeros(4, 16, 2, 64)
+    with pytest.raises(BackendError, match="computes in float16, bfloat16"):
+        hip_attention.attend(q, KVBuffers(fp32, fp32, KVLayoutKind.NHD, RAW_CODEC), meta, q.clone(), scale=1.0)
+    with pytest.raises(BackendError, match="runs on a HIP device"):
+        hip_attention.attend(q, _cpu_buffers(), meta, q.clone(), scale=1.0)
+    bad_v = torch.zeros(4, 16, 2, 65, dtype=torch.bfloat16)
+    with pytest.raises(BackendError, match=r"buffers.v must be bfloat16 \[4, 16, 2, 64\]"):
+        hip_kvcache.store(q[:, :2], q[:, :2], _cpu_buffers(v=bad_v), meta)
+
+
+def test_registry_selection_and_refusals(monkeypatch: pytest.MonkeyPatch) -> None:
+    monkeypatch.setattr(registry, "_registry", dict(registry._registry))
+    calls: list[str] = []
+
+    def fake_loader() -> dict[str, object]:
+        calls.append("fake")
+        return {"attention": "fake-attention", "kvcache": "fake-kvcache"}
+
+    registry.register_backend(
+        registry.BackendCaps(
+            name="fake", families=frozenset({"attention", "kvcache"}), platforms=frozenset({"linux"}),
+            devices=frozenset({"cpu"}), dtypes=frozenset({DType.BF16}), multi_row_attention=True,
+        ),
+        fake_loader,
+    )
+    chosen = registry.load_backend(["hip", "fake"], device="cpu", dtype=DType.BF16)
+    assert chosen.providers == {"kvcache": "fake", "attention": "fake"} and calls == ["fake"]
+    with pytest.raises(ConfigError, match="hip has no cpu support"):
+        registry.load_backend(["hip"], device="cpu", dtype=DType.BF16)
+    with pytest.raises(ConfigError, match="cannot run inside a CUDA graph"):
+        registry.load_backend(["fake"], device="cpu", dtype=DType.BF16, cuda_graph=True)
+    with pytest.raises(ConfigError, match="BACKEND_UNKNOWN"):
+        registry.load_backend(["nope"], device="cpu", dtype=DType.BF16)
+    with pytest.raises(ValueError, match="already registered"):
+        registry.register_backend(registry.available_backends()[0], fake_loader)
+
+
+def test_hip_backend_is_unavailable_without_a_device(monkeypatch: pytest.MonkeyPatch) -> None:
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    with pytest.raises(CapabilityError, match="no HIP device"):
+        from ayaka_amd.hip import load
+
+        load()
+    with pytest.raises(ConfigError, match="hip is unavailable"):
+        registry.load_backend(["hip"], device="cuda", dtype=DType.BF16)
