@@ -120,6 +120,9 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
     p.token_stride = D;
     p.head_stride = B * D;
   }
+  if (p.block_stride > UINT32_MAX || p.token_stride > UINT32_MAX)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: a block of %lld elements exceeds the 32-bit offsets", op,
+                (long long)p.block_stride);
   p.n_rows = c.n_rows;
   p.num_heads = c.num_heads;
   p.group = group;

@@ -37,8 +37,6 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
-constexpr int kWaves = 4;
-constexpr int kThreads = kWave * kWaves;
 // Block-table entries staged in LDS per segment of a row's context.
 constexpr int kTableCap = 512;
 
@@ -98,6 +96,12 @@ __device__ __forceinline__ float group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// K/V are read exactly once per call: nontemporal loads keep them from displacing
+// reusable lines and stream measurably faster on MI355X than plain loads.
+__device__ __forceinline__ u32x4 stream_load(const uint16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
 // Length of row `row`'s context and its request, clamped so no read leaves the table.
 __device__ __forceinline__ void row_context(const AttnParams& p, int row, int& req, int& len) {
   req = p.request_of_row ? p.request_of_row[row] : row;
@@ -106,17 +110,25 @@ __device__ __forceinline__ void row_context(const AttnParams& p, int row, int& r
   len = max(0, min(len, p.max_len));
 }
 
-template <int D, int GC, int NLD, bool BF16, bool SPLIT>
-__global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnParams p) {
+// Running-max sentinel: below any real score yet finite, so exp2(sentinel - m) is 0
+// for a real m and 1 when nothing has been seen, and no -inf - -inf NaN can arise.
+constexpr float kNoScore = -1.0e30f;
+// How far (log2 units) the running max may trail a chunk's max before the
+// accumulators are rescaled: weights stay below 2^8, far inside fp32.
+constexpr float kRescaleSlack = 8.0f;
+
+template <int D, int GC, int NLD, int WAVES, bool BF16, bool SPLIT>
+__global__ __launch_bounds__(WAVES * kWave) void paged_attention_kernel(const AttnParams p) {
   using E = Elem<BF16>;
+  constexpr int THREADS = WAVES * kWave;
   constexpr int LPT = D / 8;         // lanes per token (8 elements = 16 bytes each)
   constexpr int TPL = kWave / LPT;   // tokens per load instruction
   constexpr int CH = TPL * NLD;      // tokens per chunk (one chunk per wave per step)
 
   __shared__ int s_tbl[kTableCap];
-  __shared__ float s_o[kWaves][GC][D];
-  __shared__ float s_m[kWaves][GC];
-  __shared__ float s_l[kWaves][GC];
+  __shared__ float s_o[WAVES][GC][D];
+  __shared__ float s_m[WAVES][GC];
+  __shared__ float s_l[WAVES][GC];
 
   const int row = blockIdx.x;
   const int kvh = blockIdx.y / p.head_chunks;
@@ -137,7 +149,7 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
   } else if (len == 0) {
     // Padding row: zeros, and nothing of the cache is read.
     uint16_t* out = static_cast<uint16_t*>(p.out);
-    for (int it = tid; it < GC * LPT; it += kThreads) {
+    for (int it = tid; it < GC * LPT; it += THREADS) {
       const int g = it / LPT, cc = it % LPT;
       *reinterpret_cast<u32x4*>(out + ((int64_t)row * p.num_heads + h0 + g) * D + cc * 8) =
           u32x4{0u, 0u, 0u, 0u};
@@ -157,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
   float m[GC], l[GC], o[GC][8];
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
-    m[g] = -INFINITY;
+    m[g] = kNoScore;
     l[g] = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
@@ -167,6 +179,9 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
   const int shift = p.bs_shift;
   const int bs_mask = (1 << shift) - 1;
   const int seg_len = (((kTableCap - 1) << shift) / CH) * CH;
+  const uint32_t block_stride = (uint32_t)p.block_stride;  // the host checks these fit 32 bits
+  const uint32_t token_stride = (uint32_t)p.token_stride;
+  const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + c * 8;
   const uint16_t* vbase = p.v_cache + (int64_t)kvh * p.head_stride + c * 8;
 
@@ -175,43 +190,27 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
     const int b0 = s0 >> shift;
     const int nb = ((s1 - 1) >> shift) - b0 + 1;
     __syncthreads();  // the previous segment is done with s_tbl
-    for (int i = tid; i < nb; i += kThreads) {
+    for (int i = tid; i < nb; i += THREADS) {
       const int b = tbl[b0 + i];
       s_tbl[i] = ((unsigned)b < (unsigned)p.num_blocks) ? b : 0;
     }
     __syncthreads();
 
     const int nch = (s1 - s0 + CH - 1) / CH;
-    int64_t offs[NLD];
-    u32x4 kc[NLD];
-    auto token_offsets = [&](int ci, int64_t* dst) {
+
+    // Element offsets of this lane's NLD tokens of chunk ci (past-the-end tokens
+    // are clamped to the last one and masked later).
+    auto offsets = [&](int ci, uint64_t(&dst)[NLD]) {
 #pragma unroll
       for (int j = 0; j < NLD; ++j) {
         const int t = min(s0 + ci * CH + j * TPL + r, s1 - 1);
-        const int blk = s_tbl[(t >> shift) - b0];
-        dst[j] = (int64_t)blk * p.block_stride + (int64_t)(t & bs_mask) * p.token_stride;
+        const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
+        dst[j] = (uint64_t)blk * block_stride + (uint32_t)(t & bs_mask) * token_stride;
       }
     };
 
-    int ci = wave;
-    if (ci < nch) {
-      token_offsets(ci, offs);
-#pragma unroll
-      for (int j = 0; j < NLD; ++j) kc[j] = *reinterpret_cast<const u32x4*>(kbase + offs[j]);
-    }
-    while (ci < nch) {
-      u32x4 vc[NLD];
-#pragma unroll
-      for (int j = 0; j < NLD; ++j) vc[j] = *reinterpret_cast<const u32x4*>(vbase + offs[j]);
-      const int cn = ci + kWaves;
-      int64_t noffs[NLD];
-      u32x4 kn[NLD];
-      if (cn < nch) {
-        token_offsets(cn, noffs);
-#pragma unroll
-        for (int j = 0; j < NLD; ++j) kn[j] = *reinterpret_cast<const u32x4*>(kbase + noffs[j]);
-      }
-
+    // Fold one chunk of keys and values into the running state.
+    auto consume = [&](int ci, const u32x4(&kc)[NLD], const u32x4(&vc)[NLD]) {
       const int tb = s0 + ci * CH;
       const bool tail = tb + CH > s1;
       float s[NLD][GC];
@@ -222,10 +221,39 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
           float a = E::dot2(qw[g][0], kc[j].x, 0.f);
           a = E::dot2(qw[g][1], kc[j].y, a);
           a = E::dot2(qw[g][2], kc[j].z, a);
-          a = E::dot2(qw[g][3], kc[j].w, a);
-          s[j][g] = group_sum<LPT>(a) * p.scale_log2;
+          s[j][g] = E::dot2(qw[g][3], kc[j].w, a);
         }
       }
+      // Butterfly over the LPT lanes of each token, one stage at a time across all
+      // NLD x GC partial sums, so consecutive DPP reads never wait on each other.
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[j][g] += dpp<0xB1>(s[j][g]);  // lane ^ 1
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[j][g] += dpp<0x4E>(s[j][g]);  // lane ^ 2
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[j][g] += dpp<0x141>(s[j][g]);  // other quad of 8
+      if constexpr (LPT >= 16) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j)
+#pragma unroll
+          for (int g = 0; g < GC; ++g) s[j][g] += dpp<0x140>(s[j][g]);  // other 8 of 16
+      }
+      if constexpr (LPT >= 32) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j)
+#pragma unroll
+          for (int g = 0; g < GC; ++g) s[j][g] += __shfl_xor(s[j][g], 16);
+      }
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[j][g] *= scale_log2;
       if (tail) {
 #pragma unroll
         for (int j = 0; j < NLD; ++j)
@@ -234,24 +262,35 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
             for (int g = 0; g < GC; ++g) s[j][g] = -INFINITY;
           }
       }
+      // Online softmax with a lazily raised max: the accumulators are rescaled
+      // only when some lane's chunk max exceeds its running max by the slack.
+      float mx[GC];
+      bool grow = false;
 #pragma unroll
       for (int g = 0; g < GC; ++g) {
-        float mx = s[0][g];
+        mx[g] = s[0][g];
 #pragma unroll
-        for (int j = 1; j < NLD; ++j) mx = fmaxf(mx, s[j][g]);
-        const float mn = fmaxf(m[g], mx);
-        const float mr = (mn == -INFINITY) ? 0.f : mn;
-        const float alpha = fast_exp2(m[g] - mr);
-        float sum = 0.f;
+        for (int j = 1; j < NLD; ++j) mx[g] = fmaxf(mx[g], s[j][g]);
+        grow |= mx[g] > m[g] + kRescaleSlack;
+      }
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+          const float mn = fmaxf(m[g], mx[g]);
+          const float alpha = fast_exp2(m[g] - mn);
+          l[g] *= alpha;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+          m[g] = mn;
+        }
+      }
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
 #pragma unroll
         for (int j = 0; j < NLD; ++j) {
-          s[j][g] = fast_exp2(s[j][g] - mr);
-          sum += s[j][g];
+          s[j][g] = fast_exp2(s[j][g] - m[g]);
+          l[g] += s[j][g];
         }
-        l[g] = l[g] * alpha + sum;
-        m[g] = mn;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
       }
 #pragma unroll
       for (int j = 0; j < NLD; ++j) {
@@ -271,13 +310,40 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
           for (int e = 0; e < 8; ++e) o[g][e] = fmaf(s[j][g], vf[e], o[g][e]);
         }
       }
+    };
 
-      ci = cn;
+    // Two register sets, used alternately: while one chunk is folded in, the
+    // keys of the next chunk are already in flight (unrolled twice so no copies).
+    uint64_t offA[NLD], offB[NLD];
+    u32x4 kA[NLD], kB[NLD], vc[NLD];
+    int ci = wave;
+    if (ci < nch) {
+      offsets(ci, offA);
 #pragma unroll
-      for (int j = 0; j < NLD; ++j) {
-        offs[j] = noffs[j];
-        kc[j] = kn[j];
+      for (int j = 0; j < NLD; ++j) kA[j] = stream_load(kbase + offA[j]);
+    }
+    while (ci < nch) {
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) vc[j] = stream_load(vbase + offA[j]);
+      int cn = ci + WAVES;
+      if (cn < nch) {
+        offsets(cn, offB);
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) kB[j] = stream_load(kbase + offB[j]);
       }
+      consume(ci, kA, vc);
+      ci = cn;
+      if (ci >= nch) break;
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) vc[j] = stream_load(vbase + offB[j]);
+      cn = ci + WAVES;
+      if (cn < nch) {
+        offsets(cn, offA);
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) kA[j] = stream_load(kbase + offA[j]);
+      }
+      consume(ci, kB, vc);
+      ci = cn;
     }
   }
 
@@ -289,9 +355,8 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
       const float m2 = __shfl_xor(m[g], st);
       const float l2 = __shfl_xor(l[g], st);
       const float mn = fmaxf(m[g], m2);
-      const float mr = (mn == -INFINITY) ? 0.f : mn;
-      const float a = fast_exp2(m[g] - mr);
-      const float b = fast_exp2(m2 - mr);
+      const float a = fast_exp2(m[g] - mn);
+      const float b = fast_exp2(m2 - mn);
       l[g] = l[g] * a + l2 * b;
       m[g] = mn;
 #pragma unroll
@@ -311,18 +376,17 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
   }
   __syncthreads();
 
-  // Merge the 4 waves and write: one thread per (head, 8 elements).
-  for (int it = tid; it < GC * LPT; it += kThreads) {
+  // Merge the waves and write: one thread per (head, 8 elements).
+  for (int it = tid; it < GC * LPT; it += THREADS) {
     const int g = it / LPT, cc = it % LPT;
     float mn = s_m[0][g];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) mn = fmaxf(mn, s_m[w][g]);
-    const float mr = (mn == -INFINITY) ? 0.f : mn;
-    float wt[kWaves];
+    for (int w = 1; w < WAVES; ++w) mn = fmaxf(mn, s_m[w][g]);
+    float wt[WAVES];
     float L = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      wt[w] = fast_exp2(s_m[w][g] - mr);
+    for (int w = 0; w < WAVES; ++w) {
+      wt[w] = fast_exp2(s_m[w][g] - mn);
       L += s_l[w][g] * wt[w];
     }
     float acc[8];
@@ -330,7 +394,7 @@ __global__ __launch_bounds__(kThreads) void paged_attention_kernel(const AttnPar
     for (int e = 0; e < 8; ++e) {
       float a = 0.f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) a = fmaf(wt[w], s_o[w][g][cc * 8 + e], a);
+      for (int w = 0; w < WAVES; ++w) a = fmaf(wt[w], s_o[w][g][cc * 8 + e], a);
       acc[e] = a;
     }
     const float inv = L > 0.f ? 1.0f / L : 0.f;
@@ -414,14 +478,15 @@ __global__ __launch_bounds__(kWave) void partition_reduce_kernel(const AttnParam
 template <int D, int GC, bool BF16>
 static hipError_t launch_typed(const AttnParams& p, bool split, hipStream_t stream) {
   constexpr int NLD = (D == 64) ? 2 : 4;
-  const dim3 block(kThreads);
+  constexpr int WAVES = 4;
+  const dim3 block(WAVES * kWave);
   const int hy = (p.num_heads / p.group) * p.head_chunks;
   if (!split) {
-    hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, BF16, false>), dim3(p.n_rows, hy, 1),
+    hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, WAVES, BF16, false>), dim3(p.n_rows, hy, 1),
                        block, 0, stream, p);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, BF16, true>),
+  hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, WAVES, BF16, true>),
                      dim3(p.n_rows, hy, p.max_partitions), block, 0, stream, p);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;

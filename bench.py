@@ -40,6 +40,8 @@ def parse() -> argparse.Namespace:
                     help="time only this launch (for profiler runs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=8, help="rows of the CPU baseline sample")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 5 plain device copies of MIB MiB (scales profiler byte counters)")
     return ap.parse_args()
 
 
@@ -104,6 +106,15 @@ def main() -> int:
               "(decode attention needs no collective; see the sharding note in DESIGN.md)", file=sys.stderr)
         return 2
     import torch
+
+    if args.copy_calibration:
+        src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": src.numel()}))
+        return 0
 
     from ayaka_amd import workloads
     from ayaka_amd.enums import ForwardMode, KVLayoutKind
