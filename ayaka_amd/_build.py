@@ -10,13 +10,14 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
-__all__ = ["LIB_PATH", "build_library", "hipcc_command"]
+__all__ = ["FLAGS", "LIB_PATH", "build_library", "hipcc_command"]
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_DIR = PACKAGE_DIR.parent
-SOURCES = ("api.hip", "paged_attention.hip", "kv_cache.hip")
+SOURCES = ("api.hip", "paged_attention.hip", "paged_attention_mfma.hip", "kv_cache.hip")
 LIB_PATH = PACKAGE_DIR / "lib" / "libayaka_hip.so"
 ARCH = "gfx950"
 
@@ -28,40 +29,46 @@ def _hipcc() -> str:
     return found
 
 
-def hipcc_command(output: Path = LIB_PATH, extra: tuple[str, ...] = ()) -> list[str]:
-    """The one hipcc line that builds the shared library."""
+FLAGS = (
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    # Packed fp32 VALU ops are kept out of every kernel.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+)
+
+
+def hipcc_command(source: Path, output: Path) -> list[str]:
+    """The hipcc line that compiles one source into an object."""
     csrc = PACKAGE_DIR / "csrc"
-    return [
-        _hipcc(),
-        f"--offload-arch={ARCH}",
-        "-O3",
-        "-std=c++17",
-        "-fPIC",
-        "-shared",
-        "-Wall",
-        # Packed fp32 VALU ops are kept out of every kernel.
-        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-        f"-I{REPO_DIR / 'include'}",
-        f"-I{csrc}",
-        *extra,
-        *(str(csrc / name) for name in SOURCES),
-        "-o",
-        str(output),
-    ]
+    return [_hipcc(), *FLAGS, f"-I{REPO_DIR / 'include'}", f"-I{csrc}", "-c", str(source), "-o", str(output)]
 
 
-def build_library(*, verbose: bool = False) -> Path:
-    """Compile every HIP source into ``ayaka_amd/lib/libayaka_hip.so`` and return its path."""
-    LIB_PATH.parent.mkdir(parents=True, exist_ok=True)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = hipcc_command(tmp)
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
-    env = dict(os.environ)
-    result = subprocess.run(cmd, capture_output=True, text=True, env=env, check=False)
+    result = subprocess.run(cmd, capture_output=True, text=True, check=False)
     if result.returncode != 0:
         sys.stderr.write(result.stdout + result.stderr)
-        raise RuntimeError(f"hipcc failed with exit code {result.returncode}")
+        raise RuntimeError(f"hipcc failed with exit code {result.returncode}: {' '.join(cmd)}")
+
+
+def build_library(*, verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every HIP source (in parallel) and link ``ayaka_amd/lib/libayaka_hip.so``."""
+    out_dir = LIB_PATH.parent
+    obj_dir = out_dir / "obj"
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    csrc = PACKAGE_DIR / "csrc"
+    objects = [obj_dir / (Path(name).stem + ".o") for name in SOURCES]
+    workers = jobs or min(len(SOURCES), os.cpu_count() or 1, 16)
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        for future in [pool.submit(_run, hipcc_command(csrc / name, obj), verbose)
+                       for name, obj in zip(SOURCES, objects)]:
+            future.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

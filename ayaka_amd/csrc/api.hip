@@ -96,9 +96,6 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
     return fail(AYK_ERR_ARGUMENT, "%s: a required pointer is null", op);
   const int group = c.num_heads / c.num_kv_heads;
   const int chunks = head_chunks_for(group);
-  if ((int64_t)c.num_kv_heads * chunks > 65535)
-    return fail(AYK_ERR_UNSUPPORTED, "%s: %d key/value heads x %d head chunks exceed the grid", op,
-                c.num_kv_heads, chunks);
   heads_per_chunk = group / chunks;
   p = ayk::AttnParams{};
   p.out = c.out;
@@ -120,13 +117,14 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
     p.token_stride = D;
     p.head_stride = B * D;
   }
-  if (p.block_stride > UINT32_MAX || p.token_stride > UINT32_MAX)
-    return fail(AYK_ERR_UNSUPPORTED, "%s: a block of %lld elements exceeds the 32-bit offsets", op,
-                (long long)p.block_stride);
+  if ((uint64_t)c.num_blocks * (uint64_t)p.block_stride > UINT32_MAX)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: a cache of %d blocks of %lld elements exceeds 32-bit element offsets",
+                op, c.num_blocks, (long long)p.block_stride);
   p.n_rows = c.n_rows;
   p.num_heads = c.num_heads;
   p.group = group;
   p.head_chunks = chunks;
+  p.num_virtual_heads = c.num_kv_heads * chunks;
   p.num_blocks = c.num_blocks;
   p.bs_shift = shift;
   const int64_t table_len = (int64_t)c.max_blocks << shift;
@@ -137,11 +135,36 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
   return AYK_OK;
 }
 
+// Heads per wave from which the library picks the matrix-core q.k kernel.
+constexpr int kMfmaMinHeads = 6;
+
+// The q.k path and workgroup shape for a launch, then the kernel(s).
+int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool bf16, bool split, int32_t flags,
+           void* stream) {
+  if (flags & ~(AYK_FLAG_QK_DPP | AYK_FLAG_QK_MFMA))
+    return fail(AYK_ERR_ARGUMENT, "%s: unknown flags 0x%x", op, flags);
+  if ((flags & AYK_FLAG_QK_DPP) && (flags & AYK_FLAG_QK_MFMA))
+    return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_QK_DPP and AYK_FLAG_QK_MFMA exclude each other", op);
+  // Measured on MI355X: the DPP kernel streams best up to 4 heads per wave; at 6-8
+  // heads its q.k work makes it VALU-bound and the matrix-core kernel wins.
+  const bool mfma = (flags & AYK_FLAG_QK_MFMA) || (!(flags & AYK_FLAG_QK_DPP) && gc >= kMfmaMinHeads);
+  const int waves = 4;
+  const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);
+  const int64_t workgroups = items * p.num_virtual_heads;
+  if (workgroups > INT32_MAX || (int64_t)p.n_rows * p.num_heads > INT32_MAX)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: %lld workgroups exceed one launch", op, (long long)workgroups);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err = mfma ? ayk::launch_attention_mfma(p, head_dim, gc, bf16, split, waves, s)
+                        : ayk::launch_attention_dpp(p, head_dim, gc, bf16, split, waves, s);
+  if (err == hipSuccess && split) err = ayk::launch_partition_reduce(p, head_dim, bf16, s);
+  return launched(err, op);
+}
+
 }  // namespace
 
 extern "C" {
 
-int ayk_abi_version(void) { return 1; }
+int ayk_abi_version(void) { return 3; }
 
 const char* ayk_last_error(void) { return g_last_error.c_str(); }
 
@@ -174,7 +197,7 @@ int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const 
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           float scale, void* stream) {
+                           float scale, int32_t flags, void* stream) {
   const char* op = "ayk_paged_attention_v1";
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
@@ -184,9 +207,7 @@ int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const 
   const int rc = prepare(op, c, p, gc);
   if (rc != AYK_OK) return rc;
   if (n_rows == 0) return ok();
-  return launched(ayk::launch_paged_attention(p, head_dim, gc, dtype == AYK_DTYPE_BF16, false,
-                                              static_cast<hipStream_t>(stream)),
-                  op);
+  return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, false, flags, stream);
 }
 
 size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads, int32_t head_dim,
@@ -204,7 +225,8 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
                            float scale, int32_t partition_size, int32_t max_partitions,
-                           void* workspace, size_t workspace_bytes, void* stream) {
+                           const int32_t* work_items, int32_t n_work_items, void* workspace,
+                           size_t workspace_bytes, int32_t flags, void* stream) {
   const char* op = "ayk_paged_attention_v2";
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
@@ -218,6 +240,8 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                 partition_size);
   if (max_partitions <= 0 || max_partitions > 65535)
     return fail(AYK_ERR_ARGUMENT, "%s: max_partitions %d is not in [1, 65535]", op, max_partitions);
+  if (n_work_items < 0 || (n_work_items > 0 && !work_items))
+    return fail(AYK_ERR_ARGUMENT, "%s: %d work items at %p", op, n_work_items, (const void*)work_items);
   if (n_rows == 0) return ok();
   const size_t need =
       ayk_paged_attention_v2_workspace_bytes(n_rows, num_heads, head_dim, max_partitions);
@@ -231,10 +255,10 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
   p.part_ml = p.part_o + parts * head_dim;
   p.partition_size = partition_size;
   p.max_partitions = max_partitions;
+  p.work = n_work_items > 0 ? work_items : nullptr;
+  p.n_work = n_work_items;
   p.max_len = (int32_t)std::min<int64_t>(p.max_len, (int64_t)partition_size * max_partitions);
-  return launched(ayk::launch_paged_attention(p, head_dim, gc, dtype == AYK_DTYPE_BF16, true,
-                                              static_cast<hipStream_t>(stream)),
-                  op);
+  return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, true, flags, stream);
 }
 
 static int block_op_checks(const char* op, int64_t n, int32_t num_blocks, int64_t block_bytes) {

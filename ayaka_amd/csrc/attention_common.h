@@ -1,0 +1,243 @@
+// Device helpers shared by the paged-attention kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "ayaka_hip_internal.h"
+
+namespace ayk {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+// Block-table entries staged in LDS per segment of a row's context.
+constexpr int kTableCap = 512;
+// Most waves in one workgroup (one per virtual head).
+constexpr int kMaxWaves = 8;
+
+template <bool BF16>
+struct Elem;
+
+template <>
+struct Elem<true> {
+  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, b), c, false);
+  }
+  // Round to nearest even, NaN kept quiet (what torch's float -> bfloat16 does).
+  static __device__ __forceinline__ uint32_t round(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u >> 16;
+  }
+};
+
+template <>
+struct Elem<false> {
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  }
+  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
+                                  false);
+  }
+  static __device__ __forceinline__ uint32_t round(float f) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of LPT lanes (8, 16 or 32); every lane gets its group's sum.
+template <int LPT>
+__device__ __forceinline__ float group_sum(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
+  x += dpp<0x141>(x);  // row_half_mirror: the other quad of the 8
+  if constexpr (LPT >= 16) x += dpp<0x140>(x);  // row_mirror: the other 8 of the 16
+  if constexpr (LPT >= 32) x += __shfl_xor(x, 16);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// K/V are read exactly once per call: nontemporal loads keep them from displacing
+// reusable lines and stream measurably faster on MI355X than plain loads.
+__device__ __forceinline__ u32x4 stream_load(const uint16_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// The (row, head group, partition) a workgroup serves. The grid is flat and
+// workgroups are handed to the 8 XCDs round-robin by linear id, so the order
+// decides the balance across XCDs:
+//  * with a work list (v2 planned on the host), workgroup id covers item
+//    id / groups, head group id % groups: consecutive items -- the list holds
+//    only partitions with tokens, longest first -- go to different XCDs;
+//  * without one, the grid is dense over rows x groups x partitions with the
+//    partition fastest, so the partitions of one row spread over every XCD
+//    instead of all landing on XCD row % 8.
+struct WgCoord {
+  int row;
+  int group;
+  int part;
+};
+
+__device__ __forceinline__ WgCoord wg_coord(const AttnParams& p, int groups, bool split) {
+  int id = blockIdx.x;
+  if (split && p.work) {
+    const int item = id / groups;
+    return WgCoord{p.work[2 * item], id % groups, p.work[2 * item + 1]};
+  }
+  const int parts = split ? p.max_partitions : 1;
+  const int part = id % parts;
+  id /= parts;
+  return WgCoord{id / groups, id % groups, part};
+}
+
+// Length of row `row`'s context and its request, clamped so no read leaves the table.
+__device__ __forceinline__ void row_context(const AttnParams& p, int row, int& req, int& len) {
+  req = p.request_of_row ? p.request_of_row[row] : row;
+  len = p.kv_lengths[req];
+  if (len > 0 && p.positions) len = min(len, p.positions[row] + 1);
+  len = max(0, min(len, p.max_len));
+}
+
+// Running-max sentinel: below any real score yet finite, so exp2(sentinel - m) is 0
+// for a real m and 1 when nothing has been seen, and no -inf - -inf NaN can arise.
+constexpr float kNoScore = -1.0e30f;
+// How far (log2 units) the running max may trail a chunk's max before the
+// accumulators are rescaled: weights stay below 2^8, far inside fp32.
+constexpr float kRescaleSlack = 8.0f;
+
+// Per-wave partial results of one workgroup, merged by merge_waves_and_store.
+template <int D, int GC, int WAVES>
+struct WaveParts {
+  float o[WAVES][GC][D];  // unnormalised sums, relative to m
+  float m[WAVES][GC];     // running max (log2 domain)
+  float l[WAVES][GC];     // sum of weights
+};
+
+// Merge the waves' (m, l, o) of GC heads and write them: the rounded output
+// (v1) or the normalised partial and its (m, l) (v2 partition z). Call after a
+// __syncthreads() that follows the waves' writes; one thread per (head, 8 elements).
+template <int D, int GC, int WAVES, bool BF16, bool SPLIT>
+__device__ __forceinline__ void merge_waves_and_store(const AttnParams& p, const WaveParts<D, GC, WAVES>& parts,
+                                                      int row, int part, int h0, int tid) {
+  using E = Elem<BF16>;
+  constexpr int LPT = D / 8;
+  for (int it = tid; it < GC * LPT; it += WAVES * kWave) {
+    const int g = it / LPT, cc = it % LPT;
+    float mn = parts.m[0][g];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) mn = fmaxf(mn, parts.m[w][g]);
+    float wt[WAVES];
+    float L = 0.f;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      wt[w] = fast_exp2(parts.m[w][g] - mn);
+      L += parts.l[w][g] * wt[w];
+    }
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float a = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) a = fmaf(wt[w], parts.o[w][g][cc * 8 + e], a);
+      acc[e] = a;
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    const int64_t head_row = (int64_t)row * p.num_heads + h0 + g;
+    if constexpr (SPLIT) {
+      float* po = p.part_o + (head_row * p.max_partitions + part) * D + cc * 8;
+      *reinterpret_cast<f32x4*>(po) = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+      *reinterpret_cast<f32x4*>(po + 4) =
+          f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
+      if (cc == 0) {
+        float* pml = p.part_ml + (head_row * p.max_partitions + part) * 2;
+        pml[0] = mn;
+        pml[1] = L;
+      }
+    } else {
+      uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D + cc * 8;
+      u32x4 w;
+      w.x = E::round(acc[0] * inv) | (E::round(acc[1] * inv) << 16);
+      w.y = E::round(acc[2] * inv) | (E::round(acc[3] * inv) << 16);
+      w.z = E::round(acc[4] * inv) | (E::round(acc[5] * inv) << 16);
+      w.w = E::round(acc[6] * inv) | (E::round(acc[7] * inv) << 16);
+      *reinterpret_cast<u32x4*>(out) = w;
+    }
+  }
+}
+
+// Write one head's merged state from lane c (its 8 elements): the rounded
+// output (v1) or the normalised partial and its (m, l) (v2 partition z).
+template <int D, bool BF16, bool SPLIT>
+__device__ __forceinline__ void store_head(const AttnParams& p, int row, int part, int head, int c,
+                                           const float (&o)[8], float m, float l) {
+  using E = Elem<BF16>;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  const int64_t head_row = (int64_t)row * p.num_heads + head;
+  if constexpr (SPLIT) {
+    float* po = p.part_o + (head_row * p.max_partitions + part) * D + c * 8;
+    *reinterpret_cast<f32x4*>(po) = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+    *reinterpret_cast<f32x4*>(po + 4) = f32x4{o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv};
+    if (c == 0) {
+      float* pml = p.part_ml + (head_row * p.max_partitions + part) * 2;
+      pml[0] = m;
+      pml[1] = l;
+    }
+  } else {
+    uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D + c * 8;
+    u32x4 w;
+    w.x = E::round(o[0] * inv) | (E::round(o[1] * inv) << 16);
+    w.y = E::round(o[2] * inv) | (E::round(o[3] * inv) << 16);
+    w.z = E::round(o[4] * inv) | (E::round(o[5] * inv) << 16);
+    w.w = E::round(o[6] * inv) | (E::round(o[7] * inv) << 16);
+    *reinterpret_cast<u32x4*>(out) = w;
+  }
+}
+
+// Zero the output rows of GC heads of a padding row (v1): nothing of the cache is read.
+template <int D, int GC, int THREADS>
+__device__ __forceinline__ void store_zero_rows(const AttnParams& p, int row, int h0, int tid) {
+  constexpr int LPT = D / 8;
+  uint16_t* out = static_cast<uint16_t*>(p.out);
+  for (int it = tid; it < GC * LPT; it += THREADS) {
+    const int g = it / LPT, cc = it % LPT;
+    *reinterpret_cast<u32x4*>(out + ((int64_t)row * p.num_heads + h0 + g) * D + cc * 8) =
+        u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// Stage the block-table entries of positions [s0, s1) in LDS (ids outside the
+// pool become the padding block 0); returns the first staged block index.
+__device__ __forceinline__ int stage_table(const AttnParams& p, const int32_t* tbl, int* s_tbl, int s0, int s1,
+                                           int tid, int threads) {
+  const int b0 = s0 >> p.bs_shift;
+  const int nb = ((s1 - 1) >> p.bs_shift) - b0 + 1;
+  __syncthreads();  // the previous segment is done with s_tbl
+  for (int i = tid; i < nb; i += threads) {
+    const int b = tbl[b0 + i];
+    s_tbl[i] = ((unsigned)b < (unsigned)p.num_blocks) ? b : 0;
+  }
+  __syncthreads();
+  return b0;
+}
+
+}  // namespace ayk

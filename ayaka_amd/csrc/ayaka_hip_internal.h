@@ -17,6 +17,7 @@ struct AttnParams {
   const int32_t* kv_lengths;
   const int32_t* request_of_row;  // nullptr: row n is request n
   const int32_t* positions;       // nullptr: row n attends to its whole context
+  const int32_t* work;            // v2 only, optional: n_work (row, partition) pairs to run
   float* part_o;                  // v2 only: [n_rows, num_heads, max_partitions, head_dim]
   float* part_ml;                 // v2 only: [n_rows, num_heads, max_partitions, 2] = (m, l)
   int64_t table_stride;
@@ -26,17 +27,24 @@ struct AttnParams {
   int32_t n_rows;
   int32_t num_heads;
   int32_t group;        // query heads per key/value head
-  int32_t head_chunks;  // workgroups that split one group's heads (group / head_chunks each)
+  int32_t head_chunks;  // chunks one group's heads are split into (group / head_chunks each)
+  int32_t num_virtual_heads;  // num_kv_heads * head_chunks: the unit one wave serves
   int32_t num_blocks;
   int32_t bs_shift;     // log2(block_size)
   int32_t max_len;      // no row reads positions at or past this
   int32_t partition_size;
   int32_t max_partitions;
+  int32_t n_work;
   float scale_log2;     // scale * log2(e): scores live in the log2 domain
 };
 
-hipError_t launch_paged_attention(const AttnParams& p, int head_dim, int heads_per_chunk, bool bf16,
-                                  bool split, hipStream_t stream);
+// The per-(row, head[, partition]) attention kernels; `waves` is the workgroup size in waves.
+hipError_t launch_attention_dpp(const AttnParams& p, int head_dim, int heads_per_chunk, bool bf16,
+                                bool split, int waves, hipStream_t stream);
+hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int heads_per_chunk, bool bf16,
+                                 bool split, int waves, hipStream_t stream);
+// The v2 log-sum-exp merge of the partitions of every (row, head).
+hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);
 
 hipError_t launch_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
                                     const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,

@@ -28,114 +28,32 @@
 #include <cmath>
 #include <cstdint>
 
-#include "ayaka_hip_internal.h"
+#include "attention_common.h"
 
 namespace ayk {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-constexpr int kWave = 64;
-// Block-table entries staged in LDS per segment of a row's context.
-constexpr int kTableCap = 512;
-
-template <bool BF16>
-struct Elem;
-
-template <>
-struct Elem<true> {
-  static __device__ __forceinline__ float lo(uint32_t w) { return __uint_as_float(w << 16); }
-  static __device__ __forceinline__ float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
-                                           __builtin_bit_cast(bf16x2, b), c, false);
-  }
-  // Round to nearest even, NaN kept quiet (what torch's float -> bfloat16 does).
-  static __device__ __forceinline__ uint32_t round(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
-  }
-};
-
-template <>
-struct Elem<false> {
-  static __device__ __forceinline__ float lo(uint32_t w) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
-  }
-  static __device__ __forceinline__ float hi(uint32_t w) {
-    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
-  }
-  static __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
-                                  false);
-  }
-  static __device__ __forceinline__ uint32_t round(float f) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);
-  }
-};
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
-}
-
-// Sum over each aligned group of LPT lanes (8, 16 or 32); every lane gets its group's sum.
-template <int LPT>
-__device__ __forceinline__ float group_sum(float x) {
-  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]: lane ^ 1
-  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]: lane ^ 2
-  x += dpp<0x141>(x);  // row_half_mirror: the other quad of the 8
-  if constexpr (LPT >= 16) x += dpp<0x140>(x);  // row_mirror: the other 8 of the 16
-  if constexpr (LPT >= 32) x += __shfl_xor(x, 16);
-  return x;
-}
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// K/V are read exactly once per call: nontemporal loads keep them from displacing
-// reusable lines and stream measurably faster on MI355X than plain loads.
-__device__ __forceinline__ u32x4 stream_load(const uint16_t* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-}
-
-// Length of row `row`'s context and its request, clamped so no read leaves the table.
-__device__ __forceinline__ void row_context(const AttnParams& p, int row, int& req, int& len) {
-  req = p.request_of_row ? p.request_of_row[row] : row;
-  len = p.kv_lengths[req];
-  if (len > 0 && p.positions) len = min(len, p.positions[row] + 1);
-  len = max(0, min(len, p.max_len));
-}
-
-// Running-max sentinel: below any real score yet finite, so exp2(sentinel - m) is 0
-// for a real m and 1 when nothing has been seen, and no -inf - -inf NaN can arise.
-constexpr float kNoScore = -1.0e30f;
-// How far (log2 units) the running max may trail a chunk's max before the
-// accumulators are rescaled: weights stay below 2^8, far inside fp32.
-constexpr float kRescaleSlack = 8.0f;
-
-template <int D, int GC, int NLD, int WAVES, bool BF16, bool SPLIT>
-__global__ __launch_bounds__(WAVES * kWave) void paged_attention_kernel(const AttnParams p) {
+template <int D, int GC, int NLD, bool BF16, bool SPLIT>
+__global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(const AttnParams p) {
   using E = Elem<BF16>;
-  constexpr int THREADS = WAVES * kWave;
   constexpr int LPT = D / 8;         // lanes per token (8 elements = 16 bytes each)
   constexpr int TPL = kWave / LPT;   // tokens per load instruction
-  constexpr int CH = TPL * NLD;      // tokens per chunk (one chunk per wave per step)
+  constexpr int CH = TPL * NLD;      // tokens per chunk
 
   __shared__ int s_tbl[kTableCap];
-  __shared__ float s_o[WAVES][GC][D];
-  __shared__ float s_m[WAVES][GC];
-  __shared__ float s_l[WAVES][GC];
 
-  const int row = blockIdx.x;
-  const int kvh = blockIdx.y / p.head_chunks;
-  const int h0 = kvh * p.group + (blockIdx.y % p.head_chunks) * GC;
   const int tid = threadIdx.x;
+  const int threads = blockDim.x;
+  const int waves = threads / kWave;
+  const WgCoord wg = wg_coord(p, (p.num_virtual_heads + waves - 1) / waves, SPLIT);
+  const int row = wg.row;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
+  // Wave w serves "virtual head" group * waves + w: a key/value head, or a chunk
+  // of GC of its query heads when the group is split.
+  const int vh = wg.group * waves + wave;
+  const bool active = vh < p.num_virtual_heads;
+  const int kvh = vh / p.head_chunks;
+  const int h0 = kvh * p.group + (vh % p.head_chunks) * GC;
   const int r = lane / LPT;
   const int c = lane % LPT;
 
@@ -143,27 +61,22 @@ __global__ __launch_bounds__(WAVES * kWave) void paged_attention_kernel(const At
   row_context(p, row, req, len);
   int t_begin = 0, t_end = len;
   if constexpr (SPLIT) {
-    t_begin = blockIdx.z * p.partition_size;
+    t_begin = wg.part * p.partition_size;
     t_end = min(len, t_begin + p.partition_size);
     if (t_begin >= t_end) return;  // the reduce kernel reads only partitions that hold tokens
   } else if (len == 0) {
-    // Padding row: zeros, and nothing of the cache is read.
-    uint16_t* out = static_cast<uint16_t*>(p.out);
-    for (int it = tid; it < GC * LPT; it += THREADS) {
-      const int g = it / LPT, cc = it % LPT;
-      *reinterpret_cast<u32x4*>(out + ((int64_t)row * p.num_heads + h0 + g) * D + cc * 8) =
-          u32x4{0u, 0u, 0u, 0u};
-    }
+    if (active) store_zero_rows<D, GC, kWave>(p, row, h0, lane);
     return;
   }
 
   // This lane's 8 elements of each of the GC query heads, kept packed for v_dot2.
   uint32_t qw[GC][4];
+  if (active) {
 #pragma unroll
-  for (int g = 0; g < GC; ++g) {
-    const u32x4 v = *reinterpret_cast<const u32x4*>(p.q + ((int64_t)row * p.num_heads + h0 + g) * D +
-                                                    c * 8);
-    qw[g][0] = v.x; qw[g][1] = v.y; qw[g][2] = v.z; qw[g][3] = v.w;
+    for (int g = 0; g < GC; ++g) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(p.q + ((int64_t)row * p.num_heads + h0 + g) * D + c * 8);
+      qw[g][0] = v.x; qw[g][1] = v.y; qw[g][2] = v.z; qw[g][3] = v.w;
+    }
   }
 
   float m[GC], l[GC], o[GC][8];
@@ -179,7 +92,7 @@ __global__ __launch_bounds__(WAVES * kWave) void paged_attention_kernel(const At
   const int shift = p.bs_shift;
   const int bs_mask = (1 << shift) - 1;
   const int seg_len = (((kTableCap - 1) << shift) / CH) * CH;
-  const uint32_t block_stride = (uint32_t)p.block_stride;  // the host checks these fit 32 bits
+  const uint32_t block_stride = (uint32_t)p.block_stride;  // the host checks the pool fits 32 bits
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + c * 8;
@@ -187,25 +100,18 @@ __global__ __launch_bounds__(WAVES * kWave) void paged_attention_kernel(const At
 
   for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
     const int s1 = min(t_end, s0 + seg_len);
-    const int b0 = s0 >> shift;
-    const int nb = ((s1 - 1) >> shift) - b0 + 1;
-    __syncthreads();  // the previous segment is done with s_tbl
-    for (int i = tid; i < nb; i += THREADS) {
-      const int b = tbl[b0 + i];
-      s_tbl[i] = ((unsigned)b < (unsigned)p.num_blocks) ? b : 0;
-    }
-    __syncthreads();
-
+    const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, threads);
+    if (!active) continue;
     const int nch = (s1 - s0 + CH - 1) / CH;
 
     // Element offsets of this lane's NLD tokens of chunk ci (past-the-end tokens
     // are clamped to the last one and masked later).
-    auto offsets = [&](int ci, uint64_t(&dst)[NLD]) {
+    auto offsets = [&](int ci, uint32_t(&dst)[NLD]) {
 #pragma unroll
       for (int j = 0; j < NLD; ++j) {
         const int t = min(s0 + ci * CH + j * TPL + r, s1 - 1);
         const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
-        dst[j] = (uint64_t)blk * block_stride + (uint32_t)(t & bs_mask) * token_stride;
+        dst[j] = blk * block_stride + (uint32_t)(t & bs_mask) * token_stride;
       }
     };
 
@@ -314,38 +220,34 @@ __global__ __launch_bounds__(WAVES * kWave) void paged_attention_kernel(const At
 
     // Two register sets, used alternately: while one chunk is folded in, the
     // keys of the next chunk are already in flight (unrolled twice so no copies).
-    uint64_t offA[NLD], offB[NLD];
+    uint32_t offA[NLD], offB[NLD];
     u32x4 kA[NLD], kB[NLD], vc[NLD];
-    int ci = wave;
-    if (ci < nch) {
-      offsets(ci, offA);
+    int ci = 0;
+    offsets(0, offA);
 #pragma unroll
-      for (int j = 0; j < NLD; ++j) kA[j] = stream_load(kbase + offA[j]);
-    }
+    for (int j = 0; j < NLD; ++j) kA[j] = stream_load(kbase + offA[j]);
     while (ci < nch) {
 #pragma unroll
       for (int j = 0; j < NLD; ++j) vc[j] = stream_load(vbase + offA[j]);
-      int cn = ci + WAVES;
-      if (cn < nch) {
-        offsets(cn, offB);
+      if (ci + 1 < nch) {
+        offsets(ci + 1, offB);
 #pragma unroll
         for (int j = 0; j < NLD; ++j) kB[j] = stream_load(kbase + offB[j]);
       }
       consume(ci, kA, vc);
-      ci = cn;
-      if (ci >= nch) break;
+      if (++ci >= nch) break;
 #pragma unroll
       for (int j = 0; j < NLD; ++j) vc[j] = stream_load(vbase + offB[j]);
-      cn = ci + WAVES;
-      if (cn < nch) {
-        offsets(cn, offA);
+      if (ci + 1 < nch) {
+        offsets(ci + 1, offA);
 #pragma unroll
         for (int j = 0; j < NLD; ++j) kA[j] = stream_load(kbase + offA[j]);
       }
       consume(ci, kB, vc);
-      ci = cn;
+      ++ci;
     }
   }
+  if (!active) return;
 
   // Merge the TPL lane groups of this wave (butterfly: every group ends with the merged state).
 #pragma unroll
@@ -365,60 +267,7 @@ __global__ __launch_bounds__(WAVES * kWave) void paged_attention_kernel(const At
   }
   if (r == 0) {
 #pragma unroll
-    for (int g = 0; g < GC; ++g) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s_o[wave][g][c * 8 + e] = o[g][e];
-      if (c == 0) {
-        s_m[wave][g] = m[g];
-        s_l[wave][g] = l[g];
-      }
-    }
-  }
-  __syncthreads();
-
-  // Merge the waves and write: one thread per (head, 8 elements).
-  for (int it = tid; it < GC * LPT; it += THREADS) {
-    const int g = it / LPT, cc = it % LPT;
-    float mn = s_m[0][g];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) mn = fmaxf(mn, s_m[w][g]);
-    float wt[WAVES];
-    float L = 0.f;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      wt[w] = fast_exp2(s_m[w][g] - mn);
-      L += s_l[w][g] * wt[w];
-    }
-    float acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float a = 0.f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) a = fmaf(wt[w], s_o[w][g][cc * 8 + e], a);
-      acc[e] = a;
-    }
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
-    const int64_t head_row = (int64_t)row * p.num_heads + h0 + g;
-    if constexpr (SPLIT) {
-      float* po = p.part_o + (head_row * p.max_partitions + blockIdx.z) * D + cc * 8;
-      typedef float f32x4 __attribute__((ext_vector_type(4)));
-      *reinterpret_cast<f32x4*>(po) = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
-      *reinterpret_cast<f32x4*>(po + 4) =
-          f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
-      if (cc == 0) {
-        float* pml = p.part_ml + (head_row * p.max_partitions + blockIdx.z) * 2;
-        pml[0] = mn;
-        pml[1] = L;
-      }
-    } else {
-      uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D + cc * 8;
-      u32x4 w;
-      w.x = E::round(acc[0] * inv) | (E::round(acc[1] * inv) << 16);
-      w.y = E::round(acc[2] * inv) | (E::round(acc[3] * inv) << 16);
-      w.z = E::round(acc[4] * inv) | (E::round(acc[5] * inv) << 16);
-      w.w = E::round(acc[6] * inv) | (E::round(acc[7] * inv) << 16);
-      *reinterpret_cast<u32x4*>(out) = w;
-    }
+    for (int g = 0; g < GC; ++g) store_head<D, BF16, SPLIT>(p, row, wg.part, h0 + g, c, o[g], m[g], l[g]);
   }
 }
 
@@ -429,8 +278,8 @@ template <int D, bool BF16>
 __global__ __launch_bounds__(kWave) void partition_reduce_kernel(const AttnParams p) {
   using E = Elem<BF16>;
   constexpr int EPL = D / kWave;  // 1, 2 or 4 elements per lane
-  const int h = blockIdx.x;
-  const int row = blockIdx.y;
+  const int h = blockIdx.x % p.num_heads;
+  const int row = blockIdx.x / p.num_heads;
   const int lane = threadIdx.x;
   int req, len;
   row_context(p, row, req, len);
@@ -476,51 +325,69 @@ __global__ __launch_bounds__(kWave) void partition_reduce_kernel(const AttnParam
 // Host-side dispatch.
 
 template <int D, int GC, bool BF16>
-static hipError_t launch_typed(const AttnParams& p, bool split, hipStream_t stream) {
-  constexpr int NLD = (D == 64) ? 2 : 4;
-  constexpr int WAVES = 4;
-  const dim3 block(WAVES * kWave);
-  const int hy = (p.num_heads / p.group) * p.head_chunks;
-  if (!split) {
-    hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, WAVES, BF16, false>), dim3(p.n_rows, hy, 1),
-                       block, 0, stream, p);
-    return hipGetLastError();
-  }
-  hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, WAVES, BF16, true>),
-                     dim3(p.n_rows, hy, p.max_partitions), block, 0, stream, p);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  hipLaunchKernelGGL((partition_reduce_kernel<D, BF16>), dim3(p.num_heads, p.n_rows, 1),
-                     dim3(kWave), 0, stream, p);
+static hipError_t launch_dpp_typed(const AttnParams& p, bool split, hipStream_t stream) {
+  // Two loads per token slot per chunk: 8 tokens (D 128), 16 (D 64) or 4 (D 256) per
+  // chunk keeps a group of 4 under 128 VGPRs, so two 8-wave workgroups share a CU.
+  constexpr int NLD = 2;
+  // One wave per virtual head, up to kMaxWaves per workgroup.
+  const int waves = p.num_virtual_heads < kMaxWaves ? p.num_virtual_heads : kMaxWaves;
+  const int groups = (p.num_virtual_heads + waves - 1) / waves;
+  const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);
+  const dim3 grid((unsigned)(items * groups)), block(waves * kWave);
+  if (split)
+    hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, BF16, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((paged_attention_kernel<D, GC, NLD, BF16, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
 template <int D, bool BF16>
-static hipError_t launch_gc(const AttnParams& p, int gc, bool split, hipStream_t stream) {
+static hipError_t launch_dpp_gc(const AttnParams& p, int gc, bool split, hipStream_t stream) {
   switch (gc) {
-    case 1: return launch_typed<D, 1, BF16>(p, split, stream);
-    case 2: return launch_typed<D, 2, BF16>(p, split, stream);
-    case 3: return launch_typed<D, 3, BF16>(p, split, stream);
-    case 4: return launch_typed<D, 4, BF16>(p, split, stream);
-    case 5: return launch_typed<D, 5, BF16>(p, split, stream);
-    case 6: return launch_typed<D, 6, BF16>(p, split, stream);
-    case 7: return launch_typed<D, 7, BF16>(p, split, stream);
-    case 8: return launch_typed<D, 8, BF16>(p, split, stream);
+    case 1: return launch_dpp_typed<D, 1, BF16>(p, split, stream);
+    case 2: return launch_dpp_typed<D, 2, BF16>(p, split, stream);
+    case 3: return launch_dpp_typed<D, 3, BF16>(p, split, stream);
+    case 4: return launch_dpp_typed<D, 4, BF16>(p, split, stream);
+    case 5: return launch_dpp_typed<D, 5, BF16>(p, split, stream);
+    case 6: return launch_dpp_typed<D, 6, BF16>(p, split, stream);
+    case 7: return launch_dpp_typed<D, 7, BF16>(p, split, stream);
+    case 8: return launch_dpp_typed<D, 8, BF16>(p, split, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t launch_paged_attention(const AttnParams& p, int head_dim, int gc, bool bf16, bool split,
-                                  hipStream_t stream) {
+hipError_t launch_attention_dpp(const AttnParams& p, int head_dim, int gc, bool bf16, bool split, int waves,
+                                hipStream_t stream) {
+  (void)waves;  // one workgroup shape (4 waves) for this kernel
   switch (head_dim) {
-    case 64: return bf16 ? launch_gc<64, true>(p, gc, split, stream)
-                         : launch_gc<64, false>(p, gc, split, stream);
-    case 128: return bf16 ? launch_gc<128, true>(p, gc, split, stream)
-                          : launch_gc<128, false>(p, gc, split, stream);
-    case 256: return bf16 ? launch_gc<256, true>(p, gc, split, stream)
-                          : launch_gc<256, false>(p, gc, split, stream);
+    case 64: return bf16 ? launch_dpp_gc<64, true>(p, gc, split, stream)
+                         : launch_dpp_gc<64, false>(p, gc, split, stream);
+    case 128: return bf16 ? launch_dpp_gc<128, true>(p, gc, split, stream)
+                          : launch_dpp_gc<128, false>(p, gc, split, stream);
+    case 256: return bf16 ? launch_dpp_gc<256, true>(p, gc, split, stream)
+                          : launch_dpp_gc<256, false>(p, gc, split, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream) {
+  const dim3 grid((unsigned)((int64_t)p.num_heads * p.n_rows)), block(kWave);
+  switch (head_dim) {
+    case 64:
+      if (bf16) hipLaunchKernelGGL((partition_reduce_kernel<64, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((partition_reduce_kernel<64, false>), grid, block, 0, stream, p);
+      break;
+    case 128:
+      if (bf16) hipLaunchKernelGGL((partition_reduce_kernel<128, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((partition_reduce_kernel<128, false>), grid, block, 0, stream, p);
+      break;
+    case 256:
+      if (bf16) hipLaunchKernelGGL((partition_reduce_kernel<256, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((partition_reduce_kernel<256, false>), grid, block, 0, stream, p);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace ayk

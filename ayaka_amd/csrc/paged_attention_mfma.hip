@@ -1,0 +1,291 @@
+// Paged-attention decode with the q.k contraction on the matrix cores (gfx950).
+//
+// Same semantics, grid and outputs as the DPP kernel in paged_attention.hip;
+// only the way a wave turns a chunk of 16 keys into weights differs:
+//
+//  * q.k for 16 tokens x (up to 16) query heads is one 16x16 tile, accumulated
+//    over head_dim in k-steps of 32 by v_mfma_f32_16x16x32_{bf16,f16}: exact
+//    products, fp32 sums. Lane l feeds token l%16 / head l%16 and k-slice
+//    8*(l/16) of each step, so a load instruction reads 64 contiguous bytes of
+//    16 different tokens and q needs only head_dim/32 registers per lane,
+//    whatever the group size. Lane l gets the scores of tokens 4*(l/16)+i,
+//    i < 4, for head l%16.
+//  * The softmax runs on those 4 scores per lane (max across the 4 lane
+//    groups with two shuffles); the weights go through a small per-wave LDS
+//    tile to the lanes that hold the values.
+//  * P.V stays on the VALU in fp32 (a bf16 P would cost ~2e-3 relative error),
+//    with the value layout of the DPP kernel: lane (r, c) holds 8 elements of
+//    tokens j*TPL + r.
+//
+// With 4-8 query heads per key/value head this removes the per-token dot2 and
+// butterfly work that makes the DPP kernel VALU-bound.
+#include "attention_common.h"
+
+namespace ayk {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma_qk(u32x4 k, u32x4 q, f32x4 acc) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, k),
+                                                   __builtin_bit_cast(bf16x8, q), acc, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, k),
+                                                  __builtin_bit_cast(f16x8, q), acc, 0, 0, 0);
+  }
+}
+
+// Order the LDS traffic of one wave: lanes read what other lanes of the same
+// wave wrote just before (the wave's LDS operations execute in program order).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int D, int GC, int WAVES, bool BF16, bool SPLIT>
+__global__ __launch_bounds__(WAVES * kWave) void paged_attention_mfma_kernel(const AttnParams p) {
+  using E = Elem<BF16>;
+  constexpr int THREADS = WAVES * kWave;
+  constexpr int CH = 16;            // tokens per chunk: the MFMA tile height
+  constexpr int KS = D / 32;        // MFMA k-steps over head_dim
+  constexpr int LPT = D / 8;        // value lanes per token
+  constexpr int TPL = kWave / LPT;  // tokens per value load
+  constexpr int NV = CH / TPL;      // value loads per chunk
+  constexpr int PW = ((GC + 3) / 4) * 4;  // weights per token in LDS, padded to float4
+
+  __shared__ int s_tbl[kTableCap];
+  __shared__ WaveParts<D, GC, WAVES> parts;
+  __shared__ float s_p[WAVES][2][CH][PW];  // weights of the chunk, double-buffered
+  __shared__ float s_alpha[WAVES][PW];
+
+  const WgCoord wg = wg_coord(p, p.num_virtual_heads, SPLIT);
+  const int row = wg.row;
+  const int kvh = wg.group / p.head_chunks;
+  const int h0 = kvh * p.group + (wg.group % p.head_chunks) * GC;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int mt = lane % 16;  // MFMA: token of the key operand, head of q and of the scores
+  const int mq = lane / 16;  // MFMA: k-slice of the operands, token group of the scores
+  const int r = lane / LPT;  // values: token within a load
+  const int c = lane % LPT;  // values: 8-element slice of head_dim
+
+  int req, len;
+  row_context(p, row, req, len);
+  int t_begin = 0, t_end = len;
+  if constexpr (SPLIT) {
+    t_begin = wg.part * p.partition_size;
+    t_end = min(len, t_begin + p.partition_size);
+    if (t_begin >= t_end) return;
+  } else if (len == 0) {
+    store_zero_rows<D, GC, THREADS>(p, row, h0, tid);
+    return;
+  }
+
+  // q as the MFMA B operand: head mt (zero columns past the group), k-slice mq.
+  u32x4 qb[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    qb[s] = (mt < GC) ? *reinterpret_cast<const u32x4*>(p.q + ((int64_t)row * p.num_heads + h0 + mt) * D +
+                                                         s * 32 + mq * 8)
+                      : u32x4{0u, 0u, 0u, 0u};
+  }
+
+  float m_h = kNoScore;  // running max of head mt (same in its 4 lanes)
+  float l_h = 0.f;       // this lane's share of head mt's weight sum
+  float o[GC][8];
+#pragma unroll
+  for (int g = 0; g < GC; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+
+  const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
+  const int shift = p.bs_shift;
+  const int bs_mask = (1 << shift) - 1;
+  const int seg_len = (((kTableCap - 1) << shift) / CH) * CH;
+  const uint32_t block_stride = (uint32_t)p.block_stride;
+  const uint32_t token_stride = (uint32_t)p.token_stride;
+  const float scale_log2 = p.scale_log2;
+  const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + mq * 8;
+  const uint16_t* vbase = p.v_cache + (int64_t)kvh * p.head_stride + c * 8;
+
+  for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
+    const int s1 = min(t_end, s0 + seg_len);
+    const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, THREADS);
+    const int nch = (s1 - s0 + CH - 1) / CH;
+
+    auto offset_of = [&](int t) -> uint64_t {
+      t = min(t, s1 - 1);
+      const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
+      return (uint64_t)blk * block_stride + (uint32_t)(t & bs_mask) * token_stride;
+    };
+    auto load_keys = [&](int ci, u32x4(&kc)[KS]) {
+      const uint16_t* a = kbase + offset_of(s0 + ci * CH + mt);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kc[s] = stream_load(a + s * 32);
+    };
+    auto load_values = [&](int ci, u32x4(&vc)[NV]) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) vc[j] = stream_load(vbase + offset_of(s0 + ci * CH + j * TPL + r));
+    };
+
+    auto consume = [&](int ci, int buf, const u32x4(&kc)[KS], const u32x4(&vc)[NV]) {
+      const int tb = s0 + ci * CH;
+      const bool tail = tb + CH > s1;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) acc = mfma_qk<BF16>(kc[s], qb[s], acc);
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = acc[i] * scale_log2;
+        if (mt >= GC || (tail && tb + 4 * mq + i >= s1)) sc[i] = -INFINITY;
+      }
+      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if (__builtin_amdgcn_ballot_w64(mx > m_h + kRescaleSlack)) {
+        const float mn = fmaxf(m_h, mx);
+        const float alpha = fast_exp2(m_h - mn);
+        l_h *= alpha;
+        m_h = mn;
+        if (mq == 0 && mt < PW) s_alpha[wave][mt] = alpha;
+        wave_lds_sync();
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+          const float a = s_alpha[wave][g];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[g][e] *= a;
+        }
+      }
+      float w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        w[i] = fast_exp2(sc[i] - m_h);
+        l_h += w[i];
+      }
+      if (mt < PW) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_p[wave][buf][4 * mq + i][mt] = w[i];
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        float pw[PW];
+#pragma unroll
+        for (int g4 = 0; g4 < PW; g4 += 4) {
+          const f32x4 v4 = *reinterpret_cast<const f32x4*>(&s_p[wave][buf][j * TPL + r][g4]);
+          pw[g4] = v4.x; pw[g4 + 1] = v4.y; pw[g4 + 2] = v4.z; pw[g4 + 3] = v4.w;
+        }
+        float vf[8];
+        vf[0] = E::lo(vc[j].x); vf[1] = E::hi(vc[j].x);
+        vf[2] = E::lo(vc[j].y); vf[3] = E::hi(vc[j].y);
+        vf[4] = E::lo(vc[j].z); vf[5] = E::hi(vc[j].z);
+        vf[6] = E::lo(vc[j].w); vf[7] = E::hi(vc[j].w);
+        if (tail && tb + j * TPL + r >= s1) {
+          // A slot past the context may hold anything, NaN included, and 0 * NaN is NaN.
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vf[e] = 0.f;
+        }
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pw[g], vf[e], o[g][e]);
+        }
+      }
+    };
+
+    // Keys of the next chunk are in flight while the current one is folded in.
+    u32x4 kA[KS], kB[KS], vc[NV];
+    int ci = wave;
+    if (ci < nch) load_keys(ci, kA);
+    while (ci < nch) {
+      load_values(ci, vc);
+      int cn = ci + WAVES;
+      if (cn < nch) load_keys(cn, kB);
+      consume(ci, 0, kA, vc);
+      ci = cn;
+      if (ci >= nch) break;
+      load_values(ci, vc);
+      cn = ci + WAVES;
+      if (cn < nch) load_keys(cn, kA);
+      consume(ci, 1, kB, vc);
+      ci = cn;
+    }
+  }
+
+  // Head mt's weight sum over the wave's 4 token groups; the value lanes' partial
+  // sums share the wave's running max, so they add without rescaling.
+  l_h += __shfl_xor(l_h, 16);
+  l_h += __shfl_xor(l_h, 32);
+#pragma unroll
+  for (int st = LPT; st < kWave; st <<= 1)
+#pragma unroll
+    for (int g = 0; g < GC; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] += __shfl_xor(o[g][e], st);
+  if (r == 0) {
+#pragma unroll
+    for (int g = 0; g < GC; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) parts.o[wave][g][c * 8 + e] = o[g][e];
+  }
+  if (mq == 0 && mt < GC) {
+    parts.m[wave][mt] = m_h;
+    parts.l[wave][mt] = l_h;
+  }
+  __syncthreads();
+  merge_waves_and_store<D, GC, WAVES, BF16, SPLIT>(p, parts, row, wg.part, h0, tid);
+}
+
+template <int D, int GC, bool BF16>
+static hipError_t launch_mfma_typed(const AttnParams& p, bool split, int waves, hipStream_t stream) {
+  const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);
+  const dim3 grid((unsigned)(items * p.num_virtual_heads));
+#define AYK_LAUNCH(W)                                                                               \
+  if (split)                                                                                        \
+    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, W, BF16, true>), grid, dim3(W * kWave), 0, \
+                       stream, p);                                                                  \
+  else                                                                                              \
+    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, W, BF16, false>), grid, dim3(W * kWave),  \
+                       0, stream, p);
+  switch (waves) {
+    case 2: AYK_LAUNCH(2) break;
+    default: AYK_LAUNCH(4) break;
+  }
+#undef AYK_LAUNCH
+  return hipGetLastError();
+}
+
+template <int D, bool BF16>
+static hipError_t launch_mfma_gc(const AttnParams& p, int gc, bool split, int waves, hipStream_t stream) {
+  switch (gc) {
+    case 1: return launch_mfma_typed<D, 1, BF16>(p, split, waves, stream);
+    case 2: return launch_mfma_typed<D, 2, BF16>(p, split, waves, stream);
+    case 3: return launch_mfma_typed<D, 3, BF16>(p, split, waves, stream);
+    case 4: return launch_mfma_typed<D, 4, BF16>(p, split, waves, stream);
+    case 5: return launch_mfma_typed<D, 5, BF16>(p, split, waves, stream);
+    case 6: return launch_mfma_typed<D, 6, BF16>(p, split, waves, stream);
+    case 7: return launch_mfma_typed<D, 7, BF16>(p, split, waves, stream);
+    case 8: return launch_mfma_typed<D, 8, BF16>(p, split, waves, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int gc, bool bf16, bool split, int waves,
+                                 hipStream_t stream) {
+  switch (head_dim) {
+    case 64: return bf16 ? launch_mfma_gc<64, true>(p, gc, split, waves, stream)
+                         : launch_mfma_gc<64, false>(p, gc, split, waves, stream);
+    case 128: return bf16 ? launch_mfma_gc<128, true>(p, gc, split, waves, stream)
+                          : launch_mfma_gc<128, false>(p, gc, split, waves, stream);
+    case 256: return bf16 ? launch_mfma_gc<256, true>(p, gc, split, waves, stream)
+                          : launch_mfma_gc<256, false>(p, gc, split, waves, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace ayk

@@ -28,7 +28,7 @@ launch shape comes from the bucket's table width.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
@@ -53,18 +53,26 @@ __all__ = [
     "attend",
     "attend_with",
     "choose_partitions",
+    "choose_split",
     "graph_metadata",
     "plan",
     "update_graph_metadata",
 ]
 
-#: Positions per v2 partition (a multiple of 64).
+#: Positions per v2 partition when only the table width is known (graph metadata).
 PARTITION_SIZE = 512
+#: The smallest partition an eagerly planned step is split into.
+MIN_PARTITION = 256
+#: Positions per partition for the matrix-core kernel.
+MFMA_PARTITION = 2048
+#: Heads per wave from which the library runs q.k on the matrix cores (mirrors the C library).
+MFMA_MIN_HEADS = 6
 #: Compute units of one MI355X; the split heuristic aims to keep all of them busy.
 COMPUTE_UNITS = 256
 
 _LAYOUT_CODES = {KVLayoutKind.NHD: 0, KVLayoutKind.HND: 1}
 _DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+_QK_FLAGS = {None: 0, "dpp": 1, "mfma": 2}
 
 
 @dataclass(frozen=True, slots=True)
@@ -78,6 +86,30 @@ class HipAttentionPlan:
     rows: tuple[int, ...]
     kv_lengths: tuple[int, ...]
     max_length: int
+    total_length: int
+    row_lengths: tuple[int, ...] = ()
+    # v2 work lists built by the step's first attend, keyed by partition size, for the later layers
+    work: dict[int, torch.Tensor] = field(default_factory=dict, compare=False, repr=False)
+
+    def work_items(self, partition_size: int, device: torch.device) -> torch.Tensor:
+        """The (row, partition) pairs of the step that hold tokens, longest first, on ``device``.
+
+        Every full partition comes before any partial one, so the last
+        workgroups to start are the short ones and consecutive workgroups land on
+        different XCDs.
+        """
+        found = self.work.get(partition_size)
+        if found is None:
+            items = []
+            for row, length in enumerate(self.row_lengths):
+                for part in range(-(-length // partition_size)):
+                    size = min(partition_size, length - part * partition_size)
+                    items.append((-size, row, part))
+            items.sort()
+            flat = [v for _, row, part in items for v in (row, part)]
+            found = torch.tensor(flat, dtype=torch.int32).to(device)
+            self.work[partition_size] = found
+        return found
 
 
 @dataclass(frozen=True, slots=True, eq=False)
@@ -161,6 +193,7 @@ def plan(
     request_of_row: list[int] = []
     positions: list[int] = []
     slots: list[int] = []
+    row_lengths: list[int] = []
     table_list = table_host.tolist()
     for request, (count, length) in enumerate(zip(rows, lengths)):
         for j in range(count):
@@ -168,9 +201,11 @@ def plan(
             if length == 0:
                 positions.append(0)
                 slots.append(0)
+                row_lengths.append(0)
             else:
                 position = length - count + j
                 positions.append(position)
+                row_lengths.append(position + 1)
                 slots.append(
                     table_list[request][position // block_size] * block_size
                     + position % block_size
@@ -186,33 +221,68 @@ def plan(
         slot_mapping=torch.tensor(slots, dtype=torch.int64, device=device),
         kv_lengths=torch.tensor(lengths, dtype=torch.int32, device=device),
         block_table=block_rows.to(device=device, dtype=torch.int32).contiguous(),
-        plan=HipAttentionPlan(rows, lengths, max(lengths, default=0)),
+        plan=HipAttentionPlan(rows, lengths, max(lengths, default=0), sum(row_lengths), tuple(row_lengths)),
     )
 
 
 def head_chunks(group: int) -> int:
-    """Workgroups that share one key/value head's query heads (at most 8 heads each)."""
+    """Chunks the query heads of one key/value head are split into (at most 8 heads each)."""
     for chunks in range(1, group + 1):
         if group % chunks == 0 and group // chunks <= 8:
             return chunks
     return group
 
 
-def choose_partitions(n_rows: int, num_kv_heads: int, group: int, max_length: int) -> int:
-    """Partitions per row for v2, or 0 to run v1.
+def uses_matrix_cores(group: int) -> bool:
+    """Whether the library picks the MFMA q.k kernel for this group size (6+ heads per wave)."""
+    return group // head_chunks(group) >= MFMA_MIN_HEADS
 
-    v1 gives one workgroup per (row, key/value head). When that is too few
-    workgroups to keep the 256 compute units streaming, or a context is long
-    enough that one workgroup's serial walk dominates, the context is split into
-    :data:`PARTITION_SIZE` pieces. Depends only on the step's shape.
+
+@dataclass(frozen=True, slots=True)
+class Split:
+    """A launch: ``partitions == 0`` is v1, otherwise v2 over partitions of ``partition_size``."""
+
+    partition_size: int
+    partitions: int
+
+
+def choose_split(
+    n_rows: int, num_kv_heads: int, group: int, max_length: int, total_length: int | None = None
+) -> Split:
+    """Pick v1 or v2 and the partition size from the step's shape.
+
+    The DPP kernel runs one workgroup of up to 8 waves (one per key/value head)
+    per (row, partition); two such workgroups fit a compute unit, so
+    ``2 * COMPUTE_UNITS`` workgroups run in one round. With the total context
+    known (an eagerly planned step), the partition is sized so the whole grid is
+    about one round -- no tail -- but never below :data:`MIN_PARTITION`
+    positions, whose fixed cost per workgroup would dominate. Without it (graph
+    metadata, where only the table width is fixed) partitions are
+    :data:`PARTITION_SIZE`. The matrix-core kernel runs 4-wave workgroups per
+    (row, key/value head, partition) and streams best in partitions of
+    :data:`MFMA_PARTITION`. A context that fits one partition runs v1.
     """
-    if max_length <= PARTITION_SIZE:
-        return 0
-    workgroups = n_rows * num_kv_heads * head_chunks(group)
-    partitions = -(-max_length // PARTITION_SIZE)
-    if workgroups >= 8 * COMPUTE_UNITS and partitions <= 2:
-        return 0
-    return partitions
+    if max_length <= 0:
+        return Split(0, 0)
+    if uses_matrix_cores(group):
+        size = MFMA_PARTITION
+    elif total_length is None:
+        size = PARTITION_SIZE
+    else:
+        virtual = num_kv_heads * head_chunks(group)
+        groups = -(-virtual // 8)
+        slots = 2 * COMPUTE_UNITS
+        size = -(-(total_length * groups) // slots)
+        size = max(MIN_PARTITION, -(-size // 64) * 64)
+    if max_length <= size:
+        return Split(0, 0)
+    return Split(size, -(-max_length // size))
+
+
+def choose_partitions(n_rows: int, num_kv_heads: int, group: int, max_length: int) -> int:
+    """Partitions of :data:`PARTITION_SIZE` for a step known only by its longest context (0 = v1)."""
+    split = choose_split(n_rows, num_kv_heads, group, max_length)
+    return split.partitions
 
 
 _workspaces: dict[torch.device, torch.Tensor] = {}
@@ -259,13 +329,17 @@ def attend_with(
     *,
     scale: float,
     partitions: int | None,
+    qk: str | None = None,
+    partition_size: int | None = None,
 ) -> None:
     """:func:`attend` with the launch chosen by the caller.
 
     ``partitions`` 0 runs v1, a positive count runs v2 over that many partitions
-    (it must cover the step's longest context), ``None`` lets
-    :func:`choose_partitions` decide. Benchmarks and tests use it to time and
-    check both kernels on one step.
+    of ``partition_size`` (default :data:`PARTITION_SIZE`; together they must
+    cover the step's longest context), ``None`` lets :func:`choose_split` decide. ``qk`` forces the q.k implementation,
+    ``"dpp"`` (VALU dot2 + DPP butterflies) or ``"mfma"`` (matrix cores); ``None``
+    lets the library pick. Benchmarks and tests use it to time and check every
+    kernel on one step.
     """
     op = "attention.attend"
     require_buffers(op, buffers)
@@ -319,9 +393,9 @@ def attend_with(
     if isinstance(step, HipGraphPlan):
         if not decode:
             raise BackendError(f"{op}: graph metadata must be a DECODE step", context={"op": op})
-        max_length = step.max_blocks * block_size
+        max_length, total_length = step.max_blocks * block_size, None
     else:
-        max_length = step.max_length
+        max_length, total_length = step.max_length, step.total_length
     if n_rows == 0:
         return
     if table.dtype != torch.int32 or not table.is_contiguous() or table.ndim != 2:
@@ -355,21 +429,34 @@ def attend_with(
         float(scale),
     )
     if partitions is None:
-        partitions = choose_partitions(n_rows, kv_heads, group, max_length)
-    elif partitions and partitions * PARTITION_SIZE < max_length:
+        split = choose_split(n_rows, kv_heads, group, max_length, total_length)
+        if qk is not None and uses_matrix_cores(group) != (qk == "mfma"):
+            split = Split(PARTITION_SIZE, -(-max_length // PARTITION_SIZE)) if max_length > PARTITION_SIZE \
+                else Split(0, 0)
+        partitions, partition_size = split.partitions, split.partition_size
+    partition_size = partition_size or PARTITION_SIZE
+    if partitions and partitions * partition_size < max_length:
         raise BackendError(
-            f"{op}: {partitions} partitions of {PARTITION_SIZE} do not cover {max_length} positions",
+            f"{op}: {partitions} partitions of {partition_size} do not cover {max_length} positions",
             context={"op": op},
         )
+    flags = _QK_FLAGS[qk]
     if partitions == 0:
-        _lib.check(op, lib.ayk_paged_attention_v1(*common, stream))
+        _lib.check(op, lib.ayk_paged_attention_v1(*common, flags, stream))
         return
     nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, partitions)
     scratch = _workspace(op, device, nbytes, capturing(q))
+    # An eager step runs only the partitions that hold tokens, longest first; graph
+    # metadata keeps the dense grid, whose shape does not depend on the lengths.
+    work, n_work = 0, 0
+    if isinstance(step, HipAttentionPlan) and not capturing(q):
+        items = step.work_items(partition_size, device)
+        work, n_work = items.data_ptr(), items.numel() // 2
     _lib.check(
         op,
         lib.ayk_paged_attention_v2(
-            *common, PARTITION_SIZE, partitions, scratch.data_ptr(), scratch.numel(), stream
+            *common, partition_size, partitions, work, n_work, scratch.data_ptr(), scratch.numel(), flags,
+            stream,
         ),
     )
 

@@ -38,6 +38,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--config", type=int, default=3, help="benchmark configuration 1-5 (3 = headline)")
     ap.add_argument("--only", choices=["auto", "v1", "v2"], default=None,
                     help="time only this launch (for profiler runs)")
+    ap.add_argument("--qk", choices=["dpp", "mfma"], default=None,
+                    help="force the q.k implementation (default: the library's choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=8, help="rows of the CPU baseline sample")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -135,21 +137,23 @@ def main() -> int:
     out = torch.empty_like(step.q)
     nbytes = workloads.algorithmic_bytes(cfg)
     max_len = max(cfg.lengths)
-    auto_parts = hip_attention.choose_partitions(cfg.batch, cfg.kv_heads, cfg.heads // cfg.kv_heads, max_len)
+    auto = hip_attention.choose_split(cfg.batch, cfg.kv_heads, cfg.heads // cfg.kv_heads, max_len, sum(cfg.lengths))
     launches = {
-        "auto": auto_parts,
-        "v1": 0,
-        "v2": -(-max_len // hip_attention.PARTITION_SIZE),
+        "auto": (None, auto.partition_size),
+        "v1": (0, 0),
+        "v2": (-(-max_len // hip_attention.PARTITION_SIZE), hip_attention.PARTITION_SIZE),
     }
     if args.only:
         launches = {args.only: launches[args.only]}
 
     results = {}
-    for name, parts in launches.items():
-        def call(parts=parts):
-            hip_attention.attend_with(step.q, buffers, meta, out, scale=cfg.scale, partitions=parts)
+    for name, (parts, size) in launches.items():
+        def call(parts=parts, size=size):
+            hip_attention.attend_with(step.q, buffers, meta, out, scale=cfg.scale, partitions=parts, qk=args.qk,
+                                      partition_size=size or None)
         results[name] = time_calls(call, args.steps, args.warmup)
-        results[name]["partitions"] = parts
+        results[name]["partitions"] = auto.partitions if parts is None else parts
+        results[name]["partition_size"] = size
         results[name]["gbs"] = nbytes / (results[name]["median_us"] * 1e-6) / 1e9
         print(f"[bench] {cfg.name} {name}: {results[name]['median_us']:.1f} us/call "
               f"{results[name]['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
@@ -180,10 +184,11 @@ def main() -> int:
                         f"pool {cfg.num_blocks} blocks",
             "algorithmic_bytes_per_call": nbytes,
             "launch": "v1" if head["partitions"] == 0 else f"v2 x{head['partitions']} partitions of "
-                                                          f"{hip_attention.PARTITION_SIZE}",
+                                                          f"{head['partition_size']}",
         },
         "kernels": {k: {"us_per_call": round(v["median_us"], 2), "gbs": round(v["gbs"], 1),
-                        "partitions": v["partitions"]} for k, v in results.items()},
+                        "partitions": v["partitions"], "partition_size": v["partition_size"]}
+                    for k, v in results.items()},
         "kv_write": {"us_per_call": round(store_us, 2), "rows": int(step.k_new.shape[0]),
                      "bytes": workloads.store_bytes(cfg)},
         "roofline": {

@@ -40,6 +40,12 @@ enum {
 };
 
 enum { AYK_DTYPE_FP16 = 0, AYK_DTYPE_BF16 = 1 };
+
+/* flags of the attention calls: 0 lets the library pick the q.k path. */
+enum {
+  AYK_FLAG_QK_DPP = 1,  /* q.k on the VALU: v_dot2 + DPP butterflies */
+  AYK_FLAG_QK_MFMA = 2  /* q.k on the matrix cores: v_mfma_f32_16x16x32 */
+};
 enum { AYK_LAYOUT_NHD = 0, AYK_LAYOUT_HND = 1 };
 
 /* Version of this ABI; bumped on any signature change. */
@@ -73,7 +79,9 @@ int ayk_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_c
  * (reference python/ayaka/ops/attention.py:12-30). A row whose request has
  * kv_lengths 0 is a padding row and gets zeros. Scores are scale * q.k in fp32,
  * the softmax and the value sum are fp32, and out is rounded once.
- * head_dim must be 64, 128 or 256 and block_size a power of two.
+ * head_dim must be 64, 128 or 256 and block_size a power of two. `flags`
+ * (AYK_FLAG_QK_*) forces one q.k implementation; 0 picks by group size
+ * (matrix cores from 6 query heads per key/value head).
  */
 int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,
                            const int32_t* block_table, int64_t table_stride,
@@ -81,7 +89,7 @@ int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const 
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           float scale, void* stream);
+                           float scale, int32_t flags, void* stream);
 
 /* Bytes of scratch ayk_paged_attention_v2 needs for these sizes. */
 size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads, int32_t head_dim,
@@ -93,10 +101,16 @@ size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads,
  * log-sum-exp state into `workspace`, then a reduce kernel merges the
  * partitions of each (row, head) and rounds once. Same arguments and semantics
  * as v1, plus the partition size (a positive multiple of 64) and the number of
- * partitions the grid covers: every row's length must be at most
- * max_partitions * partition_size (positions beyond it are not read). The math
- * the reference delegates to flashinfer's split-KV decode
- * (python/ayaka/ops/backends/flashinfer/attention.py:240-251, :326).
+ * partitions per row the scratch holds: every row's length must be at most
+ * max_partitions * partition_size (positions beyond it are not read).
+ * work_items, if not NULL, lists n_work_items (row, partition) int32 pairs --
+ * the partitions that hold tokens, in the order to run them (longest first
+ * balances best); partitions not listed are not computed, so the list must
+ * cover every partition below ceil(length / partition_size) of every row. With
+ * NULL the grid covers every (row, partition < max_partitions), which is what a
+ * graph replay with fixed launch shape needs. The math the reference delegates
+ * to flashinfer's split-KV decode and its plan-time schedule
+ * (python/ayaka/ops/backends/flashinfer/attention.py:221-251, :326).
  */
 int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const void* v_cache,
                            const int32_t* block_table, int64_t table_stride,
@@ -105,7 +119,8 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
                            float scale, int32_t partition_size, int32_t max_partitions,
-                           void* workspace, size_t workspace_bytes, void* stream);
+                           const int32_t* work_items, int32_t n_work_items, void* workspace,
+                           size_t workspace_bytes, int32_t flags, void* stream);
 
 /*
  * Whole-block copies of both caches; block_bytes is the size of one block of

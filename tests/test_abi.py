@@ -38,7 +38,7 @@ def test_workspace_size() -> None:
 def _v1(lib: ctypes.CDLL, **kw: object) -> int:
     args = dict(out=1, q=1, k=1, v=1, table=1, stride=4, lengths=1, ror=None, pos=None, n_rows=1,
                 heads=8, kv_heads=2, head_dim=128, num_blocks=10, block_size=16, max_blocks=4,
-                layout=0, dtype=1, scale=ctypes.c_float(1.0), stream=None)
+                layout=0, dtype=1, scale=ctypes.c_float(1.0), flags=0, stream=None)
     args.update(kw)
     return lib.ayk_paged_attention_v1(*args.values())
 
@@ -54,6 +54,8 @@ def _v1(lib: ctypes.CDLL, **kw: object) -> int:
         ({"ror": 1}, 1, b"together"),
         ({"q": None}, 1, b"null"),
         ({"stride": 2}, 1, b"table_stride"),
+        ({"flags": 3}, 1, b"exclude each other"),
+        ({"flags": 8}, 1, b"unknown flags"),
     ],
 )
 def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, message: bytes) -> None:
@@ -65,10 +67,12 @@ def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, me
 def test_v2_and_store_refusals() -> None:
     lib = _lib.lib()
     base = [1, 1, 1, 1, 1, 4, 1, None, None, 1, 8, 2, 128, 10, 16, 4, 0, 1, ctypes.c_float(1.0)]
-    assert lib.ayk_paged_attention_v2(*base, 100, 4, 1, 1 << 20, None) == 1
+    assert lib.ayk_paged_attention_v2(*base, 100, 4, None, 0, 1, 1 << 20, 0, None) == 1
     assert b"multiple of 64" in lib.ayk_last_error()
-    assert lib.ayk_paged_attention_v2(*base, 512, 4, 1, 16, None) == 4
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 1, 16, 0, None) == 4
     assert b"workspace" in lib.ayk_last_error()
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 3, 1, 1 << 20, 0, None) == 1
+    assert b"work items" in lib.ayk_last_error()
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 3, None) == 2
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 0, 2, 64, 10, 16, 0, 2, None) == 0
     assert lib.ayk_zero_blocks(1, 1, 1, 0, 2, 0, 64, None) == 1
