@@ -141,7 +141,7 @@ constexpr int kMfmaMinHeads = 6;
 // The q.k path and workgroup shape for a launch, then the kernel(s).
 int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool bf16, bool split, int32_t flags,
            void* stream) {
-  if (flags & ~(AYK_FLAG_QK_DPP | AYK_FLAG_QK_MFMA))
+  if (flags & ~(AYK_FLAG_QK_DPP | AYK_FLAG_QK_MFMA | AYK_FLAG_PARTIALS_ONLY))
     return fail(AYK_ERR_ARGUMENT, "%s: unknown flags 0x%x", op, flags);
   if ((flags & AYK_FLAG_QK_DPP) && (flags & AYK_FLAG_QK_MFMA))
     return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_QK_DPP and AYK_FLAG_QK_MFMA exclude each other", op);
@@ -156,7 +156,8 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err = mfma ? ayk::launch_attention_mfma(p, head_dim, gc, bf16, split, waves, s)
                         : ayk::launch_attention_dpp(p, head_dim, gc, bf16, split, waves, s);
-  if (err == hipSuccess && split) err = ayk::launch_partition_reduce(p, head_dim, bf16, s);
+  if (err == hipSuccess && split && !(flags & AYK_FLAG_PARTIALS_ONLY))
+    err = ayk::launch_partition_reduce(p, head_dim, bf16, s);
   return launched(err, op);
 }
 

@@ -272,53 +272,81 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
 }
 
 // Merge the partitions of one (row, head): o = sum_p w_p o_p / sum_p w_p with
-// w_p = l_p * 2^(m_p - max m). A row with one partition copies it, so v2 with a
-// single partition rounds exactly the value v1 rounds.
+// w_p = l_p * 2^(m_p - max m). Thread t owns 4 elements (t % (D/4)) of every
+// SLOTS-th partition from t / (D/4) on and merges them online (its own running
+// max), so all partial loads are independent; the SLOTS partial merges then
+// meet in LDS with the same log-sum-exp rule. A row with one partition copies
+// it, so v2 with a single partition rounds exactly the value v1 rounds.
+constexpr int kReduceThreads = 256;
+
 template <int D, bool BF16>
-__global__ __launch_bounds__(kWave) void partition_reduce_kernel(const AttnParams p) {
+__global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const AttnParams p) {
   using E = Elem<BF16>;
-  constexpr int EPL = D / kWave;  // 1, 2 or 4 elements per lane
+  constexpr int QUADS = D / 4;                     // float4 groups of a row
+  constexpr int SLOTS = kReduceThreads / QUADS;    // partitions merged side by side
+  __shared__ f32x4 s_acc[SLOTS][QUADS];
+  __shared__ float s_m[SLOTS];
+  __shared__ float s_l[SLOTS];
+
   const int h = blockIdx.x % p.num_heads;
   const int row = blockIdx.x / p.num_heads;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
+  const int quad = tid % QUADS;
+  const int slot = tid / QUADS;
   int req, len;
   row_context(p, row, req, len);
   const int64_t head_row = (int64_t)row * p.num_heads + h;
-  uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D + lane * EPL;
-
-  float res[EPL];
+  uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D;
   const int np = (len + p.partition_size - 1) / p.partition_size;
   const float* ml = p.part_ml + head_row * p.max_partitions * 2;
-  const float* po = p.part_o + head_row * p.max_partitions * D + lane * EPL;
-  if (np == 0) {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) res[e] = 0.f;
-  } else if (np == 1) {
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) res[e] = po[e];
-  } else {
-    float mx = -INFINITY;
-    for (int i = lane; i < np; i += kWave) mx = fmaxf(mx, ml[2 * i]);
-#pragma unroll
-    for (int st = 1; st < kWave; st <<= 1) mx = fmaxf(mx, __shfl_xor(mx, st));
-    const float mr = (mx == -INFINITY) ? 0.f : mx;
-    float acc[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) acc[e] = 0.f;
-    float L = 0.f;
+  const f32x4* po = reinterpret_cast<const f32x4*>(p.part_o + head_row * p.max_partitions * D);
+
+  if (np <= 1) {
+    if (slot == 0) {
+      const f32x4 v = np == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : po[quad];
+      uint32_t* o32 = reinterpret_cast<uint32_t*>(out) + quad * 2;
+      o32[0] = E::round(v.x) | (E::round(v.y) << 16);
+      o32[1] = E::round(v.z) | (E::round(v.w) << 16);
+    }
+    return;
+  }
+  float m = kNoScore, l = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
-    for (int i = 0; i < np; ++i) {
-      const float w = ml[2 * i + 1] * fast_exp2(ml[2 * i] - mr);
-      L += w;
+  for (int i = slot; i < np; i += SLOTS) {
+    const float mi = ml[2 * i];
+    const float wi = ml[2 * i + 1];
+    const f32x4 v = po[(int64_t)i * QUADS + quad];
+    const float mn = fmaxf(m, mi);
+    const float a = fast_exp2(m - mn);
+    const float b = wi * fast_exp2(mi - mn);
+    l = l * a + b;
+    acc = acc * a + v * b;
+    m = mn;
+  }
+  s_acc[slot][quad] = acc;
+  if (quad == 0) {
+    s_m[slot] = m;
+    s_l[slot] = l;
+  }
+  __syncthreads();
+  if (slot == 0) {
+    float mn = s_m[0];
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[e] = fmaf(w, po[(int64_t)i * D + e], acc[e]);
+    for (int s = 1; s < SLOTS; ++s) mn = fmaxf(mn, s_m[s]);
+    f32x4 total = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s) {
+      const float w = fast_exp2(s_m[s] - mn);
+      L += s_l[s] * w;
+      total += s_acc[s][quad] * w;
     }
     const float inv = L > 0.f ? 1.0f / L : 0.f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) res[e] = acc[e] * inv;
+    uint32_t* o32 = reinterpret_cast<uint32_t*>(out) + quad * 2;
+    o32[0] = E::round(total.x * inv) | (E::round(total.y * inv) << 16);
+    o32[1] = E::round(total.z * inv) | (E::round(total.w * inv) << 16);
   }
-#pragma unroll
-  for (int e = 0; e < EPL; ++e) out[e] = (uint16_t)E::round(res[e]);
 }
 
 // ---------------------------------------------------------------------------
@@ -371,7 +399,7 @@ hipError_t launch_attention_dpp(const AttnParams& p, int head_dim, int gc, bool 
 }
 
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream) {
-  const dim3 grid((unsigned)((int64_t)p.num_heads * p.n_rows)), block(kWave);
+  const dim3 grid((unsigned)((int64_t)p.num_heads * p.n_rows)), block(kReduceThreads);
   switch (head_dim) {
     case 64:
       if (bf16) hipLaunchKernelGGL((partition_reduce_kernel<64, true>), grid, block, 0, stream, p);

@@ -73,6 +73,8 @@ COMPUTE_UNITS = 256
 _LAYOUT_CODES = {KVLayoutKind.NHD: 0, KVLayoutKind.HND: 1}
 _DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 _QK_FLAGS = {None: 0, "dpp": 1, "mfma": 2}
+#: v2 flag: launch the partition kernel only (benchmarks time the dominant kernel with it).
+PARTIALS_ONLY = 4
 
 
 @dataclass(frozen=True, slots=True)
@@ -331,6 +333,7 @@ def attend_with(
     partitions: int | None,
     qk: str | None = None,
     partition_size: int | None = None,
+    partials_only: bool = False,
 ) -> None:
     """:func:`attend` with the launch chosen by the caller.
 
@@ -338,8 +341,9 @@ def attend_with(
     of ``partition_size`` (default :data:`PARTITION_SIZE`; together they must
     cover the step's longest context), ``None`` lets :func:`choose_split` decide. ``qk`` forces the q.k implementation,
     ``"dpp"`` (VALU dot2 + DPP butterflies) or ``"mfma"`` (matrix cores); ``None``
-    lets the library pick. Benchmarks and tests use it to time and check every
-    kernel on one step.
+    lets the library pick. ``partials_only`` (v2) runs the partition kernel alone
+    and leaves ``out`` unwritten. Benchmarks and tests use it to time and check
+    every kernel on one step.
     """
     op = "attention.attend"
     require_buffers(op, buffers)
@@ -440,7 +444,7 @@ def attend_with(
             f"{op}: {partitions} partitions of {partition_size} do not cover {max_length} positions",
             context={"op": op},
         )
-    flags = _QK_FLAGS[qk]
+    flags = _QK_FLAGS[qk] | (PARTIALS_ONLY if partials_only else 0)
     if partitions == 0:
         _lib.check(op, lib.ayk_paged_attention_v1(*common, flags, stream))
         return

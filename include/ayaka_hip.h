@@ -44,7 +44,8 @@ enum { AYK_DTYPE_FP16 = 0, AYK_DTYPE_BF16 = 1 };
 /* flags of the attention calls: 0 lets the library pick the q.k path. */
 enum {
   AYK_FLAG_QK_DPP = 1,  /* q.k on the VALU: v_dot2 + DPP butterflies */
-  AYK_FLAG_QK_MFMA = 2  /* q.k on the matrix cores: v_mfma_f32_16x16x32 */
+  AYK_FLAG_QK_MFMA = 2, /* q.k on the matrix cores: v_mfma_f32_16x16x32 */
+  AYK_FLAG_PARTIALS_ONLY = 4 /* v2: run only the partition kernel (out is not written); for timing it */
 };
 enum { AYK_LAYOUT_NHD = 0, AYK_LAYOUT_HND = 1 };
 

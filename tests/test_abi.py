@@ -55,7 +55,7 @@ def _v1(lib: ctypes.CDLL, **kw: object) -> int:
         ({"q": None}, 1, b"null"),
         ({"stride": 2}, 1, b"table_stride"),
         ({"flags": 3}, 1, b"exclude each other"),
-        ({"flags": 8}, 1, b"unknown flags"),
+        ({"flags": 16}, 1, b"unknown flags"),
     ],
 )
 def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, message: bytes) -> None:
