@@ -28,7 +28,7 @@ __all__ = ["AttentionMetadata", "AttentionOps"]
 
 
 @dataclass(frozen=True, slots=True, eq=False)
-class AttentionMetadata:
+class _AttentionMetadata:
     """Everything one step's attention and cache writes need (reference ``:62-95``).
 
     ``rows_per_request`` [B] int32, ``request_of_row`` [N] int32, ``positions``
@@ -47,6 +47,13 @@ class AttentionMetadata:
     kv_lengths: Tensor
     block_table: object
     plan: object | None
+
+
+try:  # pragma: no cover - only where the engine is installed
+    # Inside the engine, hand out its own record so nothing downstream sees a foreign type.
+    from ayaka.ops.attention import AttentionMetadata  # type: ignore[import-not-found]
+except ImportError:
+    AttentionMetadata = _AttentionMetadata  # type: ignore[misc]
 
 
 class AttentionOps(Protocol):

@@ -53,3 +53,9 @@ class DType(enum.Enum):
 
 
 COMPUTE_DTYPES = frozenset({DType.FP32, DType.FP16, DType.BF16})
+
+try:  # pragma: no cover - only where the engine is installed
+    # Inside the engine its enums are the ones in every record; ours compare equal by value.
+    from ayaka.core.types import ForwardMode, KVLayoutKind  # type: ignore[import-not-found] # noqa: F811
+except ImportError:
+    pass

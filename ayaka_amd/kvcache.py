@@ -31,7 +31,7 @@ __all__ = ["RAW_CODEC", "KVBuffers", "KVCacheOps"]
 RAW_CODEC = "raw"
 
 
-class KVBuffers(NamedTuple):
+class _KVBuffers(NamedTuple):
     """The key and value tensors of one layer (reference ``ops/kvcache.py:58-91``)."""
 
     k: Tensor
@@ -54,6 +54,12 @@ class KVBuffers(NamedTuple):
     @property
     def head_dim(self) -> int:
         return int(self.k.shape[3])
+
+
+try:  # pragma: no cover - only where the engine is installed
+    from ayaka.ops.kvcache import KVBuffers  # type: ignore[import-not-found]
+except ImportError:
+    KVBuffers = _KVBuffers  # type: ignore[misc]
 
 
 class KVCacheOps(Protocol):

@@ -29,6 +29,21 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 
+# HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE on `bench.py --config C --only auto` and scaled by what the same counters read
+# for a 1 GiB device copy (FETCH x2.0, WRITE x1.0). Reported only when this run's launch is
+# the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
+PROFILED_TRAFFIC = {
+    (3, "paged_attention_kernel (v2 partitions)", 512):
+        (1_078_181_791, 8_912_896, "profiles/paged_attention_kernel_c3_llama3_8b_decode.md"),
+    (4, "paged_attention_kernel (v2 partitions)", 320):
+        (663_490_983, 8_877_760, "profiles/paged_attention_kernel_c4_long_context.md"),
+    (5, "paged_attention_mfma_kernel (v2 partitions)", 2048):
+        (2_593_796_354, 16_767_328, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
+    (2, "paged_attention_kernel (v2 partitions)", 256):
+        (143_389_751, 2_638_848, "profiles/paged_attention_kernel_c2_llama32_1b_decode.md"),
+}
+
 
 def parse() -> argparse.Namespace:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
@@ -42,6 +57,8 @@ def parse() -> argparse.Namespace:
                     help="force the q.k implementation (default: the library's choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=8, help="rows of the CPU baseline sample")
+    ap.add_argument("--access-probe", action="store_true",
+                    help="only run the read-only access-pattern probes (ayaka_amd/lib/access_probe)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (scales profiler byte counters)")
     return ap.parse_args()
@@ -111,9 +128,17 @@ def cpu_baseline(step, cfg, rows: int) -> dict:
 def main() -> int:
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(decode attention needs no collective; see the sharding note in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: this build runs the "
+              "decode path on one MI355X (sequences and key/value heads shard across GPUs without a "
+              "collective, so a multi-GPU figure would be N independent copies of this one)", file=sys.stderr)
         return 2
+    if args.access_probe:
+        import subprocess
+
+        from ayaka_amd._build import PROBE_PATH
+
+        return subprocess.run([str(PROBE_PATH)], check=False).returncode
+
     import torch
 
     if args.copy_calibration:
@@ -184,6 +209,7 @@ def main() -> int:
                                               qk=args.qk, partition_size=size or None, partials_only=True),
             args.steps, args.warmup)["median_us"]
     kernel_gbs = nbytes / (kernel_us * 1e-6) / 1e9
+    profiled = PROFILED_TRAFFIC.get((cfg.index, kernel, head["partition_size"]))
     line = {
         "metric": "decode-attention µs/call + achieved HBM GB/s (% of peak) at 1 MI355X",
         "value": round(head["gbs"], 1),
@@ -221,7 +247,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": None if profiled is None else profiled[0] + profiled[1],
+            "traffic_read_write": None if profiled is None else [profiled[0], profiled[1]],
+            "traffic_source": None if profiled is None else profiled[2],
         },
     }
     if not args.no_cpu_baseline:
