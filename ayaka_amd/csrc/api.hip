@@ -136,7 +136,7 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
 }
 
 // Heads per wave from which the library picks the matrix-core q.k kernel.
-constexpr int kMfmaMinHeads = 6;
+constexpr int kMfmaMinHeads = 3;
 
 // The q.k path and workgroup shape for a launch, then the kernel(s).
 int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool bf16, bool split, int32_t flags,
@@ -145,8 +145,9 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
     return fail(AYK_ERR_ARGUMENT, "%s: unknown flags 0x%x", op, flags);
   if ((flags & AYK_FLAG_QK_DPP) && (flags & AYK_FLAG_QK_MFMA))
     return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_QK_DPP and AYK_FLAG_QK_MFMA exclude each other", op);
-  // Measured on MI355X: the DPP kernel streams best up to 4 heads per wave; at 6-8
-  // heads its q.k work makes it VALU-bound and the matrix-core kernel wins.
+  // Measured on MI355X: from 3 heads per wave the matrix-core kernel (keys staged
+  // through LDS) streams faster than the DPP kernel, whose per-token dot2 and
+  // butterfly work grows with the group; 1-2 heads stay on the DPP kernel.
   const bool mfma = (flags & AYK_FLAG_QK_MFMA) || (!(flags & AYK_FLAG_QK_DPP) && gc >= kMfmaMinHeads);
   const int waves = 4;
   const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);

@@ -1,15 +1,17 @@
 // Paged-attention decode with the q.k contraction on the matrix cores (gfx950).
 //
-// Same semantics, grid and outputs as the DPP kernel in paged_attention.hip;
-// only the way a wave turns a chunk of 16 keys into weights differs:
+// Same semantics, grid and outputs as the DPP kernel in paged_attention.hip (a
+// workgroup per (row, partition), one wave per key/value head); only the way a
+// wave turns a chunk of 16 keys into weights differs:
 //
+//  * Keys are loaded like the values -- 256 contiguous bytes per token, the
+//    pattern HBM streams best -- and staged through a per-wave LDS tile, from
+//    which each lane reads its MFMA operand: 16 bytes of token l%16 at k-slice
+//    8*(l/16) of each 32-wide step (a swizzle keeps those reads conflict-free).
 //  * q.k for 16 tokens x (up to 16) query heads is one 16x16 tile, accumulated
-//    over head_dim in k-steps of 32 by v_mfma_f32_16x16x32_{bf16,f16}: exact
-//    products, fp32 sums. Lane l feeds token l%16 / head l%16 and k-slice
-//    8*(l/16) of each step, so a load instruction reads 64 contiguous bytes of
-//    16 different tokens and q needs only head_dim/32 registers per lane,
-//    whatever the group size. Lane l gets the scores of tokens 4*(l/16)+i,
-//    i < 4, for head l%16.
+//    over head_dim by v_mfma_f32_16x16x32_{bf16,f16}: exact products, fp32
+//    sums; q needs only head_dim/32 registers per lane whatever the group size.
+//    Lane l gets the scores of tokens 4*(l/16)+i, i < 4, for head l%16.
 //  * The softmax runs on those 4 scores per lane (max across the 4 lane
 //    groups with two shuffles); the weights go through a small per-wave LDS
 //    tile to the lanes that hold the values.
@@ -17,7 +19,7 @@
 //    with the value layout of the DPP kernel: lane (r, c) holds 8 elements of
 //    tokens j*TPL + r.
 //
-// With 4-8 query heads per key/value head this removes the per-token dot2 and
+// With 6-8 query heads per key/value head this removes the per-token dot2 and
 // butterfly work that makes the DPP kernel VALU-bound.
 #include "attention_common.h"
 
@@ -45,33 +47,40 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int D, int GC, int WAVES, bool BF16, bool SPLIT>
-__global__ __launch_bounds__(WAVES * kWave) void paged_attention_mfma_kernel(const AttnParams p) {
+template <int D, int GC, bool BF16, bool SPLIT>
+__global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel(const AttnParams p) {
   using E = Elem<BF16>;
-  constexpr int THREADS = WAVES * kWave;
   constexpr int CH = 16;            // tokens per chunk: the MFMA tile height
   constexpr int KS = D / 32;        // MFMA k-steps over head_dim
-  constexpr int LPT = D / 8;        // value lanes per token
-  constexpr int TPL = kWave / LPT;  // tokens per value load
-  constexpr int NV = CH / TPL;      // value loads per chunk
+  constexpr int CPT = D / 8;        // 16-byte pieces per token (= value lanes per token)
+  constexpr int TPL = kWave / CPT;  // tokens per load instruction
+  constexpr int NL = CH / TPL;      // load instructions per chunk, for K and for V
   constexpr int PW = ((GC + 3) / 4) * 4;  // weights per token in LDS, padded to float4
 
   __shared__ int s_tbl[kTableCap];
-  __shared__ WaveParts<D, GC, WAVES> parts;
-  __shared__ float s_p[WAVES][2][CH][PW];  // weights of the chunk, double-buffered
-  __shared__ float s_alpha[WAVES][PW];
+  __shared__ u32x4 s_k[kMaxWaves][CH * CPT];       // the chunk's keys, swizzled (see key_slot)
+  __shared__ float s_p[kMaxWaves][2][CH][PW];      // the chunk's weights, double-buffered
+  __shared__ float s_alpha[kMaxWaves][PW];
 
-  const WgCoord wg = wg_coord(p, p.num_virtual_heads, SPLIT);
-  const int row = wg.row;
-  const int kvh = wg.group / p.head_chunks;
-  const int h0 = kvh * p.group + (wg.group % p.head_chunks) * GC;
   const int tid = threadIdx.x;
+  const int threads = blockDim.x;
+  const int waves = threads / kWave;
+  const WgCoord wg = wg_coord(p, (p.num_virtual_heads + waves - 1) / waves, SPLIT);
+  const int row = wg.row;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
-  const int mt = lane % 16;  // MFMA: token of the key operand, head of q and of the scores
-  const int mq = lane / 16;  // MFMA: k-slice of the operands, token group of the scores
-  const int r = lane / LPT;  // values: token within a load
-  const int c = lane % LPT;  // values: 8-element slice of head_dim
+  const int vh = wg.group * waves + wave;
+  const bool active = vh < p.num_virtual_heads;
+  const int kvh = vh / p.head_chunks;
+  const int h0 = kvh * p.group + (vh % p.head_chunks) * GC;
+  const int mt = lane % 16;  // MFMA: token of the key operand; head of q and of the scores
+  const int mq = lane / 16;  // MFMA: k-slice of the operands; token group of the scores
+  const int r = lane / CPT;  // loads: token within a load instruction
+  const int c = lane % CPT;  // loads: 16-byte piece of head_dim
+
+  // A token's 16-byte pieces sit in LDS at piece ^ (token % CPT): the 16 lanes that
+  // read one k-slice of 16 different tokens hit 16 different bank groups.
+  auto key_slot = [](int token, int piece) { return token * CPT + (piece ^ (token & (CPT - 1))); };
 
   int req, len;
   row_context(p, row, req, len);
@@ -81,18 +90,17 @@ __global__ __launch_bounds__(WAVES * kWave) void paged_attention_mfma_kernel(con
     t_end = min(len, t_begin + p.partition_size);
     if (t_begin >= t_end) return;
   } else if (len == 0) {
-    store_zero_rows<D, GC, THREADS>(p, row, h0, tid);
+    if (active) store_zero_rows<D, GC, kWave>(p, row, h0, lane);
     return;
   }
 
-  // q as the MFMA B operand: head mt (zero columns past the group), k-slice mq.
+  // q as the MFMA B operand: head mt (zero columns past the group), k-slice mq of step s.
   u32x4 qb[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    qb[s] = (mt < GC) ? *reinterpret_cast<const u32x4*>(p.q + ((int64_t)row * p.num_heads + h0 + mt) * D +
-                                                         s * 32 + mq * 8)
-                      : u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int s = 0; s < KS; ++s)
+    qb[s] = (active && mt < GC)
+                ? *reinterpret_cast<const u32x4*>(p.q + ((int64_t)row * p.num_heads + h0 + mt) * D + s * 32 + mq * 8)
+                : u32x4{0u, 0u, 0u, 0u};
 
   float m_h = kNoScore;  // running max of head mt (same in its 4 lanes)
   float l_h = 0.f;       // this lane's share of head mt's weight sum
@@ -109,35 +117,34 @@ __global__ __launch_bounds__(WAVES * kWave) void paged_attention_mfma_kernel(con
   const uint32_t block_stride = (uint32_t)p.block_stride;
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
-  const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + mq * 8;
+  const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + c * 8;
   const uint16_t* vbase = p.v_cache + (int64_t)kvh * p.head_stride + c * 8;
 
   for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
     const int s1 = min(t_end, s0 + seg_len);
-    const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, THREADS);
+    const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, threads);
+    if (!active) continue;
     const int nch = (s1 - s0 + CH - 1) / CH;
 
-    auto offset_of = [&](int t) -> uint64_t {
-      t = min(t, s1 - 1);
-      const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
-      return (uint64_t)blk * block_stride + (uint32_t)(t & bs_mask) * token_stride;
-    };
-    auto load_keys = [&](int ci, u32x4(&kc)[KS]) {
-      const uint16_t* a = kbase + offset_of(s0 + ci * CH + mt);
+    auto offsets = [&](int ci, uint32_t(&dst)[NL]) {
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kc[s] = stream_load(a + s * 32);
-    };
-    auto load_values = [&](int ci, u32x4(&vc)[NV]) {
-#pragma unroll
-      for (int j = 0; j < NV; ++j) vc[j] = stream_load(vbase + offset_of(s0 + ci * CH + j * TPL + r));
+      for (int j = 0; j < NL; ++j) {
+        const int t = min(s0 + ci * CH + j * TPL + r, s1 - 1);
+        const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
+        dst[j] = blk * block_stride + (uint32_t)(t & bs_mask) * token_stride;
+      }
     };
 
-    auto consume = [&](int ci, int buf, const u32x4(&kc)[KS], const u32x4(&vc)[NV]) {
+    auto consume = [&](int ci, int buf, const u32x4(&kc)[NL], const u32x4(&vc)[NL]) {
       const int tb = s0 + ci * CH;
       const bool tail = tb + CH > s1;
+      // Keys to LDS in the load layout, back out in the MFMA operand layout.
+#pragma unroll
+      for (int j = 0; j < NL; ++j) s_k[wave][key_slot(j * TPL + r, c)] = kc[j];
+      wave_lds_sync();
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < KS; ++s) acc = mfma_qk<BF16>(kc[s], qb[s], acc);
+      for (int s = 0; s < KS; ++s) acc = mfma_qk<BF16>(s_k[wave][key_slot(mt, s * 4 + mq)], qb[s], acc);
       float sc[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -173,7 +180,7 @@ __global__ __launch_bounds__(WAVES * kWave) void paged_attention_mfma_kernel(con
       }
       wave_lds_sync();
 #pragma unroll
-      for (int j = 0; j < NV; ++j) {
+      for (int j = 0; j < NL; ++j) {
         float pw[PW];
 #pragma unroll
         for (int g4 = 0; g4 < PW; g4 += 4) {
@@ -199,64 +206,64 @@ __global__ __launch_bounds__(WAVES * kWave) void paged_attention_mfma_kernel(con
     };
 
     // Keys of the next chunk are in flight while the current one is folded in.
-    u32x4 kA[KS], kB[KS], vc[NV];
-    int ci = wave;
-    if (ci < nch) load_keys(ci, kA);
+    uint32_t offA[NL], offB[NL];
+    u32x4 kA[NL], kB[NL], vc[NL];
+    int ci = 0;
+    offsets(0, offA);
+#pragma unroll
+    for (int j = 0; j < NL; ++j) kA[j] = stream_load(kbase + offA[j]);
     while (ci < nch) {
-      load_values(ci, vc);
-      int cn = ci + WAVES;
-      if (cn < nch) load_keys(cn, kB);
+#pragma unroll
+      for (int j = 0; j < NL; ++j) vc[j] = stream_load(vbase + offA[j]);
+      if (ci + 1 < nch) {
+        offsets(ci + 1, offB);
+#pragma unroll
+        for (int j = 0; j < NL; ++j) kB[j] = stream_load(kbase + offB[j]);
+      }
       consume(ci, 0, kA, vc);
-      ci = cn;
-      if (ci >= nch) break;
-      load_values(ci, vc);
-      cn = ci + WAVES;
-      if (cn < nch) load_keys(cn, kA);
+      if (++ci >= nch) break;
+#pragma unroll
+      for (int j = 0; j < NL; ++j) vc[j] = stream_load(vbase + offB[j]);
+      if (ci + 1 < nch) {
+        offsets(ci + 1, offA);
+#pragma unroll
+        for (int j = 0; j < NL; ++j) kA[j] = stream_load(kbase + offA[j]);
+      }
       consume(ci, 1, kB, vc);
-      ci = cn;
+      ++ci;
     }
   }
+  if (!active) return;
 
   // Head mt's weight sum over the wave's 4 token groups; the value lanes' partial
   // sums share the wave's running max, so they add without rescaling.
   l_h += __shfl_xor(l_h, 16);
   l_h += __shfl_xor(l_h, 32);
 #pragma unroll
-  for (int st = LPT; st < kWave; st <<= 1)
+  for (int st = CPT; st < kWave; st <<= 1)
 #pragma unroll
     for (int g = 0; g < GC; ++g)
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[g][e] += __shfl_xor(o[g][e], st);
-  if (r == 0) {
 #pragma unroll
-    for (int g = 0; g < GC; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) parts.o[wave][g][c * 8 + e] = o[g][e];
+  for (int g = 0; g < GC; ++g) {
+    const float mg = __shfl(m_h, g);
+    const float lg = __shfl(l_h, g);
+    if (r == 0) store_head<D, BF16, SPLIT>(p, row, wg.part, h0 + g, c, o[g], mg, lg);
   }
-  if (mq == 0 && mt < GC) {
-    parts.m[wave][mt] = m_h;
-    parts.l[wave][mt] = l_h;
-  }
-  __syncthreads();
-  merge_waves_and_store<D, GC, WAVES, BF16, SPLIT>(p, parts, row, wg.part, h0, tid);
 }
 
 template <int D, int GC, bool BF16>
 static hipError_t launch_mfma_typed(const AttnParams& p, bool split, int waves, hipStream_t stream) {
+  (void)waves;  // one wave per virtual head, up to kMaxWaves per workgroup
+  const int per_wg = p.num_virtual_heads < kMaxWaves ? p.num_virtual_heads : kMaxWaves;
+  const int groups = (p.num_virtual_heads + per_wg - 1) / per_wg;
   const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);
-  const dim3 grid((unsigned)(items * p.num_virtual_heads));
-#define AYK_LAUNCH(W)                                                                               \
-  if (split)                                                                                        \
-    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, W, BF16, true>), grid, dim3(W * kWave), 0, \
-                       stream, p);                                                                  \
-  else                                                                                              \
-    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, W, BF16, false>), grid, dim3(W * kWave),  \
-                       0, stream, p);
-  switch (waves) {
-    case 2: AYK_LAUNCH(2) break;
-    default: AYK_LAUNCH(4) break;
-  }
-#undef AYK_LAUNCH
+  const dim3 grid((unsigned)(items * groups)), block(per_wg * kWave);
+  if (split)
+    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, BF16, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, BF16, false>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 

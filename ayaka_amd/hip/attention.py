@@ -28,6 +28,7 @@ launch shape comes from the bucket's table width.
 
 from __future__ import annotations
 
+import heapq
 from dataclasses import dataclass, field
 
 import torch
@@ -59,14 +60,18 @@ __all__ = [
     "update_graph_metadata",
 ]
 
-#: Positions per v2 partition when only the table width is known (graph metadata).
+#: Default positions per v2 partition (callers that force a v2 launch without a size).
 PARTITION_SIZE = 512
-#: The smallest partition an eagerly planned step is split into.
-MIN_PARTITION = 256
-#: Positions per partition for the matrix-core kernel.
-MFMA_PARTITION = 2048
+#: Partition sizes an eagerly planned step chooses from (multiples of 64).
+PARTITION_CANDIDATES = (64, 128, 192, 256, 320, 384, 448, 512, 576, 640, 704, 768, 896, 1024, 1280, 1536,
+                        2048, 3072, 4096, 8192, 16384)
+#: Fixed cost of one workgroup, in positions of streaming (start-up, merge, partial write):
+#: an extra round of 256 workgroups measured ~12 µs on the C3 shape, ~80 positions at 6.4/µs.
+WORKGROUP_COST = 80
+#: XCDs of one MI355X; workgroups are dealt to them round-robin.
+XCDS = 8
 #: Heads per wave from which the library runs q.k on the matrix cores (mirrors the C library).
-MFMA_MIN_HEADS = 6
+MFMA_MIN_HEADS = 3
 #: Compute units of one MI355X; the split heuristic aims to keep all of them busy.
 COMPUTE_UNITS = 256
 
@@ -92,6 +97,17 @@ class HipAttentionPlan:
     row_lengths: tuple[int, ...] = ()
     # v2 work lists built by the step's first attend, keyed by partition size, for the later layers
     work: dict[int, torch.Tensor] = field(default_factory=dict, compare=False, repr=False)
+    splits: dict[tuple[int, int], Split] = field(default_factory=dict, compare=False, repr=False)
+
+    def split_for(self, num_kv_heads: int, group: int) -> Split:
+        """The step's launch for this head shape, chosen once and reused by every layer."""
+        key = (num_kv_heads, group)
+        found = self.splits.get(key)
+        if found is None:
+            found = choose_split(len(self.row_lengths), num_kv_heads, group, self.max_length,
+                                 row_lengths=self.row_lengths)
+            self.splits[key] = found
+        return found
 
     def work_items(self, partition_size: int, device: torch.device) -> torch.Tensor:
         """The (row, partition) pairs of the step that hold tokens, longest first, on ``device``.
@@ -236,7 +252,7 @@ def head_chunks(group: int) -> int:
 
 
 def uses_matrix_cores(group: int) -> bool:
-    """Whether the library picks the MFMA q.k kernel for this group size (6+ heads per wave)."""
+    """Whether the library picks the MFMA q.k kernel for this group size (3+ heads per wave)."""
     return group // head_chunks(group) >= MFMA_MIN_HEADS
 
 
@@ -248,43 +264,98 @@ class Split:
     partitions: int
 
 
+def schedule_makespan(row_lengths: list[int], size: int, groups: int = 1) -> int:
+    """Modelled finish time, in positions, of v2 over partitions of ``size``.
+
+    Workgroups start in work-list order (longest partition first); the GPU hands
+    workgroup i to XCD i mod 8 and each XCD to whichever of its 32 CUs frees up
+    first, one 8-wave workgroup per CU at a time. A workgroup costs its
+    positions plus :data:`WORKGROUP_COST` (start-up, the final merge, writing the
+    partial).
+    """
+    items: list[int] = []
+    for length in row_lengths:
+        full, rest = divmod(length, size)
+        items.extend([size] * full)
+        if rest:
+            items.append(rest)
+    items.sort(reverse=True)
+    items = [item for item in items for _ in range(groups)]
+    per_xcd = COMPUTE_UNITS // XCDS
+    loads = [[0] * per_xcd for _ in range(XCDS)]
+    for index, item in enumerate(items):
+        heap = loads[index % XCDS]
+        heapq.heapreplace(heap, heap[0] + item + WORKGROUP_COST)
+    return max(max(heap) for heap in loads)
+
+
+_split_cache: dict[tuple, int] = {}
+#: Work lists longer than this many rounds of the GPU are not considered (start-up cost dominates).
+MAX_ROUNDS = 8
+
+
+def fits_schedule(lengths: list[int], size: int, groups: int = 1) -> bool:
+    """Whether partitions of ``size`` keep the work list within :data:`MAX_ROUNDS` rounds."""
+    items = sum(-(-n // size) for n in lengths) * groups
+    return items <= MAX_ROUNDS * COMPUTE_UNITS
+
+
+def _best_size(lengths: list[int], max_length: int, groups: int) -> int:
+    """The candidate partition size with the smallest :func:`schedule_makespan`."""
+    best: tuple[int, int] | None = None
+    for size in PARTITION_CANDIDATES:
+        if not fits_schedule(lengths, size, groups) and size != PARTITION_CANDIDATES[-1]:
+            continue
+        cost = schedule_makespan(lengths, size, groups)
+        if best is None or cost < best[0]:
+            best = (cost, size)
+        if size >= max_length:
+            break
+    assert best is not None
+    return best[1]
+
+
 def choose_split(
-    n_rows: int, num_kv_heads: int, group: int, max_length: int, total_length: int | None = None
+    n_rows: int,
+    num_kv_heads: int,
+    group: int,
+    max_length: int,
+    total_length: int | None = None,
+    row_lengths: tuple[int, ...] | None = None,
 ) -> Split:
     """Pick v1 or v2 and the partition size from the step's shape.
 
-    The DPP kernel runs one workgroup of up to 8 waves (one per key/value head)
-    per (row, partition); two such workgroups fit a compute unit, so
-    ``2 * COMPUTE_UNITS`` workgroups run in one round. With the total context
-    known (an eagerly planned step), the partition is sized so the whole grid is
-    about one round -- no tail -- but never below :data:`MIN_PARTITION`
-    positions, whose fixed cost per workgroup would dominate. Without it (graph
-    metadata, where only the table width is fixed) partitions are
-    :data:`PARTITION_SIZE`. The matrix-core kernel runs 4-wave workgroups per
-    (row, key/value head, partition) and streams best in partitions of
-    :data:`MFMA_PARTITION`. A context that fits one partition runs v1.
+    Every candidate partition size is scored with :func:`schedule_makespan` and
+    the fastest wins; a single partition per row is v1. An eagerly planned step
+    is scored on its rows' lengths; graph metadata, where only the table width
+    is fixed, on ``n_rows`` rows of ``max_length``. The choice is cached under a
+    coarse signature of the lengths (row count, longest row to a power of two,
+    total to 4 significant bits), which successive decode steps -- every length
+    one longer than the step before -- keep hitting.
     """
+    del total_length
     if max_length <= 0:
         return Split(0, 0)
-    if uses_matrix_cores(group):
-        size = MFMA_PARTITION
-    elif total_length is None:
-        size = PARTITION_SIZE
-    else:
-        virtual = num_kv_heads * head_chunks(group)
-        groups = -(-virtual // 8)
-        slots = 2 * COMPUTE_UNITS
-        size = -(-(total_length * groups) // slots)
-        size = max(MIN_PARTITION, -(-size // 64) * 64)
+    groups = -(-num_kv_heads * head_chunks(group) // 8)
+    lengths = [n for n in row_lengths if n > 0] if row_lengths is not None else [max_length] * n_rows
+    total = sum(lengths)
+    # The total to 4 significant bits, the longest row to a power of two, the row count.
+    top = max(total.bit_length() - 4, 0)
+    key = (groups, len(lengths), max_length.bit_length(), total >> top, top)
+    size = _split_cache.get(key)
+    if size is None:
+        if len(_split_cache) > 4096:
+            _split_cache.clear()
+        size = _best_size(lengths, max_length, groups)
+        _split_cache[key] = size
     if max_length <= size:
         return Split(0, 0)
     return Split(size, -(-max_length // size))
 
 
 def choose_partitions(n_rows: int, num_kv_heads: int, group: int, max_length: int) -> int:
-    """Partitions of :data:`PARTITION_SIZE` for a step known only by its longest context (0 = v1)."""
-    split = choose_split(n_rows, num_kv_heads, group, max_length)
-    return split.partitions
+    """Partitions for a step known only by its longest context, as graph metadata is (0 = v1)."""
+    return choose_split(n_rows, num_kv_heads, group, max_length).partitions
 
 
 _workspaces: dict[torch.device, torch.Tensor] = {}
@@ -397,9 +468,9 @@ def attend_with(
     if isinstance(step, HipGraphPlan):
         if not decode:
             raise BackendError(f"{op}: graph metadata must be a DECODE step", context={"op": op})
-        max_length, total_length = step.max_blocks * block_size, None
+        max_length, row_lengths = step.max_blocks * block_size, None
     else:
-        max_length, total_length = step.max_length, step.total_length
+        max_length, row_lengths = step.max_length, step.row_lengths
     if n_rows == 0:
         return
     if table.dtype != torch.int32 or not table.is_contiguous() or table.ndim != 2:
@@ -433,10 +504,8 @@ def attend_with(
         float(scale),
     )
     if partitions is None:
-        split = choose_split(n_rows, kv_heads, group, max_length, total_length)
-        if qk is not None and uses_matrix_cores(group) != (qk == "mfma"):
-            split = Split(PARTITION_SIZE, -(-max_length // PARTITION_SIZE)) if max_length > PARTITION_SIZE \
-                else Split(0, 0)
+        split = step.split_for(kv_heads, group) if isinstance(step, HipAttentionPlan) else \
+            choose_split(n_rows, kv_heads, group, max_length)
         partitions, partition_size = split.partitions, split.partition_size
     partition_size = partition_size or PARTITION_SIZE
     if partitions and partitions * partition_size < max_length:

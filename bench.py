@@ -169,7 +169,7 @@ def main() -> int:
     out = torch.empty_like(step.q)
     nbytes = workloads.algorithmic_bytes(cfg)
     max_len = max(cfg.lengths)
-    auto = hip_attention.choose_split(cfg.batch, cfg.kv_heads, cfg.heads // cfg.kv_heads, max_len, sum(cfg.lengths))
+    auto = meta.plan.split_for(cfg.kv_heads, cfg.heads // cfg.kv_heads)  # what attend will launch
     # The headline ("auto", the launch attend picks) runs last, on a GPU warmed by the others.
     launches = {
         "v1": (0, 0),

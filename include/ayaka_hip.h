@@ -82,7 +82,7 @@ int ayk_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_c
  * the softmax and the value sum are fp32, and out is rounded once.
  * head_dim must be 64, 128 or 256 and block_size a power of two. `flags`
  * (AYK_FLAG_QK_*) forces one q.k implementation; 0 picks by group size
- * (matrix cores from 6 query heads per key/value head).
+ * (matrix cores from 3 query heads per key/value head).
  */
 int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,
                            const int32_t* block_table, int64_t table_stride,

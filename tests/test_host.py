@@ -106,11 +106,34 @@ def test_graph_metadata_update_refusals() -> None:
         hip_attention.graph_metadata(0, 2, 4, torch.device("cpu"))
 
 
-def test_the_split_heuristic_depends_only_on_the_shape() -> None:
-    assert hip_attention.choose_partitions(64, 8, 4, 512) == 0
-    assert hip_attention.choose_partitions(8, 8, 4, 32768) == 64
+def test_the_split_covers_every_context_and_follows_the_modelled_schedule() -> None:
+    choose = hip_attention.choose_split
+    # one long row must be split across the GPU; a 64-position row is never split
+    assert choose(1, 8, 4, 32768, row_lengths=(32768,)).partitions > 16
+    assert choose(4, 8, 4, 64, row_lengths=(64, 1, 3, 64)).partitions == 0
+    rng = np.random.default_rng(1)
+    for _ in range(20):
+        lengths = tuple(int(x) for x in rng.integers(1, 20000, size=int(rng.integers(1, 300))))
+        hip_attention._split_cache.clear()
+        split = choose(len(lengths), 8, 4, max(lengths), row_lengths=lengths)
+        if split.partitions:
+            assert split.partition_size % 64 == 0
+            assert split.partitions * split.partition_size >= max(lengths)
+            # no worse, under the model, than any size whose work list fits the round limit
+            cost = hip_attention.schedule_makespan(list(lengths), split.partition_size)
+            for size in (256, 512, 1024, 2048):
+                if size < max(lengths) and hip_attention.fits_schedule(list(lengths), size):
+                    assert cost <= hip_attention.schedule_makespan(list(lengths), size)
+    # graph metadata (lengths unknown) is scored as every row at the table width
+    assert choose(64, 8, 4, 4096) == choose(64, 8, 4, 4096, row_lengths=(4096,) * 64)
     assert hip_attention.head_chunks(4) == 1 and hip_attention.head_chunks(12) == 2
     assert hip_attention.head_chunks(16) == 2 and hip_attention.head_chunks(11) == 11
+
+
+def test_the_modelled_schedule() -> None:
+    # 256 equal workgroups fill the 256 CUs once; one more starts a second round
+    assert hip_attention.schedule_makespan([1024] * 256, 1024) == 1024 + hip_attention.WORKGROUP_COST
+    assert hip_attention.schedule_makespan([1024] * 257, 1024) == 2 * (1024 + hip_attention.WORKGROUP_COST)
 
 
 def _cpu_buffers(**changes: object) -> KVBuffers:
