@@ -17,7 +17,7 @@ __all__ = ["FLAGS", "LIB_PATH", "PROBE_PATH", "build_library", "hipcc_command"]
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_DIR = PACKAGE_DIR.parent
-SOURCES = ("api.hip", "paged_attention.hip", "paged_attention_mfma.hip", "kv_cache.hip")
+SOURCES = ("api.hip", "paged_attention.hip", "paged_attention_mfma.hip", "paged_prefill.hip", "kv_cache.hip")
 LIB_PATH = PACKAGE_DIR / "lib" / "libayaka_hip.so"
 # A measurement tool built beside the library: read-only probes of the cache access patterns.
 PROBE_SOURCE = "access_probe.hip"

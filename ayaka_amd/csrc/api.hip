@@ -166,7 +166,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
 
 extern "C" {
 
-int ayk_abi_version(void) { return 3; }
+int ayk_abi_version(void) { return 4; }
 
 const char* ayk_last_error(void) { return g_last_error.c_str(); }
 
@@ -261,6 +261,35 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
   p.n_work = n_work_items;
   p.max_len = (int32_t)std::min<int64_t>(p.max_len, (int64_t)partition_size * max_partitions);
   return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, true, flags, stream);
+}
+
+int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
+                      const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
+                      const int32_t* positions, const int32_t* tiles, int32_t n_tiles, int32_t n_rows,
+                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                      int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype, float scale,
+                      void* stream) {
+  const char* op = "ayk_paged_prefill";
+  AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
+             kv_lengths, nullptr,   nullptr,  n_rows,       num_heads,   num_kv_heads,
+             head_dim,  num_blocks, block_size, max_blocks, layout,      dtype,       scale};
+  ayk::AttnParams p;
+  int gc = 0;
+  const int rc = prepare(op, c, p, gc);
+  if (rc != AYK_OK) return rc;
+  if (p.group > 64)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: %d query heads per key/value head exceed a tile of 64", op, p.group);
+  if (n_tiles < 0 || (n_tiles > 0 && (!tiles || !positions)))
+    return fail(AYK_ERR_ARGUMENT, "%s: %d tiles at %p, positions at %p", op, n_tiles, (const void*)tiles,
+                (const void*)positions);
+  if ((int64_t)n_tiles * num_kv_heads > INT32_MAX)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: %d tiles x %d key/value heads exceed one launch", op, n_tiles,
+                num_kv_heads);
+  if (n_tiles == 0 || n_rows == 0) return ok();
+  p.positions = positions;
+  return launched(ayk::launch_prefill(p, tiles, n_tiles, head_dim, dtype == AYK_DTYPE_BF16,
+                                      static_cast<hipStream_t>(stream)),
+                  op);
 }
 
 static int block_op_checks(const char* op, int64_t n, int32_t num_blocks, int64_t block_bytes) {

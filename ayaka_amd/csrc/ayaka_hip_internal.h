@@ -43,6 +43,9 @@ hipError_t launch_attention_dpp(const AttnParams& p, int head_dim, int heads_per
                                 bool split, int waves, hipStream_t stream);
 hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int heads_per_chunk, bool bf16,
                                  bool split, int waves, hipStream_t stream);
+// Multi-row attention: one workgroup per (tile of rows of one request, key/value head).
+hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16,
+                          hipStream_t stream);
 // The v2 log-sum-exp merge of the partitions of every (row, head).
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);
 

@@ -72,6 +72,10 @@ WORKGROUP_COST = 80
 XCDS = 8
 #: Heads per wave from which the library runs q.k on the matrix cores (mirrors the C library).
 MFMA_MIN_HEADS = 3
+#: (row, query head) pairs one workgroup of the multi-row kernel serves.
+PREFILL_PAIRS = 64
+#: Rows per request (on average) from which a multi-row step runs the multi-row kernel.
+PREFILL_MIN_ROWS = 8
 #: Compute units of one MI355X; the split heuristic aims to keep all of them busy.
 COMPUTE_UNITS = 256
 
@@ -107,6 +111,30 @@ class HipAttentionPlan:
             found = choose_split(len(self.row_lengths), num_kv_heads, group, self.max_length,
                                  row_lengths=self.row_lengths)
             self.splits[key] = found
+        return found
+
+    def prefill_tiles(self, group: int, device: torch.device) -> torch.Tensor:
+        """(first row, row count, request) triples for the multi-row kernel, heaviest first.
+
+        Each tile holds consecutive rows of one request, at most 64 (row, query
+        head) pairs; tiles ending at later positions (more context) come first.
+        """
+        key = -group
+        found = self.work.get(key)
+        if found is None:
+            per_tile = max(1, PREFILL_PAIRS // group)
+            tiles = []
+            first = 0
+            for request, (count, length) in enumerate(zip(self.rows, self.kv_lengths)):
+                for start in range(0, count, per_tile):
+                    n = min(per_tile, count - start)
+                    last = self.row_lengths[first + start + n - 1] if length else 0
+                    tiles.append((-last, first + start, n, request))
+                first += count
+            tiles.sort()
+            flat = [v for _, row, n, request in tiles for v in (row, n, request)]
+            found = torch.tensor(flat, dtype=torch.int32).to(device)
+            self.work[key] = found
         return found
 
     def work_items(self, partition_size: int, device: torch.device) -> torch.Tensor:
@@ -241,6 +269,16 @@ def plan(
         block_table=block_rows.to(device=device, dtype=torch.int32).contiguous(),
         plan=HipAttentionPlan(rows, lengths, max(lengths, default=0), sum(row_lengths), tuple(row_lengths)),
     )
+
+
+def _wants_prefill_kernel(step: object) -> bool:
+    """Multi-row steps with >= :data:`PREFILL_MIN_ROWS` rows per request (on average) use the
+    multi-row kernel; shorter windows (verify, a few rows) stream faster through the decode
+    kernels, which split long contexts across the GPU."""
+    if not isinstance(step, HipAttentionPlan):
+        return False
+    requests = sum(1 for count in step.rows if count)
+    return requests > 0 and sum(step.rows) >= PREFILL_MIN_ROWS * requests
 
 
 def head_chunks(group: int) -> int:
@@ -405,6 +443,7 @@ def attend_with(
     qk: str | None = None,
     partition_size: int | None = None,
     partials_only: bool = False,
+    prefill: bool | None = None,
 ) -> None:
     """:func:`attend` with the launch chosen by the caller.
 
@@ -478,6 +517,29 @@ def attend_with(
 
     lib = _lib.lib()
     stream = torch.cuda.current_stream(device).cuda_stream
+    if prefill is None:
+        prefill = not decode and _wants_prefill_kernel(step)
+    if prefill:
+        if not isinstance(step, HipAttentionPlan):
+            raise BackendError(f"{op}: the multi-row kernel needs a planned step", context={"op": op})
+        if heads // kv_heads > PREFILL_PAIRS:
+            raise BackendError(
+                f"{op}: {heads // kv_heads} query heads per key/value head exceed the multi-row "
+                f"kernel's tile of {PREFILL_PAIRS}",
+                context={"op": op, "argument": "q"},
+            )
+        tiles = step.prefill_tiles(heads // kv_heads, device)
+        _lib.check(
+            op,
+            lib.ayk_paged_prefill(
+                out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),
+                table.stride(0), meta.kv_lengths.data_ptr(), meta.positions.data_ptr(), tiles.data_ptr(),
+                tiles.numel() // 3, n_rows, heads, kv_heads, buffers.head_dim, buffers.num_blocks, block_size,
+                table.shape[1], _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype], float(scale),
+                stream,
+            ),
+        )
+        return
     # Decode rows need no per-row indirection: row n is request n and sees its whole context.
     row_request = 0 if decode else meta.request_of_row.data_ptr()
     row_position = 0 if decode else meta.positions.data_ptr()

@@ -124,6 +124,26 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            size_t workspace_bytes, int32_t flags, void* stream);
 
 /*
+ * Multi-row paged attention (prefill chunks, verify windows): the rows of each
+ * request are its last rows, row i at position positions[i] attends to
+ * [0, positions[i]] of its request's context; rows of a request with
+ * kv_lengths 0 get zeros. tiles lists n_tiles (first_row, row_count, request)
+ * int32 triples: consecutive rows of one request with row_count * (num_heads /
+ * num_kv_heads) <= 64, covering every row once. One workgroup per (tile,
+ * key/value head) loads each chunk of the context once into LDS for all its
+ * rows and query heads; q.k and P.V run on the matrix cores with fp32
+ * accumulation. Replaces the reference's per-request SDPA loop,
+ * python/ayaka/ops/backends/torch/attention.py:209-234, and flashinfer's batch
+ * prefill (python/ayaka/ops/backends/flashinfer/attention.py:150-152, :253-266).
+ */
+int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
+                      const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
+                      const int32_t* positions, const int32_t* tiles, int32_t n_tiles, int32_t n_rows,
+                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                      int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype, float scale,
+                      void* stream);
+
+/*
  * Whole-block copies of both caches; block_bytes is the size of one block of
  * one cache (block_size * num_kv_heads * head_dim * elem_bytes), the same in
  * either layout. Ids are int64 when ids_are_64bit, else int32.

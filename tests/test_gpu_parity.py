@@ -79,12 +79,15 @@ def plan_scenario(s: Scenario):
 QK = ["dpp", "mfma"]
 
 
-def run_attention(s: Scenario, partitions: int | None = None, qk: str | None = None) -> torch.Tensor:
+def run_attention(s: Scenario, partitions: int | None = None, qk: str | None = None,
+                  prefill: bool | None = None) -> torch.Tensor:
     buffers = scenario_buffers(s)
     meta = plan_scenario(s)
     q = to_device(s.q_bits, s.dtype)
     out = torch.full_like(q, 7.0)
-    hip_attention.attend_with(q, buffers, meta, out, scale=s.scale, partitions=partitions, qk=qk)
+    if partitions is not None and prefill is None:
+        prefill = False  # a forced v1/v2 launch means the decode kernels
+    hip_attention.attend_with(q, buffers, meta, out, scale=s.scale, partitions=partitions, qk=qk, prefill=prefill)
     torch.cuda.synchronize()
     return out
 
@@ -154,10 +157,10 @@ def test_attention_contract_cases(dtype: str, layout: str, name: str, steps: lis
     s = build_scenario(steps, dtype=dtype, layout=layout, heads=8, kv_heads=2, head_dim=64,
                        block_size=16, mode=mode, seed=31)
     expected = s.expected(np.float64)
-    for partitions in (0, 1):
-        out = run_attention(s, partitions, qk)
-        assert_parity(out, expected, dtype, f"{name}/{partitions}")
-        padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
+    padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
+    for partitions, prefill in ((0, False), (1, False), (None, True)):
+        out = run_attention(s, partitions, qk, prefill)
+        assert_parity(out, expected, dtype, f"{name}/{partitions}/{prefill}")
         if padding_rows:
             assert torch.count_nonzero(out[padding_rows]) == 0
 
@@ -173,12 +176,36 @@ def test_grouped_query_heads(heads: int, kv_heads: int, head_dim: int, qk: str) 
         assert_parity(out, s.expected(np.float64), "bf16", f"{heads}/{kv_heads}/{head_dim}/{partitions}")
 
 
+PREFILL_CASES = [
+    ("long-prompt", [(300, 300)]),
+    ("chunk-after-context", [(77, 1500), (5, 40)]),
+    ("verify-windows", [(5, 900), (3, 17), (1, 2), (4, 0)]),
+    ("many-requests", [(int(n), int(n) + 11) for n in np.random.default_rng(2).integers(1, 60, size=12)]),
+]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(8, 2, 64), (32, 8, 128), (12, 4, 128), (4, 4, 256),
+                                                     (64, 8, 128), (16, 1, 64)])
+@pytest.mark.parametrize("name,steps", PREFILL_CASES, ids=[c[0] for c in PREFILL_CASES])
+def test_multi_row_kernel(dtype: str, heads: int, kv_heads: int, head_dim: int, name: str, steps: list) -> None:
+    s = build_scenario(steps, dtype=dtype, heads=heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16,
+                       mode="mixed", seed=67, spare_blocks=2)
+    out = run_attention(s, None, None, True)
+    assert_parity(out, s.expected(np.float64), dtype, f"prefill/{name}")
+    padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
+    if padding_rows:
+        assert torch.count_nonzero(out[padding_rows]) == 0
+
+
 @pytest.mark.parametrize("block_size", [1, 4, 8, 16, 32, 64])
 @pytest.mark.parametrize("qk", QK)
 def test_block_sizes(block_size: int, qk: str) -> None:
     s = build_scenario([(1, 1), (1, 63), (1, 130), (2, 70)], block_size=block_size, head_dim=128,
                        heads=8, kv_heads=2, seed=43)
-    assert_parity(run_attention(s, None, qk), s.expected(np.float64), "bf16", f"bs{block_size}")
+    for prefill in (False, True):
+        out = run_attention(s, None, qk, prefill)
+        assert_parity(out, s.expected(np.float64), "bf16", f"bs{block_size}/{prefill}")
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
@@ -361,8 +388,8 @@ def test_graph_metadata_replays_match_eager_steps() -> None:
         graph.replay()
         torch.cuda.synchronize()
         replayed = out.clone()
-        # The same step planned eagerly. With the replay's launch shape (dense grid,
-        # partitions of PARTITION_SIZE) it is the same arithmetic, bit for bit; with
+        # The same step planned eagerly. With the replay's launch shape (the split a
+        # graph bucket gets from its table width) it is the same arithmetic, bit for bit; with
         # the eager plan's own split it agrees within the contract's tolerance
         # (the reference compares graph and planned steps with a tolerance too,
         # tests/ops/test_attention_graph.py:56-73).
@@ -370,10 +397,10 @@ def test_graph_metadata_replays_match_eager_steps() -> None:
                                         lengths.to(DEV), table.to(DEV), bs)
         assert eager_meta.slot_mapping.tolist() == meta.slot_mapping.tolist()
         assert eager_meta.positions.tolist() == meta.positions.tolist()
-        parts = -(-max_blocks * bs // hip_attention.PARTITION_SIZE)
+        graph_split = hip_attention.choose_split(bucket, kv_heads, heads // kv_heads, max_blocks * bs)
         same_shape = torch.empty_like(out)
-        hip_attention.attend_with(q, buffers, eager_meta, same_shape, scale=dim**-0.5, partitions=parts,
-                                  partition_size=hip_attention.PARTITION_SIZE)
+        hip_attention.attend_with(q, buffers, eager_meta, same_shape, scale=dim**-0.5,
+                                  partitions=graph_split.partitions, partition_size=graph_split.partition_size or None)
         eager_out = torch.empty_like(out)
         hip_attention.attend(q, buffers, eager_meta, eager_out, scale=dim**-0.5)
         torch.cuda.synchronize()
