@@ -135,16 +135,46 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
   return AYK_OK;
 }
 
+// Compute units of the current device (queried once per device).
+int compute_units() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Whether v2 merges its partitions inside the partition kernel (rather than in
+// a reduce kernel) for a grid of `workgroups`. Measured on MI355X: the in-kernel
+// merge costs each workgroup a device-scope release (an L2 write-back) and the
+// last one of a row the merge; when the whole grid fits about one round of the
+// GPU these land together in the kernel's tail and cost more (~10 us) than the
+// reduce launch (~5 us), while over several rounds they overlap the streaming
+// of later workgroups. A grid of a few dozen workgroups is latency-bound, and
+// there the second launch is the larger cost.
+bool merge_in_kernel(int64_t workgroups) {
+  const int64_t cus = compute_units();
+  return workgroups > 2 * cus || workgroups <= cus / 4;
+}
+
 // Heads per wave from which the library picks the matrix-core q.k kernel.
 constexpr int kMfmaMinHeads = 3;
 
 // The q.k path and workgroup shape for a launch, then the kernel(s).
 int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool bf16, bool split, int32_t flags,
            void* stream) {
-  if (flags & ~(AYK_FLAG_QK_DPP | AYK_FLAG_QK_MFMA | AYK_FLAG_PARTIALS_ONLY))
+  if (flags & ~(AYK_FLAG_QK_DPP | AYK_FLAG_QK_MFMA | AYK_FLAG_PARTIALS_ONLY | AYK_FLAG_SEPARATE_REDUCE |
+                AYK_FLAG_SINGLE_LAUNCH))
     return fail(AYK_ERR_ARGUMENT, "%s: unknown flags 0x%x", op, flags);
   if ((flags & AYK_FLAG_QK_DPP) && (flags & AYK_FLAG_QK_MFMA))
     return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_QK_DPP and AYK_FLAG_QK_MFMA exclude each other", op);
+  if ((flags & AYK_FLAG_SEPARATE_REDUCE) && (flags & AYK_FLAG_SINGLE_LAUNCH))
+    return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_SEPARATE_REDUCE and AYK_FLAG_SINGLE_LAUNCH exclude each other",
+                op);
   // Measured on MI355X: from 3 heads per wave the matrix-core kernel (keys staged
   // through LDS) streams faster than the DPP kernel, whose per-token dot2 and
   // butterfly work grows with the group; 1-2 heads stay on the DPP kernel.
@@ -154,11 +184,16 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   const int64_t workgroups = items * p.num_virtual_heads;
   if (workgroups > INT32_MAX || (int64_t)p.n_rows * p.num_heads > INT32_MAX)
     return fail(AYK_ERR_UNSUPPORTED, "%s: %lld workgroups exceed one launch", op, (long long)workgroups);
+  ayk::AttnParams q = p;
+  // The grid: one workgroup per item and group of up to kMaxWaves virtual heads.
+  const int64_t grid = items * ((p.num_virtual_heads + ayk::kMaxWavesPerGroup - 1) / ayk::kMaxWavesPerGroup);
+  if (split && q.arrivals && !(flags & AYK_FLAG_SINGLE_LAUNCH) && !merge_in_kernel(grid))
+    q.arrivals = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t err = mfma ? ayk::launch_attention_mfma(p, head_dim, gc, bf16, split, waves, s)
-                        : ayk::launch_attention_dpp(p, head_dim, gc, bf16, split, waves, s);
-  if (err == hipSuccess && split && !(flags & AYK_FLAG_PARTIALS_ONLY))
-    err = ayk::launch_partition_reduce(p, head_dim, bf16, s);
+  hipError_t err = mfma ? ayk::launch_attention_mfma(q, head_dim, gc, bf16, split, waves, s)
+                        : ayk::launch_attention_dpp(q, head_dim, gc, bf16, split, waves, s);
+  if (err == hipSuccess && split && !q.arrivals && !(flags & AYK_FLAG_PARTIALS_ONLY))
+    err = ayk::launch_partition_reduce(q, head_dim, bf16, s);
   return launched(err, op);
 }
 
@@ -166,7 +201,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
 
 extern "C" {
 
-int ayk_abi_version(void) { return 4; }
+int ayk_abi_version(void) { return 5; }
 
 const char* ayk_last_error(void) { return g_last_error.c_str(); }
 
@@ -228,7 +263,7 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
                            float scale, int32_t partition_size, int32_t max_partitions,
                            const int32_t* work_items, int32_t n_work_items, void* workspace,
-                           size_t workspace_bytes, int32_t flags, void* stream) {
+                           size_t workspace_bytes, uint32_t* arrivals, int32_t flags, void* stream) {
   const char* op = "ayk_paged_attention_v2";
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
@@ -259,6 +294,9 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
   p.max_partitions = max_partitions;
   p.work = n_work_items > 0 ? work_items : nullptr;
   p.n_work = n_work_items;
+  // The single launch merges in the partition kernel; without counters, or when
+  // asked, a reduce kernel does (and PARTIALS_ONLY runs neither merge).
+  p.arrivals = (flags & (AYK_FLAG_SEPARATE_REDUCE | AYK_FLAG_PARTIALS_ONLY)) ? nullptr : arrivals;
   p.max_len = (int32_t)std::min<int64_t>(p.max_len, (int64_t)partition_size * max_partitions);
   return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, true, flags, stream);
 }

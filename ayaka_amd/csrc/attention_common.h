@@ -19,7 +19,7 @@ constexpr int kWave = 64;
 // Block-table entries staged in LDS per segment of a row's context.
 constexpr int kTableCap = 512;
 // Most waves in one workgroup (one per virtual head).
-constexpr int kMaxWaves = 8;
+constexpr int kMaxWaves = kMaxWavesPerGroup;
 
 template <bool BF16>
 struct Elem;
@@ -186,14 +186,16 @@ __device__ __forceinline__ void merge_waves_and_store(const AttnParams& p, const
 }
 
 // Write one head's merged state from lane c (its 8 elements): the rounded
-// output (v1) or the normalised partial and its (m, l) (v2 partition z).
+// output (v1, or v2 for a row whose context is one partition: nothing to merge,
+// so it rounds exactly what v1 rounds) or the normalised partial and its (m, l)
+// (v2 partition `part` of `np`).
 template <int D, bool BF16, bool SPLIT>
-__device__ __forceinline__ void store_head(const AttnParams& p, int row, int part, int head, int c,
+__device__ __forceinline__ void store_head(const AttnParams& p, int row, int part, int np, int head, int c,
                                            const float (&o)[8], float m, float l) {
   using E = Elem<BF16>;
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   const int64_t head_row = (int64_t)row * p.num_heads + head;
-  if constexpr (SPLIT) {
+  if (SPLIT && np > 1) {
     float* po = p.part_o + (head_row * p.max_partitions + part) * D + c * 8;
     *reinterpret_cast<f32x4*>(po) = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
     *reinterpret_cast<f32x4*>(po + 4) = f32x4{o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv};
@@ -211,6 +213,110 @@ __device__ __forceinline__ void store_head(const AttnParams& p, int row, int par
     w.w = E::round(o[6] * inv) | (E::round(o[7] * inv) << 16);
     *reinterpret_cast<u32x4*>(out) = w;
   }
+}
+
+// Merge partitions [0, np) of heads [head_lo, head_hi) of `row` and round into
+// out: o = sum_i w_i o_i / sum_i w_i with w_i = l_i 2^(m_i - max m), folded in
+// partition order (so the result does not depend on which workgroup merges).
+// Thread t owns items t, t + threads, ... (an item = one head's 4 elements), at
+// most IPT of them, and loads partition i of all its items before folding them,
+// two partitions at a time, so the loads of one thread overlap.
+template <int D, int IPT, bool BF16>
+__device__ __forceinline__ void merge_partitions(const AttnParams& p, int row, int np, int head_lo, int head_hi,
+                                                 int tid, int threads) {
+  using E = Elem<BF16>;
+  constexpr int QUADS = D / 4;
+  const int items = (head_hi - head_lo) * QUADS;
+  const int64_t stride = (int64_t)p.max_partitions;
+  const float* ml[IPT];
+  const f32x4* po[IPT];
+  float m[IPT], l[IPT];
+  f32x4 acc[IPT];
+#pragma unroll
+  for (int k = 0; k < IPT; ++k) {
+    const int it = min(tid + k * threads, items - 1);  // spare slots repeat the last item, unstored
+    const int64_t head_row = (int64_t)row * p.num_heads + head_lo + it / QUADS;
+    ml[k] = p.part_ml + head_row * stride * 2;
+    po[k] = reinterpret_cast<const f32x4*>(p.part_o + head_row * stride * D) + it % QUADS;
+    m[k] = kNoScore;
+    l[k] = 0.f;
+    acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  auto fold = [&](int k, float mi, float wi, f32x4 v) {
+    const float mn = fmaxf(m[k], mi);
+    const float a = fast_exp2(m[k] - mn);
+    const float b = wi * fast_exp2(mi - mn);
+    l[k] = l[k] * a + b;
+    acc[k] = acc[k] * a + v * b;
+    m[k] = mn;
+  };
+  int i = 0;
+  for (; i + 2 <= np; i += 2) {
+    float2 s0[IPT], s1[IPT];
+    f32x4 v0[IPT], v1[IPT];
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+      s0[k] = reinterpret_cast<const float2*>(ml[k])[i];
+      s1[k] = reinterpret_cast<const float2*>(ml[k])[i + 1];
+      v0[k] = po[k][(int64_t)i * QUADS];
+      v1[k] = po[k][(int64_t)(i + 1) * QUADS];
+    }
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+      fold(k, s0[k].x, s0[k].y, v0[k]);
+      fold(k, s1[k].x, s1[k].y, v1[k]);
+    }
+  }
+  if (i < np) {
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+      const float2 s0 = reinterpret_cast<const float2*>(ml[k])[i];
+      fold(k, s0.x, s0.y, po[k][(int64_t)i * QUADS]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < IPT; ++k) {
+    const int it = tid + k * threads;
+    if (it >= items) break;
+    const float inv = l[k] > 0.f ? 1.0f / l[k] : 0.f;
+    const int64_t head_row = (int64_t)row * p.num_heads + head_lo + it / QUADS;
+    uint32_t* o32 = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + head_row * D) + (it % QUADS) * 2;
+    o32[0] = E::round(acc[k].x * inv) | (E::round(acc[k].y * inv) << 16);
+    o32[1] = E::round(acc[k].z * inv) | (E::round(acc[k].w * inv) << 16);
+  }
+}
+
+// End of a v2 workgroup of the single-launch path (p.arrivals set). Every
+// thread calls it after its partial stores. Each workgroup of a (row, head
+// group) with tokens adds one to that pair's arrival counter once its partials
+// are visible device-wide; the workgroup whose add completes the count -- the
+// row's np partitions -- merges them, then returns the counter to zero for the
+// next call. Nothing waits on another workgroup. `s_flag` is one int of LDS.
+//
+// Ordering: the barrier orders every wave's partial stores before thread 0's
+// device-scope release fence, which precedes its counter add; the merging
+// workgroup's acquire fence follows the add that read every other one. One
+// release (an L2 write-back) per workgroup and one acquire (an L2 invalidate)
+// per merge: per-thread device fences would cost far more than the merge saves.
+template <int D, int GC, bool BF16>
+__device__ __forceinline__ void arrive_and_merge(const AttnParams& p, int row, int group, int groups, int np,
+                                                 int head_lo, int head_hi, int tid, int threads, int* s_flag) {
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t* counter = p.arrivals + (int64_t)row * groups + group;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = before + 1 == (uint32_t)np;
+    if (last) {
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    *s_flag = last;
+  }
+  __syncthreads();
+  if (!*s_flag) return;
+  // A workgroup holds at most GC heads per wave, so GC * D / 4 items per 64 threads.
+  merge_partitions<D, (GC * D / 4 + kWave - 1) / kWave, BF16>(p, row, np, head_lo, head_hi, tid, threads);
 }
 
 // Zero the output rows of GC heads of a padding row (v1): nothing of the cache is read.

@@ -7,6 +7,9 @@
 
 namespace ayk {
 
+// Most waves (one per virtual head) in one decode workgroup.
+constexpr int kMaxWavesPerGroup = 8;
+
 // Everything one paged-attention launch reads. Strides are in elements.
 struct AttnParams {
   void* out;
@@ -20,6 +23,8 @@ struct AttnParams {
   const int32_t* work;            // v2 only, optional: n_work (row, partition) pairs to run
   float* part_o;                  // v2 only: [n_rows, num_heads, max_partitions, head_dim]
   float* part_ml;                 // v2 only: [n_rows, num_heads, max_partitions, 2] = (m, l)
+  uint32_t* arrivals;             // v2 single launch: [n_rows, head groups] counters, zero between calls;
+                                  // nullptr: a separate reduce kernel merges the partitions
   int64_t table_stride;
   int64_t block_stride;
   int64_t token_stride;

@@ -21,8 +21,10 @@
 //    4 waves through LDS at the end.
 //  * K of the next chunk is loaded while the current chunk is computed.
 //  * The v2 ("split") variant covers partition z of each row and writes the
-//    normalised partial output plus (m, l) to scratch; a reduce kernel merges
-//    the partitions with the log-sum-exp identity.
+//    normalised partial output plus (m, l) to scratch; the last workgroup of a
+//    row to finish merges the partitions with the log-sum-exp identity
+//    (arrive_and_merge), or a separate reduce kernel does. A row whose context
+//    fits one partition is written directly, exactly as v1 writes it.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -40,11 +42,13 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
   constexpr int CH = TPL * NLD;      // tokens per chunk
 
   __shared__ int s_tbl[kTableCap];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int threads = blockDim.x;
   const int waves = threads / kWave;
-  const WgCoord wg = wg_coord(p, (p.num_virtual_heads + waves - 1) / waves, SPLIT);
+  const int groups = (p.num_virtual_heads + waves - 1) / waves;
+  const WgCoord wg = wg_coord(p, groups, SPLIT);
   const int row = wg.row;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -60,10 +64,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
   int req, len;
   row_context(p, row, req, len);
   int t_begin = 0, t_end = len;
+  const int np = SPLIT ? (len > 0 ? (len - 1) / p.partition_size + 1 : 0) : 1;  // partitions with tokens
   if constexpr (SPLIT) {
     t_begin = wg.part * p.partition_size;
     t_end = min(len, t_begin + p.partition_size);
-    if (t_begin >= t_end) return;  // the reduce kernel reads only partitions that hold tokens
+    if (t_begin >= t_end) {  // only partitions that hold tokens are merged
+      if (len == 0 && wg.part == 0 && active) store_zero_rows<D, GC, kWave>(p, row, h0, lane);  // a padding row
+      return;
+    }
   } else if (len == 0) {
     if (active) store_zero_rows<D, GC, kWave>(p, row, h0, lane);
     return;
@@ -247,27 +255,35 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
       ++ci;
     }
   }
-  if (!active) return;
-
-  // Merge the TPL lane groups of this wave (butterfly: every group ends with the merged state).
+  if (active) {
+    // Merge the TPL lane groups of this wave (butterfly: every group ends with the merged state).
 #pragma unroll
-  for (int st = LPT; st < kWave; st <<= 1) {
+    for (int st = LPT; st < kWave; st <<= 1) {
 #pragma unroll
-    for (int g = 0; g < GC; ++g) {
-      const float m2 = __shfl_xor(m[g], st);
-      const float l2 = __shfl_xor(l[g], st);
-      const float mn = fmaxf(m[g], m2);
-      const float a = fast_exp2(m[g] - mn);
-      const float b = fast_exp2(m2 - mn);
-      l[g] = l[g] * a + l2 * b;
-      m[g] = mn;
+      for (int g = 0; g < GC; ++g) {
+        const float m2 = __shfl_xor(m[g], st);
+        const float l2 = __shfl_xor(l[g], st);
+        const float mn = fmaxf(m[g], m2);
+        const float a = fast_exp2(m[g] - mn);
+        const float b = fast_exp2(m2 - mn);
+        l[g] = l[g] * a + l2 * b;
+        m[g] = mn;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] = o[g][e] * a + __shfl_xor(o[g][e], st) * b;
+        for (int e = 0; e < 8; ++e) o[g][e] = o[g][e] * a + __shfl_xor(o[g][e], st) * b;
+      }
+    }
+    if (r == 0) {
+#pragma unroll
+      for (int g = 0; g < GC; ++g)
+        store_head<D, BF16, SPLIT>(p, row, wg.part, np, h0 + g, c, o[g], m[g], l[g]);
     }
   }
-  if (r == 0) {
-#pragma unroll
-    for (int g = 0; g < GC; ++g) store_head<D, BF16, SPLIT>(p, row, wg.part, h0 + g, c, o[g], m[g], l[g]);
+  if constexpr (SPLIT) {
+    if (np > 1 && p.arrivals) {
+      const int vh_lo = wg.group * waves;
+      const int vh_hi = min(p.num_virtual_heads, vh_lo + waves);
+      arrive_and_merge<D, GC, BF16>(p, row, wg.group, groups, np, vh_lo * GC, vh_hi * GC, tid, threads, &s_last);
+    }
   }
 }
 
@@ -297,13 +313,14 @@ __global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const 
   row_context(p, row, req, len);
   const int64_t head_row = (int64_t)row * p.num_heads + h;
   uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D;
-  const int np = (len + p.partition_size - 1) / p.partition_size;
+  const int np = len > 0 ? (len - 1) / p.partition_size + 1 : 0;
   const float* ml = p.part_ml + head_row * p.max_partitions * 2;
   const f32x4* po = reinterpret_cast<const f32x4*>(p.part_o + head_row * p.max_partitions * D);
 
-  if (np <= 1) {
+  if (np == 1) return;  // the partition kernel wrote the row's output itself
+  if (np == 0) {
     if (slot == 0) {
-      const f32x4 v = np == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : po[quad];
+      const f32x4 v = {0.f, 0.f, 0.f, 0.f};
       uint32_t* o32 = reinterpret_cast<uint32_t*>(out) + quad * 2;
       o32[0] = E::round(v.x) | (E::round(v.y) << 16);
       o32[1] = E::round(v.z) | (E::round(v.w) << 16);

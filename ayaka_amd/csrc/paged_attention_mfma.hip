@@ -61,11 +61,13 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   __shared__ u32x4 s_k[kMaxWaves][CH * CPT];       // the chunk's keys, swizzled (see key_slot)
   __shared__ float s_p[kMaxWaves][2][CH][PW];      // the chunk's weights, double-buffered
   __shared__ float s_alpha[kMaxWaves][PW];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int threads = blockDim.x;
   const int waves = threads / kWave;
-  const WgCoord wg = wg_coord(p, (p.num_virtual_heads + waves - 1) / waves, SPLIT);
+  const int groups = (p.num_virtual_heads + waves - 1) / waves;
+  const WgCoord wg = wg_coord(p, groups, SPLIT);
   const int row = wg.row;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -85,10 +87,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   int req, len;
   row_context(p, row, req, len);
   int t_begin = 0, t_end = len;
+  const int np = SPLIT ? (len > 0 ? (len - 1) / p.partition_size + 1 : 0) : 1;  // partitions with tokens
   if constexpr (SPLIT) {
     t_begin = wg.part * p.partition_size;
     t_end = min(len, t_begin + p.partition_size);
-    if (t_begin >= t_end) return;
+    if (t_begin >= t_end) {  // only partitions that hold tokens are merged
+      if (len == 0 && wg.part == 0 && active) store_zero_rows<D, GC, kWave>(p, row, h0, lane);  // a padding row
+      return;
+    }
   } else if (len == 0) {
     if (active) store_zero_rows<D, GC, kWave>(p, row, h0, lane);
     return;
@@ -233,23 +239,30 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
       ++ci;
     }
   }
-  if (!active) return;
-
-  // Head mt's weight sum over the wave's 4 token groups; the value lanes' partial
-  // sums share the wave's running max, so they add without rescaling.
-  l_h += __shfl_xor(l_h, 16);
-  l_h += __shfl_xor(l_h, 32);
+  if (active) {
+    // Head mt's weight sum over the wave's 4 token groups; the value lanes' partial
+    // sums share the wave's running max, so they add without rescaling.
+    l_h += __shfl_xor(l_h, 16);
+    l_h += __shfl_xor(l_h, 32);
 #pragma unroll
-  for (int st = CPT; st < kWave; st <<= 1)
+    for (int st = CPT; st < kWave; st <<= 1)
 #pragma unroll
-    for (int g = 0; g < GC; ++g)
+      for (int g = 0; g < GC; ++g)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] += __shfl_xor(o[g][e], st);
+        for (int e = 0; e < 8; ++e) o[g][e] += __shfl_xor(o[g][e], st);
 #pragma unroll
-  for (int g = 0; g < GC; ++g) {
-    const float mg = __shfl(m_h, g);
-    const float lg = __shfl(l_h, g);
-    if (r == 0) store_head<D, BF16, SPLIT>(p, row, wg.part, h0 + g, c, o[g], mg, lg);
+    for (int g = 0; g < GC; ++g) {
+      const float mg = __shfl(m_h, g);
+      const float lg = __shfl(l_h, g);
+      if (r == 0) store_head<D, BF16, SPLIT>(p, row, wg.part, np, h0 + g, c, o[g], mg, lg);
+    }
+  }
+  if constexpr (SPLIT) {
+    if (np > 1 && p.arrivals) {
+      const int vh_lo = wg.group * waves;
+      const int vh_hi = min(p.num_virtual_heads, vh_lo + waves);
+      arrive_and_merge<D, GC, BF16>(p, row, wg.group, groups, np, vh_lo * GC, vh_hi * GC, tid, threads, &s_last);
+    }
   }
 }
 

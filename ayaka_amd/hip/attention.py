@@ -84,6 +84,7 @@ _DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 _QK_FLAGS = {None: 0, "dpp": 1, "mfma": 2}
 #: v2 flag: launch the partition kernel only (benchmarks time the dominant kernel with it).
 PARTIALS_ONLY = 4
+_MERGE_FLAGS = {None: 0, "reduce-kernel": 8, "in-kernel": 16}
 
 
 @dataclass(frozen=True, slots=True)
@@ -138,7 +139,8 @@ class HipAttentionPlan:
         return found
 
     def work_items(self, partition_size: int, device: torch.device) -> torch.Tensor:
-        """The (row, partition) pairs of the step that hold tokens, longest first, on ``device``.
+        """The (row, partition) pairs of the step that hold tokens, longest first, on ``device``
+        (plus partition 0 of each row without context, last).
 
         Every full partition comes before any partial one, so the last
         workgroups to start are the short ones and consecutive workgroups land on
@@ -148,7 +150,8 @@ class HipAttentionPlan:
         if found is None:
             items = []
             for row, length in enumerate(self.row_lengths):
-                for part in range(-(-length // partition_size)):
+                # a row without context still gets partition 0, which writes its zeros
+                for part in range(max(1, -(-length // partition_size))):
                     size = min(partition_size, length - part * partition_size)
                     items.append((-size, row, part))
             items.sort()
@@ -294,6 +297,16 @@ def uses_matrix_cores(group: int) -> bool:
     return group // head_chunks(group) >= MFMA_MIN_HEADS
 
 
+def merge_site(num_kv_heads: int, group: int, step: "HipAttentionPlan", partition_size: int) -> str:
+    """Where the library merges the v2 partitions of an eagerly planned step: ``"in-kernel"``
+    when its grid spans more than two rounds of the compute units or a quarter round at
+    most, ``"reduce-kernel"`` otherwise (the rule of ``merge_in_kernel`` in ``api.hip``)."""
+    groups = -(-num_kv_heads * head_chunks(group) // 8)
+    items = sum(max(1, -(-n // partition_size)) for n in step.row_lengths)
+    workgroups = items * groups
+    return "in-kernel" if workgroups > 2 * COMPUTE_UNITS or workgroups <= COMPUTE_UNITS // 4 else "reduce-kernel"
+
+
 @dataclass(frozen=True, slots=True)
 class Split:
     """A launch: ``partitions == 0`` is v1, otherwise v2 over partitions of ``partition_size``."""
@@ -420,6 +433,30 @@ def _workspace(op: str, device: torch.device, nbytes: int, capture: bool) -> tor
     return fresh
 
 
+_counters: dict[torch.device, torch.Tensor] = {}
+
+
+def _arrivals(op: str, device: torch.device, words: int, capture: bool) -> torch.Tensor:
+    """The v2 arrival counters of ``device``: zero-filled once, and every v2 call
+    leaves them zero again, so they are shared by all calls on the device's stream."""
+    found = _counters.get(device)
+    if found is not None and found.numel() >= words:
+        return found
+    if capture:
+        raise BackendError(
+            f"{op}: the v2 arrival counters for this step ({words} words) outnumber the ones "
+            "allocated so far; run the step once eagerly before capturing it",
+            context={"op": op},
+        )
+    size = max(words, 2 * found.numel() if found is not None else 0, 1 << 14)
+    with torch.inference_mode(False):
+        fresh = torch.zeros(size, dtype=torch.int32, device=device)
+    if found is not None:
+        _retired.append(found)
+    _counters[device] = fresh
+    return fresh
+
+
 def attend(
     q: torch.Tensor,
     buffers: KVBuffers,
@@ -444,6 +481,7 @@ def attend_with(
     partition_size: int | None = None,
     partials_only: bool = False,
     prefill: bool | None = None,
+    merge: str | None = None,
 ) -> None:
     """:func:`attend` with the launch chosen by the caller.
 
@@ -452,8 +490,11 @@ def attend_with(
     cover the step's longest context), ``None`` lets :func:`choose_split` decide. ``qk`` forces the q.k implementation,
     ``"dpp"`` (VALU dot2 + DPP butterflies) or ``"mfma"`` (matrix cores); ``None``
     lets the library pick. ``partials_only`` (v2) runs the partition kernel alone
-    and leaves ``out`` unwritten. Benchmarks and tests use it to time and check
-    every kernel on one step.
+    and leaves the rows of several partitions unwritten; ``merge`` (v2) forces
+    where the partitions are merged, ``"in-kernel"`` (the partition kernel's
+    last workgroup of a row) or ``"reduce-kernel"`` (a second launch); ``None``
+    lets the library pick.
+    Benchmarks and tests use them to time and check every kernel on one step.
     """
     op = "attention.attend"
     require_buffers(op, buffers)
@@ -575,12 +616,13 @@ def attend_with(
             f"{op}: {partitions} partitions of {partition_size} do not cover {max_length} positions",
             context={"op": op},
         )
-    flags = _QK_FLAGS[qk] | (PARTIALS_ONLY if partials_only else 0)
+    flags = _QK_FLAGS[qk] | (PARTIALS_ONLY if partials_only else 0) | _MERGE_FLAGS[merge]
     if partitions == 0:
         _lib.check(op, lib.ayk_paged_attention_v1(*common, flags, stream))
         return
     nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, partitions)
     scratch = _workspace(op, device, nbytes, capturing(q))
+    arrivals = _arrivals(op, device, n_rows * heads, capturing(q))
     # An eager step runs only the partitions that hold tokens, longest first; graph
     # metadata keeps the dense grid, whose shape does not depend on the lengths.
     work, n_work = 0, 0
@@ -590,8 +632,8 @@ def attend_with(
     _lib.check(
         op,
         lib.ayk_paged_attention_v2(
-            *common, partition_size, partitions, work, n_work, scratch.data_ptr(), scratch.numel(), flags,
-            stream,
+            *common, partition_size, partitions, work, n_work, scratch.data_ptr(), scratch.numel(),
+            arrivals.data_ptr(), flags, stream,
         ),
     )
 

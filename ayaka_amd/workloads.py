@@ -95,7 +95,7 @@ class Step:
     """One synthetic decode step: a filled pool, its table, the rows to store and the queries."""
 
     config: Config
-    k_cache: torch.Tensor  # [num_blocks, block_size, kv_heads, head_dim] (NHD)
+    k_cache: torch.Tensor  # [num_blocks, block_size, kv_heads, head_dim] (NHD) or HND
     v_cache: torch.Tensor
     table: torch.Tensor  # [B, max_blocks] int32
     lengths: torch.Tensor  # [B] int32
@@ -105,9 +105,10 @@ class Step:
     q: torch.Tensor  # [B, heads, head_dim], the decode queries
 
 
-def build(cfg: Config, device: torch.device | str = "cpu", *, poison: bool = True) -> Step:
+def build(cfg: Config, device: torch.device | str = "cpu", *, poison: bool = True, layout: str = "nhd") -> Step:
     """Fill a pool for ``cfg`` on ``device``. The newest ``new_tokens`` positions of every
-    sequence are left unwritten (NaN): the step's KV write fills them."""
+    sequence are left unwritten (NaN): the step's KV write fills them. ``layout`` "hnd"
+    returns the same values in HND caches (``[num_blocks, kv_heads, block_size, head_dim]``)."""
     device = torch.device(device)
     gen = torch.Generator(device=device).manual_seed(1000 + cfg.index)
     host = np.random.default_rng(2000 + cfg.index)
@@ -152,6 +153,9 @@ def build(cfg: Config, device: torch.device | str = "cpu", *, poison: bool = Tru
     k_new = (torch.randn((sum(rows), hkv, dim), generator=gen, device=device) * cfg.kv_std).to(cfg.dtype)
     v_new = (torch.randn((sum(rows), hkv, dim), generator=gen, device=device) * cfg.kv_std).to(cfg.dtype)
     q = (torch.randn((cfg.batch, cfg.heads, dim), generator=gen, device=device) * cfg.q_std).to(cfg.dtype)
+    if layout == "hnd":
+        k_cache = k_cache.permute(0, 2, 1, 3).contiguous()
+        v_cache = v_cache.permute(0, 2, 1, 3).contiguous()
     return Step(
         config=cfg,
         k_cache=k_cache,
@@ -198,9 +202,12 @@ def sample_rows(step: Step, rows: list[int]) -> dict[str, np.ndarray]:
         n = -(-int(lengths[b]) // bs)
         new_table[b, :n] = [remap[int(x)] for x in table[b, :n]]
     index = torch.tensor(ids, dtype=torch.int64, device=step.k_cache.device)
-    nan_block = torch.full((1, *step.k_cache.shape[1:]), float("nan"))
-    k = torch.cat([nan_block, step.k_cache[index].float().cpu()]).numpy()
-    v = torch.cat([nan_block, step.v_cache[index].float().cpu()]).numpy()
+    k_nhd, v_nhd = step.k_cache[index], step.v_cache[index]
+    if k_nhd.shape[1] != bs:  # HND caches: back to [block, offset, head, dim]
+        k_nhd, v_nhd = k_nhd.permute(0, 2, 1, 3), v_nhd.permute(0, 2, 1, 3)
+    nan_block = torch.full((1, *k_nhd.shape[1:]), float("nan"))
+    k = torch.cat([nan_block, k_nhd.float().cpu()]).numpy()
+    v = torch.cat([nan_block, v_nhd.float().cpu()]).numpy()
     return {
         "q": step.q[rows].float().cpu().numpy(),
         "k": k,

@@ -51,8 +51,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=3, help="benchmark configuration 1-5 (3 = headline)")
-    ap.add_argument("--only", choices=["auto", "v1", "v2"], default=None,
+    ap.add_argument("--only", choices=["auto", "auto/reduce-kernel", "auto/in-kernel", "v1", "v2"], default=None,
                     help="time only this launch (for profiler runs)")
+    ap.add_argument("--layout", choices=["nhd", "hnd"], default=None,
+                    help="cache layout (default: the one the hip backend asks the pool for)")
     ap.add_argument("--qk", choices=["dpp", "mfma"], default=None,
                     help="force the q.k implementation (default: the library's choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -160,8 +162,9 @@ def main() -> int:
     _lib.lib()
     dev = torch.device("cuda:0")
     cfg = workloads.config(args.config)
-    step = workloads.build(cfg, dev, poison=False)
-    buffers = KVBuffers(step.k_cache, step.v_cache, KVLayoutKind.NHD, RAW_CODEC)
+    layout = KVLayoutKind(args.layout) if args.layout else KVLayoutKind(hip_kvcache.layout())
+    step = workloads.build(cfg, dev, poison=False, layout=str(layout.value))
+    buffers = KVBuffers(step.k_cache, step.v_cache, layout, RAW_CODEC)
     write = hip_attention.plan(ForwardMode.MIXED, step.rows_per_request, step.lengths, step.table, cfg.block_size)
     hip_kvcache.store(step.k_new, step.v_new, buffers, write)
     meta = hip_attention.plan(ForwardMode.DECODE, torch.ones(cfg.batch, dtype=torch.int32, device=dev),
@@ -171,20 +174,23 @@ def main() -> int:
     max_len = max(cfg.lengths)
     auto = meta.plan.split_for(cfg.kv_heads, cfg.heads // cfg.kv_heads)  # what attend will launch
     # The headline ("auto", the launch attend picks) runs last, on a GPU warmed by the others.
+    # name: (partitions, partition size, where v2 merges: None = the library's choice)
     launches = {
-        "v1": (0, 0),
-        "v2": (-(-max_len // hip_attention.PARTITION_SIZE), hip_attention.PARTITION_SIZE),
-        "auto": (None, auto.partition_size),
+        "v1": (0, 0, None),
+        "v2": (-(-max_len // hip_attention.PARTITION_SIZE), hip_attention.PARTITION_SIZE, None),
+        "auto/reduce-kernel": (None, auto.partition_size, "reduce-kernel"),
+        "auto/in-kernel": (None, auto.partition_size, "in-kernel"),
+        "auto": (None, auto.partition_size, None),
     }
     if args.only:
         launches = {args.only: launches[args.only]}
 
     results = {}
     head_name = "auto" if "auto" in launches else next(iter(launches))
-    for name, (parts, size) in launches.items():
-        def call(parts=parts, size=size):
+    for name, (parts, size, merge) in launches.items():
+        def call(parts=parts, size=size, merge=merge):
             hip_attention.attend_with(step.q, buffers, meta, out, scale=cfg.scale, partitions=parts, qk=args.qk,
-                                      partition_size=size or None)
+                                      partition_size=size or None, merge=merge)
         # The headline launch times exactly K steps once; the others take the median of 3 regions.
         results[name] = time_calls(call, args.steps, args.warmup, repeats=1 if name == head_name else 3)
         results[name]["partitions"] = auto.partitions if parts is None else parts
@@ -195,15 +201,19 @@ def main() -> int:
 
     head = results[head_name]
     store_us = time_calls(lambda: hip_kvcache.store(step.k_new, step.v_new, buffers, write), 50, 5)["median_us"]
-    # The dominant kernel: the attention kernel itself. For v2, time the partition
-    # kernel alone (the reduce kernel is skipped) with the same events.
+    # The dominant kernel: the attention kernel itself. v1 and a v2 that merges in
+    # its partition kernel are one kernel per call, so the call's time is the
+    # kernel's; with a reduce kernel, time the partition kernel alone with the
+    # same events.
     mfma = args.qk == "mfma" or (args.qk is None and hip_attention.uses_matrix_cores(cfg.heads // cfg.kv_heads))
+    parts, size, merge = launches[head_name]
+    if merge is None and head["partitions"]:
+        merge = hip_attention.merge_site(cfg.kv_heads, cfg.heads // cfg.kv_heads, meta.plan, size)
     kernel = ("paged_attention_mfma_kernel" if mfma else "paged_attention_kernel") + \
-        (" (v1)" if head["partitions"] == 0 else " (v2 partitions)")
-    if head["partitions"] == 0:
+        (" (v1)" if head["partitions"] == 0 else f" (v2, merge {merge})")
+    if head["partitions"] == 0 or merge == "in-kernel":
         kernel_us = head["median_us"]
     else:
-        parts, size = launches[head_name]
         kernel_us = time_calls(
             lambda: hip_attention.attend_with(step.q, buffers, meta, out, scale=cfg.scale, partitions=parts,
                                               qk=args.qk, partition_size=size or None, partials_only=True),
@@ -227,7 +237,8 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) K/V/Q, random block permutation)",
         "config": {
             "workload": f"C{cfg.index} {cfg.name} decode attention: Hq {cfg.heads}, Hkv {cfg.kv_heads}, "
-                        f"D {cfg.head_dim}, {cfg.dtype_label}, block {cfg.block_size}, batch {cfg.batch}, "
+                        f"D {cfg.head_dim}, {cfg.dtype_label}, {layout.value.upper()} cache, "
+                        f"block {cfg.block_size}, batch {cfg.batch}, "
                         f"context {min(cfg.lengths)}-{max(cfg.lengths)} (sum {sum(cfg.lengths)}), "
                         f"pool {cfg.num_blocks} blocks",
             "algorithmic_bytes_per_call": nbytes,

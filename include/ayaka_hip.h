@@ -45,7 +45,10 @@ enum { AYK_DTYPE_FP16 = 0, AYK_DTYPE_BF16 = 1 };
 enum {
   AYK_FLAG_QK_DPP = 1,  /* q.k on the VALU: v_dot2 + DPP butterflies */
   AYK_FLAG_QK_MFMA = 2, /* q.k on the matrix cores: v_mfma_f32_16x16x32 */
-  AYK_FLAG_PARTIALS_ONLY = 4 /* v2: run only the partition kernel (out is not written); for timing it */
+  AYK_FLAG_PARTIALS_ONLY = 4, /* v2: run only the partition kernel (rows of several partitions are not
+                                 written); for timing it */
+  AYK_FLAG_SEPARATE_REDUCE = 8, /* v2: merge partitions in a second kernel even when arrivals is given */
+  AYK_FLAG_SINGLE_LAUNCH = 16   /* v2: merge partitions in the partition kernel (needs arrivals) */
 };
 enum { AYK_LAYOUT_NHD = 0, AYK_LAYOUT_HND = 1 };
 
@@ -99,15 +102,29 @@ size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads,
 /*
  * Paged attention, split context ("v2"): one workgroup per (row, key/value
  * head, partition of partition_size positions) writes a partial result and its
- * log-sum-exp state into `workspace`, then a reduce kernel merges the
- * partitions of each (row, head) and rounds once. Same arguments and semantics
+ * log-sum-exp state into `workspace`; the partitions of each (row, head) are
+ * then merged and rounded once. A row whose context fits one partition skips
+ * the scratch and is rounded exactly as v1 rounds it.
+ *
+ * With `arrivals` (n_rows * num_heads uint32 words, all zero before the first
+ * call that uses them) the merge can happen in the same launch: the workgroup
+ * that finishes a row's partitions last merges them, and leaves its counter at
+ * zero again, so the buffer stays ready for the next call. It must not be
+ * shared by calls that overlap in time. The library takes the single launch
+ * when the grid spans more than two rounds of the GPU's compute units or is
+ * tiny, and a second (reduce) kernel otherwise; AYK_FLAG_SINGLE_LAUNCH and
+ * AYK_FLAG_SEPARATE_REDUCE force one. With NULL arrivals the reduce kernel
+ * merges. Either way the merge folds the partitions in partition order,
+ * so results do not depend on scheduling. Same arguments and semantics
  * as v1, plus the partition size (a positive multiple of 64) and the number of
  * partitions per row the scratch holds: every row's length must be at most
  * max_partitions * partition_size (positions beyond it are not read).
  * work_items, if not NULL, lists n_work_items (row, partition) int32 pairs --
  * the partitions that hold tokens, in the order to run them (longest first
  * balances best); partitions not listed are not computed, so the list must
- * cover every partition below ceil(length / partition_size) of every row. With
+ * cover every partition below ceil(length / partition_size) of every row,
+ * each once (the arrival count relies on it), and partition 0 of every row
+ * with no context (that workgroup writes the row's zeros). With
  * NULL the grid covers every (row, partition < max_partitions), which is what a
  * graph replay with fixed launch shape needs. The math the reference delegates
  * to flashinfer's split-KV decode and its plan-time schedule
@@ -121,7 +138,7 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
                            float scale, int32_t partition_size, int32_t max_partitions,
                            const int32_t* work_items, int32_t n_work_items, void* workspace,
-                           size_t workspace_bytes, int32_t flags, void* stream);
+                           size_t workspace_bytes, uint32_t* arrivals, int32_t flags, void* stream);
 
 /*
  * Multi-row paged attention (prefill chunks, verify windows): the rows of each

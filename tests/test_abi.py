@@ -55,7 +55,7 @@ def _v1(lib: ctypes.CDLL, **kw: object) -> int:
         ({"q": None}, 1, b"null"),
         ({"stride": 2}, 1, b"table_stride"),
         ({"flags": 3}, 1, b"exclude each other"),
-        ({"flags": 16}, 1, b"unknown flags"),
+        ({"flags": 32}, 1, b"unknown flags"),
     ],
 )
 def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, message: bytes) -> None:
@@ -67,12 +67,14 @@ def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, me
 def test_v2_and_store_refusals() -> None:
     lib = _lib.lib()
     base = [1, 1, 1, 1, 1, 4, 1, None, None, 1, 8, 2, 128, 10, 16, 4, 0, 1, ctypes.c_float(1.0)]
-    assert lib.ayk_paged_attention_v2(*base, 100, 4, None, 0, 1, 1 << 20, 0, None) == 1
+    assert lib.ayk_paged_attention_v2(*base, 100, 4, None, 0, 1, 1 << 20, None, 0, None) == 1
     assert b"multiple of 64" in lib.ayk_last_error()
-    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 1, 16, 0, None) == 4
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 1, 16, None, 0, None) == 4
     assert b"workspace" in lib.ayk_last_error()
-    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 3, 1, 1 << 20, 0, None) == 1
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 3, 1, 1 << 20, None, 0, None) == 1
     assert b"work items" in lib.ayk_last_error()
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 16, 1 << 20, None, 8 | 16, None) == 1
+    assert b"exclude each other" in lib.ayk_last_error()
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 3, None) == 2
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 0, 2, 64, 10, 16, 0, 2, None) == 0
     assert lib.ayk_zero_blocks(1, 1, 1, 0, 2, 0, 64, None) == 1

@@ -80,14 +80,15 @@ QK = ["dpp", "mfma"]
 
 
 def run_attention(s: Scenario, partitions: int | None = None, qk: str | None = None,
-                  prefill: bool | None = None) -> torch.Tensor:
+                  prefill: bool | None = None, **launch) -> torch.Tensor:
     buffers = scenario_buffers(s)
     meta = plan_scenario(s)
     q = to_device(s.q_bits, s.dtype)
     out = torch.full_like(q, 7.0)
     if partitions is not None and prefill is None:
         prefill = False  # a forced v1/v2 launch means the decode kernels
-    hip_attention.attend_with(q, buffers, meta, out, scale=s.scale, partitions=partitions, qk=qk, prefill=prefill)
+    hip_attention.attend_with(q, buffers, meta, out, scale=s.scale, partitions=partitions, qk=qk, prefill=prefill,
+                              **launch)
     torch.cuda.synchronize()
     return out
 
@@ -224,6 +225,35 @@ def test_split_partitions_agree_with_the_oracle_and_v1(dtype: str, head_dim: int
     assert_parity(auto, expected, dtype, "auto")
 
 
+def counters_are_clear() -> bool:
+    return all(int(c.abs().max()) == 0 for c in hip_attention._counters.values())
+
+
+@pytest.mark.parametrize("qk", QK)
+@pytest.mark.parametrize("heads,kv_heads", [(8, 2), (40, 10), (96, 12), (12, 12)])
+def test_single_launch_merge_agrees_with_the_reduce_kernel(qk: str, heads: int, kv_heads: int) -> None:
+    # 10 and 12 key/value heads leave idle waves in the second workgroup of a row; rows of
+    # 0, 1 and many partitions, one ending inside a partition
+    s = build_scenario([(1, 2500), (1, 0), (1, 64), (1, 1024), (1, 1500), (1, 7)], heads=heads,
+                       kv_heads=kv_heads, head_dim=128, block_size=16, mode="decode", seed=67)
+    expected = s.expected(np.float64)
+    fused = run_attention(s, 10, qk, merge="in-kernel")
+    assert counters_are_clear()
+    separate = run_attention(s, 10, qk, partition_size=256, merge="reduce-kernel")
+    fused256 = run_attention(s, 10, qk, partition_size=256, merge="in-kernel")
+    assert counters_are_clear()
+    for name, out in (("fused", fused), ("separate", separate), ("fused256", fused256)):
+        assert_parity(out, expected, "bf16", name)
+    # a smaller step in between leaves the counters ready for the next one
+    small = build_scenario([(1, 700), (1, 300)], heads=heads, kv_heads=kv_heads, head_dim=128, block_size=16,
+                           mode="decode", seed=68)
+    assert_parity(run_attention(small, 3, qk, partition_size=256, merge="in-kernel"), small.expected(np.float64),
+                  "bf16", "small")
+    again = run_attention(s, 10, qk, merge="in-kernel")
+    assert counters_are_clear()
+    assert torch.equal(fused.view(torch.int16), again.view(torch.int16))
+
+
 @pytest.mark.parametrize("qk", QK)
 def test_one_partition_reproduces_v1_bit_for_bit(qk: str) -> None:
     s = build_scenario([(1, 300), (1, 17), (1, 512)], heads=8, kv_heads=2, head_dim=128, block_size=16,
@@ -320,10 +350,13 @@ def test_benchmark_configuration(index: int) -> None:
                                 step.lengths, step.table, cfg.block_size)
     outs = {}
     v2_parts = -(-max(cfg.lengths) // hip_attention.PARTITION_SIZE)
-    for name, parts, qk in (("v1-dpp", 0, "dpp"), ("v1-mfma", 0, "mfma"), ("v2-dpp", v2_parts, "dpp"),
-                            ("v2-mfma", v2_parts, "mfma"), ("auto", None, None)):
+    for name, parts, qk, merge in (("v1-dpp", 0, "dpp", None), ("v1-mfma", 0, "mfma", None),
+                                   ("v2-dpp", v2_parts, "dpp", None), ("v2-mfma", v2_parts, "mfma", None),
+                                   ("v2-reduce-kernel", v2_parts, None, "reduce-kernel"),
+                                   ("v2-in-kernel", v2_parts, None, "in-kernel"), ("auto", None, None, None)):
         out = torch.empty_like(step.q)
-        hip_attention.attend_with(step.q, buffers, decode, out, scale=cfg.scale, partitions=parts, qk=qk)
+        hip_attention.attend_with(step.q, buffers, decode, out, scale=cfg.scale, partitions=parts, qk=qk,
+                                  merge=merge)
         outs[name] = out
     torch.cuda.synchronize()
     rows = SAMPLES[index]
@@ -338,7 +371,8 @@ def test_benchmark_configuration(index: int) -> None:
     # size-independent: v1 and v2 agree on every row, and every row is finite
     for out in outs.values():
         assert torch.isfinite(out.float()).all()
-    for name in ("v1-mfma", "v2-dpp", "v2-mfma"):
+    assert counters_are_clear()
+    for name in ("v1-mfma", "v2-dpp", "v2-mfma", "v2-reduce-kernel", "v2-in-kernel"):
         diff = (outs["v1-dpp"].float() - outs[name].float()).abs().max().item()
         assert diff <= 4 * EPS[cfg.dtype_label] * outs["v1-dpp"].float().abs().max().item() + 1e-6, name
 
