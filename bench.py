@@ -34,14 +34,16 @@ HBM_PEAK_GBS = 8000.0
 # for a 1 GiB device copy (FETCH x2.0, WRITE x1.0). Reported only when this run's launch is
 # the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
 PROFILED_TRAFFIC = {
-    (3, "paged_attention_kernel (v2 partitions)", 512):
-        (1_078_181_791, 8_912_896, "profiles/paged_attention_kernel_c3_llama3_8b_decode.md"),
-    (4, "paged_attention_kernel (v2 partitions)", 320):
-        (663_490_983, 8_877_760, "profiles/paged_attention_kernel_c4_long_context.md"),
-    (5, "paged_attention_mfma_kernel (v2 partitions)", 2048):
-        (2_593_796_354, 16_767_328, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
-    (2, "paged_attention_kernel (v2 partitions)", 256):
-        (143_389_751, 2_638_848, "profiles/paged_attention_kernel_c2_llama32_1b_decode.md"),
+    (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 1024):
+        (1_076_129_483, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
+    (4, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 704):
+        (663_477_641, 4_055_024, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
+    (5, "paged_attention_mfma_kernel (v2, merge in-kernel)", 1280):
+        (2_612_887_537, 22_281_024, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
+    (2, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 320):
+        (143_291_927, 2_127_872, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
+    (1, "paged_attention_mfma_kernel (v2, merge in-kernel)", 64):
+        (1_751_257, 88_064, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
 }
 
 
@@ -61,6 +63,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-rows", type=int, default=8, help="rows of the CPU baseline sample")
     ap.add_argument("--access-probe", action="store_true",
                     help="only run the read-only access-pattern probes (ayaka_amd/lib/access_probe)")
+    ap.add_argument("--multi-row", action="store_true",
+                    help="only time the multi-row (prefill / verify) kernel on its workloads, one JSON line each")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (scales profiler byte counters)")
     return ap.parse_args()
@@ -127,6 +131,67 @@ def cpu_baseline(step, cfg, rows: int) -> dict:
     }
 
 
+# Multi-row workloads, all Llama-3-8B-shaped (D 128, bf16, block 16) unless noted:
+# (requests, rows per request, context per request, query heads, key/value heads).
+MULTI_ROW_WORKLOADS = [
+    (4, 512, 4096, 32, 8),    # chunked prefill: 512-row chunks at the end of 4K contexts
+    (1, 2048, 2048, 32, 8),   # one whole 2K prompt
+    (8, 128, 2048, 32, 8),    # small chunks
+    (16, 8, 1024, 32, 8),     # verify windows of 8 draft tokens
+    (4, 512, 4096, 64, 8),    # GQA 8
+]
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def multi_row(args) -> int:
+    """Time the multi-row kernel and, beside it, the same step through the per-row decode kernels."""
+    import torch
+
+    from ayaka_amd.enums import ForwardMode, KVLayoutKind
+    from ayaka_amd.hip import _lib
+    from ayaka_amd.hip import attention as hip_attention
+    from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    for requests, rows, context, heads, kv_heads in MULTI_ROW_WORKLOADS:
+        bs, dim = 16, 128
+        blocks = requests * (context // bs) + 1
+        gen = torch.Generator(device=dev).manual_seed(rows)
+        k = torch.randn((blocks, bs, kv_heads, dim), generator=gen, device=dev).to(torch.bfloat16)
+        v = torch.randn((blocks, bs, kv_heads, dim), generator=gen, device=dev).to(torch.bfloat16)
+        ids = torch.randperm(blocks - 1, generator=gen, device=dev)[: blocks - 1] + 1
+        table = ids.view(requests, context // bs).to(torch.int32)
+        meta = hip_attention.plan(ForwardMode.MIXED, torch.full((requests,), rows, dtype=torch.int32, device=dev),
+                                  torch.full((requests,), context, dtype=torch.int32, device=dev), table, bs)
+        q = torch.randn((requests * rows, heads, dim), generator=gen, device=dev).to(torch.bfloat16)
+        out, per_row = torch.empty_like(q), torch.empty_like(q)
+        buffers = KVBuffers(k, v, KVLayoutKind.NHD, RAW_CODEC)
+        scale = dim ** -0.5
+        kernel = time_calls(lambda: hip_attention.attend_with(q, buffers, meta, out, scale=scale, partitions=None,
+                                                              prefill=True), args.steps, args.warmup)
+        old = time_calls(lambda: hip_attention.attend_with(q, buffers, meta, per_row, scale=scale, partitions=None,
+                                                           prefill=False), 3, 1, repeats=1)
+        torch.cuda.synchronize()
+        # positions each row sees (causal within the chunk), and the flops of q.k and p.v on them
+        visible = requests * sum(context - rows + j + 1 for j in range(rows))
+        flops = 4 * heads * dim * visible
+        kv_bytes = requests * context * kv_heads * dim * 2 * 2
+        us = kernel["median_us"]
+        print(json.dumps({
+            "workload": f"{requests} requests x {rows} rows over {context} positions, Hq {heads}, Hkv {kv_heads}, "
+                        f"D {dim}, bf16, block {bs}",
+            "us_per_call": round(us, 2),
+            "tflops": round(flops / us / 1e6, 1),
+            "mfma_fraction": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
+            "kv_gbs": round(kv_bytes / us / 1e3, 1),
+            "per_row_decode_kernels_us": round(old["median_us"], 1),
+            "speedup": round(old["median_us"] / us, 2),
+            "max_abs_diff_vs_per_row": float((out.float() - per_row.float()).abs().max()),
+        }), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -143,6 +208,8 @@ def main() -> int:
 
     import torch
 
+    if args.multi_row:
+        return multi_row(args)
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
