@@ -77,6 +77,15 @@ __device__ __forceinline__ float group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier that orders LDS only. __syncthreads() also waits for every
+// outstanding global load, which would drain a software pipeline of prefetched
+// chunks at each step; here loads in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // K/V are read exactly once per call: nontemporal loads keep them from displacing
 // reusable lines and stream measurably faster on MI355X than plain loads.
 __device__ __forceinline__ u32x4 stream_load(const uint16_t* p) {

@@ -31,6 +31,8 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPrefillWaves = 4;
+// Chunks of K/V in flight per workgroup (register ring of the cooperative loads).
+constexpr int DEPTH = 4;
 constexpr int kPairsPerWave = 16;
 constexpr int kPairsPerTile = kPrefillWaves * kPairsPerWave;
 
@@ -150,9 +152,11 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
     const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, THREADS);
     const int nch = (s1 - s0 + CH - 1) / CH;
 
-    // Cooperative chunk load: thread tid carries pieces tid, tid + THREADS, ...
-    u32x4 kr[PER_THREAD], vr[PER_THREAD];
-    auto load_chunk = [&](int ci) {
+    // Cooperative chunk loads: thread tid carries pieces tid, tid + THREADS, ... of
+    // every chunk. A ring of DEPTH register slots keeps DEPTH chunks in flight, so the
+    // HBM latency of one chunk overlaps the compute of the DEPTH - 1 before it.
+    u32x4 kr[DEPTH][PER_THREAD], vr[DEPTH][PER_THREAD];
+    auto load_chunk = [&](int ci, u32x4(&kd)[PER_THREAD], u32x4(&vd)[PER_THREAD]) {
 #pragma unroll
       for (int u = 0; u < PER_THREAD; ++u) {
         const int piece = tid + u * THREADS;
@@ -160,19 +164,19 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
           const int t = min(s0 + ci * CH + piece / CPT, s1 - 1);
           const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
           const uint32_t off = blk * block_stride + (uint32_t)(t & bs_mask) * token_stride + (piece % CPT) * 8;
-          kr[u] = stream_load(kbase + off);
-          vr[u] = stream_load(vbase + off);
+          kd[u] = stream_load(kbase + off);
+          vd[u] = stream_load(vbase + off);
         }
       }
     };
-    auto stage_chunk = [&](int buf) {
+    auto stage_chunk = [&](int buf, const u32x4(&kd)[PER_THREAD], const u32x4(&vd)[PER_THREAD]) {
 #pragma unroll
       for (int u = 0; u < PER_THREAD; ++u) {
         const int piece = tid + u * THREADS;
         if (PIECES % THREADS == 0 || piece < PIECES) {
           const int tok = piece / CPT, c = piece % CPT;
-          s_k[buf][key_slot(tok, c)] = kr[u];
-          const uint32_t w[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+          s_k[buf][key_slot(tok, c)] = kd[u];
+          const uint32_t w[4] = {vd[u].x, vd[u].y, vd[u].z, vd[u].w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             s_vt[buf][(c * 8 + 2 * e) * VT_STRIDE + tok] = (uint16_t)(w[e] & 0xffffu);
@@ -182,14 +186,9 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
       }
     };
 
-    load_chunk(0);
-    stage_chunk(0);
-    __syncthreads();
-    for (int ci = 0; ci < nch; ++ci) {
-      const int buf = ci & 1;
-      if (ci + 1 < nch) load_chunk(ci + 1);
+    // Fold chunk ci (staged in LDS buffer buf) into every pair's running state.
+    auto consume = [&](int ci, int buf) {
       const int tb = s0 + ci * CH;
-
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s) acc = mfma_qk32<BF16>(s_k[buf][key_slot(mt, s * 4 + mq)], qb[s], acc);
@@ -197,7 +196,7 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = tb + 4 * mq + i;
-        sc[i] = (t <= my_pos) ? acc[i] * scale_log2 : -INFINITY;
+        sc[i] = (t <= my_pos && t < s1) ? acc[i] * scale_log2 : -INFINITY;
       }
       float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       mx = fmaxf(mx, __shfl_xor(mx, 16));
@@ -224,8 +223,31 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
         o[t] = mfma_pv16<BF16>(va, phi, o[t]);
         o[t] = mfma_pv16<BF16>(va, plo, o[t]);
       }
-      if (ci + 1 < nch) stage_chunk(buf ^ 1);
-      __syncthreads();
+    };
+
+    // Loads past the last chunk re-read it (clamped) rather than being skipped, so
+    // every iteration issues the same loads and the wait before each stage can
+    // leave the younger chunks in flight.
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) load_chunk(min(d, nch - 1), kr[d], vr[d]);
+    stage_chunk(0, kr[0], vr[0]);
+    lds_barrier();
+    // Iteration ci: chunk ci is in LDS buffer ci & 1, chunk ci + 1 in slot (ci + 1) % DEPTH.
+    // Slot ci % DEPTH was staged one iteration ago and takes chunk ci + DEPTH.
+    // The chunk count is rounded up to a multiple of DEPTH, so the unrolled body has
+    // no exit and the waits stay static; the extra chunks re-read the last one and
+    // their positions (>= s1) are masked, so their weights are 0 (the data is real,
+    // so 0 times it is 0).
+    const int nch_padded = (nch + DEPTH - 1) / DEPTH * DEPTH;
+    for (int base = 0; base < nch_padded; base += DEPTH) {
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int ci = base + d;
+        load_chunk(min(ci + DEPTH, nch - 1), kr[d], vr[d]);
+        consume(ci, ci & 1);
+        stage_chunk((ci + 1) & 1, kr[(d + 1) % DEPTH], vr[(d + 1) % DEPTH]);
+        lds_barrier();
+      }
     }
   }
 

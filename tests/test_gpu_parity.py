@@ -209,6 +209,17 @@ def test_block_sizes(block_size: int, qk: str) -> None:
         assert_parity(out, s.expected(np.float64), "bf16", f"bs{block_size}/{prefill}")
 
 
+@pytest.mark.parametrize("block_size", [1, 2])
+def test_table_segments(block_size: int) -> None:
+    # a workgroup stages at most 511 table entries at a time: with blocks of 1-2 positions these
+    # contexts span several staged segments, and the rows end at positions in different ones
+    s = build_scenario([(40, 1300), (1, 1100), (9, 1400)], block_size=block_size, head_dim=128, heads=8,
+                       kv_heads=2, mode="mixed", seed=44)
+    expected = s.expected(np.float64)
+    for prefill in (False, True):
+        assert_parity(run_attention(s, None, None, prefill), expected, "bf16", f"bs{block_size}/{prefill}")
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("head_dim", [64, 128, 256])
 @pytest.mark.parametrize("qk", QK)
