@@ -64,7 +64,7 @@ struct AttnCall {
   const int32_t* request_of_row;
   const int32_t* positions;
   int32_t n_rows, num_heads, num_kv_heads, head_dim, num_blocks, block_size, max_blocks, layout,
-      dtype;
+      dtype, kv_dtype;
   float scale;
 };
 
@@ -75,6 +75,9 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
     return fail(AYK_ERR_UNSUPPORTED, "%s: head_dim %d is not one of 64, 128, 256", op, c.head_dim);
   if (c.dtype != AYK_DTYPE_FP16 && c.dtype != AYK_DTYPE_BF16)
     return fail(AYK_ERR_UNSUPPORTED, "%s: dtype %d is not fp16 (0) or bf16 (1)", op, c.dtype);
+  if (c.kv_dtype != c.dtype && c.kv_dtype != AYK_DTYPE_FP8_E4M3)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: kv_dtype %d is neither the dtype (%d) nor fp8 e4m3 (2)", op, c.kv_dtype,
+                c.dtype);
   if (c.layout != AYK_LAYOUT_NHD && c.layout != AYK_LAYOUT_HND)
     return fail(AYK_ERR_UNSUPPORTED, "%s: layout %d is not NHD (0) or HND (1)", op, c.layout);
   if (c.num_kv_heads <= 0 || c.num_heads <= 0 || c.num_heads % c.num_kv_heads != 0)
@@ -165,8 +168,8 @@ bool merge_in_kernel(int64_t workgroups) {
 constexpr int kMfmaMinHeads = 3;
 
 // The q.k path and workgroup shape for a launch, then the kernel(s).
-int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool bf16, bool split, int32_t flags,
-           void* stream) {
+int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool bf16, bool kv8, bool split,
+           int32_t flags, void* stream) {
   if (flags & ~(AYK_FLAG_QK_DPP | AYK_FLAG_QK_MFMA | AYK_FLAG_PARTIALS_ONLY | AYK_FLAG_SEPARATE_REDUCE |
                 AYK_FLAG_SINGLE_LAUNCH))
     return fail(AYK_ERR_ARGUMENT, "%s: unknown flags 0x%x", op, flags);
@@ -175,10 +178,13 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   if ((flags & AYK_FLAG_SEPARATE_REDUCE) && (flags & AYK_FLAG_SINGLE_LAUNCH))
     return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_SEPARATE_REDUCE and AYK_FLAG_SINGLE_LAUNCH exclude each other",
                 op);
+  if (kv8 && (flags & AYK_FLAG_QK_DPP))
+    return fail(AYK_ERR_UNSUPPORTED, "%s: the DPP kernel reads 16-bit caches only, not fp8", op);
   // Measured on MI355X: from 3 heads per wave the matrix-core kernel (keys staged
   // through LDS) streams faster than the DPP kernel, whose per-token dot2 and
   // butterfly work grows with the group; 1-2 heads stay on the DPP kernel.
-  const bool mfma = (flags & AYK_FLAG_QK_MFMA) || (!(flags & AYK_FLAG_QK_DPP) && gc >= kMfmaMinHeads);
+  // fp8 caches are read by the matrix-core kernel only.
+  const bool mfma = kv8 || (flags & AYK_FLAG_QK_MFMA) || (!(flags & AYK_FLAG_QK_DPP) && gc >= kMfmaMinHeads);
   const int waves = 4;
   const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);
   const int64_t workgroups = items * p.num_virtual_heads;
@@ -190,7 +196,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   if (split && q.arrivals && !(flags & AYK_FLAG_SINGLE_LAUNCH) && !merge_in_kernel(grid))
     q.arrivals = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t err = mfma ? ayk::launch_attention_mfma(q, head_dim, gc, bf16, split, waves, s)
+  hipError_t err = mfma ? ayk::launch_attention_mfma(q, head_dim, gc, bf16, split, kv8, waves, s)
                         : ayk::launch_attention_dpp(q, head_dim, gc, bf16, split, waves, s);
   if (err == hipSuccess && split && !q.arrivals && !(flags & AYK_FLAG_PARTIALS_ONLY))
     err = ayk::launch_partition_reduce(q, head_dim, bf16, s);
@@ -201,7 +207,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
 
 extern "C" {
 
-int ayk_abi_version(void) { return 5; }
+int ayk_abi_version(void) { return 6; }
 
 const char* ayk_last_error(void) { return g_last_error.c_str(); }
 
@@ -228,23 +234,46 @@ int ayk_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_c
                   op);
 }
 
+int ayk_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void* v_cache,
+                               const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t num_blocks, int32_t block_size, int32_t layout, int32_t src_dtype,
+                               void* stream) {
+  const char* op = "ayk_reshape_and_cache_e4m3";
+  if (n_rows < 0) return fail(AYK_ERR_ARGUMENT, "%s: n_rows is negative", op);
+  if (num_kv_heads <= 0 || head_dim <= 0 || num_blocks <= 0 || block_size <= 0)
+    return fail(AYK_ERR_ARGUMENT, "%s: num_kv_heads %d, head_dim %d, num_blocks %d, block_size %d",
+                op, num_kv_heads, head_dim, num_blocks, block_size);
+  if (src_dtype != AYK_DTYPE_FP16 && src_dtype != AYK_DTYPE_BF16)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: src_dtype %d is not fp16 (0) or bf16 (1)", op, src_dtype);
+  if (layout != AYK_LAYOUT_NHD && layout != AYK_LAYOUT_HND)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: layout %d is not NHD (0) or HND (1)", op, layout);
+  if (n_rows == 0) return ok();
+  if (!k || !v || !k_cache || !v_cache || !slot_mapping)
+    return fail(AYK_ERR_ARGUMENT, "%s: a required pointer is null", op);
+  return launched(ayk::launch_reshape_and_cache_e4m3(k, v, k_cache, v_cache, slot_mapping, n_rows, num_kv_heads,
+                                                     head_dim, num_blocks, block_size, layout == AYK_LAYOUT_HND,
+                                                     src_dtype == AYK_DTYPE_BF16, static_cast<hipStream_t>(stream)),
+                  op);
+}
+
 int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,
                            const int32_t* block_table, int64_t table_stride,
                            const int32_t* kv_lengths, const int32_t* request_of_row,
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           float scale, int32_t flags, void* stream) {
+                           int32_t kv_dtype, float scale, int32_t flags, void* stream) {
   const char* op = "ayk_paged_attention_v1";
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
-             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, scale};
+             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, kv_dtype, scale};
   ayk::AttnParams p;
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
   if (rc != AYK_OK) return rc;
   if (n_rows == 0) return ok();
-  return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, false, flags, stream);
+  return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, kv_dtype == AYK_DTYPE_FP8_E4M3, false, flags,
+                stream);
 }
 
 size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads, int32_t head_dim,
@@ -261,13 +290,13 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           float scale, int32_t partition_size, int32_t max_partitions,
+                           int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
                            const int32_t* work_items, int32_t n_work_items, void* workspace,
                            size_t workspace_bytes, uint32_t* arrivals, int32_t flags, void* stream) {
   const char* op = "ayk_paged_attention_v2";
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
-             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, scale};
+             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, kv_dtype, scale};
   ayk::AttnParams p;
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
@@ -298,19 +327,20 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
   // asked, a reduce kernel does (and PARTIALS_ONLY runs neither merge).
   p.arrivals = (flags & (AYK_FLAG_SEPARATE_REDUCE | AYK_FLAG_PARTIALS_ONLY)) ? nullptr : arrivals;
   p.max_len = (int32_t)std::min<int64_t>(p.max_len, (int64_t)partition_size * max_partitions);
-  return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, true, flags, stream);
+  return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, kv_dtype == AYK_DTYPE_FP8_E4M3, true, flags,
+                stream);
 }
 
 int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
                       const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
                       const int32_t* positions, const int32_t* tiles, int32_t n_tiles, int32_t n_rows,
                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
-                      int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype, float scale,
-                      void* stream) {
+                      int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype, int32_t kv_dtype,
+                      float scale, void* stream) {
   const char* op = "ayk_paged_prefill";
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, nullptr,   nullptr,  n_rows,       num_heads,   num_kv_heads,
-             head_dim,  num_blocks, block_size, max_blocks, layout,      dtype,       scale};
+             head_dim,  num_blocks, block_size, max_blocks, layout,      dtype,       kv_dtype, scale};
   ayk::AttnParams p;
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
@@ -326,7 +356,7 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   if (n_tiles == 0 || n_rows == 0) return ok();
   p.positions = positions;
   return launched(ayk::launch_prefill(p, tiles, n_tiles, head_dim, dtype == AYK_DTYPE_BF16,
-                                      static_cast<hipStream_t>(stream)),
+                                      kv_dtype == AYK_DTYPE_FP8_E4M3, static_cast<hipStream_t>(stream)),
                   op);
 }
 

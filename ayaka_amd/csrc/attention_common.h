@@ -14,6 +14,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 // Block-table entries staged in LDS per segment of a row's context.
@@ -90,6 +92,43 @@ __device__ __forceinline__ void lds_barrier() {
 // reusable lines and stream measurably faster on MI355X than plain loads.
 __device__ __forceinline__ u32x4 stream_load(const uint16_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// ---------------------------------------------------------------------------
+// fp8 KV caches (codec "fp8_e4m3": OCP e4m3, the float8_e4m3fn format).
+//
+// Two codes of a word (its low or high half) to a packed pair of the compute
+// type. v_cvt_pk_f32_fp8 decodes them to fp32; every e4m3 value (|x| <= 448,
+// at most 4 significant bits, down to 2^-9) is exactly a bf16 and an fp16
+// value, so taking the top half of the fp32 (bf16) or converting with either
+// rounding (fp16) loses nothing. The NaN code decodes to NaN.
+template <bool BF16, bool HIGH>
+__device__ __forceinline__ uint32_t e4m3_pair(uint32_t word) {
+  const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, HIGH);
+  if constexpr (BF16) return __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
+  else return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f[0], f[1]));
+}
+
+// Address of element `elem` of a cache: 2-byte elements, or 1-byte fp8 codes.
+template <bool KV8>
+__device__ __forceinline__ const uint16_t* kv_at(const uint16_t* base, int64_t elem) {
+  if constexpr (KV8) return reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(base) + elem);
+  return base + elem;
+}
+
+// The 8 elements at element offset `off` from `base` (see kv_at), as 8 packed
+// compute-type values: one 16-byte load, or one 8-byte load of fp8 codes decoded
+// in registers. Both nontemporal: the cache is streamed once per call.
+template <bool KV8, bool BF16>
+__device__ __forceinline__ u32x4 load_kv(const uint16_t* base, uint32_t off) {
+  if constexpr (KV8) {
+    const u32x2 w =
+        __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(base) + off));
+    return u32x4{e4m3_pair<BF16, false>(w.x), e4m3_pair<BF16, true>(w.x), e4m3_pair<BF16, false>(w.y),
+                 e4m3_pair<BF16, true>(w.y)};
+  } else {
+    return stream_load(base + off);
+  }
 }
 
 // The (row, head group, partition) a workgroup serves. The grid is flat and

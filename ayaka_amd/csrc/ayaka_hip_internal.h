@@ -46,11 +46,12 @@ struct AttnParams {
 // The per-(row, head[, partition]) attention kernels; `waves` is the workgroup size in waves.
 hipError_t launch_attention_dpp(const AttnParams& p, int head_dim, int heads_per_chunk, bool bf16,
                                 bool split, int waves, hipStream_t stream);
+// kv8: the caches hold fp8 e4m3 codes (1 byte per element), decoded on load.
 hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int heads_per_chunk, bool bf16,
-                                 bool split, int waves, hipStream_t stream);
+                                 bool split, bool kv8, int waves, hipStream_t stream);
 // Multi-row attention: one workgroup per (tile of rows of one request, key/value head).
 hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16,
-                          hipStream_t stream);
+                          bool kv8, hipStream_t stream);
 // The v2 log-sum-exp merge of the partitions of every (row, head).
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);
 
@@ -58,6 +59,12 @@ hipError_t launch_reshape_and_cache(const void* k, const void* v, void* k_cache,
                                     const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,
                                     int32_t head_dim, int32_t num_blocks, int32_t block_size,
                                     bool hnd, int32_t elem_bytes, hipStream_t stream);
+
+// KV write into fp8 e4m3 caches from fp16 (bf16 = false) or bf16 rows.
+hipError_t launch_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void* v_cache,
+                                         const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t num_blocks, int32_t block_size, bool hnd,
+                                         bool bf16, hipStream_t stream);
 
 // mode: 0 = gather (dst index i), 1 = copy (dst ids), 2 = zero (no source)
 hipError_t launch_block_op(int mode, const void* src_k, const void* src_v, void* dst_k, void* dst_v,

@@ -30,6 +30,116 @@ struct VecOf<4> { typedef uint32_t T; };
 template <>
 struct VecOf<2> { typedef uint16_t T; };
 
+template <>
+struct VecOf<1> { typedef uint8_t T; };
+
+// fp32 to an OCP fp8 e4m3 code (the float8_e4m3fn format: sign, 4 exponent bits
+// with bias 7, 3 mantissa bits, no infinity, NaN = 0x7F/0xFF), rounding to
+// nearest even. A magnitude that rounds above the largest finite value, 448,
+// becomes NaN, as does NaN: the format has no saturation here. Below 2^-6 the
+// codes are the subnormals m * 2^-9.
+__device__ __forceinline__ uint32_t e4m3_code(float f) {
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t mag = u & 0x7fffffffu;
+  const float a = __uint_as_float(mag);
+  uint32_t code;
+  if (a < 0.015625f) {
+    code = (uint32_t)__builtin_rintf(a * 512.0f);  // ties to even; 8 is the smallest normal, 2^-6
+  } else {
+    // keep 3 mantissa bits, ties to even, and move the exponent from bias 127 to bias 7
+    code = ((mag + 0x7ffffu + ((mag >> 20) & 1u)) >> 20) - (120u << 3);
+    if (code > 0x7eu) code = 0x7fu;  // above 448, infinity or NaN
+  }
+  return code | sign;
+}
+
+template <bool BF16>
+__device__ __forceinline__ float widen(uint32_t h) {
+  if constexpr (BF16) return __uint_as_float(h << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// KV write into fp8 caches: as reshape_and_cache, but each lane reads EPL
+// consecutive 16-bit elements of a row and writes their EPL codes.
+template <int EPL, bool BF16>
+__global__ __launch_bounds__(256) void reshape_and_cache_e4m3_kernel(
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint8_t* __restrict__ k_cache,
+    uint8_t* __restrict__ v_cache, const int64_t* __restrict__ slot_mapping, int64_t total_groups,
+    int32_t groups_per_row, int32_t groups_per_head, int64_t num_slots, int32_t block_size, int32_t num_kv_heads,
+    int32_t head_dim, int32_t hnd) {
+  typedef typename VecOf<2 * EPL>::T In;
+  typedef typename VecOf<EPL>::T Out;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total_groups) return;
+  const int64_t row = idx / groups_per_row;
+  const int32_t gi = (int32_t)(idx - row * groups_per_row);
+  const int64_t slot = slot_mapping[row];
+  if (slot < 0 || slot >= num_slots) return;  // outside the pool: dropped, never written
+  const int64_t row_elems = (int64_t)groups_per_row * EPL;
+  const int64_t src = row * row_elems + (int64_t)gi * EPL;
+  int64_t dst;
+  if (!hnd) {
+    dst = slot * row_elems + (int64_t)gi * EPL;
+  } else {
+    const int64_t blk = slot / block_size;
+    const int64_t off = slot - blk * block_size;
+    const int32_t h = gi / groups_per_head;
+    const int32_t w = gi - h * groups_per_head;
+    dst = ((blk * num_kv_heads + h) * block_size + off) * head_dim + (int64_t)w * EPL;
+  }
+  const uint16_t* srcs[2] = {k + src, v + src};
+  uint8_t* dsts[2] = {k_cache + dst, v_cache + dst};
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const In in = *reinterpret_cast<const In*>(srcs[t]);
+    uint16_t h[EPL];
+    __builtin_memcpy(h, &in, sizeof(In));
+    uint8_t c[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) c[e] = (uint8_t)e4m3_code(widen<BF16>(h[e]));
+    Out out;
+    __builtin_memcpy(&out, c, sizeof(Out));
+    *reinterpret_cast<Out*>(dsts[t]) = out;
+  }
+}
+
+hipError_t launch_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void* v_cache,
+                                         const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t num_blocks, int32_t block_size, bool hnd,
+                                         bool bf16, hipStream_t stream) {
+  const int epl = (head_dim % 8 == 0) ? 8 : (head_dim % 4 == 0) ? 4 : (head_dim % 2 == 0) ? 2 : 1;
+  const int32_t groups_per_head = head_dim / epl;
+  const int32_t groups_per_row = groups_per_head * num_kv_heads;
+  const int64_t total = n_rows * groups_per_row;
+  if (total == 0) return hipSuccess;
+  const int64_t num_slots = (int64_t)num_blocks * block_size;
+  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  const uint16_t* kb = static_cast<const uint16_t*>(k);
+  const uint16_t* vb = static_cast<const uint16_t*>(v);
+  uint8_t* kc = static_cast<uint8_t*>(k_cache);
+  uint8_t* vc = static_cast<uint8_t*>(v_cache);
+#define AYK_E4M3_STORE(E)                                                                               \
+  do {                                                                                                  \
+    if (bf16)                                                                                           \
+      hipLaunchKernelGGL((reshape_and_cache_e4m3_kernel<E, true>), grid, block, 0, stream, kb, vb, kc, vc, \
+                         slot_mapping, total, groups_per_row, groups_per_head, num_slots, block_size,      \
+                         num_kv_heads, head_dim, (int32_t)hnd);                                         \
+    else                                                                                                \
+      hipLaunchKernelGGL((reshape_and_cache_e4m3_kernel<E, false>), grid, block, 0, stream, kb, vb, kc, vc, \
+                         slot_mapping, total, groups_per_row, groups_per_head, num_slots, block_size,      \
+                         num_kv_heads, head_dim, (int32_t)hnd);                                         \
+  } while (0)
+  switch (epl) {
+    case 8: AYK_E4M3_STORE(8); break;
+    case 4: AYK_E4M3_STORE(4); break;
+    case 2: AYK_E4M3_STORE(2); break;
+    default: AYK_E4M3_STORE(1); break;
+  }
+#undef AYK_E4M3_STORE
+  return hipGetLastError();
+}
+
 template <int VEC>
 __global__ __launch_bounds__(256) void reshape_and_cache_kernel(
     const uint8_t* __restrict__ k, const uint8_t* __restrict__ v, uint8_t* __restrict__ k_cache,

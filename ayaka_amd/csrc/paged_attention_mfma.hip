@@ -47,7 +47,7 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int D, int GC, bool BF16, bool SPLIT>
+template <int D, int GC, bool BF16, bool SPLIT, bool KV8>
 __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel(const AttnParams p) {
   using E = Elem<BF16>;
   constexpr int CH = 16;            // tokens per chunk: the MFMA tile height
@@ -123,8 +123,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   const uint32_t block_stride = (uint32_t)p.block_stride;
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
-  const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + c * 8;
-  const uint16_t* vbase = p.v_cache + (int64_t)kvh * p.head_stride + c * 8;
+  const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride + c * 8);
+  const uint16_t* vbase = kv_at<KV8>(p.v_cache, (int64_t)kvh * p.head_stride + c * 8);
 
   for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
     const int s1 = min(t_end, s0 + seg_len);
@@ -217,23 +217,23 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     int ci = 0;
     offsets(0, offA);
 #pragma unroll
-    for (int j = 0; j < NL; ++j) kA[j] = stream_load(kbase + offA[j]);
+    for (int j = 0; j < NL; ++j) kA[j] = load_kv<KV8, BF16>(kbase, offA[j]);
     while (ci < nch) {
 #pragma unroll
-      for (int j = 0; j < NL; ++j) vc[j] = stream_load(vbase + offA[j]);
+      for (int j = 0; j < NL; ++j) vc[j] = load_kv<KV8, BF16>(vbase, offA[j]);
       if (ci + 1 < nch) {
         offsets(ci + 1, offB);
 #pragma unroll
-        for (int j = 0; j < NL; ++j) kB[j] = stream_load(kbase + offB[j]);
+        for (int j = 0; j < NL; ++j) kB[j] = load_kv<KV8, BF16>(kbase, offB[j]);
       }
       consume(ci, 0, kA, vc);
       if (++ci >= nch) break;
 #pragma unroll
-      for (int j = 0; j < NL; ++j) vc[j] = stream_load(vbase + offB[j]);
+      for (int j = 0; j < NL; ++j) vc[j] = load_kv<KV8, BF16>(vbase, offB[j]);
       if (ci + 1 < nch) {
         offsets(ci + 1, offA);
 #pragma unroll
-        for (int j = 0; j < NL; ++j) kA[j] = stream_load(kbase + offA[j]);
+        for (int j = 0; j < NL; ++j) kA[j] = load_kv<KV8, BF16>(kbase, offA[j]);
       }
       consume(ci, 1, kB, vc);
       ++ci;
@@ -266,44 +266,50 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   }
 }
 
-template <int D, int GC, bool BF16>
-static hipError_t launch_mfma_typed(const AttnParams& p, bool split, int waves, hipStream_t stream) {
-  (void)waves;  // one wave per virtual head, up to kMaxWaves per workgroup
+template <int D, int GC, bool BF16, bool KV8>
+static hipError_t launch_mfma_typed(const AttnParams& p, bool split, hipStream_t stream) {
+  // one wave per virtual head, up to kMaxWaves per workgroup
   const int per_wg = p.num_virtual_heads < kMaxWaves ? p.num_virtual_heads : kMaxWaves;
   const int groups = (p.num_virtual_heads + per_wg - 1) / per_wg;
   const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);
   const dim3 grid((unsigned)(items * groups)), block(per_wg * kWave);
   if (split)
-    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, BF16, true>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, BF16, true, KV8>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, BF16, false>), grid, block, 0, stream, p);
+    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, GC, BF16, false, KV8>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 
-template <int D, bool BF16>
-static hipError_t launch_mfma_gc(const AttnParams& p, int gc, bool split, int waves, hipStream_t stream) {
+template <int D, bool BF16, bool KV8>
+static hipError_t launch_mfma_gc(const AttnParams& p, int gc, bool split, hipStream_t stream) {
   switch (gc) {
-    case 1: return launch_mfma_typed<D, 1, BF16>(p, split, waves, stream);
-    case 2: return launch_mfma_typed<D, 2, BF16>(p, split, waves, stream);
-    case 3: return launch_mfma_typed<D, 3, BF16>(p, split, waves, stream);
-    case 4: return launch_mfma_typed<D, 4, BF16>(p, split, waves, stream);
-    case 5: return launch_mfma_typed<D, 5, BF16>(p, split, waves, stream);
-    case 6: return launch_mfma_typed<D, 6, BF16>(p, split, waves, stream);
-    case 7: return launch_mfma_typed<D, 7, BF16>(p, split, waves, stream);
-    case 8: return launch_mfma_typed<D, 8, BF16>(p, split, waves, stream);
+    case 1: return launch_mfma_typed<D, 1, BF16, KV8>(p, split, stream);
+    case 2: return launch_mfma_typed<D, 2, BF16, KV8>(p, split, stream);
+    case 3: return launch_mfma_typed<D, 3, BF16, KV8>(p, split, stream);
+    case 4: return launch_mfma_typed<D, 4, BF16, KV8>(p, split, stream);
+    case 5: return launch_mfma_typed<D, 5, BF16, KV8>(p, split, stream);
+    case 6: return launch_mfma_typed<D, 6, BF16, KV8>(p, split, stream);
+    case 7: return launch_mfma_typed<D, 7, BF16, KV8>(p, split, stream);
+    case 8: return launch_mfma_typed<D, 8, BF16, KV8>(p, split, stream);
     default: return hipErrorInvalidValue;
   }
 }
 
-hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int gc, bool bf16, bool split, int waves,
-                                 hipStream_t stream) {
+template <int D>
+static hipError_t launch_mfma_d(const AttnParams& p, int gc, bool bf16, bool split, bool kv8, hipStream_t stream) {
+  if (kv8) return bf16 ? launch_mfma_gc<D, true, true>(p, gc, split, stream)
+                       : launch_mfma_gc<D, false, true>(p, gc, split, stream);
+  return bf16 ? launch_mfma_gc<D, true, false>(p, gc, split, stream)
+              : launch_mfma_gc<D, false, false>(p, gc, split, stream);
+}
+
+hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int gc, bool bf16, bool split, bool kv8,
+                                 int waves, hipStream_t stream) {
+  (void)waves;
   switch (head_dim) {
-    case 64: return bf16 ? launch_mfma_gc<64, true>(p, gc, split, waves, stream)
-                         : launch_mfma_gc<64, false>(p, gc, split, waves, stream);
-    case 128: return bf16 ? launch_mfma_gc<128, true>(p, gc, split, waves, stream)
-                          : launch_mfma_gc<128, false>(p, gc, split, waves, stream);
-    case 256: return bf16 ? launch_mfma_gc<256, true>(p, gc, split, waves, stream)
-                          : launch_mfma_gc<256, false>(p, gc, split, waves, stream);
+    case 64: return launch_mfma_d<64>(p, gc, bf16, split, kv8, stream);
+    case 128: return launch_mfma_d<128>(p, gc, bf16, split, kv8, stream);
+    case 256: return launch_mfma_d<256>(p, gc, bf16, split, kv8, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -71,7 +71,7 @@ __device__ __forceinline__ void split_weights(const float (&w)[4], u32x2& hi, u3
   lo = u32x2{r[0] | (r[1] << 16), r[2] | (r[3] << 16)};
 }
 
-template <int D, bool BF16>
+template <int D, bool BF16, bool KV8>
 __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(const AttnParams p, const int32_t* tiles) {
   using E = Elem<BF16>;
   constexpr int THREADS = kPrefillWaves * kWave;
@@ -141,8 +141,8 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
   const uint32_t block_stride = (uint32_t)p.block_stride;
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
-  const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride;
-  const uint16_t* vbase = p.v_cache + (int64_t)kvh * p.head_stride;
+  const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride);
+  const uint16_t* vbase = kv_at<KV8>(p.v_cache, (int64_t)kvh * p.head_stride);
   auto key_slot = [](int token, int piece) { return token * CPT + (piece ^ (token & (CPT - 1))); };
   constexpr int PER_THREAD = (PIECES + THREADS - 1) / THREADS;
 
@@ -164,8 +164,8 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
           const int t = min(s0 + ci * CH + piece / CPT, s1 - 1);
           const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
           const uint32_t off = blk * block_stride + (uint32_t)(t & bs_mask) * token_stride + (piece % CPT) * 8;
-          kd[u] = stream_load(kbase + off);
-          vd[u] = stream_load(vbase + off);
+          kd[u] = load_kv<KV8, BF16>(kbase, off);
+          vd[u] = load_kv<KV8, BF16>(vbase, off);
         }
       }
     };
@@ -266,26 +266,29 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
   }
 }
 
-hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16,
-                          hipStream_t stream) {
-  const dim3 grid((unsigned)((int64_t)n_tiles * (p.num_heads / p.group))), block(kPrefillWaves * kWave);
-  switch (head_dim) {
-    case 64:
-      if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<64, true>), grid, block, 0, stream, p, tiles);
-      else hipLaunchKernelGGL((paged_prefill_kernel<64, false>), grid, block, 0, stream, p, tiles);
-      break;
-    case 128:
-      if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<128, true>), grid, block, 0, stream, p, tiles);
-      else hipLaunchKernelGGL((paged_prefill_kernel<128, false>), grid, block, 0, stream, p, tiles);
-      break;
-    case 256:
-      if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<256, true>), grid, block, 0, stream, p, tiles);
-      else hipLaunchKernelGGL((paged_prefill_kernel<256, false>), grid, block, 0, stream, p, tiles);
-      break;
-    default:
-      return hipErrorInvalidValue;
+template <int D>
+static hipError_t launch_prefill_d(const AttnParams& p, const int32_t* tiles, dim3 grid, bool bf16, bool kv8,
+                                   hipStream_t stream) {
+  const dim3 block(kPrefillWaves * kWave);
+  if (kv8) {
+    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, true>), grid, block, 0, stream, p, tiles);
+    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, true>), grid, block, 0, stream, p, tiles);
+  } else {
+    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, false>), grid, block, 0, stream, p, tiles);
+    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, false>), grid, block, 0, stream, p, tiles);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16, bool kv8,
+                          hipStream_t stream) {
+  const dim3 grid((unsigned)((int64_t)n_tiles * (p.num_heads / p.group)));
+  switch (head_dim) {
+    case 64: return launch_prefill_d<64>(p, tiles, grid, bf16, kv8, stream);
+    case 128: return launch_prefill_d<128>(p, tiles, grid, bf16, kv8, stream);
+    case 256: return launch_prefill_d<256>(p, tiles, grid, bf16, kv8, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace ayk

@@ -3,7 +3,8 @@
 The messages follow the reference's (``python/ayaka/ops/backends/torch/_checks.py:21-59``,
 ``kvcache.py:39-62``) so that callers and tests read the same refusals. The
 hip backend computes in fp16 and bf16 only, on HIP devices, for head widths of
-64, 128 and 256 and power-of-two block sizes.
+64, 128 and 256 and power-of-two block sizes; it stores the ``"raw"`` codec
+(fp16/bf16 caches) and ``"fp8_e4m3"`` (``float8_e4m3fn`` caches).
 """
 
 from __future__ import annotations
@@ -14,11 +15,12 @@ import torch
 
 from ayaka_amd.enums import KVLayoutKind
 from ayaka_amd.errors import BackendError
-from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+from ayaka_amd.kvcache import FP8_E4M3_CODEC, RAW_CODEC, KVBuffers
 
 __all__ = [
     "HEAD_DIMS",
     "capturing",
+    "compute_dtype",
     "dtype_name",
     "require_buffers",
     "require_device",
@@ -35,7 +37,10 @@ _NAMES = {
     torch.float64: "float64",
     torch.int32: "int32",
     torch.int64: "int64",
+    torch.float8_e4m3fn: "float8_e4m3fn",
 }
+# The cache element type of each codec this backend stores.
+_CODEC_DTYPES = {RAW_CODEC: _DTYPES, FP8_E4M3_CODEC: (torch.float8_e4m3fn,)}
 
 
 def dtype_name(dtype: torch.dtype) -> str:
@@ -77,6 +82,20 @@ def require_device(op: str, name: str, tensor: torch.Tensor, device: torch.devic
         )
 
 
+def compute_dtype(op: str, name: str, tensor: torch.Tensor, buffers: KVBuffers) -> torch.dtype:
+    """The compute dtype of a call: the cache's for ``"raw"``, ``tensor``'s (fp16 or bf16)
+    for a quantised codec, whose cache does not say."""
+    if buffers.codec == RAW_CODEC:
+        return buffers.k.dtype
+    if tensor.dtype not in _DTYPES:
+        raise BackendError(
+            f"{op}: {name} is {dtype_name(tensor.dtype)}; over a {buffers.codec!r} cache the hip "
+            "backend computes in float16, bfloat16",
+            context={"op": op, "argument": name},
+        )
+    return tensor.dtype
+
+
 def require_buffers(op: str, buffers: KVBuffers) -> None:
     """Refuse a cache these kernels cannot read: layout, codec, shape, dtype, device, strides."""
     if buffers.layout not in (KVLayoutKind.NHD, KVLayoutKind.HND):
@@ -84,16 +103,18 @@ def require_buffers(op: str, buffers: KVBuffers) -> None:
             f"{op}: the hip backend serves the NHD and HND layouts, not {buffers.layout}",
             context={"op": op, "argument": "buffers"},
         )
-    if buffers.codec != RAW_CODEC:
+    if buffers.codec not in _CODEC_DTYPES:
         raise BackendError(
-            f"{op}: the hip backend stores the {RAW_CODEC!r} codec, not {buffers.codec!r}",
+            f"{op}: the hip backend stores the {RAW_CODEC!r} and {FP8_E4M3_CODEC!r} codecs, "
+            f"not {buffers.codec!r}",
             context={"op": op, "argument": "buffers"},
         )
     k = buffers.k
-    if k.dtype not in _DTYPES:
+    if k.dtype not in _CODEC_DTYPES[buffers.codec]:
+        allowed = ", ".join(dtype_name(d) for d in _CODEC_DTYPES[buffers.codec])
+        what = "computes in" if buffers.codec == RAW_CODEC else f"stores the {buffers.codec!r} codec as"
         raise BackendError(
-            f"{op}: buffers.k is {dtype_name(k.dtype)}; the hip backend computes in "
-            "float16, bfloat16",
+            f"{op}: buffers.k is {dtype_name(k.dtype)}; the hip backend {what} {allowed}",
             context={"op": op, "argument": "buffers.k"},
         )
     if k.ndim != 4:

@@ -38,6 +38,7 @@ from ayaka_amd.attention import AttentionMetadata
 from ayaka_amd.errors import BackendError
 from ayaka_amd.hip import _lib
 from ayaka_amd.hip._checks import (
+    compute_dtype,
     HEAD_DIMS,
     capturing,
     require_buffers,
@@ -45,7 +46,7 @@ from ayaka_amd.hip._checks import (
     require_index_tensor,
     require_like,
 )
-from ayaka_amd.kvcache import KVBuffers
+from ayaka_amd.kvcache import FP8_E4M3_CODEC, KVBuffers
 
 __all__ = [
     "PARTITION_SIZE",
@@ -81,6 +82,12 @@ COMPUTE_UNITS = 256
 
 _LAYOUT_CODES = {KVLayoutKind.NHD: 0, KVLayoutKind.HND: 1}
 _DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+_KV_FP8_E4M3 = 2
+
+
+def _kv_code(buffers: KVBuffers, dtype: torch.dtype) -> int:
+    """The C ABI's cache element type: the compute dtype, or fp8 e4m3 codes."""
+    return _KV_FP8_E4M3 if buffers.codec == FP8_E4M3_CODEC else _DTYPE_CODES[dtype]
 _QK_FLAGS = {None: 0, "dpp": 1, "mfma": 2}
 #: v2 flag: launch the partition kernel only (benchmarks time the dominant kernel with it).
 PARTIALS_ONLY = 4
@@ -513,7 +520,7 @@ def attend_with(
         )
     heads = q.shape[1] if q.ndim == 3 else 0
     n_rows = meta.request_of_row.shape[0]
-    require_like(op, "q", q, (n_rows, heads, buffers.head_dim), buffers.k.dtype)
+    require_like(op, "q", q, (n_rows, heads, buffers.head_dim), compute_dtype(op, "q", q, buffers))
     require_like(op, "out", out, q.shape, q.dtype)
     kv_heads = buffers.num_kv_heads
     if heads == 0 or heads % kv_heads:
@@ -576,7 +583,8 @@ def attend_with(
                 out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),
                 table.stride(0), meta.kv_lengths.data_ptr(), meta.positions.data_ptr(), tiles.data_ptr(),
                 tiles.numel() // 3, n_rows, heads, kv_heads, buffers.head_dim, buffers.num_blocks, block_size,
-                table.shape[1], _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype], float(scale),
+                table.shape[1], _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype],
+                _kv_code(buffers, q.dtype), float(scale),
                 stream,
             ),
         )
@@ -604,6 +612,7 @@ def attend_with(
         table.shape[1],
         _LAYOUT_CODES[KVLayoutKind(buffers.layout)],
         _DTYPE_CODES[q.dtype],
+        _kv_code(buffers, q.dtype),
         float(scale),
     )
     if partitions is None:

@@ -2,7 +2,8 @@
 
 ``store`` is the KV write (``ayk_reshape_and_cache``): row ``i`` of ``k``/``v``
 lands bit for bit in slot ``meta.slot_mapping[i]`` (reference
-``python/ayaka/ops/backends/torch/kvcache.py:65-80``). ``gather``,
+``python/ayaka/ops/backends/torch/kvcache.py:65-80``); into a ``"fp8_e4m3"``
+cache it lands encoded (``ayk_reshape_and_cache_e4m3``). ``gather``,
 ``copy_blocks`` and ``zero_blocks`` move whole blocks (same file, ``:83-115``).
 Both layouts are served; NHD is preferred, as the reference's ``layout()``
 returns (``:30-31``).
@@ -16,12 +17,19 @@ from ayaka_amd.attention import AttentionMetadata
 from ayaka_amd.enums import KVLayoutKind
 from ayaka_amd.errors import BackendError
 from ayaka_amd.hip import _lib
-from ayaka_amd.hip._checks import require_buffers, require_device, require_index_tensor, require_like
-from ayaka_amd.kvcache import KVBuffers
+from ayaka_amd.hip._checks import (
+    compute_dtype,
+    require_buffers,
+    require_device,
+    require_index_tensor,
+    require_like,
+)
+from ayaka_amd.kvcache import FP8_E4M3_CODEC, KVBuffers
 
 __all__ = ["copy_blocks", "gather", "layout", "store", "zero_blocks"]
 
 _LAYOUT_CODES = {KVLayoutKind.NHD: 0, KVLayoutKind.HND: 1}
+_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
 
 def layout() -> KVLayoutKind:
@@ -54,8 +62,9 @@ def store(k: torch.Tensor, v: torch.Tensor, buffers: KVBuffers, meta: AttentionM
         )
     rows = meta.slot_mapping.shape[0]
     shape = (rows, buffers.num_kv_heads, buffers.head_dim)
-    require_like(op, "k", k, shape, buffers.k.dtype)
-    require_like(op, "v", v, shape, buffers.k.dtype)
+    dtype = compute_dtype(op, "k", k, buffers)
+    require_like(op, "k", k, shape, dtype)
+    require_like(op, "v", v, shape, dtype)
     device = buffers.k.device
     for name, tensor in (("k", k), ("v", v), ("meta.slot_mapping", meta.slot_mapping)):
         require_device(op, name, tensor, device)
@@ -63,6 +72,16 @@ def store(k: torch.Tensor, v: torch.Tensor, buffers: KVBuffers, meta: AttentionM
     if slots.dtype != torch.int64 or not slots.is_contiguous():
         raise BackendError(f"{op}: meta.slot_mapping must be a contiguous int64 tensor")
     if rows == 0:
+        return
+    if buffers.codec == FP8_E4M3_CODEC:
+        _lib.check(
+            op,
+            _lib.lib().ayk_reshape_and_cache_e4m3(
+                k.data_ptr(), v.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), slots.data_ptr(), rows,
+                buffers.num_kv_heads, buffers.head_dim, buffers.num_blocks, buffers.block_size,
+                _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[dtype], _stream(device),
+            ),
+        )
         return
     _lib.check(
         op,

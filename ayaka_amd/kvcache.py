@@ -10,7 +10,11 @@ Restates the reference's layout definition (``python/ayaka/ops/kvcache.py:1-38``
   ``ceil(length / block_size)`` entries of its table.
 * Block 0 is the padding block: never assigned to a request; padding rows are
   stored into slot 0 and its contents are never read as context.
-* ``codec`` ``"raw"`` (the only one): values are stored in the compute dtype.
+* ``codec`` names how values are stored. The reference defines ``"raw"`` only
+  (values in the compute dtype). This package adds ``"fp8_e4m3"``: the
+  tensors are ``torch.float8_e4m3fn``, one byte per element, holding what
+  torch's cast to that type gives (round to nearest even; a magnitude that
+  rounds above 448 becomes NaN); readers decode it exactly to the compute dtype.
 
 Importing this module does not import torch.
 """
@@ -26,9 +30,11 @@ if TYPE_CHECKING:
 
     from ayaka_amd.attention import AttentionMetadata
 
-__all__ = ["RAW_CODEC", "KVBuffers", "KVCacheOps"]
+__all__ = ["FP8_E4M3_CODEC", "RAW_CODEC", "KVBuffers", "KVCacheOps"]
 
 RAW_CODEC = "raw"
+#: Keys and values as OCP fp8 e4m3 codes (``torch.float8_e4m3fn``), no scale.
+FP8_E4M3_CODEC = "fp8_e4m3"
 
 
 class _KVBuffers(NamedTuple):

@@ -105,10 +105,12 @@ class Step:
     q: torch.Tensor  # [B, heads, head_dim], the decode queries
 
 
-def build(cfg: Config, device: torch.device | str = "cpu", *, poison: bool = True, layout: str = "nhd") -> Step:
+def build(cfg: Config, device: torch.device | str = "cpu", *, poison: bool = True, layout: str = "nhd",
+          codec: str = "raw") -> Step:
     """Fill a pool for ``cfg`` on ``device``. The newest ``new_tokens`` positions of every
     sequence are left unwritten (NaN): the step's KV write fills them. ``layout`` "hnd"
-    returns the same values in HND caches (``[num_blocks, kv_heads, block_size, head_dim]``)."""
+    returns the same values in HND caches (``[num_blocks, kv_heads, block_size, head_dim]``);
+    ``codec`` "fp8_e4m3" returns them cast to ``torch.float8_e4m3fn``."""
     device = torch.device(device)
     gen = torch.Generator(device=device).manual_seed(1000 + cfg.index)
     host = np.random.default_rng(2000 + cfg.index)
@@ -156,6 +158,10 @@ def build(cfg: Config, device: torch.device | str = "cpu", *, poison: bool = Tru
     if layout == "hnd":
         k_cache = k_cache.permute(0, 2, 1, 3).contiguous()
         v_cache = v_cache.permute(0, 2, 1, 3).contiguous()
+    if codec == "fp8_e4m3":
+        k_cache, v_cache = k_cache.to(torch.float8_e4m3fn), v_cache.to(torch.float8_e4m3fn)
+    elif codec != "raw":
+        raise ValueError(f"unknown codec {codec!r}")
     return Step(
         config=cfg,
         k_cache=k_cache,
@@ -169,20 +175,22 @@ def build(cfg: Config, device: torch.device | str = "cpu", *, poison: bool = Tru
     )
 
 
-def algorithmic_bytes(cfg: Config) -> int:
-    """Bytes one decode-attention call must move: K and V of every context position, q read,
-    out written, the used table entries and the lengths (v2 scratch not counted)."""
+def algorithmic_bytes(cfg: Config, kv_bytes: int = 2) -> int:
+    """Bytes one decode-attention call must move: K and V of every context position (``kv_bytes``
+    per element: 2, or 1 for fp8 caches), q read, out written, the used table entries and the
+    lengths (v2 scratch not counted)."""
     s = 2
-    kv = sum(cfg.lengths) * cfg.kv_heads * cfg.head_dim * 2 * s
+    kv = sum(cfg.lengths) * cfg.kv_heads * cfg.head_dim * 2 * kv_bytes
     qo = 2 * cfg.batch * cfg.heads * cfg.head_dim * s
     table = 4 * sum(-(-n // cfg.block_size) for n in cfg.lengths)
     return kv + qo + table + 4 * cfg.batch
 
 
-def store_bytes(cfg: Config) -> int:
-    """Bytes of the step's KV write: read and write k and v rows, read the slots."""
+def store_bytes(cfg: Config, kv_bytes: int = 2) -> int:
+    """Bytes of the step's KV write: read k and v rows (2 bytes per element), write them
+    (``kv_bytes`` per element), read the slots."""
     rows = sum(min(cfg.new_tokens, n) for n in cfg.lengths)
-    return 4 * rows * cfg.kv_heads * cfg.head_dim * 2 + 8 * rows
+    return 2 * rows * cfg.kv_heads * cfg.head_dim * (2 + kv_bytes) + 8 * rows
 
 
 def sample_rows(step: Step, rows: list[int]) -> dict[str, np.ndarray]:

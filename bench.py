@@ -57,6 +57,8 @@ def parse() -> argparse.Namespace:
                     help="time only this launch (for profiler runs)")
     ap.add_argument("--layout", choices=["nhd", "hnd"], default=None,
                     help="cache layout (default: the one the hip backend asks the pool for)")
+    ap.add_argument("--codec", choices=["raw", "fp8_e4m3"], default="raw",
+                    help="KV-cache codec: 16-bit values, or fp8 e4m3 codes decoded in the kernel")
     ap.add_argument("--qk", choices=["dpp", "mfma"], default=None,
                     help="force the q.k implementation (default: the library's choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -98,7 +100,7 @@ def time_calls(fn, steps: int, warmup: int, repeats: int = 5) -> dict:
             "wall_ms_per_step": statistics.median(walls) * 1000.0 / steps}
 
 
-def cpu_baseline(step, cfg, rows: int) -> dict:
+def cpu_baseline(step, cfg, rows: int, kv_bytes: int = 2) -> dict:
     """The oracle's restatement of the reference CPU decode, timed on a sample of the batch."""
     import numpy as np
 
@@ -121,7 +123,7 @@ def cpu_baseline(step, cfg, rows: int) -> dict:
         runs.append(time.perf_counter() - t0)
     seconds = statistics.median(runs[1:]) * cfg.batch / rows  # scaled to the whole batch
     return {
-        "value": workloads.algorithmic_bytes(cfg) / seconds / 1e9,
+        "value": workloads.algorithmic_bytes(cfg, kv_bytes) / seconds / 1e9,
         "unit": "GB/s",
         "us_per_call": seconds * 1e6,
         "cores": threads,
@@ -224,20 +226,21 @@ def main() -> int:
     from ayaka_amd.hip import _lib
     from ayaka_amd.hip import attention as hip_attention
     from ayaka_amd.hip import kvcache as hip_kvcache
-    from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+    from ayaka_amd.kvcache import KVBuffers
 
     _lib.lib()
     dev = torch.device("cuda:0")
     cfg = workloads.config(args.config)
     layout = KVLayoutKind(args.layout) if args.layout else KVLayoutKind(hip_kvcache.layout())
-    step = workloads.build(cfg, dev, poison=False, layout=str(layout.value))
-    buffers = KVBuffers(step.k_cache, step.v_cache, layout, RAW_CODEC)
+    step = workloads.build(cfg, dev, poison=False, layout=str(layout.value), codec=args.codec)
+    buffers = KVBuffers(step.k_cache, step.v_cache, layout, args.codec)
+    kv_bytes = 1 if args.codec == "fp8_e4m3" else 2
     write = hip_attention.plan(ForwardMode.MIXED, step.rows_per_request, step.lengths, step.table, cfg.block_size)
     hip_kvcache.store(step.k_new, step.v_new, buffers, write)
     meta = hip_attention.plan(ForwardMode.DECODE, torch.ones(cfg.batch, dtype=torch.int32, device=dev),
                               step.lengths, step.table, cfg.block_size)
     out = torch.empty_like(step.q)
-    nbytes = workloads.algorithmic_bytes(cfg)
+    nbytes = workloads.algorithmic_bytes(cfg, kv_bytes)
     max_len = max(cfg.lengths)
     auto = meta.plan.split_for(cfg.kv_heads, cfg.heads // cfg.kv_heads)  # what attend will launch
     # The headline ("auto", the launch attend picks) runs last, on a GPU warmed by the others.
@@ -277,7 +280,8 @@ def main() -> int:
     if merge is None and head["partitions"]:
         merge = hip_attention.merge_site(cfg.kv_heads, cfg.heads // cfg.kv_heads, meta.plan, size)
     kernel = ("paged_attention_mfma_kernel" if mfma else "paged_attention_kernel") + \
-        (" (v1)" if head["partitions"] == 0 else f" (v2, merge {merge})")
+        (" (v1" if head["partitions"] == 0 else f" (v2, merge {merge}") + \
+        (", fp8 cache)" if kv_bytes == 1 else ")")
     if head["partitions"] == 0 or merge == "in-kernel":
         kernel_us = head["median_us"]
     else:
@@ -304,7 +308,8 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) K/V/Q, random block permutation)",
         "config": {
             "workload": f"C{cfg.index} {cfg.name} decode attention: Hq {cfg.heads}, Hkv {cfg.kv_heads}, "
-                        f"D {cfg.head_dim}, {cfg.dtype_label}, {layout.value.upper()} cache, "
+                        f"D {cfg.head_dim}, {cfg.dtype_label}, {layout.value.upper()} "
+                        f"{'fp8 e4m3 ' if kv_bytes == 1 else ''}cache, "
                         f"block {cfg.block_size}, batch {cfg.batch}, "
                         f"context {min(cfg.lengths)}-{max(cfg.lengths)} (sum {sum(cfg.lengths)}), "
                         f"pool {cfg.num_blocks} blocks",
@@ -316,7 +321,7 @@ def main() -> int:
                         "partitions": v["partitions"], "partition_size": v["partition_size"]}
                     for k, v in results.items()},
         "kv_write": {"us_per_call": round(store_us, 2), "rows": int(step.k_new.shape[0]),
-                     "bytes": workloads.store_bytes(cfg)},
+                     "bytes": workloads.store_bytes(cfg, kv_bytes)},
         "roofline": {
             "bound": "hbm",
             "kernel": kernel,
@@ -331,7 +336,7 @@ def main() -> int:
         },
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(step, cfg, args.cpu_rows)
+        line["cpu_baseline"] = cpu_baseline(step, cfg, args.cpu_rows, kv_bytes)
     print(json.dumps(line), flush=True)
     return 0
 

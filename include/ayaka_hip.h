@@ -39,7 +39,10 @@ enum {
   AYK_ERR_WORKSPACE = 4    /* the v2 workspace is smaller than ayk_paged_attention_v2_workspace_bytes */
 };
 
-enum { AYK_DTYPE_FP16 = 0, AYK_DTYPE_BF16 = 1 };
+/* Element types. fp16/bf16 for q, out and 16-bit caches; AYK_DTYPE_FP8_E4M3 for
+ * caches of the "fp8_e4m3" codec: OCP fp8 e4m3 codes (torch.float8_e4m3fn), 1
+ * byte per element, decoded exactly to the compute dtype when read. */
+enum { AYK_DTYPE_FP16 = 0, AYK_DTYPE_BF16 = 1, AYK_DTYPE_FP8_E4M3 = 2 };
 
 /* flags of the attention calls: 0 lets the library pick the q.k path. */
 enum {
@@ -71,6 +74,21 @@ int ayk_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_c
                           int32_t layout, int32_t elem_bytes, void* stream);
 
 /*
+ * KV write into caches of the "fp8_e4m3" codec: row i of k and v (fp16 or bf16
+ * per src_dtype, [n_rows, num_kv_heads, head_dim], contiguous) is encoded to
+ * fp8 e4m3 codes and written to slot slot_mapping[i] (1 byte per element).
+ * Encoding rounds to nearest even; a magnitude that rounds above 448, and NaN,
+ * give the NaN code (no saturation), exactly as torch's cast to float8_e4m3fn.
+ * The reference defines the codec field and only the "raw" codec
+ * (python/ayaka/ops/kvcache.py:35-36, :54-55); this is KVCacheOps.store
+ * (python/ayaka/ops/backends/torch/kvcache.py:65-80) for a quantised one.
+ */
+int ayk_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void* v_cache,
+                               const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t num_blocks, int32_t block_size, int32_t layout, int32_t src_dtype,
+                               void* stream);
+
+/*
  * Paged attention, single pass ("v1"): one workgroup per (row, key/value head)
  * streams every page of that row's context once and serves the query heads of
  * the group from it. Replaces the reference's decode attention,
@@ -83,9 +101,11 @@ int ayk_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_c
  * (reference python/ayaka/ops/attention.py:12-30). A row whose request has
  * kv_lengths 0 is a padding row and gets zeros. Scores are scale * q.k in fp32,
  * the softmax and the value sum are fp32, and out is rounded once.
- * head_dim must be 64, 128 or 256 and block_size a power of two. `flags`
- * (AYK_FLAG_QK_*) forces one q.k implementation; 0 picks by group size
- * (matrix cores from 3 query heads per key/value head).
+ * head_dim must be 64, 128 or 256 and block_size a power of two. `dtype` is
+ * the type of q and out; `kv_dtype` that of the caches: the same, or
+ * AYK_DTYPE_FP8_E4M3 (decoded exactly to `dtype` as it is read; matrix-core
+ * kernel only). `flags` (AYK_FLAG_QK_*) forces one q.k implementation; 0 picks
+ * by group size (matrix cores from 3 query heads per key/value head).
  */
 int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,
                            const int32_t* block_table, int64_t table_stride,
@@ -93,7 +113,7 @@ int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const 
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           float scale, int32_t flags, void* stream);
+                           int32_t kv_dtype, float scale, int32_t flags, void* stream);
 
 /* Bytes of scratch ayk_paged_attention_v2 needs for these sizes. */
 size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads, int32_t head_dim,
@@ -136,7 +156,7 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           float scale, int32_t partition_size, int32_t max_partitions,
+                           int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
                            const int32_t* work_items, int32_t n_work_items, void* workspace,
                            size_t workspace_bytes, uint32_t* arrivals, int32_t flags, void* stream);
 
@@ -157,8 +177,8 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
                       const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
                       const int32_t* positions, const int32_t* tiles, int32_t n_tiles, int32_t n_rows,
                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
-                      int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype, float scale,
-                      void* stream);
+                      int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype, int32_t kv_dtype,
+                      float scale, void* stream);
 
 /*
  * Whole-block copies of both caches; block_bytes is the size of one block of

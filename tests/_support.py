@@ -51,12 +51,14 @@ class Scenario:
     def v(self) -> np.ndarray:
         return bits_to_f32(self.v_bits, self.dtype)
 
-    def expected(self, precision: type = np.float64) -> np.ndarray:
+    def expected(self, precision: type = np.float64, k: np.ndarray | None = None,
+                 v: np.ndarray | None = None) -> np.ndarray:
+        """The oracle's output; ``k``/``v`` replace the cache values (e.g. decoded fp8 codes)."""
         decode = self.mode == "decode"
         return paged.attention(
             self.q,
-            self.k,
-            self.v,
+            self.k if k is None else k,
+            self.v if v is None else v,
             self.table,
             np.asarray(self.lengths),
             scale=self.scale,

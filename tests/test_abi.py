@@ -21,7 +21,7 @@ def declared() -> list[str]:
 
 def test_every_declared_function_is_exported_and_bound() -> None:
     names = declared()
-    assert len(names) == 10
+    assert len(names) == 11
     lib = _lib.lib()
     for name in names:
         assert hasattr(lib, name), name
@@ -38,7 +38,7 @@ def test_workspace_size() -> None:
 def _v1(lib: ctypes.CDLL, **kw: object) -> int:
     args = dict(out=1, q=1, k=1, v=1, table=1, stride=4, lengths=1, ror=None, pos=None, n_rows=1,
                 heads=8, kv_heads=2, head_dim=128, num_blocks=10, block_size=16, max_blocks=4,
-                layout=0, dtype=1, scale=ctypes.c_float(1.0), flags=0, stream=None)
+                layout=0, dtype=1, kv_dtype=1, scale=ctypes.c_float(1.0), flags=0, stream=None)
     args.update(kw)
     return lib.ayk_paged_attention_v1(*args.values())
 
@@ -48,6 +48,8 @@ def _v1(lib: ctypes.CDLL, **kw: object) -> int:
     [
         ({"head_dim": 96}, 2, b"head_dim 96"),
         ({"dtype": 5}, 2, b"dtype 5"),
+        ({"kv_dtype": 0}, 2, b"kv_dtype 0"),
+        ({"kv_dtype": 2, "flags": 1}, 2, b"16-bit caches only"),
         ({"layout": 3}, 2, b"layout 3"),
         ({"heads": 6, "kv_heads": 4}, 1, b"not a positive multiple"),
         ({"block_size": 12}, 2, b"power of two"),
@@ -66,7 +68,7 @@ def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, me
 
 def test_v2_and_store_refusals() -> None:
     lib = _lib.lib()
-    base = [1, 1, 1, 1, 1, 4, 1, None, None, 1, 8, 2, 128, 10, 16, 4, 0, 1, ctypes.c_float(1.0)]
+    base = [1, 1, 1, 1, 1, 4, 1, None, None, 1, 8, 2, 128, 10, 16, 4, 0, 1, 1, ctypes.c_float(1.0)]
     assert lib.ayk_paged_attention_v2(*base, 100, 4, None, 0, 1, 1 << 20, None, 0, None) == 1
     assert b"multiple of 64" in lib.ayk_last_error()
     assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 1, 16, None, 0, None) == 4
@@ -76,5 +78,8 @@ def test_v2_and_store_refusals() -> None:
     assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 16, 1 << 20, None, 8 | 16, None) == 1
     assert b"exclude each other" in lib.ayk_last_error()
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 3, None) == 2
+    assert lib.ayk_reshape_and_cache_e4m3(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 2, None) == 2
+    assert b"src_dtype 2" in lib.ayk_last_error()
+    assert lib.ayk_reshape_and_cache_e4m3(1, 1, 1, 1, 1, 0, 2, 64, 10, 16, 0, 1, None) == 0
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 0, 2, 64, 10, 16, 0, 2, None) == 0
     assert lib.ayk_zero_blocks(1, 1, 1, 0, 2, 0, 64, None) == 1

@@ -26,9 +26,9 @@ from ayaka_amd.errors import BackendError
 from ayaka_amd.hip import _lib
 from ayaka_amd.hip import attention as hip_attention
 from ayaka_amd.hip import kvcache as hip_kvcache
-from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+from ayaka_amd.kvcache import FP8_E4M3_CODEC, RAW_CODEC, KVBuffers
 from oracle import paged
-from oracle.numerics import bits_to_f32, f32_to_bits, parity_report
+from oracle.numerics import bits_to_f32, e4m3_to_f32, f32_to_bits, f32_to_e4m3, parity_report
 from tests._support import Scenario, build_scenario
 
 pytestmark = pytest.mark.gpu
@@ -234,6 +234,77 @@ def test_split_partitions_agree_with_the_oracle_and_v1(dtype: str, head_dim: int
     assert_parity(v2, expected, dtype, "v2")
     auto = run_attention(s, None, qk)
     assert_parity(auto, expected, dtype, "auto")
+
+
+# --- fp8 e4m3 codec ---------------------------------------------------------------------------
+
+
+def fp8_buffers(s: Scenario) -> tuple[KVBuffers, np.ndarray, np.ndarray]:
+    """The scenario's caches encoded to fp8 codes by the oracle (NaN slots stay NaN codes)."""
+    kc, vc = f32_to_e4m3(s.k), f32_to_e4m3(s.v)
+    layout = KVLayoutKind.NHD if s.layout == "nhd" else KVLayoutKind.HND
+    k = torch.from_numpy(kc).view(torch.float8_e4m3fn).to(DEV)
+    v = torch.from_numpy(vc).view(torch.float8_e4m3fn).to(DEV)
+    return KVBuffers(k, v, layout, FP8_E4M3_CODEC), kc, vc
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+@pytest.mark.parametrize("head_dim", [64, 128, 12, 8])
+def test_fp8_store_is_bit_exact(dtype: str, layout: str, head_dim: int) -> None:
+    s = build_scenario([(3, 9), (1, 2), (2, 30)], dtype=dtype, layout=layout, head_dim=head_dim, block_size=4,
+                       kv_heads=2, seed=83)
+    buffers, kc, vc = fp8_buffers(s)
+    rng = np.random.default_rng(84)
+    n = len(s.plan["slot_mapping"])
+    vals = rng.standard_normal((2, n, s.kv_heads, head_dim)) * np.exp2(rng.uniform(-13, 9, (2, n, s.kv_heads, 1)))
+    special = [448.0, 464.0, 470.0, 500.0, -0.0, 1e-3, 2.0 ** -10, 3 * 2.0 ** -10, np.nan, np.inf, -600.0]
+    vals.reshape(-1)[: len(special)] = special
+    bits = f32_to_bits(vals.astype(np.float32), dtype)
+    rows = bits_to_f32(bits, dtype)
+    meta = plan_scenario(s)
+    hip_kvcache.store(to_device(bits[0], dtype), to_device(bits[1], dtype), buffers, meta)
+    torch.cuda.synchronize()
+    paged.store(kc, vc, f32_to_e4m3(rows[0]), f32_to_e4m3(rows[1]), s.plan["slot_mapping"], layout)
+    assert np.array_equal(buffers.k.view(torch.uint8).cpu().numpy(), kc)
+    assert np.array_equal(buffers.v.view(torch.uint8).cpu().numpy(), vc)
+    with pytest.raises(BackendError, match="over a 'fp8_e4m3' cache the hip backend computes in float16"):
+        hip_kvcache.store(to_device(bits[0], dtype).float(), to_device(bits[1], dtype).float(), buffers, meta)
+
+
+FP8_CASES = [
+    ("decode", [(1, 16), (1, 0), (1, 1300), (1, 33), (1, 517)], "decode"),
+    ("mixed", [(7, 7), (1, 9), (40, 600), (2, 0), (3, 1100)], "mixed"),
+]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(8, 2, 128), (32, 8, 64), (64, 8, 128), (4, 4, 256)])
+@pytest.mark.parametrize("name,steps,mode", FP8_CASES, ids=[c[0] for c in FP8_CASES])
+def test_fp8_attention_matches_the_oracle_on_decoded_values(dtype: str, layout: str, heads: int, kv_heads: int,
+                                                            head_dim: int, name: str, steps: list, mode: str) -> None:
+    s = build_scenario(steps, dtype=dtype, layout=layout, heads=heads, kv_heads=kv_heads, head_dim=head_dim,
+                       block_size=16, mode=mode, seed=89)
+    buffers, kc, vc = fp8_buffers(s)
+    expected = s.expected(np.float64, k=e4m3_to_f32(kc), v=e4m3_to_f32(vc))
+    meta = plan_scenario(s)
+    q = to_device(s.q_bits, dtype)
+    padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
+    launches = [("v1", dict(partitions=0, prefill=False)),
+                ("v2/in-kernel", dict(partitions=6, partition_size=256, merge="in-kernel", prefill=False)),
+                ("v2/reduce-kernel", dict(partitions=6, partition_size=256, merge="reduce-kernel", prefill=False)),
+                ("auto", dict(partitions=None))]
+    if mode == "mixed":
+        launches.append(("multi-row", dict(partitions=None, prefill=True)))
+    for label, launch in launches:
+        out = torch.full_like(q, 7.0)
+        hip_attention.attend_with(q, buffers, meta, out, scale=s.scale, **launch)
+        torch.cuda.synchronize()
+        assert_parity(out, expected, dtype, f"fp8 {name} {label}")
+        if padding_rows:
+            assert torch.count_nonzero(out[padding_rows]) == 0
+    assert counters_are_clear()
 
 
 def counters_are_clear() -> bool:
@@ -495,13 +566,13 @@ def test_c_abi_direct_call() -> None:
     stream = torch.cuda.current_stream().cuda_stream
     rc = lib.ayk_paged_attention_v1(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
                                     table.shape[1], lengths.data_ptr(), None, None, 3, 8, 2, 128,
-                                    k.shape[0], 16, table.shape[1], 0, 1, ctypes.c_float(s.scale), 0, stream)
+                                    k.shape[0], 16, table.shape[1], 0, 1, 1, ctypes.c_float(s.scale), 0, stream)
     assert rc == 0, lib.ayk_last_error()
     torch.cuda.synchronize()
     assert_parity(out, s.expected(np.float64), "bf16", "abi")
     rc = lib.ayk_paged_attention_v1(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
                                     table.shape[1], lengths.data_ptr(), None, None, 3, 8, 2, 96,
-                                    k.shape[0], 16, table.shape[1], 0, 1, ctypes.c_float(1.0), 0, stream)
+                                    k.shape[0], 16, table.shape[1], 0, 1, 1, ctypes.c_float(1.0), 0, stream)
     assert rc == 2 and b"head_dim 96" in lib.ayk_last_error()
 
 

@@ -20,7 +20,7 @@ from ayaka_amd.enums import DType, ForwardMode, KVLayoutKind
 from ayaka_amd.errors import BackendError, CapabilityError, ConfigError
 from ayaka_amd.hip import attention as hip_attention
 from ayaka_amd.hip import kvcache as hip_kvcache
-from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+from ayaka_amd.kvcache import FP8_E4M3_CODEC, RAW_CODEC, KVBuffers
 from oracle import paged
 
 KNOWN = json.loads((Path(__file__).resolve().parent / "golden" / "known_answers.json").read_text())
@@ -147,11 +147,13 @@ def test_ops_refuse_caches_they_cannot_serve() -> None:
     q = torch.zeros(1, 4, 64, dtype=torch.bfloat16)
     with pytest.raises(BackendError, match="serves the NHD and HND layouts"):
         hip_attention.attend(q, _cpu_buffers(layout=KVLayoutKind.NLD), meta, q.clone(), scale=1.0)
-    with pytest.raises(BackendError, match="stores the 'raw' codec, not 'fp8'"):
+    with pytest.raises(BackendError, match="stores the 'raw' and 'fp8_e4m3' codecs, not 'fp8'"):
         hip_kvcache.store(q[:, :2], q[:, :2], _cpu_buffers(codec="fp8"), meta)
     fp32 = torch.zeros(4, 16, 2, 64)
     with pytest.raises(BackendError, match="computes in float16, bfloat16"):
         hip_attention.attend(q, KVBuffers(fp32, fp32, KVLayoutKind.NHD, RAW_CODEC), meta, q.clone(), scale=1.0)
+    with pytest.raises(BackendError, match="stores the 'fp8_e4m3' codec as float8_e4m3fn"):
+        hip_attention.attend(q, _cpu_buffers(codec=FP8_E4M3_CODEC), meta, q.clone(), scale=1.0)
     with pytest.raises(BackendError, match="runs on a HIP device"):
         hip_attention.attend(q, _cpu_buffers(), meta, q.clone(), scale=1.0)
     bad_v = torch.zeros(4, 16, 2, 65, dtype=torch.bfloat16)

@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from oracle import paged
-from oracle.numerics import bits_to_f32, f32_to_bits, half_ulp, parity_report
+from oracle.numerics import bits_to_f32, e4m3_to_f32, f32_to_bits, f32_to_e4m3, half_ulp, parity_report
 from tests._support import build_scenario, brute_force
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -50,6 +50,40 @@ def test_rounding_matches_torch(dtype: str, torch_dtype: torch.dtype) -> None:
     nan = np.isnan(values)
     assert np.array_equal(ours[~nan], theirs[~nan])
     assert np.isnan(bits_to_f32(ours[nan], dtype)).all()
+
+
+def test_e4m3_decoding_matches_torch_for_every_code() -> None:
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = e4m3_to_f32(codes)
+    assert np.array_equal(np.isnan(want), np.isnan(got))
+    assert np.array_equal(want[~np.isnan(want)], got[~np.isnan(got)])
+    assert got[0x7E] == 448.0 and got[0x01] == 2.0 ** -9 and got[0x08] == 2.0 ** -6 and np.isnan(got[0xFF])
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp16"])
+def test_e4m3_encoding_matches_torch_for_every_16_bit_input(dtype: str) -> None:
+    # every bf16 / fp16 value a KV write can receive, NaN and infinities included
+    values = bits_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16), dtype)
+    want = torch.from_numpy(values).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(f32_to_e4m3(values), want)
+
+
+def test_e4m3_encoding_matches_torch_on_float32_and_the_rounding_edges() -> None:
+    rng = np.random.default_rng(5)
+    values = (rng.standard_normal(200_000) * np.exp2(rng.uniform(-14, 10, 200_000))).astype(np.float32)
+    edges = np.array([448.0, 464.0, np.nextafter(464.0, 500.0), 479.9, 480.0, 1e30, 0.0, -0.0,
+                      2.0 ** -10, 1.5 * 2.0 ** -9, 2.5 * 2.0 ** -9, 2.0 ** -6, 2.0 ** -6 - 2.0 ** -10,
+                      np.inf, -np.inf, np.nan], dtype=np.float32)
+    values = np.concatenate([values, edges, -edges])
+    want = torch.from_numpy(values).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(f32_to_e4m3(values), want)
+    # ties go to the even code: 464 is halfway between 448 (0x7E) and the NaN code, 2.5 * 2^-9 between 2 and 3
+    assert f32_to_e4m3(np.array([464.0, 1.5 * 2.0 ** -9, 2.5 * 2.0 ** -9], np.float32)).tolist() == [0x7E, 2, 2]
+    # decoding what was encoded returns the value wherever it is representable
+    finite = e4m3_to_f32(np.arange(256, dtype=np.uint8))
+    finite = finite[~np.isnan(finite)]
+    assert np.array_equal(e4m3_to_f32(f32_to_e4m3(finite)), finite)
 
 
 def test_half_ulp_and_metrics_on_hand_computed_values() -> None:
