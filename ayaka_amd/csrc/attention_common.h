@@ -116,18 +116,54 @@ __device__ __forceinline__ const uint16_t* kv_at(const uint16_t* base, int64_t e
   return base + elem;
 }
 
-// The 8 elements at element offset `off` from `base` (see kv_at), as 8 packed
-// compute-type values: one 16-byte load, or one 8-byte load of fp8 codes decoded
-// in registers. Both nontemporal: the cache is streamed once per call.
+// Raw loads and decoding are separate, so prefetched chunks stay in flight: a
+// decode at the load would make the wave wait for the data right away.
+// The 8 elements at element offset `off` from `base` (see kv_at) as loaded:
+// 16 bytes of fp16/bf16, or 8 bytes of fp8 codes. Nontemporal: the cache is
+// streamed once per call.
+template <bool KV8>
+struct KvRaw {
+  typedef u32x4 T;
+};
+template <>
+struct KvRaw<true> {
+  typedef u32x2 T;
+};
+
+template <bool KV8>
+__device__ __forceinline__ typename KvRaw<KV8>::T load_kv_raw(const uint16_t* base, uint32_t off) {
+  if constexpr (KV8)
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(base) + off));
+  else
+    return stream_load(base + off);
+}
+
+// Loaded elements as 8 packed compute-type values (4 pairs).
 template <bool KV8, bool BF16>
-__device__ __forceinline__ u32x4 load_kv(const uint16_t* base, uint32_t off) {
-  if constexpr (KV8) {
-    const u32x2 w =
-        __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(base) + off));
+__device__ __forceinline__ u32x4 kv_pairs(typename KvRaw<KV8>::T w) {
+  if constexpr (KV8)
     return u32x4{e4m3_pair<BF16, false>(w.x), e4m3_pair<BF16, true>(w.x), e4m3_pair<BF16, false>(w.y),
                  e4m3_pair<BF16, true>(w.y)};
+  else
+    return w;
+}
+
+// Loaded elements as 8 fp32 values (fp8 codes decode straight to fp32).
+template <bool KV8, bool BF16>
+__device__ __forceinline__ void kv_floats(typename KvRaw<KV8>::T w, float (&f)[8]) {
+  if constexpr (KV8) {
+    const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.x, false);
+    const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.x, true);
+    const f32x2 c = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.y, false);
+    const f32x2 d = __builtin_amdgcn_cvt_pk_f32_fp8((int)w.y, true);
+    f[0] = a[0]; f[1] = a[1]; f[2] = b[0]; f[3] = b[1];
+    f[4] = c[0]; f[5] = c[1]; f[6] = d[0]; f[7] = d[1];
   } else {
-    return stream_load(base + off);
+    using E = Elem<BF16>;
+    f[0] = E::lo(w.x); f[1] = E::hi(w.x);
+    f[2] = E::lo(w.y); f[3] = E::hi(w.y);
+    f[4] = E::lo(w.z); f[5] = E::hi(w.z);
+    f[6] = E::lo(w.w); f[7] = E::hi(w.w);
   }
 }
 

@@ -49,17 +49,21 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 template <int D, int GC, bool BF16, bool SPLIT, bool KV8>
 __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel(const AttnParams p) {
-  using E = Elem<BF16>;
-  constexpr int CH = 16;            // tokens per chunk: the MFMA tile height
+  constexpr int MT = 16;            // tokens per MFMA tile
+  // Tiles per chunk: fp8 loads carry half the bytes of a 16-bit load, so a chunk
+  // of two tiles keeps as many bytes in flight per wave as the 16-bit kernel.
+  constexpr int SUB = KV8 ? 2 : 1;
+  constexpr int CH = MT * SUB;      // tokens per chunk
   constexpr int KS = D / 32;        // MFMA k-steps over head_dim
-  constexpr int CPT = D / 8;        // 16-byte pieces per token (= value lanes per token)
+  constexpr int CPT = D / 8;        // 8-element pieces per token (= value lanes per token)
   constexpr int TPL = kWave / CPT;  // tokens per load instruction
-  constexpr int NL = CH / TPL;      // load instructions per chunk, for K and for V
+  constexpr int NL1 = MT / TPL;     // load instructions per tile, for K and for V
+  constexpr int NL = CH / TPL;      // load instructions per chunk
   constexpr int PW = ((GC + 3) / 4) * 4;  // weights per token in LDS, padded to float4
 
   __shared__ int s_tbl[kTableCap];
-  __shared__ u32x4 s_k[kMaxWaves][CH * CPT];       // the chunk's keys, swizzled (see key_slot)
-  __shared__ float s_p[kMaxWaves][2][CH][PW];      // the chunk's weights, double-buffered
+  __shared__ u32x4 s_k[kMaxWaves][MT * CPT];       // a tile's keys, swizzled (see key_slot)
+  __shared__ float s_p[kMaxWaves][2][MT][PW];      // a tile's weights, double-buffered
   __shared__ float s_alpha[kMaxWaves][PW];
   __shared__ int s_last;
 
@@ -141,99 +145,102 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
       }
     };
 
-    auto consume = [&](int ci, int buf, const u32x4(&kc)[NL], const u32x4(&vc)[NL]) {
-      const int tb = s0 + ci * CH;
-      const bool tail = tb + CH > s1;
-      // Keys to LDS in the load layout, back out in the MFMA operand layout.
+    typedef typename KvRaw<KV8>::T Raw;
+    auto consume = [&](int ci, int buf, const Raw(&kc)[NL], const Raw(&vc)[NL]) {
 #pragma unroll
-      for (int j = 0; j < NL; ++j) s_k[wave][key_slot(j * TPL + r, c)] = kc[j];
-      wave_lds_sync();
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int sub = 0; sub < SUB; ++sub) {
+        const int tb = s0 + ci * CH + sub * MT;
+        const bool tail = tb + MT > s1;
+        const int pb = SUB == 1 ? buf : sub;  // the weight buffer of this tile
+        // Keys to LDS in the load layout, back out in the MFMA operand layout.
 #pragma unroll
-      for (int s = 0; s < KS; ++s) acc = mfma_qk<BF16>(s_k[wave][key_slot(mt, s * 4 + mq)], qb[s], acc);
-      float sc[4];
+        for (int j = 0; j < NL1; ++j)
+          s_k[wave][key_slot(j * TPL + r, c)] = kv_pairs<KV8, BF16>(kc[sub * NL1 + j]);
+        wave_lds_sync();
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[i] = acc[i] * scale_log2;
-        if (mt >= GC || (tail && tb + 4 * mq + i >= s1)) sc[i] = -INFINITY;
-      }
-      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      if (__builtin_amdgcn_ballot_w64(mx > m_h + kRescaleSlack)) {
-        const float mn = fmaxf(m_h, mx);
-        const float alpha = fast_exp2(m_h - mn);
-        l_h *= alpha;
-        m_h = mn;
-        if (mq == 0 && mt < PW) s_alpha[wave][mt] = alpha;
+        for (int s = 0; s < KS; ++s) acc = mfma_qk<BF16>(s_k[wave][key_slot(mt, s * 4 + mq)], qb[s], acc);
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sc[i] = acc[i] * scale_log2;
+          if (mt >= GC || (tail && tb + 4 * mq + i >= s1)) sc[i] = -INFINITY;
+        }
+        float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if (__builtin_amdgcn_ballot_w64(mx > m_h + kRescaleSlack)) {
+          const float mn = fmaxf(m_h, mx);
+          const float alpha = fast_exp2(m_h - mn);
+          l_h *= alpha;
+          m_h = mn;
+          if (mq == 0 && mt < PW) s_alpha[wave][mt] = alpha;
+          wave_lds_sync();
+#pragma unroll
+          for (int g = 0; g < GC; ++g) {
+            const float a = s_alpha[wave][g];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[g][e] *= a;
+          }
+        }
+        float w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          w[i] = fast_exp2(sc[i] - m_h);
+          l_h += w[i];
+        }
+        if (mt < PW) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) s_p[wave][pb][4 * mq + i][mt] = w[i];
+        }
         wave_lds_sync();
 #pragma unroll
-        for (int g = 0; g < GC; ++g) {
-          const float a = s_alpha[wave][g];
+        for (int j = 0; j < NL1; ++j) {
+          float pw[PW];
 #pragma unroll
-          for (int e = 0; e < 8; ++e) o[g][e] *= a;
-        }
-      }
-      float w[4];
+          for (int g4 = 0; g4 < PW; g4 += 4) {
+            const f32x4 v4 = *reinterpret_cast<const f32x4*>(&s_p[wave][pb][j * TPL + r][g4]);
+            pw[g4] = v4.x; pw[g4 + 1] = v4.y; pw[g4 + 2] = v4.z; pw[g4 + 3] = v4.w;
+          }
+          float vf[8];
+          kv_floats<KV8, BF16>(vc[sub * NL1 + j], vf);
+          if (tail && tb + j * TPL + r >= s1) {
+            // A slot past the context may hold anything, NaN included, and 0 * NaN is NaN.
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        w[i] = fast_exp2(sc[i] - m_h);
-        l_h += w[i];
-      }
-      if (mt < PW) {
+            for (int e = 0; e < 8; ++e) vf[e] = 0.f;
+          }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s_p[wave][buf][4 * mq + i][mt] = w[i];
-      }
-      wave_lds_sync();
+          for (int g = 0; g < GC; ++g) {
 #pragma unroll
-      for (int j = 0; j < NL; ++j) {
-        float pw[PW];
-#pragma unroll
-        for (int g4 = 0; g4 < PW; g4 += 4) {
-          const f32x4 v4 = *reinterpret_cast<const f32x4*>(&s_p[wave][buf][j * TPL + r][g4]);
-          pw[g4] = v4.x; pw[g4 + 1] = v4.y; pw[g4 + 2] = v4.z; pw[g4 + 3] = v4.w;
-        }
-        float vf[8];
-        vf[0] = E::lo(vc[j].x); vf[1] = E::hi(vc[j].x);
-        vf[2] = E::lo(vc[j].y); vf[3] = E::hi(vc[j].y);
-        vf[4] = E::lo(vc[j].z); vf[5] = E::hi(vc[j].z);
-        vf[6] = E::lo(vc[j].w); vf[7] = E::hi(vc[j].w);
-        if (tail && tb + j * TPL + r >= s1) {
-          // A slot past the context may hold anything, NaN included, and 0 * NaN is NaN.
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vf[e] = 0.f;
-        }
-#pragma unroll
-        for (int g = 0; g < GC; ++g) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pw[g], vf[e], o[g][e]);
+            for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pw[g], vf[e], o[g][e]);
+          }
         }
       }
     };
 
     // Keys of the next chunk are in flight while the current one is folded in.
     uint32_t offA[NL], offB[NL];
-    u32x4 kA[NL], kB[NL], vc[NL];
+    Raw kA[NL], kB[NL], vc[NL];
     int ci = 0;
     offsets(0, offA);
 #pragma unroll
-    for (int j = 0; j < NL; ++j) kA[j] = load_kv<KV8, BF16>(kbase, offA[j]);
+    for (int j = 0; j < NL; ++j) kA[j] = load_kv_raw<KV8>(kbase, offA[j]);
     while (ci < nch) {
 #pragma unroll
-      for (int j = 0; j < NL; ++j) vc[j] = load_kv<KV8, BF16>(vbase, offA[j]);
+      for (int j = 0; j < NL; ++j) vc[j] = load_kv_raw<KV8>(vbase, offA[j]);
       if (ci + 1 < nch) {
         offsets(ci + 1, offB);
 #pragma unroll
-        for (int j = 0; j < NL; ++j) kB[j] = load_kv<KV8, BF16>(kbase, offB[j]);
+        for (int j = 0; j < NL; ++j) kB[j] = load_kv_raw<KV8>(kbase, offB[j]);
       }
       consume(ci, 0, kA, vc);
       if (++ci >= nch) break;
 #pragma unroll
-      for (int j = 0; j < NL; ++j) vc[j] = load_kv<KV8, BF16>(vbase, offB[j]);
+      for (int j = 0; j < NL; ++j) vc[j] = load_kv_raw<KV8>(vbase, offB[j]);
       if (ci + 1 < nch) {
         offsets(ci + 1, offA);
 #pragma unroll
-        for (int j = 0; j < NL; ++j) kA[j] = load_kv<KV8, BF16>(kbase, offA[j]);
+        for (int j = 0; j < NL; ++j) kA[j] = load_kv_raw<KV8>(kbase, offA[j]);
       }
       consume(ci, 1, kB, vc);
       ++ci;

@@ -155,8 +155,9 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
     // Cooperative chunk loads: thread tid carries pieces tid, tid + THREADS, ... of
     // every chunk. A ring of DEPTH register slots keeps DEPTH chunks in flight, so the
     // HBM latency of one chunk overlaps the compute of the DEPTH - 1 before it.
-    u32x4 kr[DEPTH][PER_THREAD], vr[DEPTH][PER_THREAD];
-    auto load_chunk = [&](int ci, u32x4(&kd)[PER_THREAD], u32x4(&vd)[PER_THREAD]) {
+    typedef typename KvRaw<KV8>::T Raw;
+    Raw kr[DEPTH][PER_THREAD], vr[DEPTH][PER_THREAD];
+    auto load_chunk = [&](int ci, Raw(&kd)[PER_THREAD], Raw(&vd)[PER_THREAD]) {
 #pragma unroll
       for (int u = 0; u < PER_THREAD; ++u) {
         const int piece = tid + u * THREADS;
@@ -164,19 +165,20 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
           const int t = min(s0 + ci * CH + piece / CPT, s1 - 1);
           const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
           const uint32_t off = blk * block_stride + (uint32_t)(t & bs_mask) * token_stride + (piece % CPT) * 8;
-          kd[u] = load_kv<KV8, BF16>(kbase, off);
-          vd[u] = load_kv<KV8, BF16>(vbase, off);
+          kd[u] = load_kv_raw<KV8>(kbase, off);
+          vd[u] = load_kv_raw<KV8>(vbase, off);
         }
       }
     };
-    auto stage_chunk = [&](int buf, const u32x4(&kd)[PER_THREAD], const u32x4(&vd)[PER_THREAD]) {
+    auto stage_chunk = [&](int buf, const Raw(&kd)[PER_THREAD], const Raw(&vd)[PER_THREAD]) {
 #pragma unroll
       for (int u = 0; u < PER_THREAD; ++u) {
         const int piece = tid + u * THREADS;
         if (PIECES % THREADS == 0 || piece < PIECES) {
           const int tok = piece / CPT, c = piece % CPT;
-          s_k[buf][key_slot(tok, c)] = kd[u];
-          const uint32_t w[4] = {vd[u].x, vd[u].y, vd[u].z, vd[u].w};
+          s_k[buf][key_slot(tok, c)] = kv_pairs<KV8, BF16>(kd[u]);
+          const u32x4 vp = kv_pairs<KV8, BF16>(vd[u]);
+          const uint32_t w[4] = {vp.x, vp.y, vp.z, vp.w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             s_vt[buf][(c * 8 + 2 * e) * VT_STRIDE + tok] = (uint16_t)(w[e] & 0xffffu);

@@ -304,14 +304,23 @@ def uses_matrix_cores(group: int) -> bool:
     return group // head_chunks(group) >= MFMA_MIN_HEADS
 
 
+def merge_site_for(workgroups: int) -> str:
+    """Where the library merges the v2 partitions of a grid of ``workgroups``: ``"in-kernel"``
+    above two rounds of the compute units or at a quarter round at most, ``"reduce-kernel"``
+    otherwise (the rule of ``merge_in_kernel`` in ``api.hip``)."""
+    return "in-kernel" if workgroups > 2 * COMPUTE_UNITS or workgroups <= COMPUTE_UNITS // 4 else "reduce-kernel"
+
+
 def merge_site(num_kv_heads: int, group: int, step: "HipAttentionPlan", partition_size: int) -> str:
-    """Where the library merges the v2 partitions of an eagerly planned step: ``"in-kernel"``
-    when its grid spans more than two rounds of the compute units or a quarter round at
-    most, ``"reduce-kernel"`` otherwise (the rule of ``merge_in_kernel`` in ``api.hip``)."""
+    """Where the library merges the v2 partitions of an eagerly planned step (its work list)."""
     groups = -(-num_kv_heads * head_chunks(group) // 8)
     items = sum(max(1, -(-n // partition_size)) for n in step.row_lengths)
-    workgroups = items * groups
-    return "in-kernel" if workgroups > 2 * COMPUTE_UNITS or workgroups <= COMPUTE_UNITS // 4 else "reduce-kernel"
+    return merge_site_for(items * groups)
+
+
+def graph_merge_site(n_rows: int, num_kv_heads: int, group: int, partitions: int) -> str:
+    """Where the library merges the v2 partitions of a graph replay (the dense grid)."""
+    return merge_site_for(n_rows * partitions * -(-num_kv_heads * head_chunks(group) // 8))
 
 
 @dataclass(frozen=True, slots=True)

@@ -514,9 +514,13 @@ def test_graph_metadata_replays_match_eager_steps() -> None:
         assert eager_meta.slot_mapping.tolist() == meta.slot_mapping.tolist()
         assert eager_meta.positions.tolist() == meta.positions.tolist()
         graph_split = hip_attention.choose_split(bucket, kv_heads, heads // kv_heads, max_blocks * bs)
+        # the replay's dense grid and the eager work list differ in size, so the library may merge
+        # the partitions at different sites; the same site folds in the same order
+        site = hip_attention.graph_merge_site(bucket, kv_heads, heads // kv_heads, graph_split.partitions)
         same_shape = torch.empty_like(out)
         hip_attention.attend_with(q, buffers, eager_meta, same_shape, scale=dim**-0.5,
-                                  partitions=graph_split.partitions, partition_size=graph_split.partition_size or None)
+                                  partitions=graph_split.partitions, partition_size=graph_split.partition_size or None,
+                                  merge=site if graph_split.partitions else None)
         eager_out = torch.empty_like(out)
         hip_attention.attend(q, buffers, eager_meta, eager_out, scale=dim**-0.5)
         torch.cuda.synchronize()
