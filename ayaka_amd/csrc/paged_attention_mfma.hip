@@ -218,7 +218,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
       }
     };
 
-    // Keys of the next chunk are in flight while the current one is folded in.
+    // Keys of the next chunk are in flight while the current one is folded in. The
+    // prefetch is unconditional -- at the last chunk it re-reads that chunk, which
+    // has just arrived -- so the compiler's waits for the values before each use
+    // leave the next chunk's keys outstanding (a conditional load would make them
+    // wait for everything).
     uint32_t offA[NL], offB[NL];
     Raw kA[NL], kB[NL], vc[NL];
     int ci = 0;
@@ -228,20 +232,16 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     while (ci < nch) {
 #pragma unroll
       for (int j = 0; j < NL; ++j) vc[j] = load_kv_raw<KV8>(vbase, offA[j]);
-      if (ci + 1 < nch) {
-        offsets(ci + 1, offB);
+      offsets(min(ci + 1, nch - 1), offB);
 #pragma unroll
-        for (int j = 0; j < NL; ++j) kB[j] = load_kv_raw<KV8>(kbase, offB[j]);
-      }
+      for (int j = 0; j < NL; ++j) kB[j] = load_kv_raw<KV8>(kbase, offB[j]);
       consume(ci, 0, kA, vc);
       if (++ci >= nch) break;
 #pragma unroll
       for (int j = 0; j < NL; ++j) vc[j] = load_kv_raw<KV8>(vbase, offB[j]);
-      if (ci + 1 < nch) {
-        offsets(ci + 1, offA);
+      offsets(min(ci + 1, nch - 1), offA);
 #pragma unroll
-        for (int j = 0; j < NL; ++j) kA[j] = load_kv_raw<KV8>(kbase, offA[j]);
-      }
+      for (int j = 0; j < NL; ++j) kA[j] = load_kv_raw<KV8>(kbase, offA[j]);
       consume(ci, 1, kB, vc);
       ++ci;
     }
