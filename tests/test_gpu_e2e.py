@@ -1,0 +1,222 @@
+"""End to end: a small decoder generating greedily on the hip backend, eagerly and from one
+captured decode graph.
+
+The reference runs its tiny models through the engine for this (``tests/e2e/test_gpu.py``,
+``tests/execution/test_graph.py:283-402``, ``tests/e2e/test_sync_guards.py``). The engine is
+not part of this build, so the test drives the ops contract the way the engine's attention layer
+does (``layers/attention/dense.py:122,124``): per layer, ``kvcache.store`` then
+``attention.attend``, with one plan per step. A 4-layer attention-only decoder (RMSNorm, q/k/v/o
+projections, residual, tied embedding head) with seeded weights:
+
+* prefills its prompts through the multi-row kernel, then decodes greedily, eagerly planned;
+* decodes the same prompts from one decode step captured in a graph on graph metadata, every
+  step staged with ``update_graph_metadata`` and replayed under torch's sync debug mode set to
+  "error": staging and replay never wait on the device (the token read after it is the step's
+  one declared wait, as in the reference's sync-guard test);
+* is checked against the same model in plain torch float32 over contiguous K/V.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from ayaka_amd.enums import ForwardMode, KVLayoutKind
+from ayaka_amd.hip import attention as hip_attention
+from ayaka_amd.hip import kvcache as hip_kvcache
+from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+LAYERS, HIDDEN, HEADS, KV_HEADS, DIM, VOCAB, BS = 4, 256, 8, 2, 64, 512, 16
+PROMPTS = [37, 5, 120]  # prompt lengths; a fourth bucket row stays padding
+STEPS = 12
+
+
+class Model:
+    def __init__(self, seed: int) -> None:
+        g = torch.Generator(device="cpu").manual_seed(seed)
+
+        def w(*shape: int, scale: float) -> torch.Tensor:
+            return (torch.randn(shape, generator=g) * scale).to(DEV)
+
+        self.embed = w(VOCAB, HIDDEN, scale=1.0)
+        s = 1 / math.sqrt(HIDDEN)
+        self.layers = [
+            dict(wq=w(HIDDEN, HEADS * DIM, scale=s), wk=w(HIDDEN, KV_HEADS * DIM, scale=s),
+                 wv=w(HIDDEN, KV_HEADS * DIM, scale=s), wo=w(HEADS * DIM, HIDDEN, scale=s / 2))
+            for _ in range(LAYERS)
+        ]
+
+    def cast(self, dtype: torch.dtype) -> "Model":
+        out = Model.__new__(Model)
+        out.embed = self.embed.to(dtype)
+        out.layers = [{k: v.to(dtype) for k, v in layer.items()} for layer in self.layers]
+        return out
+
+
+def rms(x: torch.Tensor) -> torch.Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(x.dtype)
+
+
+def forward_hip(model: Model, x: torch.Tensor, caches: list[KVBuffers], meta) -> torch.Tensor:
+    """Hidden states of the rows of one step, through the hip ops (x: [N, HIDDEN] bf16)."""
+    n = x.shape[0]
+    for layer, buffers in zip(model.layers, caches):
+        h = rms(x)
+        q = (h @ layer["wq"]).view(n, HEADS, DIM)
+        k = (h @ layer["wk"]).view(n, KV_HEADS, DIM)
+        v = (h @ layer["wv"]).view(n, KV_HEADS, DIM)
+        hip_kvcache.store(k, v, buffers, meta)
+        o = torch.empty_like(q)
+        hip_attention.attend(q, buffers, meta, o, scale=DIM**-0.5)
+        x = x + o.view(n, HEADS * DIM) @ layer["wo"]
+    return x
+
+
+def logits(model: Model, x: torch.Tensor) -> torch.Tensor:
+    return rms(x).float() @ model.embed.float().T
+
+
+def reference_generate(model: Model, prompts: list[torch.Tensor], steps: int) -> tuple[list[list[int]], list]:
+    """Greedy decoding in plain torch float32, recomputing every sequence from scratch."""
+    m = model.cast(torch.float32)
+    tokens_out, last_hidden = [], []
+    for prompt in prompts:
+        seq = prompt.tolist()
+        hiddens = []
+        for _ in range(steps + 1):
+            x = m.embed[torch.tensor(seq, device=DEV)]
+            length = x.shape[0]
+            mask = torch.ones(length, length, device=DEV, dtype=torch.bool).tril()
+            for layer in m.layers:
+                h = rms(x)
+                q = (h @ layer["wq"]).view(length, HEADS, DIM).transpose(0, 1)
+                k = (h @ layer["wk"]).view(length, KV_HEADS, DIM).transpose(0, 1)
+                v = (h @ layer["wv"]).view(length, KV_HEADS, DIM).transpose(0, 1)
+                k = k.repeat_interleave(HEADS // KV_HEADS, 0)
+                v = v.repeat_interleave(HEADS // KV_HEADS, 0)
+                att = (q @ k.transpose(1, 2)) * DIM**-0.5
+                att = att.masked_fill(~mask, float("-inf")).softmax(-1)
+                o = (att @ v).transpose(0, 1).reshape(length, HEADS * DIM)
+                x = x + o @ layer["wo"]
+            hiddens.append(x[-1])
+            seq.append(int(logits(m, x[-1:]).argmax()))
+        tokens_out.append(seq[len(prompt):])
+        last_hidden.append(hiddens)
+    return tokens_out, last_hidden
+
+
+def new_caches(num_blocks: int) -> list[KVBuffers]:
+    shape = (num_blocks, BS, KV_HEADS, DIM)
+    return [KVBuffers(torch.full(shape, float("nan"), dtype=torch.bfloat16, device=DEV),
+                      torch.full(shape, float("nan"), dtype=torch.bfloat16, device=DEV), KVLayoutKind.NHD, RAW_CODEC)
+            for _ in range(LAYERS)]
+
+
+def prefill(model: Model, prompts: list[torch.Tensor], caches: list[KVBuffers], table: torch.Tensor) -> torch.Tensor:
+    """Run every prompt through the layers (multi-row kernel); returns each prompt's first token."""
+    lengths = [p.numel() for p in prompts]
+    meta = hip_attention.plan(ForwardMode.MIXED, torch.tensor(lengths, dtype=torch.int32, device=DEV),
+                              torch.tensor(lengths, dtype=torch.int32, device=DEV), table.to(DEV), BS)
+    x = model.embed[torch.cat(prompts)]
+    h = forward_hip(model, x, caches, meta)
+    last = torch.tensor(np.cumsum(lengths) - 1, device=DEV)
+    return logits(model, h[last]).argmax(-1)
+
+
+def test_greedy_decode_eager_and_from_a_captured_graph_agree_with_a_torch_model() -> None:
+    base = Model(seed=7)
+    model = base.cast(torch.bfloat16)
+    rng = np.random.default_rng(8)
+    prompts = [torch.from_numpy(rng.integers(0, VOCAB, n)).to(DEV) for n in PROMPTS]
+    bucket = len(PROMPTS) + 1
+    max_blocks = -(-(max(PROMPTS) + STEPS + 1) // BS)
+    num_blocks = 1 + bucket * max_blocks
+    perm = rng.permutation(np.arange(1, num_blocks)).reshape(bucket, max_blocks).astype(np.int32)
+    table_cpu = torch.from_numpy(perm)
+
+    # eager: prefill, then one planned decode step at a time
+    eager_caches = new_caches(num_blocks)
+    first = prefill(model, prompts, eager_caches, table_cpu[: len(PROMPTS)])
+    graph_caches = [KVBuffers(b.k.clone(), b.v.clone(), b.layout, b.codec) for b in eager_caches]
+    eager_tokens, eager_hidden = [first.tolist()], []
+    tokens = first
+    lengths = list(PROMPTS)
+    for _ in range(STEPS):
+        lengths = [n + 1 for n in lengths]
+        meta = hip_attention.plan(ForwardMode.DECODE, torch.ones(len(PROMPTS), dtype=torch.int32, device=DEV),
+                                  torch.tensor(lengths, dtype=torch.int32, device=DEV),
+                                  table_cpu[: len(PROMPTS)].to(DEV), BS)
+        h = forward_hip(model, model.embed[tokens], eager_caches, meta)
+        eager_hidden.append(h.float())
+        tokens = logits(model, h).argmax(-1)
+        eager_tokens.append(tokens.tolist())
+
+    # graph: one captured decode step over a bucket with a padding row, replayed per step
+    meta = hip_attention.graph_metadata(bucket, max_blocks, BS, DEV)
+    static_tokens = torch.zeros(bucket, dtype=torch.int64, device=DEV)
+    static_out = torch.zeros(bucket, HIDDEN, dtype=torch.bfloat16, device=DEV)
+
+    def step() -> None:
+        static_out.copy_(forward_hip(model, model.embed[static_tokens], graph_caches, meta))
+
+    # warm-up and capture run the step once each; they write the caches, so save and restore them
+    saved = [(b.k.clone(), b.v.clone()) for b in graph_caches]
+    hip_attention.update_graph_metadata(meta, torch.tensor([*PROMPTS, 0], dtype=torch.int32), table_cpu)
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        step()
+    torch.cuda.synchronize()
+    for (k, v), buffers in zip(saved, graph_caches):
+        buffers.k.copy_(k)
+        buffers.v.copy_(v)
+    torch.cuda.synchronize()
+
+    graph_tokens = [first.tolist()]
+    tokens = torch.cat([first, torch.zeros(1, dtype=first.dtype, device=DEV)])
+    lengths = list(PROMPTS)
+    for i in range(STEPS):
+        lengths = [n + 1 for n in lengths]
+        host_lengths = torch.tensor([*lengths, 0], dtype=torch.int32)
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            hip_attention.update_graph_metadata(meta, host_lengths, table_cpu)
+            static_tokens.copy_(tokens)
+            graph.replay()
+            tokens = logits(model, static_out).argmax(-1)
+        finally:
+            torch.cuda.set_sync_debug_mode("default")
+        out = static_out.float()
+        diff = (out[: len(PROMPTS)] - eager_hidden[i]).abs().max().item()
+        scale = eager_hidden[i].abs().max().item()
+        assert diff <= 2e-2 * scale, f"step {i}: graph vs eager hidden {diff} (max {scale})"
+        graph_tokens.append(tokens[: len(PROMPTS)].tolist())
+
+    ref_tokens, ref_hidden = reference_generate(base, prompts, STEPS)
+    eager_by_seq = [[step_tokens[b] for step_tokens in eager_tokens] for b in range(len(PROMPTS))]
+    graph_by_seq = [[step_tokens[b] for step_tokens in graph_tokens] for b in range(len(PROMPTS))]
+    assert graph_by_seq == eager_by_seq
+    # the bf16 model follows the float32 one until a near-tie flips a token; compare the hidden
+    # states while the tokens agree
+    for b in range(len(PROMPTS)):
+        agree = 0
+        while agree < STEPS + 1 and eager_by_seq[b][agree] == ref_tokens[b][agree]:
+            agree += 1
+        assert agree >= 1, f"sequence {b}: the prefill token differs from the float32 model's"
+        for i in range(min(agree, STEPS)):
+            ours, ref = eager_hidden[i][b], ref_hidden[b][i + 1]
+            rel = ((ours - ref).norm() / ref.norm()).item()
+            assert rel < 3e-2, f"sequence {b} step {i}: relative error {rel} against float32"
