@@ -35,15 +35,19 @@ HBM_PEAK_GBS = 8000.0
 # the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
 PROFILED_TRAFFIC = {
     (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 1024):
-        (1_076_129_483, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
+        (1_081_806_671, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
     (4, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 704):
-        (663_477_641, 4_055_024, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
+        (668_718_836, 4_054_848, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
     (5, "paged_attention_mfma_kernel (v2, merge in-kernel)", 1280):
-        (2_612_887_537, 22_281_024, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
+        (2_625_555_146, 22_414_144, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
     (2, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 320):
-        (143_291_927, 2_127_872, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
+        (144_727_705, 2_128_032, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
     (1, "paged_attention_mfma_kernel (v2, merge in-kernel)", 64):
-        (1_751_257, 88_064, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
+        (1_754_970, 88_768, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
+    (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1024):
+        (546_161_012, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
+    (5, "paged_attention_mfma_kernel (v2, merge in-kernel, fp8 cache)", 1280):
+        (1_334_593_254, 22_338_416, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
 }
 
 
