@@ -207,7 +207,9 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
 
 extern "C" {
 
-int ayk_abi_version(void) { return 6; }
+int ayk_abi_version(void) { return 7; }
+
+int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 
 const char* ayk_last_error(void) { return g_last_error.c_str(); }
 
@@ -345,8 +347,10 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
   if (rc != AYK_OK) return rc;
-  if (p.group > 64)
-    return fail(AYK_ERR_UNSUPPORTED, "%s: %d query heads per key/value head exceed a tile of 64", op, p.group);
+  const int tile_pairs = ayk::prefill_tile_pairs_for(head_dim);
+  if (p.group > tile_pairs)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: %d query heads per key/value head exceed a tile of %d", op, p.group,
+                tile_pairs);
   if (n_tiles < 0 || (n_tiles > 0 && (!tiles || !positions)))
     return fail(AYK_ERR_ARGUMENT, "%s: %d tiles at %p, positions at %p", op, n_tiles, (const void*)tiles,
                 (const void*)positions);

@@ -6,110 +6,138 @@
 // scores scale * q.k, softmax and P.V in fp32, the output rounded once; rows of a
 // padding request (kv_lengths 0) are zero.
 //
-// A workgroup of 4 waves serves one tile: up to 64 (row, query head) pairs of
-// one request and one key/value head -- the 64 / G consecutive rows of the
-// request whose G query heads read that key/value head. Every 16-position chunk
-// of keys and values is loaded once per tile, cooperatively, into LDS, and each
-// wave multiplies its 16 pairs against it:
+// A workgroup of 4 waves serves one tile: up to TILE_PAIRS (row, query head)
+// pairs of one request and one key/value head -- the TILE_PAIRS / G consecutive
+// rows of the request whose G query heads read that key/value head. Each wave
+// owns PT groups of 16 pairs. The context streams through LDS in chunks of 64
+// positions, loaded once per tile, cooperatively, one chunk ahead in registers:
 //
-//  * S^T = K Q^T: one v_mfma_f32_16x16x32 tile per chunk (keys from a swizzled
-//    LDS tile, 16 query pairs as the B operand). Lane l holds the scores of
-//    positions 4*(l/16)+i for pair l%16, so every per-pair quantity (running
-//    max, weight sum, rescale) lives in the lane's own column.
-//  * O^T += V^T P^T: v_mfma_f32_16x16x16 over 16-element slices of head_dim,
-//    the values read from a transposed LDS tile and P^T straight from the S^T
-//    registers, split into a bf16 (or fp16) high part and the residual so the
-//    product keeps fp32-level accuracy (one bf16 P would cost ~2e-3 relative).
+//  * S^T = K Q^T, per 16-position tile and 16-pair group: v_mfma_f32_16x16x32
+//    over head_dim, keys from a swizzled LDS tile (A operand), q from registers
+//    (B operand). Lane l holds the scores of positions 4*(l/16)+i of pair l%16,
+//    so every per-pair quantity (running max, weight sum, rescale) lives in the
+//    lane's own column.
+//  * O^T += V^T P^T, per 16-element slice of head_dim and 32 positions:
+//    v_mfma_f32_16x16x32 with P^T taken straight from the lane's scores (its
+//    8 k-slots are positions 4*(l/16)+i of two adjacent 16-position tiles) and
+//    V^T read from a transposed LDS tile in that same position order. P is split
+//    into a bf16 (or fp16) high part and the rounded residual, two MFMAs, which
+//    keeps the product at fp32-level accuracy (one 16-bit P would cost ~2e-3
+//    relative).
+//  * The transposed value tile is written with 32-bit LDS stores: each thread
+//    carries the same 8 elements of two adjacent positions. Its row stride and the
+//    threads' value-load mapping keep stores and reads nearly free of bank
+//    conflicts with plain additive addresses.
 #include "attention_common.h"
 
 namespace ayk {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kPrefillWaves = 4;
-// Chunks of K/V in flight per workgroup (register ring of the cooperative loads).
-constexpr int DEPTH = 4;
-constexpr int kPairsPerWave = 16;
-constexpr int kPairsPerTile = kPrefillWaves * kPairsPerWave;
+constexpr int kPrefillThreads = kPrefillWaves * kWave;
+
+// (row, head) pairs one workgroup serves: 2 groups of 16 per wave, 1 at head_dim 256
+// (the accumulators of 2 groups would not fit the register file there).
+__host__ __device__ constexpr int prefill_tile_pairs(int head_dim) {
+  return kPrefillWaves * 16 * (head_dim == 256 ? 1 : 2);
+}
 
 template <bool BF16>
-__device__ __forceinline__ f32x4 mfma_qk32(u32x4 k, u32x4 q, f32x4 acc) {
+__device__ __forceinline__ f32x4 mfma32(u32x4 a, u32x4 b, f32x4 acc) {
   if constexpr (BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, k), __builtin_bit_cast(bf16x8, q),
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
                                                    acc, 0, 0, 0);
   else
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, k), __builtin_bit_cast(f16x8, q),
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
                                                   acc, 0, 0, 0);
 }
 
+// Split 8 fp32 weights w (finite, >= 0) into packed 16-bit high parts h and packed
+// 16-bit parts l of the remainder w - h, both by truncation: |w - h - l| < 2^-14 w
+// for bf16 (2^-20 w for fp16), against ~2^-9 w for a single rounded 16-bit weight.
+// bf16 truncation is the top half of the fp32 bits (one v_perm_b32 packs two);
+// fp16 uses v_cvt_pkrtz (round toward zero).
 template <bool BF16>
-__device__ __forceinline__ f32x4 mfma_pv16(u32x2 v, u32x2 p, f32x4 acc) {
-  if constexpr (BF16)
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, v), __builtin_bit_cast(i16x4, p),
-                                                     acc, 0, 0, 0);
-  else
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, v), __builtin_bit_cast(f16x4, p), acc,
-                                                 0, 0, 0);
-}
-
-// Split 4 fp32 weights into a packed 16-bit high part and the packed residual.
-template <bool BF16>
-__device__ __forceinline__ void split_weights(const float (&w)[4], u32x2& hi, u32x2& lo) {
-  using E = Elem<BF16>;
+__device__ __forceinline__ void split_weights(const float (&w)[8], u32x4& hi, u32x4& lo) {
   uint32_t h[4], r[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    h[i] = E::round(w[i]);
-    const float back = BF16 ? __uint_as_float(h[i] << 16) : (float)__builtin_bit_cast(_Float16, (uint16_t)h[i]);
-    r[i] = E::round(w[i] - back);
+    const float a = w[2 * i], b = w[2 * i + 1];
+    if constexpr (BF16) {
+      const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+      h[i] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
+      const float ra = a - __uint_as_float(ua & 0xffff0000u);
+      const float rb = b - __uint_as_float(ub & 0xffff0000u);
+      r[i] = __builtin_amdgcn_perm(__float_as_uint(rb), __float_as_uint(ra), 0x07060302u);
+    } else {
+      const auto hv = __builtin_amdgcn_cvt_pkrtz(a, b);
+      h[i] = __builtin_bit_cast(uint32_t, hv);
+      r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a - (float)hv[0], b - (float)hv[1]));
+    }
   }
-  hi = u32x2{h[0] | (h[1] << 16), h[2] | (h[3] << 16)};
-  lo = u32x2{r[0] | (r[1] << 16), r[2] | (r[3] << 16)};
+  hi = u32x4{h[0], h[1], h[2], h[3]};
+  lo = u32x4{r[0], r[1], r[2], r[3]};
 }
 
 template <int D, bool BF16, bool KV8>
-__global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(const AttnParams p, const int32_t* tiles) {
+__global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(const AttnParams p, const int32_t* tiles) {
   using E = Elem<BF16>;
-  constexpr int THREADS = kPrefillWaves * kWave;
-  constexpr int CH = 16;           // positions per chunk
-  constexpr int KS = D / 32;       // q.k k-steps
-  constexpr int DT = D / 16;       // 16-element slices of head_dim for P.V
-  constexpr int CPT = D / 8;       // 16-byte pieces per position
-  constexpr int PIECES = CH * CPT; // 16-byte pieces per chunk of K (or V)
-  constexpr int VT_STRIDE = CH + 4;  // halfs per transposed value row (padded against bank conflicts)
+  constexpr int THREADS = kPrefillThreads;
+  constexpr int PT = D == 256 ? 1 : 2;          // 16-pair groups per wave
+  constexpr int TILE_PAIRS = prefill_tile_pairs(D);
+  constexpr int CH = 64;                        // positions per chunk
+  constexpr int PTL = CH / 16;                  // 16-position tiles per chunk
+  constexpr int KS = D / 32;                    // q.k k-steps
+  constexpr int DT = D / 16;                    // 16-element slices of head_dim for P.V
+  constexpr int CPT = D / 8;                    // 8-element pieces per position
+  constexpr int PIECES = CH * CPT;              // pieces per chunk of K (or V)
+  constexpr int PER_THREAD = PIECES / THREADS;  // 2 (D 64), 4 (D 128), 8 (D 256): even
+  constexpr int POS_STEP = 2 * THREADS / CPT;   // positions covered by one pair of a thread's pieces
+  // Transposed value tile: row d holds the 32 position pairs of element d as 32-bit
+  // words, rows 34 words apart. The odd half of 34 spreads the 16 rows one read
+  // instruction touches over the banks (at most 3 words per bank) while the reads
+  // stay 8-byte aligned and every offset is a per-lane base plus a constant.
+  constexpr int VT2 = CH / 2 + 2;
+  // Value loads: a wave covers VSW slices of VNP position pairs per instruction, so the
+  // transposed stores of one instruction (rows 8 apart per slice, consecutive pairs)
+  // hit distinct banks under that stride.
+  constexpr int VSW = CPT / 4;                  // value slices per wave
+  constexpr int VNP = kWave / VSW;              // value position pairs per wave instruction
+  static_assert(PER_THREAD % 2 == 0 && PIECES % THREADS == 0, "piece split");
 
   __shared__ int s_tbl[kTableCap];
   __shared__ u32x4 s_k[2][PIECES];
-  __shared__ __attribute__((aligned(16))) uint16_t s_vt[2][D * VT_STRIDE];
+  __shared__ __attribute__((aligned(16))) uint32_t s_vt[2][D * VT2];
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
   const int mt = lane % 16;
   const int mq = lane / 16;
-  const int kvh = blockIdx.x % (p.num_heads / p.group);
-  const int tile = blockIdx.x / (p.num_heads / p.group);
+  const int kv_heads = p.num_heads / p.group;
+  const int kvh = blockIdx.x % kv_heads;
+  const int tile = blockIdx.x / kv_heads;
   const int first_row = tiles[3 * tile];
-  const int n_rows = tiles[3 * tile + 1];
-  const int req = tiles[3 * tile + 2];
   const int group = p.group;
-  const int n_pairs = n_rows * group;
+  const int n_pairs = min(tiles[3 * tile + 1] * group, TILE_PAIRS);
+  const int n_rows = (n_pairs + group - 1) / group;
+  const int req = tiles[3 * tile + 2];
 
-  // This lane's (row, query head) pair.
-  const int pair = wave * kPairsPerWave + mt;
-  const bool real_pair = pair < n_pairs;
-  const int prow = first_row + (real_pair ? pair / group : 0);
-  const int phead = kvh * group + (real_pair ? pair % group : 0);
+  // This lane's (row, query head) pair of each of its groups.
+  bool real[PT];
+  int prow[PT], phead[PT];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    const int pair = (wave * PT + j) * 16 + mt;
+    real[j] = pair < n_pairs;
+    prow[j] = first_row + (real[j] ? pair / group : 0);
+    phead[j] = kvh * group + (real[j] ? pair % group : 0);
+  }
 
   int kv_len = p.kv_lengths[req];
   kv_len = max(0, min(kv_len, p.max_len));
-  const int last_pos = kv_len > 0 ? min(p.positions[first_row + n_rows - 1], kv_len - 1) : -1;
-  const int my_pos = real_pair && kv_len > 0 ? min(p.positions[prow], kv_len - 1) : -1;
-
   if (kv_len == 0) {
     // A padding request: zero rows.
     uint16_t* out = static_cast<uint16_t*>(p.out);
@@ -120,19 +148,39 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
     }
     return;
   }
-
-  // q as the B operand of S^T = K Q^T: pair mt, k-slice mq of step s.
-  u32x4 qb[KS];
+  const int last_pos = min(p.positions[first_row + n_rows - 1], kv_len - 1);
+  // Idle pairs (past the tile's rows) see everything: their results are not stored, and
+  // they must not force the masked path on chunks every real pair sees whole.
+  int my_pos[PT];
 #pragma unroll
-  for (int s = 0; s < KS; ++s)
-    qb[s] = real_pair ? *reinterpret_cast<const u32x4*>(p.q + ((int64_t)prow * p.num_heads + phead) * D + s * 32 +
-                                                        mq * 8)
-                      : u32x4{0u, 0u, 0u, 0u};
-
-  float m = kNoScore, l = 0.f;
-  f32x4 o[DT];
+  for (int j = 0; j < PT; ++j) my_pos[j] = real[j] ? min(p.positions[prow[j]], kv_len - 1) : last_pos;
+  // The earliest position any pair of this wave stops at: chunks ending at or
+  // before it need no causal mask.
+  int wave_min_pos = my_pos[0];
 #pragma unroll
-  for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 1; j < PT; ++j) wave_min_pos = min(wave_min_pos, my_pos[j]);
+#pragma unroll
+  for (int st = 1; st < kWave; st <<= 1) wave_min_pos = min(wave_min_pos, __shfl_xor(wave_min_pos, st));
+
+  // q as the B operand of S^T = K Q^T: pair mt of group j, k-slice mq of step s.
+  u32x4 qb[PT][KS];
+#pragma unroll
+  for (int j = 0; j < PT; ++j)
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qb[j][s] = real[j] ? *reinterpret_cast<const u32x4*>(p.q + ((int64_t)prow[j] * p.num_heads + phead[j]) * D +
+                                                           s * 32 + mq * 8)
+                         : u32x4{0u, 0u, 0u, 0u};
+
+  float m[PT], l[PT];
+  f32x4 o[PT][DT];
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    m[j] = kNoScore;
+    l[j] = 0.f;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[j][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
   const int shift = p.bs_shift;
@@ -144,7 +192,15 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
   const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride);
   const uint16_t* vbase = kv_at<KV8>(p.v_cache, (int64_t)kvh * p.head_stride);
   auto key_slot = [](int token, int piece) { return token * CPT + (piece ^ (token & (CPT - 1))); };
-  constexpr int PER_THREAD = (PIECES + THREADS - 1) / THREADS;
+  auto vt_word = [](int d, int c2) { return d * VT2 + c2; };
+  // Piece u of this thread: position piece_pos(u) (pieces 2v and 2v + 1 are adjacent
+  // positions), 8-element slice piece_c of it; consecutive threads read consecutive
+  // slices of one position.
+  const int piece_c = tid % CPT;
+  auto piece_pos = [&](int u) { return (u >> 1) * POS_STEP + 2 * (tid / CPT) + (u & 1); };
+  // Value piece u of this thread: position vpiece_pos(u) (again pairs 2v, 2v + 1), slice vpiece_c.
+  const int vpiece_c = wave * VSW + lane / VNP;
+  auto vpiece_pos = [&](int u) { return (u >> 1) * (2 * VNP) + 2 * (lane % VNP) + (u & 1); };
 
   const int t_end = last_pos + 1;
   for (int s0 = 0; s0 < t_end; s0 += seg_len) {
@@ -152,126 +208,157 @@ __global__ __launch_bounds__(kPrefillWaves * kWave) void paged_prefill_kernel(co
     const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, THREADS);
     const int nch = (s1 - s0 + CH - 1) / CH;
 
-    // Cooperative chunk loads: thread tid carries pieces tid, tid + THREADS, ... of
-    // every chunk. A ring of DEPTH register slots keeps DEPTH chunks in flight, so the
-    // HBM latency of one chunk overlaps the compute of the DEPTH - 1 before it.
     typedef typename KvRaw<KV8>::T Raw;
-    Raw kr[DEPTH][PER_THREAD], vr[DEPTH][PER_THREAD];
-    auto load_chunk = [&](int ci, Raw(&kd)[PER_THREAD], Raw(&vd)[PER_THREAD]) {
+    Raw kr[PER_THREAD], vr[PER_THREAD];
+    auto load_chunk = [&](int ci) {
 #pragma unroll
       for (int u = 0; u < PER_THREAD; ++u) {
-        const int piece = tid + u * THREADS;
-        if (PIECES % THREADS == 0 || piece < PIECES) {
-          const int t = min(s0 + ci * CH + piece / CPT, s1 - 1);
-          const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
-          const uint32_t off = blk * block_stride + (uint32_t)(t & bs_mask) * token_stride + (piece % CPT) * 8;
-          kd[u] = load_kv_raw<KV8>(kbase, off);
-          vd[u] = load_kv_raw<KV8>(vbase, off);
+        // past the end: a real position, whose weight is 0
+        const int tk = min(s0 + ci * CH + piece_pos(u), s1 - 1);
+        const int tv = min(s0 + ci * CH + vpiece_pos(u), s1 - 1);
+        const uint32_t bk = (uint32_t)s_tbl[(tk >> shift) - b0];
+        const uint32_t bv = (uint32_t)s_tbl[(tv >> shift) - b0];
+        kr[u] = load_kv_raw<KV8>(kbase, bk * block_stride + (uint32_t)(tk & bs_mask) * token_stride + piece_c * 8);
+        vr[u] = load_kv_raw<KV8>(vbase, bv * block_stride + (uint32_t)(tv & bs_mask) * token_stride + vpiece_c * 8);
+      }
+    };
+    auto stage_chunk = [&](int buf) {
+#pragma unroll
+      for (int u = 0; u < PER_THREAD; u += 2) {
+        const int pos = piece_pos(u);
+        s_k[buf][key_slot(pos, piece_c)] = kv_pairs<KV8, BF16>(kr[u]);
+        s_k[buf][key_slot(pos + 1, piece_c)] = kv_pairs<KV8, BF16>(kr[u + 1]);
+        const int vpos = vpiece_pos(u);
+        const u32x4 a = kv_pairs<KV8, BF16>(vr[u]), b = kv_pairs<KV8, BF16>(vr[u + 1]);
+        const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          // elements 2e and 2e + 1 of the slice, each as (position vpos, vpos + 1)
+          s_vt[buf][vt_word(vpiece_c * 8 + 2 * e, vpos >> 1)] = (wa[e] & 0xffffu) | (wb[e] << 16);
+          s_vt[buf][vt_word(vpiece_c * 8 + 2 * e + 1, vpos >> 1)] = (wa[e] >> 16) | (wb[e] & 0xffff0000u);
         }
       }
     };
-    auto stage_chunk = [&](int buf, const Raw(&kd)[PER_THREAD], const Raw(&vd)[PER_THREAD]) {
+
+    // Fold chunk ci (in LDS buffer buf) into every pair's running state.
+    auto consume = [&](int ci, int buf) {
+      const int tb = s0 + ci * CH;
+      const bool whole = tb + CH <= s1 && tb + CH - 1 <= wave_min_pos;  // uniform: no position masked
+      f32x4 acc[PTL][PT];
 #pragma unroll
-      for (int u = 0; u < PER_THREAD; ++u) {
-        const int piece = tid + u * THREADS;
-        if (PIECES % THREADS == 0 || piece < PIECES) {
-          const int tok = piece / CPT, c = piece % CPT;
-          s_k[buf][key_slot(tok, c)] = kv_pairs<KV8, BF16>(kd[u]);
-          const u32x4 vp = kv_pairs<KV8, BF16>(vd[u]);
-          const uint32_t w[4] = {vp.x, vp.y, vp.z, vp.w};
+      for (int pt = 0; pt < PTL; ++pt)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            s_vt[buf][(c * 8 + 2 * e) * VT_STRIDE + tok] = (uint16_t)(w[e] & 0xffffu);
-            s_vt[buf][(c * 8 + 2 * e + 1) * VT_STRIDE + tok] = (uint16_t)(w[e] >> 16);
+        for (int j = 0; j < PT; ++j) acc[pt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int pt = 0; pt < PTL; ++pt) {
+          const u32x4 ka = s_k[buf][key_slot(pt * 16 + mt, s * 4 + mq)];
+#pragma unroll
+          for (int j = 0; j < PT; ++j) acc[pt][j] = mfma32<BF16>(ka, qb[j][s], acc[pt][j]);
+        }
+#pragma unroll
+      for (int j = 0; j < PT; ++j) {
+        float mx = -INFINITY;
+        if (whole) {
+#pragma unroll
+          for (int pt = 0; pt < PTL; ++pt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[pt][j][i] *= scale_log2;
+              mx = fmaxf(mx, acc[pt][j][i]);
+            }
+        } else {
+          // position tb + pt*16 + 4*mq + i is visible iff pt*16 + i <= lim
+          const int lim = min(my_pos[j], s1 - 1) - tb - 4 * mq;
+#pragma unroll
+          for (int pt = 0; pt < PTL; ++pt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[pt][j][i] = pt * 16 + i <= lim ? acc[pt][j][i] * scale_log2 : -INFINITY;
+              mx = fmaxf(mx, acc[pt][j][i]);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        if (__builtin_amdgcn_ballot_w64(mx > m[j] + kRescaleSlack)) {
+          const float mn = fmaxf(m[j], mx);
+          const float alpha = fast_exp2(m[j] - mn);
+          l[j] *= alpha;
+#pragma unroll
+          for (int t = 0; t < DT; ++t) o[j][t] *= alpha;
+          m[j] = mn;
+        }
+#pragma unroll
+        for (int pt = 0; pt < PTL; ++pt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float w = fast_exp2(acc[pt][j][i] - m[j]);
+            acc[pt][j][i] = w;
+            l[j] += w;
+          }
+      }
+      // O^T += V^T P^T over two 32-position k-steps.
+#pragma unroll
+      for (int ks = 0; ks < PTL / 2; ++ks) {
+        u32x4 phi[PT], plo[PT];
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+          const float w[8] = {acc[2 * ks][j][0],     acc[2 * ks][j][1],     acc[2 * ks][j][2],
+                              acc[2 * ks][j][3],     acc[2 * ks + 1][j][0], acc[2 * ks + 1][j][1],
+                              acc[2 * ks + 1][j][2], acc[2 * ks + 1][j][3]};
+          split_weights<BF16>(w, phi[j], plo[j]);
+        }
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const uint32_t* vrow = &s_vt[buf][vt_word(t * 16 + mt, ks * 16 + 2 * mq)];
+          const u32x2 lo4 = *reinterpret_cast<const u32x2*>(vrow);
+          const u32x2 hi4 = *reinterpret_cast<const u32x2*>(vrow + 8);
+          const u32x4 va = u32x4{lo4.x, lo4.y, hi4.x, hi4.y};
+#pragma unroll
+          for (int j = 0; j < PT; ++j) {
+            o[j][t] = mfma32<BF16>(va, phi[j], o[j][t]);
+            o[j][t] = mfma32<BF16>(va, plo[j], o[j][t]);
           }
         }
       }
     };
 
-    // Fold chunk ci (staged in LDS buffer buf) into every pair's running state.
-    auto consume = [&](int ci, int buf) {
-      const int tb = s0 + ci * CH;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) acc = mfma_qk32<BF16>(s_k[buf][key_slot(mt, s * 4 + mq)], qb[s], acc);
-      float sc[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = tb + 4 * mq + i;
-        sc[i] = (t <= my_pos && t < s1) ? acc[i] * scale_log2 : -INFINITY;
-      }
-      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      if (__builtin_amdgcn_ballot_w64(mx > m + kRescaleSlack)) {
-        const float mn = fmaxf(m, mx);
-        const float alpha = fast_exp2(m - mn);
-        l *= alpha;
-#pragma unroll
-        for (int t = 0; t < DT; ++t) o[t] *= alpha;
-        m = mn;
-      }
-      float w[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        w[i] = fast_exp2(sc[i] - m);
-        l += w[i];
-      }
-      u32x2 phi, plo;
-      split_weights<BF16>(w, phi, plo);
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const u32x2 va = *reinterpret_cast<const u32x2*>(&s_vt[buf][(t * 16 + mt) * VT_STRIDE + 4 * mq]);
-        o[t] = mfma_pv16<BF16>(va, phi, o[t]);
-        o[t] = mfma_pv16<BF16>(va, plo, o[t]);
-      }
-    };
-
-    // Loads past the last chunk re-read it (clamped) rather than being skipped, so
-    // every iteration issues the same loads and the wait before each stage can
-    // leave the younger chunks in flight.
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) load_chunk(min(d, nch - 1), kr[d], vr[d]);
-    stage_chunk(0, kr[0], vr[0]);
+    load_chunk(0);
+    stage_chunk(0);
     lds_barrier();
-    // Iteration ci: chunk ci is in LDS buffer ci & 1, chunk ci + 1 in slot (ci + 1) % DEPTH.
-    // Slot ci % DEPTH was staged one iteration ago and takes chunk ci + DEPTH.
-    // The chunk count is rounded up to a multiple of DEPTH, so the unrolled body has
-    // no exit and the waits stay static; the extra chunks re-read the last one and
-    // their positions (>= s1) are masked, so their weights are 0 (the data is real,
-    // so 0 times it is 0).
-    const int nch_padded = (nch + DEPTH - 1) / DEPTH * DEPTH;
-    for (int base = 0; base < nch_padded; base += DEPTH) {
-#pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        const int ci = base + d;
-        load_chunk(min(ci + DEPTH, nch - 1), kr[d], vr[d]);
-        consume(ci, ci & 1);
-        stage_chunk((ci + 1) & 1, kr[(d + 1) % DEPTH], vr[(d + 1) % DEPTH]);
-        lds_barrier();
-      }
+    for (int ci = 0; ci < nch; ++ci) {
+      const int buf = ci & 1;
+      if (ci + 1 < nch) load_chunk(ci + 1);
+      consume(ci, buf);
+      if (ci + 1 < nch) stage_chunk(buf ^ 1);
+      lds_barrier();
     }
   }
 
-  // The pair's weight sum over the 4 position groups; lane (mq, mt) holds
-  // elements 16*t + 4*mq + i of pair mt.
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (!real_pair) return;
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
-  uint16_t* out = static_cast<uint16_t*>(p.out) + ((int64_t)prow * p.num_heads + phead) * D;
+  // Each pair's weight sum over the 4 position groups; lane (mq, mt) holds
+  // elements 16*t + 4*mq + i of pair mt of each group.
 #pragma unroll
-  for (int t = 0; t < DT; ++t) {
-    uint32_t* o32 = reinterpret_cast<uint32_t*>(out + t * 16 + 4 * mq);
-    o32[0] = E::round(o[t][0] * inv) | (E::round(o[t][1] * inv) << 16);
-    o32[1] = E::round(o[t][2] * inv) | (E::round(o[t][3] * inv) << 16);
+  for (int j = 0; j < PT; ++j) {
+    float lj = l[j];
+    lj += __shfl_xor(lj, 16);
+    lj += __shfl_xor(lj, 32);
+    if (!real[j]) continue;
+    const float inv = lj > 0.f ? 1.0f / lj : 0.f;
+    uint16_t* out = static_cast<uint16_t*>(p.out) + ((int64_t)prow[j] * p.num_heads + phead[j]) * D;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      uint32_t* o32 = reinterpret_cast<uint32_t*>(out + t * 16 + 4 * mq);
+      o32[0] = E::round(o[j][t][0] * inv) | (E::round(o[j][t][1] * inv) << 16);
+      o32[1] = E::round(o[j][t][2] * inv) | (E::round(o[j][t][3] * inv) << 16);
+    }
   }
 }
 
 template <int D>
 static hipError_t launch_prefill_d(const AttnParams& p, const int32_t* tiles, dim3 grid, bool bf16, bool kv8,
                                    hipStream_t stream) {
-  const dim3 block(kPrefillWaves * kWave);
+  const dim3 block(kPrefillThreads);
   if (kv8) {
     if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, true>), grid, block, 0, stream, p, tiles);
     else hipLaunchKernelGGL((paged_prefill_kernel<D, false, true>), grid, block, 0, stream, p, tiles);
@@ -280,6 +367,10 @@ static hipError_t launch_prefill_d(const AttnParams& p, const int32_t* tiles, di
     else hipLaunchKernelGGL((paged_prefill_kernel<D, false, false>), grid, block, 0, stream, p, tiles);
   }
   return hipGetLastError();
+}
+
+int prefill_tile_pairs_for(int head_dim) {
+  return (head_dim == 64 || head_dim == 128 || head_dim == 256) ? prefill_tile_pairs(head_dim) : 0;
 }
 
 hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16, bool kv8,

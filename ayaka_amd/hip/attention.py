@@ -73,8 +73,9 @@ WORKGROUP_COST = 80
 XCDS = 8
 #: Heads per wave from which the library runs q.k on the matrix cores (mirrors the C library).
 MFMA_MIN_HEADS = 3
-#: (row, query head) pairs one workgroup of the multi-row kernel serves.
-PREFILL_PAIRS = 64
+#: (row, query head) pairs one workgroup of the multi-row kernel serves, by head width
+#: (the C library's ``ayk_paged_prefill_tile_pairs``; a test checks they agree).
+PREFILL_PAIRS = {64: 128, 128: 128, 256: 64}
 #: Rows per request (on average) from which a multi-row step runs the multi-row kernel.
 PREFILL_MIN_ROWS = 8
 #: Compute units of one MI355X; the split heuristic aims to keep all of them busy.
@@ -121,16 +122,16 @@ class HipAttentionPlan:
             self.splits[key] = found
         return found
 
-    def prefill_tiles(self, group: int, device: torch.device) -> torch.Tensor:
+    def prefill_tiles(self, group: int, pairs: int, device: torch.device) -> torch.Tensor:
         """(first row, row count, request) triples for the multi-row kernel, heaviest first.
 
-        Each tile holds consecutive rows of one request, at most 64 (row, query
+        Each tile holds consecutive rows of one request, at most ``pairs`` (row, query
         head) pairs; tiles ending at later positions (more context) come first.
         """
-        key = -group
+        key = (-group, pairs)
         found = self.work.get(key)
         if found is None:
-            per_tile = max(1, PREFILL_PAIRS // group)
+            per_tile = max(1, pairs // group)
             tiles = []
             first = 0
             for request, (count, length) in enumerate(zip(self.rows, self.kv_lengths)):
@@ -579,13 +580,14 @@ def attend_with(
     if prefill:
         if not isinstance(step, HipAttentionPlan):
             raise BackendError(f"{op}: the multi-row kernel needs a planned step", context={"op": op})
-        if heads // kv_heads > PREFILL_PAIRS:
+        pairs = PREFILL_PAIRS[buffers.head_dim]
+        if heads // kv_heads > pairs:
             raise BackendError(
                 f"{op}: {heads // kv_heads} query heads per key/value head exceed the multi-row "
-                f"kernel's tile of {PREFILL_PAIRS}",
+                f"kernel's tile of {pairs}",
                 context={"op": op, "argument": "q"},
             )
-        tiles = step.prefill_tiles(heads // kv_heads, device)
+        tiles = step.prefill_tiles(heads // kv_heads, pairs, device)
         _lib.check(
             op,
             lib.ayk_paged_prefill(

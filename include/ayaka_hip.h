@@ -166,13 +166,19 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
  * [0, positions[i]] of its request's context; rows of a request with
  * kv_lengths 0 get zeros. tiles lists n_tiles (first_row, row_count, request)
  * int32 triples: consecutive rows of one request with row_count * (num_heads /
- * num_kv_heads) <= 64, covering every row once. One workgroup per (tile,
+ * num_kv_heads) <= ayk_paged_prefill_tile_pairs(head_dim), covering every row
+ * once (rows past that many pairs are not computed). One workgroup per (tile,
  * key/value head) loads each chunk of the context once into LDS for all its
  * rows and query heads; q.k and P.V run on the matrix cores with fp32
  * accumulation. Replaces the reference's per-request SDPA loop,
  * python/ayaka/ops/backends/torch/attention.py:209-234, and flashinfer's batch
  * prefill (python/ayaka/ops/backends/flashinfer/attention.py:150-152, :253-266).
  */
+/* (row, query head) pairs one tile of ayk_paged_prefill may hold: 128 for head_dim
+ * 64 and 128, 64 for 256, 0 for a width with no kernel. No reference counterpart: it
+ * sizes the tiles the caller builds. */
+int ayk_paged_prefill_tile_pairs(int32_t head_dim);
+
 int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
                       const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
                       const int32_t* positions, const int32_t* tiles, int32_t n_tiles, int32_t n_rows,

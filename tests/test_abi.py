@@ -21,12 +21,21 @@ def declared() -> list[str]:
 
 def test_every_declared_function_is_exported_and_bound() -> None:
     names = declared()
-    assert len(names) == 11
+    assert len(names) == 12
     lib = _lib.lib()
     for name in names:
         assert hasattr(lib, name), name
     assert sorted(names) == sorted(_lib.EXPORTS)
     assert lib.ayk_abi_version() == _lib.ABI_VERSION
+
+
+def test_multi_row_tile_capacity_matches_the_host() -> None:
+    from ayaka_amd.hip import attention as hip_attention
+
+    lib = _lib.lib()
+    for head_dim, pairs in hip_attention.PREFILL_PAIRS.items():
+        assert lib.ayk_paged_prefill_tile_pairs(head_dim) == pairs
+    assert lib.ayk_paged_prefill_tile_pairs(96) == 0
 
 
 def test_workspace_size() -> None:
