@@ -82,7 +82,7 @@ __device__ __forceinline__ void split_weights(const float (&w)[8], u32x4& hi, u3
 }
 
 template <int D, bool BF16, bool KV8>
-__global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(const AttnParams p, const int32_t* tiles) {
+__global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const AttnParams p, const int32_t* tiles) {
   using E = Elem<BF16>;
   constexpr int THREADS = kPrefillThreads;
   constexpr int PT = D == 256 ? 1 : 2;          // 16-pair groups per wave
