@@ -119,8 +119,9 @@ __device__ __forceinline__ const uint16_t* kv_at(const uint16_t* base, int64_t e
 // Raw loads and decoding are separate, so prefetched chunks stay in flight: a
 // decode at the load would make the wave wait for the data right away.
 // The 8 elements at element offset `off` from `base` (see kv_at) as loaded:
-// 16 bytes of fp16/bf16, or 8 bytes of fp8 codes. Nontemporal: the cache is
-// streamed once per call.
+// 16 bytes of fp16/bf16, or 8 bytes of fp8 codes. Nontemporal (STREAM) where
+// the cache is read once per call (decode); plain where workgroups share it
+// (the multi-row kernel's tiles of one request and head read the same chunks).
 template <bool KV8>
 struct KvRaw {
   typedef u32x4 T;
@@ -130,12 +131,12 @@ struct KvRaw<true> {
   typedef u32x2 T;
 };
 
-template <bool KV8>
+template <bool KV8, bool STREAM = true>
 __device__ __forceinline__ typename KvRaw<KV8>::T load_kv_raw(const uint16_t* base, uint32_t off) {
-  if constexpr (KV8)
-    return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(base) + off));
-  else
-    return stream_load(base + off);
+  const auto* p8 = reinterpret_cast<const uint8_t*>(base) + (KV8 ? off : 2 * (size_t)off);
+  typedef typename KvRaw<KV8>::T T;
+  if constexpr (STREAM) return __builtin_nontemporal_load(reinterpret_cast<const T*>(p8));
+  else return *reinterpret_cast<const T*>(p8);
 }
 
 // Loaded elements as 8 packed compute-type values (4 pairs).

@@ -218,8 +218,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
         const int tv = min(s0 + ci * CH + vpiece_pos(u), s1 - 1);
         const uint32_t bk = (uint32_t)s_tbl[(tk >> shift) - b0];
         const uint32_t bv = (uint32_t)s_tbl[(tv >> shift) - b0];
-        kr[u] = load_kv_raw<KV8>(kbase, bk * block_stride + (uint32_t)(tk & bs_mask) * token_stride + piece_c * 8);
-        vr[u] = load_kv_raw<KV8>(vbase, bv * block_stride + (uint32_t)(tv & bs_mask) * token_stride + vpiece_c * 8);
+        kr[u] = load_kv_raw<KV8, false>(kbase, bk * block_stride + (uint32_t)(tk & bs_mask) * token_stride + piece_c * 8);
+        vr[u] = load_kv_raw<KV8, false>(vbase, bv * block_stride + (uint32_t)(tv & bs_mask) * token_stride + vpiece_c * 8);
       }
     };
     auto stage_chunk = [&](int buf) {
