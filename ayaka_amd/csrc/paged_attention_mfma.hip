@@ -2,7 +2,8 @@
 //
 // Same semantics, grid and outputs as the DPP kernel in paged_attention.hip (a
 // workgroup per (row, partition), one wave per key/value head); only the way a
-// wave turns a chunk of 16 keys into weights differs:
+// wave turns a chunk of 16 keys into weights differs. The library runs it from 3
+// query heads per wave, and for every fp8 cache:
 //
 //  * Keys are loaded like the values -- 256 contiguous bytes per token, the
 //    pattern HBM streams best -- and staged through a per-wave LDS tile, from
@@ -18,9 +19,11 @@
 //  * P.V stays on the VALU in fp32 (a bf16 P would cost ~2e-3 relative error),
 //    with the value layout of the DPP kernel: lane (r, c) holds 8 elements of
 //    tokens j*TPL + r.
+//  * fp8 caches (KV8) are decoded at their use; a chunk then holds two 16-token
+//    tiles, so a wave keeps as many bytes in flight as with 16-bit caches.
 //
-// With 6-8 query heads per key/value head this removes the per-token dot2 and
-// butterfly work that makes the DPP kernel VALU-bound.
+// This removes the per-token dot2 and butterfly work that grows with the group
+// in the DPP kernel, and reads keys as whole 256-byte token rows.
 #include "attention_common.h"
 
 namespace ayk {

@@ -21,9 +21,9 @@
 //    v_mfma_f32_16x16x32 with P^T taken straight from the lane's scores (its
 //    8 k-slots are positions 4*(l/16)+i of two adjacent 16-position tiles) and
 //    V^T read from a transposed LDS tile in that same position order. P is split
-//    into a bf16 (or fp16) high part and the rounded residual, two MFMAs, which
-//    keeps the product at fp32-level accuracy (one 16-bit P would cost ~2e-3
-//    relative).
+//    by truncation into a 16-bit high part and the 16-bit remainder, two MFMAs,
+//    which keeps the product at fp32-level accuracy (one 16-bit P would cost
+//    ~2e-3 relative).
 //  * The transposed value tile is written with 32-bit LDS stores: each thread
 //    carries the same 8 elements of two adjacent positions. Its row stride and the
 //    threads' value-load mapping keep stores and reads nearly free of bank
