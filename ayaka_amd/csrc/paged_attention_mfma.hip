@@ -67,6 +67,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   __shared__ int s_tbl[kTableCap];
   __shared__ u32x4 s_k[kMaxWaves][MT * CPT];       // a tile's keys, swizzled (see key_slot)
   __shared__ float s_p[kMaxWaves][2][MT][PW];      // a tile's weights, double-buffered
+  static_assert(SUB >= 1 && CH % TPL == 0 && NL == SUB * NL1, "chunk shape");
   __shared__ float s_alpha[kMaxWaves][PW];
   __shared__ int s_last;
 
@@ -154,7 +155,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
       for (int sub = 0; sub < SUB; ++sub) {
         const int tb = s0 + ci * CH + sub * MT;
         const bool tail = tb + MT > s1;
-        const int pb = SUB == 1 ? buf : sub;  // the weight buffer of this tile
+        // The weight buffer of this tile: chunks alternate (SUB 1) or tiles of a chunk do.
+        // s_p holds 2 buffers; a wave's LDS accesses run in program order, so a buffer
+        // is rewritten only after its previous tile's reads.
+        const int pb = (SUB == 1 ? buf : sub) & 1;
         // Keys to LDS in the load layout, back out in the MFMA operand layout.
 #pragma unroll
         for (int j = 0; j < NL1; ++j)
