@@ -300,6 +300,34 @@ __device__ __forceinline__ void store_head(const AttnParams& p, int row, int par
   }
 }
 
+// As store_head, from a lane of the transposed P.V layout: o[t] holds elements
+// 16t + 4g + i (i < 4) of head `head`; the lanes g = 0..3 of a head hold all of it.
+template <int D, bool BF16, bool SPLIT>
+__device__ __forceinline__ void store_head_t(const AttnParams& p, int row, int part, int np, int head, int g,
+                                             const f32x4 (&o)[D / 16], float m, float l) {
+  using E = Elem<BF16>;
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  const int64_t head_row = (int64_t)row * p.num_heads + head;
+  if (SPLIT && np > 1) {
+    float* po = p.part_o + (head_row * p.max_partitions + part) * D + 4 * g;
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) *reinterpret_cast<f32x4*>(po + 16 * t) = o[t] * inv;
+    if (g == 0) {
+      float* pml = p.part_ml + (head_row * p.max_partitions + part) * 2;
+      pml[0] = m;
+      pml[1] = l;
+    }
+  } else {
+    uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D + 4 * g;
+#pragma unroll
+    for (int t = 0; t < D / 16; ++t) {
+      const f32x4 v = o[t] * inv;
+      *reinterpret_cast<u32x2*>(out + 16 * t) =
+          u32x2{E::round(v.x) | (E::round(v.y) << 16), E::round(v.z) | (E::round(v.w) << 16)};
+    }
+  }
+}
+
 // Merge partitions [0, np) of heads [head_lo, head_hi) of `row` and round into
 // out: o = sum_i w_i o_i / sum_i w_i with w_i = l_i 2^(m_i - max m), folded in
 // partition order (so the result does not depend on which workgroup merges).

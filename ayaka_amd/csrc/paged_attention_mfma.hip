@@ -30,6 +30,8 @@ namespace ayk {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 template <bool BF16>
 __device__ __forceinline__ f32x4 mfma_qk(u32x4 k, u32x4 q, f32x4 acc) {
@@ -40,6 +42,51 @@ __device__ __forceinline__ f32x4 mfma_qk(u32x4 k, u32x4 q, f32x4 acc) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, k),
                                                   __builtin_bit_cast(f16x8, q), acc, 0, 0, 0);
   }
+}
+
+// O^T += V^T P^T for a 16 x 16 tile over 16 tokens: v_mfma_f32_16x16x16.
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma_pv(u32x2 v, u32x2 w, f32x4 acc) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, v), __builtin_bit_cast(i16x4, w),
+                                                     acc, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, v), __builtin_bit_cast(f16x4, w), acc,
+                                                 0, 0, 0);
+  }
+}
+
+// 4 elements of a 16-lane group's rows, transposed: lane o of each group of 16
+// receives element o % 4 of the 8-byte rows read by lanes o / 4, o / 4 + 4,
+// o / 4 + 8 and o / 4 + 12 of its group (ds_read_b64_tr_b16, measured).
+__device__ __forceinline__ u32x2 lds_read_transposed(const uint16_t* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p)));
+}
+
+// Split 4 fp32 weights w (finite, >= 0) into packed 16-bit high parts and packed
+// 16-bit parts of the remainder, both by truncation: |w - h - l| < 2^-14 w (bf16).
+template <bool BF16>
+__device__ __forceinline__ void split_weights4(const float (&w)[4], u32x2& hi, u32x2& lo) {
+  uint32_t h[2], r[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float a = w[2 * i], b = w[2 * i + 1];
+    if constexpr (BF16) {
+      const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+      h[i] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
+      const float ra = a - __uint_as_float(ua & 0xffff0000u);
+      const float rb = b - __uint_as_float(ub & 0xffff0000u);
+      r[i] = __builtin_amdgcn_perm(__float_as_uint(rb), __float_as_uint(ra), 0x07060302u);
+    } else {
+      const auto hv = __builtin_amdgcn_cvt_pkrtz(a, b);
+      h[i] = __builtin_bit_cast(uint32_t, hv);
+      r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a - (float)hv[0], b - (float)hv[1]));
+    }
+  }
+  hi = u32x2{h[0], h[1]};
+  lo = u32x2{r[0], r[1]};
 }
 
 // Order the LDS traffic of one wave: lanes read what other lanes of the same
@@ -62,13 +109,15 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   constexpr int TPL = kWave / CPT;  // tokens per load instruction
   constexpr int NL1 = MT / TPL;     // load instructions per tile, for K and for V
   constexpr int NL = CH / TPL;      // load instructions per chunk
-  constexpr int PW = ((GC + 3) / 4) * 4;  // weights per token in LDS, padded to float4
+  constexpr int DT = D / 16;        // 16-element slices of head_dim for P.V
+  // A tile's values in LDS, token-major, rows VP elements apart: the transposing
+  // reads of one instruction (16 rows, 32 bytes each) then cover the banks evenly.
+  constexpr int VP = D + 16;
 
   __shared__ int s_tbl[kTableCap];
   __shared__ u32x4 s_k[kMaxWaves][MT * CPT];       // a tile's keys, swizzled (see key_slot)
-  __shared__ float s_p[kMaxWaves][2][MT][PW];      // a tile's weights, double-buffered
+  __shared__ __attribute__((aligned(16))) uint16_t s_v[kMaxWaves][MT * VP];  // a tile's values
   static_assert(SUB >= 1 && CH % TPL == 0 && NL == SUB * NL1, "chunk shape");
-  __shared__ float s_alpha[kMaxWaves][PW];
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
@@ -118,11 +167,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
 
   float m_h = kNoScore;  // running max of head mt (same in its 4 lanes)
   float l_h = 0.f;       // this lane's share of head mt's weight sum
-  float o[GC][8];
+  // O^T: o[t] holds elements 16t + 4*mq + i (i < 4) of head mt's unnormalised output.
+  f32x4 o[DT];
 #pragma unroll
-  for (int g = 0; g < GC; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+  for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
   const int shift = p.bs_shift;
@@ -150,19 +198,19 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     };
 
     typedef typename KvRaw<KV8>::T Raw;
-    auto consume = [&](int ci, int buf, const Raw(&kc)[NL], const Raw(&vc)[NL]) {
+    auto consume = [&](int ci, const Raw(&kc)[NL], const Raw(&vc)[NL]) {
 #pragma unroll
       for (int sub = 0; sub < SUB; ++sub) {
         const int tb = s0 + ci * CH + sub * MT;
         const bool tail = tb + MT > s1;
-        // The weight buffer of this tile: chunks alternate (SUB 1) or tiles of a chunk do.
-        // s_p holds 2 buffers; a wave's LDS accesses run in program order, so a buffer
-        // is rewritten only after its previous tile's reads.
-        const int pb = (SUB == 1 ? buf : sub) & 1;
-        // Keys to LDS in the load layout, back out in the MFMA operand layout.
+        // The tile's keys (swizzled, read back as MFMA operands) and values (token-major,
+        // read back transposed) to LDS. A wave's LDS accesses run in program order, so
+        // these stores follow the previous tile's reads.
 #pragma unroll
-        for (int j = 0; j < NL1; ++j)
+        for (int j = 0; j < NL1; ++j) {
           s_k[wave][key_slot(j * TPL + r, c)] = kv_pairs<KV8, BF16>(kc[sub * NL1 + j]);
+          *reinterpret_cast<u32x4*>(&s_v[wave][(j * TPL + r) * VP + c * 8]) = kv_pairs<KV8, BF16>(vc[sub * NL1 + j]);
+        }
         wave_lds_sync();
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -178,17 +226,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         if (__builtin_amdgcn_ballot_w64(mx > m_h + kRescaleSlack)) {
           const float mn = fmaxf(m_h, mx);
-          const float alpha = fast_exp2(m_h - mn);
+          const float alpha = fast_exp2(m_h - mn);  // head mt's, and o[] holds head mt
           l_h *= alpha;
           m_h = mn;
-          if (mq == 0 && mt < PW) s_alpha[wave][mt] = alpha;
-          wave_lds_sync();
 #pragma unroll
-          for (int g = 0; g < GC; ++g) {
-            const float a = s_alpha[wave][g];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[g][e] *= a;
-          }
+          for (int t = 0; t < DT; ++t) o[t] *= alpha;
         }
         float w[4];
 #pragma unroll
@@ -196,31 +238,17 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
           w[i] = fast_exp2(sc[i] - m_h);
           l_h += w[i];
         }
-        if (mt < PW) {
+        // O^T += V^T P^T: P^T is the lane's own weights (tokens 4*mq + i of head mt, the
+        // B operand layout); V^T comes transposed from the token-major tile (lane mt of
+        // group mq reads 4 elements of token 4*mq + mt / 4). Positions past the context
+        // hold real (clamped) values with weight 0.
+        u32x2 phi, plo;
+        split_weights4<BF16>(w, phi, plo);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) s_p[wave][pb][4 * mq + i][mt] = w[i];
-        }
-        wave_lds_sync();
-#pragma unroll
-        for (int j = 0; j < NL1; ++j) {
-          float pw[PW];
-#pragma unroll
-          for (int g4 = 0; g4 < PW; g4 += 4) {
-            const f32x4 v4 = *reinterpret_cast<const f32x4*>(&s_p[wave][pb][j * TPL + r][g4]);
-            pw[g4] = v4.x; pw[g4 + 1] = v4.y; pw[g4 + 2] = v4.z; pw[g4 + 3] = v4.w;
-          }
-          float vf[8];
-          kv_floats<KV8, BF16>(vc[sub * NL1 + j], vf);
-          if (tail && tb + j * TPL + r >= s1) {
-            // A slot past the context may hold anything, NaN included, and 0 * NaN is NaN.
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vf[e] = 0.f;
-          }
-#pragma unroll
-          for (int g = 0; g < GC; ++g) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pw[g], vf[e], o[g][e]);
-          }
+        for (int t = 0; t < DT; ++t) {
+          const u32x2 va = lds_read_transposed(&s_v[wave][(4 * mq + (mt >> 2)) * VP + t * 16 + 4 * (mt & 3)]);
+          o[t] = mfma_pv<BF16>(va, phi, o[t]);
+          o[t] = mfma_pv<BF16>(va, plo, o[t]);
         }
       }
     };
@@ -242,34 +270,22 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
       offsets(min(ci + 1, nch - 1), offB);
 #pragma unroll
       for (int j = 0; j < NL; ++j) kB[j] = load_kv_raw<KV8>(kbase, offB[j]);
-      consume(ci, 0, kA, vc);
+      consume(ci, kA, vc);
       if (++ci >= nch) break;
 #pragma unroll
       for (int j = 0; j < NL; ++j) vc[j] = load_kv_raw<KV8>(vbase, offB[j]);
       offsets(min(ci + 1, nch - 1), offA);
 #pragma unroll
       for (int j = 0; j < NL; ++j) kA[j] = load_kv_raw<KV8>(kbase, offA[j]);
-      consume(ci, 1, kB, vc);
+      consume(ci, kB, vc);
       ++ci;
     }
   }
   if (active) {
-    // Head mt's weight sum over the wave's 4 token groups; the value lanes' partial
-    // sums share the wave's running max, so they add without rescaling.
+    // Head mt's weight sum over the wave's 4 token groups (its lanes share m_h).
     l_h += __shfl_xor(l_h, 16);
     l_h += __shfl_xor(l_h, 32);
-#pragma unroll
-    for (int st = CPT; st < kWave; st <<= 1)
-#pragma unroll
-      for (int g = 0; g < GC; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] += __shfl_xor(o[g][e], st);
-#pragma unroll
-    for (int g = 0; g < GC; ++g) {
-      const float mg = __shfl(m_h, g);
-      const float lg = __shfl(l_h, g);
-      if (r == 0) store_head<D, BF16, SPLIT>(p, row, wg.part, np, h0 + g, c, o[g], mg, lg);
-    }
+    if (mt < GC) store_head_t<D, BF16, SPLIT>(p, row, wg.part, np, h0 + mt, mq, o, m_h, l_h);
   }
   if constexpr (SPLIT) {
     if (np > 1 && p.arrivals) {
