@@ -154,14 +154,14 @@ int compute_units() {
 // Whether v2 merges its partitions inside the partition kernel (rather than in
 // a reduce kernel) for a grid of `workgroups`. Measured on MI355X: the in-kernel
 // merge costs each workgroup a device-scope release (an L2 write-back) and the
-// last one of a row the merge; when the whole grid fits about one round of the
-// GPU these land together in the kernel's tail and cost more (~10 us) than the
-// reduce launch (~5 us), while over several rounds they overlap the streaming
-// of later workgroups. A grid of a few dozen workgroups is latency-bound, and
-// there the second launch is the larger cost.
+// last one of a row the merge; when the whole grid runs in one round of the GPU
+// (C2, C3, C4 at up to 256 workgroups) these land together in the kernel's tail
+// and cost more (~10 us) than the reduce launch (~5 us), while past one round
+// (C5) they overlap the streaming of later workgroups. A grid of a few dozen
+// workgroups is latency-bound, and there the second launch is the larger cost.
 bool merge_in_kernel(int64_t workgroups) {
   const int64_t cus = compute_units();
-  return workgroups > 2 * cus || workgroups <= cus / 4;
+  return workgroups > cus || workgroups <= cus / 4;
 }
 
 // Heads per wave from which the library picks the matrix-core q.k kernel.

@@ -66,9 +66,14 @@ PARTITION_SIZE = 512
 #: Partition sizes an eagerly planned step chooses from (multiples of 64).
 PARTITION_CANDIDATES = (64, 128, 192, 256, 320, 384, 448, 512, 576, 640, 704, 768, 896, 1024, 1280, 1536,
                         2048, 3072, 4096, 8192, 16384)
-#: Fixed cost of one workgroup, in positions of streaming (start-up, merge, partial write):
-#: an extra round of 256 workgroups measured ~12 µs on the C3 shape, ~80 positions at 6.4/µs.
-WORKGROUP_COST = 80
+#: Fixed cost of one workgroup, in positions of streaming (start-up, merge, partial write),
+#: by bytes per cache element. Fitted to measured partition-size sweeps (256 ... 4096
+#: positions) of the C3, C4 and C5 shapes: 320 for 16-bit caches (the modelled finish
+#: time then tracks C5's ragged curve with correlation 0.87, against 0.11 at 80) and 160
+#: for fp8 caches (0.99); with them the model picks the fastest measured size of all
+#: three shapes for both.
+WORKGROUP_COSTS = {2: 320, 1: 160}
+WORKGROUP_COST = WORKGROUP_COSTS[2]
 #: XCDs of one MI355X; workgroups are dealt to them round-robin.
 XCDS = 8
 #: Heads per wave from which the library runs q.k on the matrix cores (mirrors the C library).
@@ -110,15 +115,16 @@ class HipAttentionPlan:
     row_lengths: tuple[int, ...] = ()
     # v2 work lists built by the step's first attend, keyed by partition size, for the later layers
     work: dict[int, torch.Tensor] = field(default_factory=dict, compare=False, repr=False)
-    splits: dict[tuple[int, int], Split] = field(default_factory=dict, compare=False, repr=False)
+    splits: dict[tuple[int, int, int], Split] = field(default_factory=dict, compare=False, repr=False)
 
-    def split_for(self, num_kv_heads: int, group: int) -> Split:
-        """The step's launch for this head shape, chosen once and reused by every layer."""
-        key = (num_kv_heads, group)
+    def split_for(self, num_kv_heads: int, group: int, kv_bytes: int = 2) -> Split:
+        """The step's launch for this head shape and cache element size, chosen once and
+        reused by every layer."""
+        key = (num_kv_heads, group, kv_bytes)
         found = self.splits.get(key)
         if found is None:
             found = choose_split(len(self.row_lengths), num_kv_heads, group, self.max_length,
-                                 row_lengths=self.row_lengths)
+                                 row_lengths=self.row_lengths, kv_bytes=kv_bytes)
             self.splits[key] = found
         return found
 
@@ -307,9 +313,9 @@ def uses_matrix_cores(group: int) -> bool:
 
 def merge_site_for(workgroups: int) -> str:
     """Where the library merges the v2 partitions of a grid of ``workgroups``: ``"in-kernel"``
-    above two rounds of the compute units or at a quarter round at most, ``"reduce-kernel"``
+    above one round of the compute units or at a quarter round at most, ``"reduce-kernel"``
     otherwise (the rule of ``merge_in_kernel`` in ``api.hip``)."""
-    return "in-kernel" if workgroups > 2 * COMPUTE_UNITS or workgroups <= COMPUTE_UNITS // 4 else "reduce-kernel"
+    return "in-kernel" if workgroups > COMPUTE_UNITS or workgroups <= COMPUTE_UNITS // 4 else "reduce-kernel"
 
 
 def merge_site(num_kv_heads: int, group: int, step: "HipAttentionPlan", partition_size: int) -> str:
@@ -332,15 +338,16 @@ class Split:
     partitions: int
 
 
-def schedule_makespan(row_lengths: list[int], size: int, groups: int = 1) -> int:
+def schedule_makespan(row_lengths: list[int], size: int, groups: int = 1, cost: int | None = None) -> int:
     """Modelled finish time, in positions, of v2 over partitions of ``size``.
 
     Workgroups start in work-list order (longest partition first); the GPU hands
     workgroup i to XCD i mod 8 and each XCD to whichever of its 32 CUs frees up
     first, one 8-wave workgroup per CU at a time. A workgroup costs its
-    positions plus :data:`WORKGROUP_COST` (start-up, the final merge, writing the
-    partial).
+    positions plus ``cost`` (default :data:`WORKGROUP_COST`: start-up, the final
+    merge, writing the partial).
     """
+    cost = WORKGROUP_COST if cost is None else cost
     items: list[int] = []
     for length in row_lengths:
         full, rest = divmod(length, size)
@@ -353,7 +360,7 @@ def schedule_makespan(row_lengths: list[int], size: int, groups: int = 1) -> int
     loads = [[0] * per_xcd for _ in range(XCDS)]
     for index, item in enumerate(items):
         heap = loads[index % XCDS]
-        heapq.heapreplace(heap, heap[0] + item + WORKGROUP_COST)
+        heapq.heapreplace(heap, heap[0] + item + cost)
     return max(max(heap) for heap in loads)
 
 
@@ -368,13 +375,13 @@ def fits_schedule(lengths: list[int], size: int, groups: int = 1) -> bool:
     return items <= MAX_ROUNDS * COMPUTE_UNITS
 
 
-def _best_size(lengths: list[int], max_length: int, groups: int) -> int:
+def _best_size(lengths: list[int], max_length: int, groups: int, kv_bytes: int = 2) -> int:
     """The candidate partition size with the smallest :func:`schedule_makespan`."""
     best: tuple[int, int] | None = None
     for size in PARTITION_CANDIDATES:
         if not fits_schedule(lengths, size, groups) and size != PARTITION_CANDIDATES[-1]:
             continue
-        cost = schedule_makespan(lengths, size, groups)
+        cost = schedule_makespan(lengths, size, groups, WORKGROUP_COSTS[kv_bytes])
         if best is None or cost < best[0]:
             best = (cost, size)
         if size >= max_length:
@@ -390,6 +397,7 @@ def choose_split(
     max_length: int,
     total_length: int | None = None,
     row_lengths: tuple[int, ...] | None = None,
+    kv_bytes: int = 2,
 ) -> Split:
     """Pick v1 or v2 and the partition size from the step's shape.
 
@@ -399,7 +407,8 @@ def choose_split(
     is fixed, on ``n_rows`` rows of ``max_length``. The choice is cached under a
     coarse signature of the lengths (row count, longest row to a power of two,
     total to 4 significant bits), which successive decode steps -- every length
-    one longer than the step before -- keep hitting.
+    one longer than the step before -- keep hitting. ``kv_bytes`` is the cache's bytes
+    per element (2, or 1 for fp8), which sets the modelled workgroup cost.
     """
     del total_length
     if max_length <= 0:
@@ -409,21 +418,21 @@ def choose_split(
     total = sum(lengths)
     # The total to 4 significant bits, the longest row to a power of two, the row count.
     top = max(total.bit_length() - 4, 0)
-    key = (groups, len(lengths), max_length.bit_length(), total >> top, top)
+    key = (groups, kv_bytes, len(lengths), max_length.bit_length(), total >> top, top)
     size = _split_cache.get(key)
     if size is None:
         if len(_split_cache) > 4096:
             _split_cache.clear()
-        size = _best_size(lengths, max_length, groups)
+        size = _best_size(lengths, max_length, groups, kv_bytes)
         _split_cache[key] = size
     if max_length <= size:
         return Split(0, 0)
     return Split(size, -(-max_length // size))
 
 
-def choose_partitions(n_rows: int, num_kv_heads: int, group: int, max_length: int) -> int:
+def choose_partitions(n_rows: int, num_kv_heads: int, group: int, max_length: int, kv_bytes: int = 2) -> int:
     """Partitions for a step known only by its longest context, as graph metadata is (0 = v1)."""
-    return choose_split(n_rows, num_kv_heads, group, max_length).partitions
+    return choose_split(n_rows, num_kv_heads, group, max_length, kv_bytes=kv_bytes).partitions
 
 
 _workspaces: dict[torch.device, torch.Tensor] = {}
@@ -627,8 +636,9 @@ def attend_with(
         float(scale),
     )
     if partitions is None:
-        split = step.split_for(kv_heads, group) if isinstance(step, HipAttentionPlan) else \
-            choose_split(n_rows, kv_heads, group, max_length)
+        kv_bytes = 1 if buffers.codec == FP8_E4M3_CODEC else 2
+        split = step.split_for(kv_heads, group, kv_bytes) if isinstance(step, HipAttentionPlan) else \
+            choose_split(n_rows, kv_heads, group, max_length, kv_bytes=kv_bytes)
         partitions, partition_size = split.partitions, split.partition_size
     partition_size = partition_size or PARTITION_SIZE
     if partitions and partitions * partition_size < max_length:

@@ -246,7 +246,7 @@ def main() -> int:
     out = torch.empty_like(step.q)
     nbytes = workloads.algorithmic_bytes(cfg, kv_bytes)
     max_len = max(cfg.lengths)
-    auto = meta.plan.split_for(cfg.kv_heads, cfg.heads // cfg.kv_heads)  # what attend will launch
+    auto = meta.plan.split_for(cfg.kv_heads, cfg.heads // cfg.kv_heads, kv_bytes)  # what attend will launch
     # The headline ("auto", the launch attend picks) runs last, on a GPU warmed by the others.
     # name: (partitions, partition size, where v2 merges: None = the library's choice)
     launches = {
