@@ -98,15 +98,13 @@ __device__ __forceinline__ u32x4 stream_load(const uint16_t* p) {
 // fp8 KV caches (codec "fp8_e4m3": OCP e4m3, the float8_e4m3fn format).
 //
 // Two codes of a word (its low or high half) to a packed pair of the compute
-// type. v_cvt_pk_f32_fp8 decodes them to fp32; every e4m3 value (|x| <= 448,
-// at most 4 significant bits, down to 2^-9) is exactly a bf16 and an fp16
-// value, so taking the top half of the fp32 (bf16) or converting with either
-// rounding (fp16) loses nothing. The NaN code decodes to NaN.
+// type, in one v_cvt_scalef32_pk_{bf16,f16}_fp8 with scale 1: every e4m3 value
+// (|x| <= 448, at most 4 significant bits, down to 2^-9) is exactly a bf16 and
+// an fp16 value, so the conversion loses nothing. The NaN code decodes to NaN.
 template <bool BF16, bool HIGH>
 __device__ __forceinline__ uint32_t e4m3_pair(uint32_t word) {
-  const f32x2 f = __builtin_amdgcn_cvt_pk_f32_fp8((int)word, HIGH);
-  if constexpr (BF16) return __builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u);
-  else return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(f[0], f[1]));
+  if constexpr (BF16) return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, 1.0f, HIGH));
+  else return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.0f, HIGH));
 }
 
 // Address of element `elem` of a cache: 2-byte elements, or 1-byte fp8 codes.
