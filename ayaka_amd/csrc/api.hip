@@ -123,6 +123,9 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
   if ((uint64_t)c.num_blocks * (uint64_t)p.block_stride > UINT32_MAX)
     return fail(AYK_ERR_UNSUPPORTED, "%s: a cache of %d blocks of %lld elements exceeds 32-bit element offsets",
                 op, c.num_blocks, (long long)p.block_stride);
+  if (p.token_stride >= (1 << 24))
+    return fail(AYK_ERR_UNSUPPORTED, "%s: a token stride of %lld elements exceeds 2^24", op,
+                (long long)p.token_stride);
   p.n_rows = c.n_rows;
   p.num_heads = c.num_heads;
   p.group = group;

@@ -442,19 +442,28 @@ __device__ __forceinline__ void store_zero_rows(const AttnParams& p, int row, in
   }
 }
 
-// Stage the block-table entries of positions [s0, s1) in LDS (ids outside the
-// pool become the padding block 0); returns the first staged block index.
-__device__ __forceinline__ int stage_table(const AttnParams& p, const int32_t* tbl, int* s_tbl, int s0, int s1,
+// Stage the block-table entries of positions [s0, s1) in LDS as element offsets
+// of their blocks (block id x block stride; ids outside the pool become the
+// padding block 0); returns the first staged block index. The host checks that
+// every offset in the pool fits 32 bits.
+__device__ __forceinline__ int stage_table(const AttnParams& p, const int32_t* tbl, uint32_t* s_tbl, int s0, int s1,
                                            int tid, int threads) {
   const int b0 = s0 >> p.bs_shift;
   const int nb = ((s1 - 1) >> p.bs_shift) - b0 + 1;
   __syncthreads();  // the previous segment is done with s_tbl
   for (int i = tid; i < nb; i += threads) {
     const int b = tbl[b0 + i];
-    s_tbl[i] = ((unsigned)b < (unsigned)p.num_blocks) ? b : 0;
+    s_tbl[i] = ((unsigned)b < (unsigned)p.num_blocks) ? (uint32_t)b * (uint32_t)p.block_stride : 0u;
   }
   __syncthreads();
   return b0;
+}
+
+// Element offset of position t within its block: (t mod block size) x token
+// stride on the full-rate 24-bit multiplier (both factors are below 2^24: the
+// host refuses larger token strides).
+__device__ __forceinline__ uint32_t in_block(int t, int bs_mask, uint32_t token_stride) {
+  return __umul24((uint32_t)(t & bs_mask), token_stride);
 }
 
 }  // namespace ayk

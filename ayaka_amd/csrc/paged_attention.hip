@@ -41,7 +41,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
   constexpr int TPL = kWave / LPT;   // tokens per load instruction
   constexpr int CH = TPL * NLD;      // tokens per chunk
 
-  __shared__ int s_tbl[kTableCap];
+  __shared__ uint32_t s_tbl[kTableCap];
   __shared__ int s_last;
 
   const int tid = threadIdx.x;
@@ -100,7 +100,6 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
   const int shift = p.bs_shift;
   const int bs_mask = (1 << shift) - 1;
   const int seg_len = (((kTableCap - 1) << shift) / CH) * CH;
-  const uint32_t block_stride = (uint32_t)p.block_stride;  // the host checks the pool fits 32 bits
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + c * 8;
@@ -118,8 +117,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
 #pragma unroll
       for (int j = 0; j < NLD; ++j) {
         const int t = min(s0 + ci * CH + j * TPL + r, s1 - 1);
-        const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
-        dst[j] = blk * block_stride + (uint32_t)(t & bs_mask) * token_stride;
+        dst[j] = s_tbl[(t >> shift) - b0] + in_block(t, bs_mask, token_stride);
       }
     };
 

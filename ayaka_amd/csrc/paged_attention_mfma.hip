@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   // reads of one instruction (16 rows, 32 bytes each) then cover the banks evenly.
   constexpr int VP = D + 16;
 
-  __shared__ int s_tbl[kTableCap];
+  __shared__ uint32_t s_tbl[kTableCap];
   __shared__ u32x4 s_k[kMaxWaves][MT * CPT];       // a tile's keys, swizzled (see key_slot)
   __shared__ __attribute__((aligned(16))) uint16_t s_v[kMaxWaves][MT * VP];  // a tile's values
   static_assert(SUB >= 1 && CH % TPL == 0 && NL == SUB * NL1, "chunk shape");
@@ -176,7 +176,6 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   const int shift = p.bs_shift;
   const int bs_mask = (1 << shift) - 1;
   const int seg_len = (((kTableCap - 1) << shift) / CH) * CH;
-  const uint32_t block_stride = (uint32_t)p.block_stride;
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride + c * 8);
@@ -192,8 +191,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
 #pragma unroll
       for (int j = 0; j < NL; ++j) {
         const int t = min(s0 + ci * CH + j * TPL + r, s1 - 1);
-        const uint32_t blk = (uint32_t)s_tbl[(t >> shift) - b0];
-        dst[j] = blk * block_stride + (uint32_t)(t & bs_mask) * token_stride;
+        dst[j] = s_tbl[(t >> shift) - b0] + in_block(t, bs_mask, token_stride);
       }
     };
 

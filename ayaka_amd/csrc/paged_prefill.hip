@@ -107,7 +107,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   constexpr int VNP = kWave / VSW;              // value position pairs per wave instruction
   static_assert(PER_THREAD % 2 == 0 && PIECES % THREADS == 0, "piece split");
 
-  __shared__ int s_tbl[kTableCap];
+  __shared__ uint32_t s_tbl[kTableCap];
   __shared__ u32x4 s_k[2][PIECES];
   __shared__ __attribute__((aligned(16))) uint32_t s_vt[2][D * VT2];
 
@@ -186,7 +186,6 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   const int shift = p.bs_shift;
   const int bs_mask = (1 << shift) - 1;
   const int seg_len = (((kTableCap - 1) << shift) / CH) * CH;
-  const uint32_t block_stride = (uint32_t)p.block_stride;
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride);
@@ -210,16 +209,25 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 
     typedef typename KvRaw<KV8>::T Raw;
     Raw kr[PER_THREAD], vr[PER_THREAD];
+    // Offsets of the pieces at positions t and t + 1 (t even: the chunk and segment
+    // starts are multiples of CH), clamped to the last position: past the end a
+    // real position is read, whose weight is 0. Both positions share a block
+    // unless blocks hold one position.
+    auto pair_offsets = [&](int t, uint32_t& o0, uint32_t& o1) {
+      const int t0 = min(t, s1 - 1), t1 = min(t + 1, s1 - 1);
+      o0 = s_tbl[(t0 >> shift) - b0] + in_block(t0, bs_mask, token_stride);
+      o1 = shift ? o0 + (t1 > t0 ? token_stride : 0u) : s_tbl[t1 - b0];
+    };
     auto load_chunk = [&](int ci) {
 #pragma unroll
-      for (int u = 0; u < PER_THREAD; ++u) {
-        // past the end: a real position, whose weight is 0
-        const int tk = min(s0 + ci * CH + piece_pos(u), s1 - 1);
-        const int tv = min(s0 + ci * CH + vpiece_pos(u), s1 - 1);
-        const uint32_t bk = (uint32_t)s_tbl[(tk >> shift) - b0];
-        const uint32_t bv = (uint32_t)s_tbl[(tv >> shift) - b0];
-        kr[u] = load_kv_raw<KV8, false>(kbase, bk * block_stride + (uint32_t)(tk & bs_mask) * token_stride + piece_c * 8);
-        vr[u] = load_kv_raw<KV8, false>(vbase, bv * block_stride + (uint32_t)(tv & bs_mask) * token_stride + vpiece_c * 8);
+      for (int u = 0; u < PER_THREAD; u += 2) {
+        uint32_t k0, k1, v0, v1;
+        pair_offsets(s0 + ci * CH + piece_pos(u), k0, k1);
+        pair_offsets(s0 + ci * CH + vpiece_pos(u), v0, v1);
+        kr[u] = load_kv_raw<KV8, false>(kbase, k0 + piece_c * 8);
+        kr[u + 1] = load_kv_raw<KV8, false>(kbase, k1 + piece_c * 8);
+        vr[u] = load_kv_raw<KV8, false>(vbase, v0 + vpiece_c * 8);
+        vr[u + 1] = load_kv_raw<KV8, false>(vbase, v1 + vpiece_c * 8);
       }
     };
     auto stage_chunk = [&](int buf) {
@@ -243,7 +251,9 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
     // Fold chunk ci (in LDS buffer buf) into every pair's running state.
     auto consume = [&](int ci, int buf) {
       const int tb = s0 + ci * CH;
-      const bool whole = tb + CH <= s1 && tb + CH - 1 <= wave_min_pos;  // uniform: no position masked
+      // uniform: no position masked (and, for folding the scale into the exponent,
+      // a scale >= 0, under which the largest raw score gives the largest scaled one)
+      const bool whole = tb + CH <= s1 && tb + CH - 1 <= wave_min_pos && scale_log2 >= 0.f;
       f32x4 acc[PTL][PT];
 #pragma unroll
       for (int pt = 0; pt < PTL; ++pt)
@@ -260,14 +270,15 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 #pragma unroll
       for (int j = 0; j < PT; ++j) {
         float mx = -INFINITY;
+        // the scale applied to a score in the exponent below (1 once the scores are scaled)
+        float sc = 1.f;
         if (whole) {
 #pragma unroll
           for (int pt = 0; pt < PTL; ++pt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              acc[pt][j][i] *= scale_log2;
-              mx = fmaxf(mx, acc[pt][j][i]);
-            }
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[pt][j][i]);
+          mx *= scale_log2;
+          sc = scale_log2;
         } else {
           // position tb + pt*16 + 4*mq + i is visible iff pt*16 + i <= lim
           const int lim = min(my_pos[j], s1 - 1) - tb - 4 * mq;
@@ -293,7 +304,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
         for (int pt = 0; pt < PTL; ++pt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float w = fast_exp2(acc[pt][j][i] - m[j]);
+            const float w = fast_exp2(__builtin_fmaf(acc[pt][j][i], sc, -m[j]));
             acc[pt][j][i] = w;
             l[j] += w;
           }
