@@ -56,6 +56,7 @@ hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles
                           bool kv8, hipStream_t stream);
 // The v2 log-sum-exp merge of the partitions of every (row, head).
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);
+hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);
 
 hipError_t launch_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
                                     const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,

@@ -413,6 +413,45 @@ hipError_t launch_attention_dpp(const AttnParams& p, int head_dim, int gc, bool 
   }
 }
 
+// Merge of the multi-row kernel's partitions: one workgroup per row, all its
+// query heads (a row's heads lie next to each other in the partials), so a step
+// of many rows launches one workgroup per row rather than per (row, head). Rows
+// with one partition were written by the partition kernel and rows of padding
+// requests were zeroed by it; both return at once.
+template <int D, bool BF16>
+__global__ __launch_bounds__(kReduceThreads) void row_reduce_kernel(const AttnParams p) {
+  constexpr int IPT = 4;
+  constexpr int HEADS_PER_PASS = kReduceThreads * IPT / (D / 4);
+  const int row = blockIdx.x;
+  int req, len;
+  row_context(p, row, req, len);
+  const int np = len > 0 ? (len - 1) / p.partition_size + 1 : 0;
+  if (np <= 1) return;
+  for (int h0 = 0; h0 < p.num_heads; h0 += HEADS_PER_PASS)
+    merge_partitions<D, IPT, BF16>(p, row, np, h0, min(p.num_heads, h0 + HEADS_PER_PASS), threadIdx.x,
+                                   kReduceThreads);
+}
+
+hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream) {
+  const dim3 grid((unsigned)p.n_rows), block(kReduceThreads);
+  switch (head_dim) {
+    case 64:
+      if (bf16) hipLaunchKernelGGL((row_reduce_kernel<64, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((row_reduce_kernel<64, false>), grid, block, 0, stream, p);
+      break;
+    case 128:
+      if (bf16) hipLaunchKernelGGL((row_reduce_kernel<128, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((row_reduce_kernel<128, false>), grid, block, 0, stream, p);
+      break;
+    case 256:
+      if (bf16) hipLaunchKernelGGL((row_reduce_kernel<256, true>), grid, block, 0, stream, p);
+      else hipLaunchKernelGGL((row_reduce_kernel<256, false>), grid, block, 0, stream, p);
+      break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream) {
   const dim3 grid((unsigned)((int64_t)p.num_heads * p.n_rows)), block(kReduceThreads);
   switch (head_dim) {

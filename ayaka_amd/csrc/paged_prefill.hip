@@ -10,7 +10,11 @@
 // pairs of one request and one key/value head -- the TILE_PAIRS / G consecutive
 // rows of the request whose G query heads read that key/value head. Each wave
 // owns PT groups of 16 pairs. The context streams through LDS in chunks of 64
-// positions, loaded once per tile, cooperatively, one chunk ahead in registers:
+// positions, loaded once per tile, cooperatively, one chunk ahead in registers.
+// A launch with partitions (p.part_o set) gives each tile one workgroup per
+// partition of p.partition_size positions (a multiple of 64); a row's partitions
+// store v2 partials (the output itself when the row has one partition) for
+// partition_reduce_kernel to merge.
 //
 //  * S^T = K Q^T, per 16-position tile and 16-pair group: v_mfma_f32_16x16x32
 //    over head_dim, keys from a swizzled LDS tile (A operand), q from registers
@@ -119,11 +123,13 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   const int kv_heads = p.num_heads / p.group;
   const int kvh = blockIdx.x % kv_heads;
   const int tile = blockIdx.x / kv_heads;
-  const int first_row = tiles[3 * tile];
+  const int first_row = tiles[4 * tile];
   const int group = p.group;
-  const int n_pairs = min(tiles[3 * tile + 1] * group, TILE_PAIRS);
+  const int n_pairs = min(tiles[4 * tile + 1] * group, TILE_PAIRS);
   const int n_rows = (n_pairs + group - 1) / group;
-  const int req = tiles[3 * tile + 2];
+  const int req = tiles[4 * tile + 2];
+  const bool split = p.part_o != nullptr;
+  const int part = split ? tiles[4 * tile + 3] : 0;
 
   // This lane's (row, query head) pair of each of its groups.
   bool real[PT];
@@ -201,8 +207,10 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   const int vpiece_c = wave * VSW + lane / VNP;
   auto vpiece_pos = [&](int u) { return (u >> 1) * (2 * VNP) + 2 * (lane % VNP) + (u & 1); };
 
-  const int t_end = last_pos + 1;
-  for (int s0 = 0; s0 < t_end; s0 += seg_len) {
+  // This workgroup's positions: the tile's whole context, or one partition of it.
+  const int t_begin = split ? part * p.partition_size : 0;
+  const int t_end = split ? min(last_pos + 1, t_begin + p.partition_size) : last_pos + 1;
+  for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
     const int s1 = min(t_end, s0 + seg_len);
     const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, THREADS);
     const int nch = (s1 - s0 + CH - 1) / CH;
@@ -355,13 +363,12 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
     lj += __shfl_xor(lj, 16);
     lj += __shfl_xor(lj, 32);
     if (!real[j]) continue;
-    const float inv = lj > 0.f ? 1.0f / lj : 0.f;
-    uint16_t* out = static_cast<uint16_t*>(p.out) + ((int64_t)prow[j] * p.num_heads + phead[j]) * D;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) {
-      uint32_t* o32 = reinterpret_cast<uint32_t*>(out + t * 16 + 4 * mq);
-      o32[0] = E::round(o[j][t][0] * inv) | (E::round(o[j][t][1] * inv) << 16);
-      o32[1] = E::round(o[j][t][2] * inv) | (E::round(o[j][t][3] * inv) << 16);
+    if (split) {
+      // the row sees positions [0, my_pos]: partitions past it hold nothing of it
+      const int np = my_pos[j] / p.partition_size + 1;
+      if (part < np) store_head_t<D, BF16, true>(p, prow[j], part, np, phead[j], mq, o[j], m[j], lj);
+    } else {
+      store_head_t<D, BF16, false>(p, prow[j], 0, 1, phead[j], mq, o[j], m[j], lj);
     }
   }
 }

@@ -82,7 +82,7 @@ MFMA_MIN_HEADS = 3
 #: (the C library's ``ayk_paged_prefill_tile_pairs``; a test checks they agree).
 PREFILL_PAIRS = {64: 128, 128: 128, 256: 64}
 #: Rows per request (on average) from which a multi-row step runs the multi-row kernel.
-PREFILL_MIN_ROWS = 8
+PREFILL_MIN_ROWS = 2
 #: Compute units of one MI355X; the split heuristic aims to keep all of them busy.
 COMPUTE_UNITS = 256
 
@@ -128,26 +128,54 @@ class HipAttentionPlan:
             self.splits[key] = found
         return found
 
-    def prefill_tiles(self, group: int, pairs: int, device: torch.device) -> torch.Tensor:
-        """(first row, row count, request) triples for the multi-row kernel, heaviest first.
+    def prefill_groups(self, group: int, pairs: int) -> list[tuple[int, int, int, int]]:
+        """(context length, first row, row count, request) of each group of rows the multi-row
+        kernel serves together, heaviest first.
 
-        Each tile holds consecutive rows of one request, at most ``pairs`` (row, query
-        head) pairs; tiles ending at later positions (more context) come first.
+        Each group holds consecutive rows of one request, at most ``pairs`` (row, query head)
+        pairs; its context length is that of its last row (0 for a padding request).
         """
-        key = (-group, pairs)
+        per_tile = max(1, pairs // group)
+        groups = []
+        first = 0
+        for request, (count, length) in enumerate(zip(self.rows, self.kv_lengths)):
+            for start in range(0, count, per_tile):
+                n = min(per_tile, count - start)
+                last = self.row_lengths[first + start + n - 1] if length else 0
+                groups.append((last, first + start, n, request))
+            first += count
+        groups.sort(key=lambda g: (-g[0], g[1]))
+        return groups
+
+    def prefill_split(self, num_kv_heads: int, group: int, pairs: int, head_dim: int) -> int:
+        """The partition size of the step's multi-row launch (0: none), chosen once for every layer."""
+        key = ("prefill", num_kv_heads, group, pairs, head_dim)
+        found = self.splits.get(key)
+        if found is None:
+            lengths = [g[0] for g in self.prefill_groups(group, pairs)]
+            found = choose_prefill_partition(lengths, self.row_lengths, num_kv_heads, num_kv_heads * group,
+                                             head_dim)
+            self.splits[key] = found
+        return found
+
+    def prefill_tiles(self, group: int, pairs: int, partition_size: int, device: torch.device) -> torch.Tensor:
+        """(first row, row count, request, partition) quadruples for the multi-row kernel.
+
+        Without partitions (``partition_size`` 0) one tile per group of rows, heaviest
+        first; with them, one per partition the group's last row sees, longest first.
+        """
+        key = (-group, pairs, partition_size)
         found = self.work.get(key)
         if found is None:
-            per_tile = max(1, pairs // group)
             tiles = []
-            first = 0
-            for request, (count, length) in enumerate(zip(self.rows, self.kv_lengths)):
-                for start in range(0, count, per_tile):
-                    n = min(per_tile, count - start)
-                    last = self.row_lengths[first + start + n - 1] if length else 0
-                    tiles.append((-last, first + start, n, request))
-                first += count
+            for length, row, n, request in self.prefill_groups(group, pairs):
+                if not partition_size:
+                    tiles.append((-length, row, n, request, 0))
+                    continue
+                for part in range(max(1, -(-length // partition_size))):
+                    tiles.append((-min(partition_size, length - part * partition_size), row, n, request, part))
             tiles.sort()
-            flat = [v for _, row, n, request in tiles for v in (row, n, request)]
+            flat = [v for _, row, n, request, part in tiles for v in (row, n, request, part)]
             found = torch.tensor(flat, dtype=torch.int32).to(device)
             self.work[key] = found
         return found
@@ -290,8 +318,9 @@ def plan(
 
 def _wants_prefill_kernel(step: object) -> bool:
     """Multi-row steps with >= :data:`PREFILL_MIN_ROWS` rows per request (on average) use the
-    multi-row kernel; shorter windows (verify, a few rows) stream faster through the decode
-    kernels, which split long contexts across the GPU."""
+    multi-row kernel, which reads each request's context once for all its rows (split into
+    partitions when the tiles are too few to fill the GPU); steps of single rows use the
+    decode kernels."""
     if not isinstance(step, HipAttentionPlan):
         return False
     requests = sum(1 for count in step.rows if count)
@@ -435,6 +464,65 @@ def choose_partitions(n_rows: int, num_kv_heads: int, group: int, max_length: in
     return choose_split(n_rows, num_kv_heads, group, max_length, kv_bytes=kv_bytes).partitions
 
 
+#: Multi-row workgroups one compute unit runs at a time (the kernel's launch bounds).
+PREFILL_WORKGROUPS_PER_CU = 2
+#: Positions one multi-row workgroup folds per step, and the measured time of a step
+#: (about 3 us on MI355X, with 2 workgroups per CU or fewer; 4x512 rows over 4K run
+#: 60 steps in 222 us, a 2048-row prompt's longest tile 32 steps in 96 us).
+PREFILL_CHUNK = 64
+PREFILL_CHUNK_US = 3.0
+#: Rate (bytes per us) at which partials are written and read back, and the reduce launch.
+PREFILL_PARTIALS_BYTES_PER_US = 5.0e6
+PREFILL_REDUCE_US = 4.0
+#: Partition sizes a multi-row launch chooses from.
+PREFILL_PARTITION_CANDIDATES = (128, 256, 512, 1024, 2048, 4096)
+
+
+def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | list[int], num_kv_heads: int,
+                     num_heads: int, head_dim: int, partition_size: int) -> float:
+    """Modelled time (us) of a multi-row launch: the longer of its longest workgroup and its
+    total work spread over every workgroup slot (a lower bound of any schedule, which the
+    longest-first order nearly reaches), in chunk steps; plus, with partitions, writing and
+    reading back the partials of rows that span several, and the reduce launch."""
+    slots = COMPUTE_UNITS * PREFILL_WORKGROUPS_PER_CU
+    longest, total = 0, 0
+    for length in group_lengths:
+        if partition_size:
+            full, rest = divmod(length, partition_size)
+            pieces = [partition_size] * full + ([rest] if rest else [])
+        else:
+            pieces = [length]
+        for piece in pieces or [0]:
+            steps = -(-piece // PREFILL_CHUNK)
+            longest = max(longest, steps)
+            total += steps * num_kv_heads
+    t = max(longest, -(-total // slots)) * PREFILL_CHUNK_US
+    if partition_size:
+        parts = sum(-(-n // partition_size) for n in row_lengths if n > partition_size)
+        t += 2 * parts * num_heads * (head_dim + 2) * 4 / PREFILL_PARTIALS_BYTES_PER_US + PREFILL_REDUCE_US
+    return t
+
+
+def choose_prefill_partition(group_lengths: list[int], row_lengths: tuple[int, ...] | list[int],
+                             num_kv_heads: int, num_heads: int, head_dim: int) -> int:
+    """Partition size of a multi-row launch (0: none) for groups of rows with these context
+    lengths: the candidate with the smallest :func:`prefill_model_us`, considered only when
+    the unsplit grid fills at most two rounds of the GPU (beyond that the partials' traffic
+    outweighs any balance gained)."""
+    slots = COMPUTE_UNITS * PREFILL_WORKGROUPS_PER_CU
+    if not group_lengths or len(group_lengths) * num_kv_heads >= 2 * slots:
+        return 0
+    longest = max(group_lengths)
+    best = (prefill_model_us(group_lengths, row_lengths, num_kv_heads, num_heads, head_dim, 0), 0)
+    for size in PREFILL_PARTITION_CANDIDATES:
+        if size >= longest:
+            break
+        t = prefill_model_us(group_lengths, row_lengths, num_kv_heads, num_heads, head_dim, size)
+        if t < best[0]:
+            best = (t, size)
+    return best[1]
+
+
 _workspaces: dict[torch.device, torch.Tensor] = {}
 # Buffers a larger one replaced: a captured graph may still point at them, so they are never freed.
 _retired: list[torch.Tensor] = []
@@ -519,7 +607,11 @@ def attend_with(
     and leaves the rows of several partitions unwritten; ``merge`` (v2) forces
     where the partitions are merged, ``"in-kernel"`` (the partition kernel's
     last workgroup of a row) or ``"reduce-kernel"`` (a second launch); ``None``
-    lets the library pick.
+    lets the library pick. For the multi-row kernel (``prefill``: ``True`` forces it,
+    ``False`` the decode kernels, ``None`` lets the row count decide) ``partitions`` 0
+    covers each tile's context in one workgroup, ``partition_size`` splits it into
+    partitions of that size (a multiple of 64) merged by the reduce kernel, and ``None``
+    for both lets :func:`choose_prefill_partition` decide.
     Benchmarks and tests use them to time and check every kernel on one step.
     """
     op = "attention.attend"
@@ -596,16 +688,29 @@ def attend_with(
                 f"kernel's tile of {pairs}",
                 context={"op": op, "argument": "q"},
             )
-        tiles = step.prefill_tiles(heads // kv_heads, pairs, device)
+        group = heads // kv_heads
+        if partitions == 0:
+            size = 0
+        elif partition_size is not None:
+            size = partition_size
+        else:
+            size = step.prefill_split(kv_heads, group, pairs, buffers.head_dim)
+        tiles = step.prefill_tiles(group, pairs, size, device)
+        scratch, nbytes = None, 0
+        if size:
+            max_partitions = -(-table.shape[1] * block_size // size)
+            nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, max_partitions)
+            scratch = _workspace(op, device, nbytes, capturing(q))
         _lib.check(
             op,
             lib.ayk_paged_prefill(
                 out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),
-                table.stride(0), meta.kv_lengths.data_ptr(), meta.positions.data_ptr(), tiles.data_ptr(),
-                tiles.numel() // 3, n_rows, heads, kv_heads, buffers.head_dim, buffers.num_blocks, block_size,
-                table.shape[1], _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype],
-                _kv_code(buffers, q.dtype), float(scale),
-                stream,
+                table.stride(0), meta.kv_lengths.data_ptr(), meta.request_of_row.data_ptr(),
+                meta.positions.data_ptr(), tiles.data_ptr(), tiles.numel() // 4, n_rows, heads, kv_heads,
+                buffers.head_dim, buffers.num_blocks, block_size, table.shape[1],
+                _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype], _kv_code(buffers, q.dtype),
+                float(scale), size, scratch.data_ptr() if scratch is not None else 0,
+                scratch.numel() if scratch is not None else 0, stream,
             ),
         )
         return

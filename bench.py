@@ -145,6 +145,8 @@ MULTI_ROW_WORKLOADS = [
     (8, 128, 2048, 32, 8),    # small chunks
     (16, 8, 1024, 32, 8),     # verify windows of 8 draft tokens
     (4, 512, 4096, 64, 8),    # GQA 8
+    (32, 4, 4096, 32, 8),     # verify windows of 4 draft tokens over 4K
+    (64, 2, 2048, 32, 8),     # verify windows of 2 draft tokens over 2K
 ]
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
@@ -176,6 +178,10 @@ def multi_row(args) -> int:
         scale = dim ** -0.5
         kernel = time_calls(lambda: hip_attention.attend_with(q, buffers, meta, out, scale=scale, partitions=None,
                                                               prefill=True), args.steps, args.warmup)
+        size = meta.plan.prefill_split(kv_heads, heads // kv_heads, hip_attention.PREFILL_PAIRS[dim], dim)
+        unsplit = kernel if not size else time_calls(
+            lambda: hip_attention.attend_with(q, buffers, meta, per_row, scale=scale, partitions=0, prefill=True),
+            args.steps, args.warmup)
         old = time_calls(lambda: hip_attention.attend_with(q, buffers, meta, per_row, scale=scale, partitions=None,
                                                            prefill=False), 3, 1, repeats=1)
         torch.cuda.synchronize()
@@ -188,6 +194,8 @@ def multi_row(args) -> int:
             "workload": f"{requests} requests x {rows} rows over {context} positions, Hq {heads}, Hkv {kv_heads}, "
                         f"D {dim}, bf16, block {bs}",
             "us_per_call": round(us, 2),
+            "partition_size": size,
+            "unsplit_us": round(unsplit["median_us"], 2),
             "tflops": round(flops / us / 1e6, 1),
             "mfma_fraction": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
             "kv_gbs": round(kv_bytes / us / 1e3, 1),

@@ -164,13 +164,23 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
  * Multi-row paged attention (prefill chunks, verify windows): the rows of each
  * request are its last rows, row i at position positions[i] attends to
  * [0, positions[i]] of its request's context; rows of a request with
- * kv_lengths 0 get zeros. tiles lists n_tiles (first_row, row_count, request)
- * int32 triples: consecutive rows of one request with row_count * (num_heads /
- * num_kv_heads) <= ayk_paged_prefill_tile_pairs(head_dim), covering every row
- * once (rows past that many pairs are not computed). One workgroup per (tile,
- * key/value head) loads each chunk of the context once into LDS for all its
- * rows and query heads; q.k and P.V run on the matrix cores with fp32
- * accumulation. Replaces the reference's per-request SDPA loop,
+ * kv_lengths 0 get zeros. tiles lists n_tiles (first_row, row_count, request,
+ * partition) int32 quadruples: consecutive rows of one request with row_count *
+ * (num_heads / num_kv_heads) <= ayk_paged_prefill_tile_pairs(head_dim), covering
+ * every row once (rows past that many pairs are not computed). One workgroup per
+ * (tile, key/value head) loads each chunk of the context once into LDS for all
+ * its rows and query heads; q.k and P.V run on the matrix cores with fp32
+ * accumulation. With partition_size 0 a tile covers its whole context and its
+ * partition field must be 0. With a positive partition_size (a multiple of 64),
+ * a tile entry covers positions [partition * partition_size, +partition_size)
+ * of its rows' context, and the tiles must list, for every group of rows, each
+ * partition below ceil((last row's position + 1) / partition_size) once; the
+ * partitions store partials in workspace (at least
+ * ayk_paged_attention_v2_workspace_bytes(n_rows, num_heads, head_dim,
+ * ceil(max_blocks * block_size / partition_size)) bytes, 16-byte aligned) and
+ * a reduce kernel on the same stream merges them, each row over its own
+ * partitions in partition order. Small launches (few rows per request, verify
+ * windows) fill the GPU this way. Replaces the reference's per-request SDPA loop,
  * python/ayaka/ops/backends/torch/attention.py:209-234, and flashinfer's batch
  * prefill (python/ayaka/ops/backends/flashinfer/attention.py:150-152, :253-266).
  */
@@ -181,10 +191,11 @@ int ayk_paged_prefill_tile_pairs(int32_t head_dim);
 
 int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
                       const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
-                      const int32_t* positions, const int32_t* tiles, int32_t n_tiles, int32_t n_rows,
-                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
-                      int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype, int32_t kv_dtype,
-                      float scale, void* stream);
+                      const int32_t* request_of_row, const int32_t* positions, const int32_t* tiles,
+                      int32_t n_tiles, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t num_blocks, int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
+                      int32_t kv_dtype, float scale, int32_t partition_size, void* workspace,
+                      size_t workspace_bytes, void* stream);
 
 /*
  * Whole-block copies of both caches; block_bytes is the size of one block of

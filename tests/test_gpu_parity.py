@@ -199,6 +199,36 @@ def test_multi_row_kernel(dtype: str, heads: int, kv_heads: int, head_dim: int, 
         assert torch.count_nonzero(out[padding_rows]) == 0
 
 
+@pytest.mark.parametrize("size", [0, 64, 192, 512])
+@pytest.mark.parametrize("heads,kv_heads,head_dim,dtype", [(8, 2, 64, "fp16"), (32, 8, 128, "bf16"),
+                                                           (4, 4, 256, "bf16")])
+@pytest.mark.parametrize("name,steps", PREFILL_CASES, ids=[c[0] for c in PREFILL_CASES])
+def test_multi_row_partitions(size: int, heads: int, kv_heads: int, head_dim: int, dtype: str, name: str,
+                              steps: list) -> None:
+    # size 0: each tile's whole context in one workgroup; otherwise partitions of `size`
+    # positions merged by the reduce kernel, each row over the partitions it sees
+    s = build_scenario(steps, dtype=dtype, heads=heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16,
+                       mode="mixed", seed=68, spare_blocks=2)
+    launch = dict(partitions=0) if size == 0 else dict(partition_size=size)
+    out = run_attention(s, prefill=True, **launch)
+    assert_parity(out, s.expected(np.float64), dtype, f"prefill/{name}/{size}")
+    padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
+    if padding_rows:
+        assert torch.count_nonzero(out[padding_rows]) == 0
+
+
+@pytest.mark.parametrize("block_size", [1, 2])
+def test_multi_row_partitions_across_table_segments(block_size: int) -> None:
+    # partitions of 512 positions of one- and two-position blocks each span several staged
+    # table segments (at most 511 entries at a time)
+    s = build_scenario([(40, 1300), (9, 1400), (3, 5)], block_size=block_size, head_dim=128, heads=8,
+                       kv_heads=2, mode="mixed", seed=45)
+    expected = s.expected(np.float64)
+    for size in (0, 512, 1024):
+        launch = dict(partitions=0) if size == 0 else dict(partition_size=size)
+        assert_parity(run_attention(s, prefill=True, **launch), expected, "bf16", f"bs{block_size}/{size}")
+
+
 @pytest.mark.parametrize("block_size", [1, 4, 8, 16, 32, 64])
 @pytest.mark.parametrize("qk", QK)
 def test_block_sizes(block_size: int, qk: str) -> None:

@@ -136,6 +136,43 @@ def test_the_modelled_schedule() -> None:
     assert hip_attention.schedule_makespan([1024] * 257, 1024) == 2 * (1024 + hip_attention.WORKGROUP_COST)
 
 
+def test_multi_row_tiles_list_every_partition_a_group_sees_once() -> None:
+    rows, lengths = [37, 5, 1, 8, 0], [37, 900, 2, 130, 0]
+    table = torch.ones(len(rows), 64, dtype=torch.int32)
+    step = hip_attention.plan(ForwardMode.MIXED, _ints(*rows), _ints(*lengths), table, 16).plan
+    groups = step.prefill_groups(4, 128)  # 32 rows per group at 4 query heads per key/value head
+    assert sorted((row, n) for _, row, n, _ in groups) == [(0, 32), (32, 5), (37, 5), (42, 1), (43, 8)]
+    assert [g[0] for g in groups] == sorted((g[0] for g in groups), reverse=True)
+    for size in (0, 64, 192, 512):
+        tiles = step.prefill_tiles(4, 128, size, torch.device("cpu")).view(-1, 4).tolist()
+        for length, row, n, request in groups:
+            parts = sorted(t[3] for t in tiles if t[0] == row)
+            assert all(t[1:3] == [n, request] for t in tiles if t[0] == row)
+            assert parts == (list(range(max(1, -(-length // size)))) if size else [0]), (size, row)
+        # longest first: the positions each tile covers never grow down the list
+        length_of = {row: length for length, row, _, _ in groups}
+        work = [min(size, length_of[row] - part * size) if size else length_of[row] for row, _, _, part in tiles]
+        assert work == sorted(work, reverse=True)
+
+
+def test_multi_row_partition_choice() -> None:
+    choose = hip_attention.choose_prefill_partition
+    # 16 verify windows of 8 rows over 1K fill 128 of 512 workgroup slots: split
+    rows = [1017 + i for i in range(8)] * 16
+    assert choose([1024] * 16, rows, 8, 32, 128) > 0
+    # 4 requests x 512 rows over 4K fill the GPU already (64 tiles x 8 heads): no split
+    lengths = [3584 + 32 * (i + 1) for i in range(16)] * 4
+    assert choose(lengths, list(range(3585, 4097)) * 4, 8, 32, 128) == 0
+    # a short context is never split
+    assert choose([100, 60], [100] * 32 + [60] * 32, 8, 32, 128) == 0
+    # the chosen size is the modelled optimum among the candidates
+    model = hip_attention.prefill_model_us
+    size = choose([1024] * 16, rows, 8, 32, 128)
+    for other in (0, *hip_attention.PREFILL_PARTITION_CANDIDATES):
+        if other < 1024:
+            assert model([1024] * 16, rows, 8, 32, 128, size) <= model([1024] * 16, rows, 8, 32, 128, other)
+
+
 def _cpu_buffers(**changes: object) -> KVBuffers:
     k = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16)
     buffers = KVBuffers(k, k.clone(), KVLayoutKind.NHD, RAW_CODEC)
