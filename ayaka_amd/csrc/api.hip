@@ -210,7 +210,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
 
 extern "C" {
 
-int ayk_abi_version(void) { return 8; }
+int ayk_abi_version(void) { return 9; }
 
 int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 
@@ -339,7 +339,7 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
 int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
                       const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
                       const int32_t* request_of_row, const int32_t* positions, const int32_t* tiles,
-                      int32_t n_tiles, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t n_tiles, int32_t tile_pairs, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                       int32_t num_blocks, int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
                       int32_t kv_dtype, float scale, int32_t partition_size, void* workspace,
                       size_t workspace_bytes, void* stream) {
@@ -353,7 +353,13 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
   if (rc != AYK_OK) return rc;
-  const int tile_pairs = ayk::prefill_tile_pairs_for(head_dim);
+  // Tiles of the full capacity, or of a half or a quarter (2 or 4 waves then share
+  // each group of pairs and split its chunks).
+  const int full_pairs = ayk::prefill_tile_pairs_for(head_dim);
+  const int waves_per_group = tile_pairs > 0 && full_pairs % tile_pairs == 0 ? full_pairs / tile_pairs : 0;
+  if (waves_per_group != 1 && waves_per_group != 2 && waves_per_group != 4)
+    return fail(AYK_ERR_ARGUMENT, "%s: tile_pairs %d is not %d, %d or %d", op, tile_pairs, full_pairs,
+                full_pairs / 2, full_pairs / 4);
   if (p.group > tile_pairs)
     return fail(AYK_ERR_UNSUPPORTED, "%s: %d query heads per key/value head exceed a tile of %d", op, p.group,
                 tile_pairs);
@@ -369,7 +375,7 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (partition_size == 0)
     return launched(ayk::launch_prefill(p, tiles, n_tiles, head_dim, dtype == AYK_DTYPE_BF16,
-                                        kv_dtype == AYK_DTYPE_FP8_E4M3, s),
+                                        kv_dtype == AYK_DTYPE_FP8_E4M3, waves_per_group, s),
                     op);
   const int64_t max_partitions = ((int64_t)p.max_len + partition_size - 1) / partition_size;
   if (max_partitions < 1 || max_partitions > 65535)
@@ -386,7 +392,7 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   p.partition_size = partition_size;
   p.max_partitions = (int32_t)max_partitions;
   hipError_t err = ayk::launch_prefill(p, tiles, n_tiles, head_dim, dtype == AYK_DTYPE_BF16,
-                                       kv_dtype == AYK_DTYPE_FP8_E4M3, s);
+                                       kv_dtype == AYK_DTYPE_FP8_E4M3, waves_per_group, s);
   if (err == hipSuccess) err = ayk::launch_row_reduce(p, head_dim, dtype == AYK_DTYPE_BF16, s);
   return launched(err, op);
 }

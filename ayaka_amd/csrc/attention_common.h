@@ -459,6 +459,45 @@ __device__ __forceinline__ int stage_table(const AttnParams& p, const int32_t* t
   return b0;
 }
 
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// O^T += V^T P^T for a 16 x 16 tile over 16 tokens: v_mfma_f32_16x16x16.
+template <bool BF16>
+__device__ __forceinline__ f32x4 mfma_pv(u32x2 v, u32x2 w, f32x4 acc) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, v), __builtin_bit_cast(i16x4, w),
+                                                     acc, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, v), __builtin_bit_cast(f16x4, w), acc,
+                                                 0, 0, 0);
+  }
+}
+
+// Split 4 fp32 weights w (finite, >= 0) into packed 16-bit high parts and packed
+// 16-bit parts of the remainder, both by truncation: |w - h - l| < 2^-14 w (bf16).
+template <bool BF16>
+__device__ __forceinline__ void split_weights4(const float (&w)[4], u32x2& hi, u32x2& lo) {
+  uint32_t h[2], r[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float a = w[2 * i], b = w[2 * i + 1];
+    if constexpr (BF16) {
+      const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+      h[i] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
+      const float ra = a - __uint_as_float(ua & 0xffff0000u);
+      const float rb = b - __uint_as_float(ub & 0xffff0000u);
+      r[i] = __builtin_amdgcn_perm(__float_as_uint(rb), __float_as_uint(ra), 0x07060302u);
+    } else {
+      const auto hv = __builtin_amdgcn_cvt_pkrtz(a, b);
+      h[i] = __builtin_bit_cast(uint32_t, hv);
+      r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a - (float)hv[0], b - (float)hv[1]));
+    }
+  }
+  hi = u32x2{h[0], h[1]};
+  lo = u32x2{r[0], r[1]};
+}
+
 // Element offset of position t within its block: (t mod block size) x token
 // stride on the full-rate 24-bit multiplier (both factors are below 2^24: the
 // host refuses larger token strides).

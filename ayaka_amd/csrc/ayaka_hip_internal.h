@@ -52,8 +52,8 @@ hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int heads_pe
 // Multi-row attention: one workgroup per (tile of rows of one request, key/value head).
 // A tile holds at most prefill_tile_pairs_for(head_dim) (row, query head) pairs (0: unsupported).
 int prefill_tile_pairs_for(int head_dim);
-hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16,
-                          bool kv8, hipStream_t stream);
+hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16, bool kv8,
+                          int waves_per_group, hipStream_t stream);
 // The v2 log-sum-exp merge of the partitions of every (row, head).
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);
 hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);

@@ -30,8 +30,6 @@ namespace ayk {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 template <bool BF16>
 __device__ __forceinline__ f32x4 mfma_qk(u32x4 k, u32x4 q, f32x4 acc) {
@@ -44,18 +42,6 @@ __device__ __forceinline__ f32x4 mfma_qk(u32x4 k, u32x4 q, f32x4 acc) {
   }
 }
 
-// O^T += V^T P^T for a 16 x 16 tile over 16 tokens: v_mfma_f32_16x16x16.
-template <bool BF16>
-__device__ __forceinline__ f32x4 mfma_pv(u32x2 v, u32x2 w, f32x4 acc) {
-  if constexpr (BF16) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, v), __builtin_bit_cast(i16x4, w),
-                                                     acc, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, v), __builtin_bit_cast(f16x4, w), acc,
-                                                 0, 0, 0);
-  }
-}
-
 // 4 elements of a 16-lane group's rows, transposed: lane o of each group of 16
 // receives element o % 4 of the 8-byte rows read by lanes o / 4, o / 4 + 4,
 // o / 4 + 8 and o / 4 + 12 of its group (ds_read_b64_tr_b16, measured).
@@ -63,30 +49,6 @@ __device__ __forceinline__ u32x2 lds_read_transposed(const uint16_t* p) {
   typedef short v4i16 __attribute__((ext_vector_type(4)));
   return __builtin_bit_cast(
       u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p)));
-}
-
-// Split 4 fp32 weights w (finite, >= 0) into packed 16-bit high parts and packed
-// 16-bit parts of the remainder, both by truncation: |w - h - l| < 2^-14 w (bf16).
-template <bool BF16>
-__device__ __forceinline__ void split_weights4(const float (&w)[4], u32x2& hi, u32x2& lo) {
-  uint32_t h[2], r[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float a = w[2 * i], b = w[2 * i + 1];
-    if constexpr (BF16) {
-      const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
-      h[i] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
-      const float ra = a - __uint_as_float(ua & 0xffff0000u);
-      const float rb = b - __uint_as_float(ub & 0xffff0000u);
-      r[i] = __builtin_amdgcn_perm(__float_as_uint(rb), __float_as_uint(ra), 0x07060302u);
-    } else {
-      const auto hv = __builtin_amdgcn_cvt_pkrtz(a, b);
-      h[i] = __builtin_bit_cast(uint32_t, hv);
-      r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a - (float)hv[0], b - (float)hv[1]));
-    }
-  }
-  hi = u32x2{h[0], h[1]};
-  lo = u32x2{r[0], r[1]};
 }
 
 // Order the LDS traffic of one wave: lanes read what other lanes of the same

@@ -85,14 +85,21 @@ __device__ __forceinline__ void split_weights(const float (&w)[8], u32x4& hi, u3
   lo = u32x4{r[0], r[1], r[2], r[3]};
 }
 
-template <int D, bool BF16, bool KV8>
+// PS waves share each group of pairs and split every chunk's positions between
+// them (PS = 1, 2 or 4; tiles of prefill_tile_pairs(D) / PS pairs), so a tile of
+// few (row, head) pairs -- a short verify window -- does not spend the other
+// waves' matrix-core time on idle pairs; the waves of a group merge their
+// running states through LDS at the end.
+template <int D, bool BF16, bool KV8, int PS>
 __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const AttnParams p, const int32_t* tiles) {
   using E = Elem<BF16>;
   constexpr int THREADS = kPrefillThreads;
   constexpr int PT = D == 256 ? 1 : 2;          // 16-pair groups per wave
-  constexpr int TILE_PAIRS = prefill_tile_pairs(D);
+  constexpr int PGROUPS = kPrefillWaves / PS;   // waves with distinct pairs
+  constexpr int TILE_PAIRS = prefill_tile_pairs(D) / PS;
   constexpr int CH = 64;                        // positions per chunk
   constexpr int PTL = CH / 16;                  // 16-position tiles per chunk
+  constexpr int PTL_W = PTL / PS;               // 16-position tiles per chunk of one wave
   constexpr int KS = D / 32;                    // q.k k-steps
   constexpr int DT = D / 16;                    // 16-element slices of head_dim for P.V
   constexpr int CPT = D / 8;                    // 8-element pieces per position
@@ -110,14 +117,31 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   constexpr int VSW = CPT / 4;                  // value slices per wave
   constexpr int VNP = kWave / VSW;              // value position pairs per wave instruction
   static_assert(PER_THREAD % 2 == 0 && PIECES % THREADS == 0, "piece split");
+  static_assert(PS == 1 || PS == 2 || PS == 4, "waves per pair group");
 
+  // The staged chunks, and after the last one the running states the waves of a
+  // group with ps > 0 hand to its first wave: o of each lane, m and l per pair.
+  struct Stage {
+    u32x4 k[2][PIECES];
+    uint32_t vt[2][D * VT2];
+  };
+  constexpr int MERGE_WAVES = PS > 1 ? (PS - 1) * PGROUPS : 1;
+  union Lds {
+    Stage st;
+    f32x4 o[MERGE_WAVES][PT][DT][kWave];
+  };
+  static_assert(sizeof(f32x4[MERGE_WAVES][PT][DT][kWave]) <= sizeof(Stage), "merge fits the stage");
   __shared__ uint32_t s_tbl[kTableCap];
-  __shared__ u32x4 s_k[2][PIECES];
-  __shared__ __attribute__((aligned(16))) uint32_t s_vt[2][D * VT2];
+  __shared__ Lds lds;
+  __shared__ float s_ml[MERGE_WAVES][PT][2][16];
+  auto& s_k = lds.st.k;
+  auto& s_vt = lds.st.vt;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
+  const int pg = wave / PS;  // this wave's pair group
+  const int ps = wave % PS;  // and its share of each chunk: tiles ps * PTL_W ...
   const int mt = lane % 16;
   const int mq = lane / 16;
   const int kv_heads = p.num_heads / p.group;
@@ -136,7 +160,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   int prow[PT], phead[PT];
 #pragma unroll
   for (int j = 0; j < PT; ++j) {
-    const int pair = (wave * PT + j) * 16 + mt;
+    const int pair = (pg * PT + j) * 16 + mt;
     real[j] = pair < n_pairs;
     prow[j] = first_row + (real[j] ? pair / group : 0);
     phead[j] = kvh * group + (real[j] ? pair % group : 0);
@@ -262,18 +286,19 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
       // uniform: no position masked (and, for folding the scale into the exponent,
       // a scale >= 0, under which the largest raw score gives the largest scaled one)
       const bool whole = tb + CH <= s1 && tb + CH - 1 <= wave_min_pos && scale_log2 >= 0.f;
-      f32x4 acc[PTL][PT];
+      f32x4 acc[PTL_W][PT];
 #pragma unroll
-      for (int pt = 0; pt < PTL; ++pt)
+      for (int w = 0; w < PTL_W; ++w)
 #pragma unroll
-        for (int j = 0; j < PT; ++j) acc[pt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < PT; ++j) acc[w][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s)
 #pragma unroll
-        for (int pt = 0; pt < PTL; ++pt) {
+        for (int w = 0; w < PTL_W; ++w) {
+          const int pt = ps * PTL_W + w;
           const u32x4 ka = s_k[buf][key_slot(pt * 16 + mt, s * 4 + mq)];
 #pragma unroll
-          for (int j = 0; j < PT; ++j) acc[pt][j] = mfma32<BF16>(ka, qb[j][s], acc[pt][j]);
+          for (int j = 0; j < PT; ++j) acc[w][j] = mfma32<BF16>(ka, qb[j][s], acc[w][j]);
         }
 #pragma unroll
       for (int j = 0; j < PT; ++j) {
@@ -282,20 +307,21 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
         float sc = 1.f;
         if (whole) {
 #pragma unroll
-          for (int pt = 0; pt < PTL; ++pt)
+          for (int w = 0; w < PTL_W; ++w)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[pt][j][i]);
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[w][j][i]);
           mx *= scale_log2;
           sc = scale_log2;
         } else {
           // position tb + pt*16 + 4*mq + i is visible iff pt*16 + i <= lim
           const int lim = min(my_pos[j], s1 - 1) - tb - 4 * mq;
 #pragma unroll
-          for (int pt = 0; pt < PTL; ++pt)
+          for (int w = 0; w < PTL_W; ++w)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              acc[pt][j][i] = pt * 16 + i <= lim ? acc[pt][j][i] * scale_log2 : -INFINITY;
-              mx = fmaxf(mx, acc[pt][j][i]);
+              const int pt = ps * PTL_W + w;
+              acc[w][j][i] = pt * 16 + i <= lim ? acc[w][j][i] * scale_log2 : -INFINITY;
+              mx = fmaxf(mx, acc[w][j][i]);
             }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16));
@@ -309,35 +335,56 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
           m[j] = mn;
         }
 #pragma unroll
-        for (int pt = 0; pt < PTL; ++pt)
+        for (int w = 0; w < PTL_W; ++w)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float w = fast_exp2(__builtin_fmaf(acc[pt][j][i], sc, -m[j]));
-            acc[pt][j][i] = w;
-            l[j] += w;
+            const float e = fast_exp2(__builtin_fmaf(acc[w][j][i], sc, -m[j]));
+            acc[w][j][i] = e;
+            l[j] += e;
           }
       }
-      // O^T += V^T P^T over two 32-position k-steps.
+      if constexpr (PTL_W >= 2) {
+        // O^T += V^T P^T over this wave's 32-position k-steps (16x16x32).
 #pragma unroll
-      for (int ks = 0; ks < PTL / 2; ++ks) {
-        u32x4 phi[PT], plo[PT];
+        for (int kw = 0; kw < PTL_W / 2; ++kw) {
+          const int ks = ps * (PTL_W / 2) + kw;
+          u32x4 phi[PT], plo[PT];
+#pragma unroll
+          for (int j = 0; j < PT; ++j) {
+            const float w[8] = {acc[2 * kw][j][0],     acc[2 * kw][j][1],     acc[2 * kw][j][2],
+                                acc[2 * kw][j][3],     acc[2 * kw + 1][j][0], acc[2 * kw + 1][j][1],
+                                acc[2 * kw + 1][j][2], acc[2 * kw + 1][j][3]};
+            split_weights<BF16>(w, phi[j], plo[j]);
+          }
+#pragma unroll
+          for (int t = 0; t < DT; ++t) {
+            const uint32_t* vrow = &s_vt[buf][vt_word(t * 16 + mt, ks * 16 + 2 * mq)];
+            const u32x2 lo4 = *reinterpret_cast<const u32x2*>(vrow);
+            const u32x2 hi4 = *reinterpret_cast<const u32x2*>(vrow + 8);
+            const u32x4 va = u32x4{lo4.x, lo4.y, hi4.x, hi4.y};
+#pragma unroll
+            for (int j = 0; j < PT; ++j) {
+              o[j][t] = mfma32<BF16>(va, phi[j], o[j][t]);
+              o[j][t] = mfma32<BF16>(va, plo[j], o[j][t]);
+            }
+          }
+        }
+      } else {
+        // One 16-position tile per wave: O^T += V^T P^T on 16x16x16, the lane's 4
+        // weights (positions 4*mq + i of the tile) as its k-slots.
+        u32x2 phi[PT], plo[PT];
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
-          const float w[8] = {acc[2 * ks][j][0],     acc[2 * ks][j][1],     acc[2 * ks][j][2],
-                              acc[2 * ks][j][3],     acc[2 * ks + 1][j][0], acc[2 * ks + 1][j][1],
-                              acc[2 * ks + 1][j][2], acc[2 * ks + 1][j][3]};
-          split_weights<BF16>(w, phi[j], plo[j]);
+          const float w[4] = {acc[0][j][0], acc[0][j][1], acc[0][j][2], acc[0][j][3]};
+          split_weights4<BF16>(w, phi[j], plo[j]);
         }
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-          const uint32_t* vrow = &s_vt[buf][vt_word(t * 16 + mt, ks * 16 + 2 * mq)];
-          const u32x2 lo4 = *reinterpret_cast<const u32x2*>(vrow);
-          const u32x2 hi4 = *reinterpret_cast<const u32x2*>(vrow + 8);
-          const u32x4 va = u32x4{lo4.x, lo4.y, hi4.x, hi4.y};
+          const u32x2 va = *reinterpret_cast<const u32x2*>(&s_vt[buf][vt_word(t * 16 + mt, ps * 8 + 2 * mq)]);
 #pragma unroll
           for (int j = 0; j < PT; ++j) {
-            o[j][t] = mfma32<BF16>(va, phi[j], o[j][t]);
-            o[j][t] = mfma32<BF16>(va, plo[j], o[j][t]);
+            o[j][t] = mfma_pv<BF16>(va, phi[j], o[j][t]);
+            o[j][t] = mfma_pv<BF16>(va, plo[j], o[j][t]);
           }
         }
       }
@@ -357,11 +404,54 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 
   // Each pair's weight sum over the 4 position groups; lane (mq, mt) holds
   // elements 16*t + 4*mq + i of pair mt of each group.
+  float lsum[PT];
 #pragma unroll
   for (int j = 0; j < PT; ++j) {
-    float lj = l[j];
-    lj += __shfl_xor(lj, 16);
-    lj += __shfl_xor(lj, 32);
+    lsum[j] = l[j];
+    lsum[j] += __shfl_xor(lsum[j], 16);
+    lsum[j] += __shfl_xor(lsum[j], 32);
+  }
+  if constexpr (PS > 1) {
+    // The waves ps > 0 of a group hand their states to wave ps = 0, which folds them
+    // in: o = sum o_w 2^(m_w - M), l = sum l_w 2^(m_w - M), M = max m_w. The last
+    // loop iteration ended on a barrier, so the stage area is free.
+    if (ps > 0) {
+      const int slot = pg * (PS - 1) + ps - 1;
+#pragma unroll
+      for (int j = 0; j < PT; ++j) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t) lds.o[slot][j][t][lane] = o[j][t];
+        if (mq == 0) {
+          s_ml[slot][j][0][mt] = m[j];
+          s_ml[slot][j][1][mt] = lsum[j];
+        }
+      }
+    }
+    lds_barrier();
+    if (ps > 0) return;
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+      float mn = m[j];
+#pragma unroll
+      for (int w = 1; w < PS; ++w) mn = fmaxf(mn, s_ml[pg * (PS - 1) + w - 1][j][0][mt]);
+      const float a0 = fast_exp2(m[j] - mn);
+      lsum[j] *= a0;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) o[j][t] *= a0;
+#pragma unroll
+      for (int w = 1; w < PS; ++w) {
+        const int slot = pg * (PS - 1) + w - 1;
+        const float a = fast_exp2(s_ml[slot][j][0][mt] - mn);
+        lsum[j] += s_ml[slot][j][1][mt] * a;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) o[j][t] += lds.o[slot][j][t][lane] * a;
+      }
+      m[j] = mn;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < PT; ++j) {
+    const float lj = lsum[j];
     if (!real[j]) continue;
     if (split) {
       // the row sees positions [0, my_pos]: partitions past it hold nothing of it
@@ -373,18 +463,29 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   }
 }
 
-template <int D>
-static hipError_t launch_prefill_d(const AttnParams& p, const int32_t* tiles, dim3 grid, bool bf16, bool kv8,
-                                   hipStream_t stream) {
+template <int D, int PS>
+static hipError_t launch_prefill_ps(const AttnParams& p, const int32_t* tiles, dim3 grid, bool bf16, bool kv8,
+                                    hipStream_t stream) {
   const dim3 block(kPrefillThreads);
   if (kv8) {
-    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, true>), grid, block, 0, stream, p, tiles);
-    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, true>), grid, block, 0, stream, p, tiles);
+    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, true, PS>), grid, block, 0, stream, p, tiles);
+    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, true, PS>), grid, block, 0, stream, p, tiles);
   } else {
-    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, false>), grid, block, 0, stream, p, tiles);
-    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, false>), grid, block, 0, stream, p, tiles);
+    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, false, PS>), grid, block, 0, stream, p, tiles);
+    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, false, PS>), grid, block, 0, stream, p, tiles);
   }
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_prefill_d(const AttnParams& p, const int32_t* tiles, dim3 grid, bool bf16, bool kv8,
+                                   int waves_per_group, hipStream_t stream) {
+  switch (waves_per_group) {
+    case 1: return launch_prefill_ps<D, 1>(p, tiles, grid, bf16, kv8, stream);
+    case 2: return launch_prefill_ps<D, 2>(p, tiles, grid, bf16, kv8, stream);
+    case 4: return launch_prefill_ps<D, 4>(p, tiles, grid, bf16, kv8, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 int prefill_tile_pairs_for(int head_dim) {
@@ -392,12 +493,12 @@ int prefill_tile_pairs_for(int head_dim) {
 }
 
 hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16, bool kv8,
-                          hipStream_t stream) {
+                          int waves_per_group, hipStream_t stream) {
   const dim3 grid((unsigned)((int64_t)n_tiles * (p.num_heads / p.group)));
   switch (head_dim) {
-    case 64: return launch_prefill_d<64>(p, tiles, grid, bf16, kv8, stream);
-    case 128: return launch_prefill_d<128>(p, tiles, grid, bf16, kv8, stream);
-    case 256: return launch_prefill_d<256>(p, tiles, grid, bf16, kv8, stream);
+    case 64: return launch_prefill_d<64>(p, tiles, grid, bf16, kv8, waves_per_group, stream);
+    case 128: return launch_prefill_d<128>(p, tiles, grid, bf16, kv8, waves_per_group, stream);
+    case 256: return launch_prefill_d<256>(p, tiles, grid, bf16, kv8, waves_per_group, stream);
     default: return hipErrorInvalidValue;
   }
 }

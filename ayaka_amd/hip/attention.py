@@ -28,6 +28,8 @@ launch shape comes from the bucket's table width.
 
 from __future__ import annotations
 
+import functools
+
 import heapq
 from dataclasses import dataclass, field
 
@@ -154,7 +156,7 @@ class HipAttentionPlan:
         if found is None:
             lengths = [g[0] for g in self.prefill_groups(group, pairs)]
             found = choose_prefill_partition(lengths, self.row_lengths, num_kv_heads, num_kv_heads * group,
-                                             head_dim)
+                                             head_dim, PREFILL_PAIRS[head_dim] // pairs)
             self.splits[key] = found
         return found
 
@@ -471,6 +473,9 @@ PREFILL_WORKGROUPS_PER_CU = 2
 #: 60 steps in 222 us, a 2048-row prompt's longest tile 32 steps in 96 us).
 PREFILL_CHUNK = 64
 PREFILL_CHUNK_US = 3.0
+#: The same with tiles of a half or a quarter of the pairs, whose 2 or 4 waves per pair
+#: group split each chunk.
+PREFILL_CHUNK_US_BY_WAVES = {1: PREFILL_CHUNK_US, 2: 2.0, 4: 1.5}
 #: Rate (bytes per us) at which partials are written and read back, and the reduce launch.
 PREFILL_PARTIALS_BYTES_PER_US = 5.0e6
 PREFILL_REDUCE_US = 4.0
@@ -478,8 +483,19 @@ PREFILL_REDUCE_US = 4.0
 PREFILL_PARTITION_CANDIDATES = (128, 256, 512, 1024, 2048, 4096)
 
 
+def prefill_tile_pairs(rows: tuple[int, ...] | list[int], group: int, head_dim: int) -> int:
+    """Tile capacity of a multi-row launch: the smallest of the full tile, a half and a quarter
+    that holds the (rows x query heads) pairs of the step's largest request (and a group)."""
+    full = PREFILL_PAIRS[head_dim]
+    need = max(max(rows, default=1), 1) * group
+    for pairs in (full // 4, full // 2):
+        if pairs >= max(need, group):
+            return pairs
+    return full
+
+
 def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | list[int], num_kv_heads: int,
-                     num_heads: int, head_dim: int, partition_size: int) -> float:
+                     num_heads: int, head_dim: int, partition_size: int, waves_per_group: int = 1) -> float:
     """Modelled time (us) of a multi-row launch: the longer of its longest workgroup and its
     total work spread over every workgroup slot (a lower bound of any schedule, which the
     longest-first order nearly reaches), in chunk steps; plus, with partitions, writing and
@@ -496,7 +512,7 @@ def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | li
             steps = -(-piece // PREFILL_CHUNK)
             longest = max(longest, steps)
             total += steps * num_kv_heads
-    t = max(longest, -(-total // slots)) * PREFILL_CHUNK_US
+    t = max(longest, -(-total // slots)) * PREFILL_CHUNK_US_BY_WAVES[waves_per_group]
     if partition_size:
         parts = sum(-(-n // partition_size) for n in row_lengths if n > partition_size)
         t += 2 * parts * num_heads * (head_dim + 2) * 4 / PREFILL_PARTIALS_BYTES_PER_US + PREFILL_REDUCE_US
@@ -504,7 +520,7 @@ def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | li
 
 
 def choose_prefill_partition(group_lengths: list[int], row_lengths: tuple[int, ...] | list[int],
-                             num_kv_heads: int, num_heads: int, head_dim: int) -> int:
+                             num_kv_heads: int, num_heads: int, head_dim: int, waves_per_group: int = 1) -> int:
     """Partition size of a multi-row launch (0: none) for groups of rows with these context
     lengths: the candidate with the smallest :func:`prefill_model_us`, considered only when
     the unsplit grid fills at most two rounds of the GPU (beyond that the partials' traffic
@@ -513,11 +529,13 @@ def choose_prefill_partition(group_lengths: list[int], row_lengths: tuple[int, .
     if not group_lengths or len(group_lengths) * num_kv_heads >= 2 * slots:
         return 0
     longest = max(group_lengths)
-    best = (prefill_model_us(group_lengths, row_lengths, num_kv_heads, num_heads, head_dim, 0), 0)
+    model = functools.partial(prefill_model_us, group_lengths, row_lengths, num_kv_heads, num_heads, head_dim,
+                              waves_per_group=waves_per_group)
+    best = (model(0), 0)
     for size in PREFILL_PARTITION_CANDIDATES:
         if size >= longest:
             break
-        t = prefill_model_us(group_lengths, row_lengths, num_kv_heads, num_heads, head_dim, size)
+        t = model(size)
         if t < best[0]:
             best = (t, size)
     return best[1]
@@ -596,6 +614,7 @@ def attend_with(
     partials_only: bool = False,
     prefill: bool | None = None,
     merge: str | None = None,
+    tile_pairs: int | None = None,
 ) -> None:
     """:func:`attend` with the launch chosen by the caller.
 
@@ -611,7 +630,9 @@ def attend_with(
     ``False`` the decode kernels, ``None`` lets the row count decide) ``partitions`` 0
     covers each tile's context in one workgroup, ``partition_size`` splits it into
     partitions of that size (a multiple of 64) merged by the reduce kernel, and ``None``
-    for both lets :func:`choose_prefill_partition` decide.
+    for both lets :func:`choose_prefill_partition` decide; ``tile_pairs`` forces the tile
+    capacity (:data:`PREFILL_PAIRS`, or a half or a quarter of it; ``None``:
+    :func:`prefill_tile_pairs`).
     Benchmarks and tests use them to time and check every kernel on one step.
     """
     op = "attention.attend"
@@ -681,7 +702,7 @@ def attend_with(
     if prefill:
         if not isinstance(step, HipAttentionPlan):
             raise BackendError(f"{op}: the multi-row kernel needs a planned step", context={"op": op})
-        pairs = PREFILL_PAIRS[buffers.head_dim]
+        pairs = tile_pairs or prefill_tile_pairs(step.rows, heads // kv_heads, buffers.head_dim)
         if heads // kv_heads > pairs:
             raise BackendError(
                 f"{op}: {heads // kv_heads} query heads per key/value head exceed the multi-row "
@@ -706,7 +727,7 @@ def attend_with(
             lib.ayk_paged_prefill(
                 out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),
                 table.stride(0), meta.kv_lengths.data_ptr(), meta.request_of_row.data_ptr(),
-                meta.positions.data_ptr(), tiles.data_ptr(), tiles.numel() // 4, n_rows, heads, kv_heads,
+                meta.positions.data_ptr(), tiles.data_ptr(), tiles.numel() // 4, pairs, n_rows, heads, kv_heads,
                 buffers.head_dim, buffers.num_blocks, block_size, table.shape[1],
                 _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype], _kv_code(buffers, q.dtype),
                 float(scale), size, scratch.data_ptr() if scratch is not None else 0,

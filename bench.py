@@ -178,7 +178,8 @@ def multi_row(args) -> int:
         scale = dim ** -0.5
         kernel = time_calls(lambda: hip_attention.attend_with(q, buffers, meta, out, scale=scale, partitions=None,
                                                               prefill=True), args.steps, args.warmup)
-        size = meta.plan.prefill_split(kv_heads, heads // kv_heads, hip_attention.PREFILL_PAIRS[dim], dim)
+        pairs = hip_attention.prefill_tile_pairs(meta.plan.rows, heads // kv_heads, dim)
+        size = meta.plan.prefill_split(kv_heads, heads // kv_heads, pairs, dim)
         unsplit = kernel if not size else time_calls(
             lambda: hip_attention.attend_with(q, buffers, meta, per_row, scale=scale, partitions=0, prefill=True),
             args.steps, args.warmup)
@@ -194,6 +195,7 @@ def multi_row(args) -> int:
             "workload": f"{requests} requests x {rows} rows over {context} positions, Hq {heads}, Hkv {kv_heads}, "
                         f"D {dim}, bf16, block {bs}",
             "us_per_call": round(us, 2),
+            "tile_pairs": pairs,
             "partition_size": size,
             "unsplit_us": round(unsplit["median_us"], 2),
             "tflops": round(flops / us / 1e6, 1),

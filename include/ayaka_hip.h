@@ -166,8 +166,11 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
  * [0, positions[i]] of its request's context; rows of a request with
  * kv_lengths 0 get zeros. tiles lists n_tiles (first_row, row_count, request,
  * partition) int32 quadruples: consecutive rows of one request with row_count *
- * (num_heads / num_kv_heads) <= ayk_paged_prefill_tile_pairs(head_dim), covering
- * every row once (rows past that many pairs are not computed). One workgroup per
+ * (num_heads / num_kv_heads) <= tile_pairs, covering every row once (rows past
+ * that many pairs are not computed). tile_pairs is
+ * ayk_paged_prefill_tile_pairs(head_dim), or a half or a quarter of it: smaller
+ * tiles (few rows per request, verify windows) share each tile's chunks among 2
+ * or 4 waves instead of spending them on empty pairs. One workgroup per
  * (tile, key/value head) loads each chunk of the context once into LDS for all
  * its rows and query heads; q.k and P.V run on the matrix cores with fp32
  * accumulation. With partition_size 0 a tile covers its whole context and its
@@ -192,7 +195,7 @@ int ayk_paged_prefill_tile_pairs(int32_t head_dim);
 int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,
                       const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
                       const int32_t* request_of_row, const int32_t* positions, const int32_t* tiles,
-                      int32_t n_tiles, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t n_tiles, int32_t tile_pairs, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                       int32_t num_blocks, int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
                       int32_t kv_dtype, float scale, int32_t partition_size, void* workspace,
                       size_t workspace_bytes, void* stream);

@@ -86,6 +86,15 @@ def test_v2_and_store_refusals() -> None:
     assert b"work items" in lib.ayk_last_error()
     assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 16, 1 << 20, None, 8 | 16, None) == 1
     assert b"exclude each other" in lib.ayk_last_error()
+    # the multi-row entry: tiles of the full capacity (128 at head_dim 128), a half or a
+    # quarter; a partition size that is not a multiple of 64; the partitions' workspace
+    def prefill(tile_pairs: int, size: int = 0, workspace: int = 0) -> int:
+        return lib.ayk_paged_prefill(1, 1, 1, 1, 1, 4, 1, 1, 1, 1, 2, tile_pairs, 3, 8, 2, 128, 10, 16, 4, 0, 1, 1,
+                                     ctypes.c_float(1.0), size, 1, workspace, None)
+    assert prefill(100) == 1 and b"tile_pairs 100 is not 128, 64 or 32" in lib.ayk_last_error()
+    assert prefill(16) == 1
+    assert prefill(32, size=96) == 1 and b"multiple of 64" in lib.ayk_last_error()
+    assert prefill(64, size=64, workspace=16) == 4 and b"workspace" in lib.ayk_last_error()
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 3, None) == 2
     assert lib.ayk_reshape_and_cache_e4m3(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 2, None) == 2
     assert b"src_dtype 2" in lib.ayk_last_error()

@@ -199,19 +199,23 @@ def test_multi_row_kernel(dtype: str, heads: int, kv_heads: int, head_dim: int, 
         assert torch.count_nonzero(out[padding_rows]) == 0
 
 
+@pytest.mark.parametrize("waves", [1, 2, 4])
 @pytest.mark.parametrize("size", [0, 64, 192, 512])
 @pytest.mark.parametrize("heads,kv_heads,head_dim,dtype", [(8, 2, 64, "fp16"), (32, 8, 128, "bf16"),
                                                            (4, 4, 256, "bf16")])
 @pytest.mark.parametrize("name,steps", PREFILL_CASES, ids=[c[0] for c in PREFILL_CASES])
-def test_multi_row_partitions(size: int, heads: int, kv_heads: int, head_dim: int, dtype: str, name: str,
-                              steps: list) -> None:
+def test_multi_row_partitions(size: int, waves: int, heads: int, kv_heads: int, head_dim: int, dtype: str,
+                              name: str, steps: list) -> None:
     # size 0: each tile's whole context in one workgroup; otherwise partitions of `size`
-    # positions merged by the reduce kernel, each row over the partitions it sees
+    # positions merged by the reduce kernel, each row over the partitions it sees. waves:
+    # tiles of the full pair capacity, or of a half or a quarter whose 2 or 4 waves per
+    # pair group split every chunk and merge their states at the end
     s = build_scenario(steps, dtype=dtype, heads=heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16,
                        mode="mixed", seed=68, spare_blocks=2)
     launch = dict(partitions=0) if size == 0 else dict(partition_size=size)
-    out = run_attention(s, prefill=True, **launch)
-    assert_parity(out, s.expected(np.float64), dtype, f"prefill/{name}/{size}")
+    pairs = hip_attention.PREFILL_PAIRS[head_dim] // waves
+    out = run_attention(s, prefill=True, tile_pairs=pairs, **launch)
+    assert_parity(out, s.expected(np.float64), dtype, f"prefill/{name}/{size}/{pairs}")
     padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
     if padding_rows:
         assert torch.count_nonzero(out[padding_rows]) == 0
