@@ -314,7 +314,7 @@ FP8_CASES = [
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("layout", ["nhd", "hnd"])
-@pytest.mark.parametrize("heads,kv_heads,head_dim", [(8, 2, 128), (32, 8, 64), (64, 8, 128), (4, 4, 256)])
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(8, 2, 128), (32, 8, 64), (64, 8, 128), (4, 4, 256), (32, 8, 256)])
 @pytest.mark.parametrize("name,steps,mode", FP8_CASES, ids=[c[0] for c in FP8_CASES])
 def test_fp8_attention_matches_the_oracle_on_decoded_values(dtype: str, layout: str, heads: int, kv_heads: int,
                                                             head_dim: int, name: str, steps: list, mode: str) -> None:
