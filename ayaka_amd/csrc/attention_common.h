@@ -474,8 +474,14 @@ __device__ __forceinline__ f32x4 mfma_pv(u32x2 v, u32x2 w, f32x4 acc) {
   }
 }
 
-// Split 4 fp32 weights w (finite, >= 0) into packed 16-bit high parts and packed
-// 16-bit parts of the remainder, both by truncation: |w - h - l| < 2^-14 w (bf16).
+// The P of the P.V MFMA as packed 16-bit weights. A bf16 weight (8 significant
+// bits) is off by up to 2^-9 of itself, the size of the accuracy bar, so bf16 P
+// takes two MFMAs: packed high parts and packed parts of the remainder, both by
+// truncation, |w - h - l| < 2^-14 w. An fp16 weight rounded to nearest (11 bits)
+// is within 2^-12 w, and one MFMA suffices: then only `hi` is set.
+constexpr bool split_p(bool bf16) { return bf16; }
+
+// Split 4 fp32 weights w (finite, >= 0) as above.
 template <bool BF16>
 __device__ __forceinline__ void split_weights4(const float (&w)[4], u32x2& hi, u32x2& lo) {
   uint32_t h[2], r[2];
@@ -489,9 +495,8 @@ __device__ __forceinline__ void split_weights4(const float (&w)[4], u32x2& hi, u
       const float rb = b - __uint_as_float(ub & 0xffff0000u);
       r[i] = __builtin_amdgcn_perm(__float_as_uint(rb), __float_as_uint(ra), 0x07060302u);
     } else {
-      const auto hv = __builtin_amdgcn_cvt_pkrtz(a, b);
-      h[i] = __builtin_bit_cast(uint32_t, hv);
-      r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a - (float)hv[0], b - (float)hv[1]));
+      h[i] = __builtin_bit_cast(uint32_t, f16x2{(_Float16)a, (_Float16)b});  // v_cvt_pk_f16_f32, to nearest
+      r[i] = 0u;
     }
   }
   hi = u32x2{h[0], h[1]};

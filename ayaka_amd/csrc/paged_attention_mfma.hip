@@ -14,13 +14,16 @@
 //    sums; q needs only head_dim/32 registers per lane whatever the group size.
 //    Lane l gets the scores of tokens 4*(l/16)+i, i < 4, for head l%16.
 //  * The softmax runs on those 4 scores per lane (max across the 4 lane
-//    groups with two shuffles); the weights go through a small per-wave LDS
-//    tile to the lanes that hold the values.
-//  * P.V stays on the VALU in fp32 (a bf16 P would cost ~2e-3 relative error),
-//    with the value layout of the DPP kernel: lane (r, c) holds 8 elements of
-//    tokens j*TPL + r.
+//    groups with two shuffles).
+//  * P.V is O^T += V^T P^T on v_mfma_f32_16x16x16: the lane's 4 weights are
+//    exactly its B operand (tokens 4*(l/16)+i of head l%16), and V^T comes from
+//    a token-major LDS tile through ds_read_b64_tr_b16. A bf16 P is split into
+//    a truncated high part and the remainder (two MFMAs, fp32-level accuracy;
+//    one bf16 P would cost ~2e-3 relative); an fp16 P rounded to nearest is
+//    within 2^-12 and takes one.
 //  * fp8 caches (KV8) are decoded at their use; a chunk then holds two 16-token
-//    tiles, so a wave keeps as many bytes in flight as with 16-bit caches.
+//    tiles (one at head_dim 256), so a wave keeps as many bytes in flight as
+//    with 16-bit caches.
 //
 // This removes the per-token dot2 and butterfly work that grows with the group
 // in the DPP kernel, and reads keys as whole 256-byte token rows.
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
         for (int t = 0; t < DT; ++t) {
           const u32x2 va = lds_read_transposed(&s_v[wave][(4 * mq + (mt >> 2)) * VP + t * 16 + 4 * (mt & 3)]);
           o[t] = mfma_pv<BF16>(va, phi, o[t]);
-          o[t] = mfma_pv<BF16>(va, plo, o[t]);
+          if constexpr (split_p(BF16)) o[t] = mfma_pv<BF16>(va, plo, o[t]);
         }
       }
     };

@@ -24,10 +24,10 @@
 //  * O^T += V^T P^T, per 16-element slice of head_dim and 32 positions:
 //    v_mfma_f32_16x16x32 with P^T taken straight from the lane's scores (its
 //    8 k-slots are positions 4*(l/16)+i of two adjacent 16-position tiles) and
-//    V^T read from a transposed LDS tile in that same position order. P is split
-//    by truncation into a 16-bit high part and the 16-bit remainder, two MFMAs,
-//    which keeps the product at fp32-level accuracy (one 16-bit P would cost
-//    ~2e-3 relative).
+//    V^T read from a transposed LDS tile in that same position order. A bf16 P is
+//    split by truncation into a 16-bit high part and the 16-bit remainder, two
+//    MFMAs, which keeps the product at fp32-level accuracy (one bf16 P would cost
+//    ~2e-3 relative); an fp16 P rounded to nearest is within 2^-12 and takes one.
 //  * The transposed value tile is written with 32-bit LDS stores: each thread
 //    carries the same 8 elements of two adjacent positions. Its row stride and the
 //    threads' value-load mapping keep stores and reads nearly free of bank
@@ -58,38 +58,17 @@ __device__ __forceinline__ f32x4 mfma32(u32x4 a, u32x4 b, f32x4 acc) {
                                                   acc, 0, 0, 0);
 }
 
-// Split 8 fp32 weights w (finite, >= 0) into packed 16-bit high parts h and packed
-// 16-bit parts l of the remainder w - h, both by truncation: |w - h - l| < 2^-14 w
-// for bf16 (2^-20 w for fp16), against ~2^-9 w for a single rounded 16-bit weight.
-// bf16 truncation is the top half of the fp32 bits (one v_perm_b32 packs two);
-// fp16 uses v_cvt_pkrtz (round toward zero).
+// Split 8 fp32 weights w (finite, >= 0) as split_weights4 (bf16: high parts and
+// remainders by truncation, one v_perm_b32 packing two; fp16: rounded to nearest).
 template <bool BF16>
 __device__ __forceinline__ void split_weights(const float (&w)[8], u32x4& hi, u32x4& lo) {
-  uint32_t h[4], r[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float a = w[2 * i], b = w[2 * i + 1];
-    if constexpr (BF16) {
-      const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
-      h[i] = __builtin_amdgcn_perm(ub, ua, 0x07060302u);
-      const float ra = a - __uint_as_float(ua & 0xffff0000u);
-      const float rb = b - __uint_as_float(ub & 0xffff0000u);
-      r[i] = __builtin_amdgcn_perm(__float_as_uint(rb), __float_as_uint(ra), 0x07060302u);
-    } else {
-      const auto hv = __builtin_amdgcn_cvt_pkrtz(a, b);
-      h[i] = __builtin_bit_cast(uint32_t, hv);
-      r[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a - (float)hv[0], b - (float)hv[1]));
-    }
-  }
-  hi = u32x4{h[0], h[1], h[2], h[3]};
-  lo = u32x4{r[0], r[1], r[2], r[3]};
+  u32x2 h0, l0, h1, l1;
+  split_weights4<BF16>({w[0], w[1], w[2], w[3]}, h0, l0);
+  split_weights4<BF16>({w[4], w[5], w[6], w[7]}, h1, l1);
+  hi = u32x4{h0.x, h0.y, h1.x, h1.y};
+  lo = u32x4{l0.x, l0.y, l1.x, l1.y};
 }
 
-// PS waves share each group of pairs and split every chunk's positions between
-// them (PS = 1, 2 or 4; tiles of prefill_tile_pairs(D) / PS pairs), so a tile of
-// few (row, head) pairs -- a short verify window -- does not spend the other
-// waves' matrix-core time on idle pairs; the waves of a group merge their
-// running states through LDS at the end.
 template <int D, bool BF16, bool KV8, int PS>
 __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const AttnParams p, const int32_t* tiles) {
   using E = Elem<BF16>;
@@ -365,7 +344,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 #pragma unroll
             for (int j = 0; j < PT; ++j) {
               o[j][t] = mfma32<BF16>(va, phi[j], o[j][t]);
-              o[j][t] = mfma32<BF16>(va, plo[j], o[j][t]);
+              if constexpr (split_p(BF16)) o[j][t] = mfma32<BF16>(va, plo[j], o[j][t]);
             }
           }
         }
@@ -384,7 +363,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 #pragma unroll
           for (int j = 0; j < PT; ++j) {
             o[j][t] = mfma_pv<BF16>(va, phi[j], o[j][t]);
-            o[j][t] = mfma_pv<BF16>(va, plo[j], o[j][t]);
+            if constexpr (split_p(BF16)) o[j][t] = mfma_pv<BF16>(va, plo[j], o[j][t]);
           }
         }
       }
