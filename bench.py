@@ -147,6 +147,8 @@ MULTI_ROW_WORKLOADS = [
     (4, 512, 4096, 64, 8),    # GQA 8
     (32, 4, 4096, 32, 8),     # verify windows of 4 draft tokens over 4K
     (64, 2, 2048, 32, 8),     # verify windows of 2 draft tokens over 2K
+    (4, 512, 4096, 32, 8, 128, "fp16"),  # the first workload with an fp16 model (one P.V MFMA per step)
+    (4, 512, 4096, 32, 8, 64, "fp16"),   # Llama-3.2-1B shape (D 64, fp16)
 ]
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
@@ -162,17 +164,19 @@ def multi_row(args) -> int:
 
     _lib.lib()
     dev = torch.device("cuda:0")
-    for requests, rows, context, heads, kv_heads in MULTI_ROW_WORKLOADS:
-        bs, dim = 16, 128
+    for requests, rows, context, heads, kv_heads, *shape in MULTI_ROW_WORKLOADS:
+        dim, dtype_name = shape or (128, "bf16")
+        dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[dtype_name]
+        bs = 16
         blocks = requests * (context // bs) + 1
         gen = torch.Generator(device=dev).manual_seed(rows)
-        k = torch.randn((blocks, bs, kv_heads, dim), generator=gen, device=dev).to(torch.bfloat16)
-        v = torch.randn((blocks, bs, kv_heads, dim), generator=gen, device=dev).to(torch.bfloat16)
+        k = torch.randn((blocks, bs, kv_heads, dim), generator=gen, device=dev).to(dtype)
+        v = torch.randn((blocks, bs, kv_heads, dim), generator=gen, device=dev).to(dtype)
         ids = torch.randperm(blocks - 1, generator=gen, device=dev)[: blocks - 1] + 1
         table = ids.view(requests, context // bs).to(torch.int32)
         meta = hip_attention.plan(ForwardMode.MIXED, torch.full((requests,), rows, dtype=torch.int32, device=dev),
                                   torch.full((requests,), context, dtype=torch.int32, device=dev), table, bs)
-        q = torch.randn((requests * rows, heads, dim), generator=gen, device=dev).to(torch.bfloat16)
+        q = torch.randn((requests * rows, heads, dim), generator=gen, device=dev).to(dtype)
         out, per_row = torch.empty_like(q), torch.empty_like(q)
         buffers = KVBuffers(k, v, KVLayoutKind.NHD, RAW_CODEC)
         scale = dim ** -0.5
@@ -193,7 +197,7 @@ def multi_row(args) -> int:
         us = kernel["median_us"]
         print(json.dumps({
             "workload": f"{requests} requests x {rows} rows over {context} positions, Hq {heads}, Hkv {kv_heads}, "
-                        f"D {dim}, bf16, block {bs}",
+                        f"D {dim}, {dtype_name}, block {bs}",
             "us_per_call": round(us, 2),
             "tile_pairs": pairs,
             "partition_size": size,
