@@ -149,14 +149,45 @@ class HipAttentionPlan:
         groups.sort(key=lambda g: (-g[0], g[1]))
         return groups
 
-    def prefill_split(self, num_kv_heads: int, group: int, pairs: int, head_dim: int) -> int:
-        """The partition size of the step's multi-row launch (0: none), chosen once for every layer."""
-        key = ("prefill", num_kv_heads, group, pairs, head_dim)
+    def prefill_split(self, num_kv_heads: int, group: int, pairs: int, head_dim: int, kv_bytes: int = 2) -> int:
+        """The partition size of the step's multi-row launch with tiles of ``pairs`` (0: none),
+        chosen once for every layer."""
+        key = ("prefill", num_kv_heads, group, pairs, head_dim, kv_bytes)
         found = self.splits.get(key)
         if found is None:
             lengths = [g[0] for g in self.prefill_groups(group, pairs)]
             found = choose_prefill_partition(lengths, self.row_lengths, num_kv_heads, num_kv_heads * group,
-                                             head_dim, PREFILL_PAIRS[head_dim] // pairs)
+                                             head_dim, PREFILL_PAIRS[head_dim] // pairs,
+                                             self.context_bytes(num_kv_heads, head_dim, kv_bytes))
+            self.splits[key] = found
+        return found
+
+    def context_bytes(self, num_kv_heads: int, head_dim: int, kv_bytes: int = 2) -> int:
+        """K and V bytes of the contexts the step's multi-row requests read (once each)."""
+        positions = sum(length for count, length in zip(self.rows, self.kv_lengths) if count)
+        return positions * num_kv_heads * head_dim * 2 * kv_bytes
+
+    def prefill_launch(self, num_kv_heads: int, group: int, head_dim: int, kv_bytes: int = 2) -> tuple[int, int]:
+        """(tile pairs, partition size) of the step's multi-row launch: of the full tile, a
+        half and a quarter (each at its best partition size), the one with the smallest
+        :func:`prefill_model_us`; chosen once for every layer."""
+        key = ("prefill-launch", num_kv_heads, group, head_dim, kv_bytes)
+        found = self.splits.get(key)
+        if found is None:
+            full = PREFILL_PAIRS[head_dim]
+            context = self.context_bytes(num_kv_heads, head_dim, kv_bytes)
+            best = None
+            for waves in (1, 2, 4):
+                pairs = full // waves
+                if pairs < group:
+                    break
+                size = self.prefill_split(num_kv_heads, group, pairs, head_dim, kv_bytes)
+                lengths = [g[0] for g in self.prefill_groups(group, pairs)]
+                t = prefill_model_us(lengths, self.row_lengths, num_kv_heads, num_kv_heads * group, head_dim, size,
+                                     waves, context)
+                if best is None or t < best[0]:
+                    best = (t, pairs, size)
+            found = (best[1], best[2])
             self.splits[key] = found
         return found
 
@@ -468,51 +499,60 @@ def choose_partitions(n_rows: int, num_kv_heads: int, group: int, max_length: in
 
 #: Multi-row workgroups one compute unit runs at a time (the kernel's launch bounds).
 PREFILL_WORKGROUPS_PER_CU = 2
-#: Positions one multi-row workgroup folds per step, and the measured time of a step
-#: (about 3 us on MI355X, with 2 workgroups per CU or fewer; 4x512 rows over 4K run
-#: 60 steps in 222 us, a 2048-row prompt's longest tile 32 steps in 96 us).
+#: Positions one multi-row workgroup folds per step, and the time of a step by waves per
+#: pair group (tiles of the full capacity, a half, a quarter); with the streaming rate, the
+#: partials' rate and the reduce launch below, fitted to a sweep of 13 step shapes x 3 tile
+#: sizes x 5 partition sizes on MI355X (the model's choice averaged 1.4% and at worst 7%
+#: above the fastest measured launch).
 PREFILL_CHUNK = 64
-PREFILL_CHUNK_US = 3.0
-#: The same with tiles of a half or a quarter of the pairs, whose 2 or 4 waves per pair
-#: group split each chunk.
-PREFILL_CHUNK_US_BY_WAVES = {1: PREFILL_CHUNK_US, 2: 2.0, 4: 1.5}
+PREFILL_CHUNK_US_BY_WAVES = {1: 3.0, 2: 2.5, 4: 2.0}
+#: Rate (bytes per us) at which a launch streams K and V it reads once (about 6.5 TB/s).
+PREFILL_STREAM_BYTES_PER_US = 6.5e6
 #: Rate (bytes per us) at which partials are written and read back, and the reduce launch.
-PREFILL_PARTIALS_BYTES_PER_US = 5.0e6
-PREFILL_REDUCE_US = 4.0
+PREFILL_PARTIALS_BYTES_PER_US = 3.0e6
+PREFILL_REDUCE_US = 2.0
 #: Partition sizes a multi-row launch chooses from.
 PREFILL_PARTITION_CANDIDATES = (128, 256, 512, 1024, 2048, 4096)
 
 
-def prefill_tile_pairs(rows: tuple[int, ...] | list[int], group: int, head_dim: int) -> int:
-    """Tile capacity of a multi-row launch: the smallest of the full tile, a half and a quarter
-    that holds the (rows x query heads) pairs of the step's largest request (and a group)."""
-    full = PREFILL_PAIRS[head_dim]
-    need = max(max(rows, default=1), 1) * group
-    for pairs in (full // 4, full // 2):
-        if pairs >= max(need, group):
-            return pairs
-    return full
+def _dispatch_makespan(steps: list[int], slots: int) -> int:
+    """Finish time (in chunk steps) of workgroups of these lengths started longest first, each
+    in the first of ``slots`` identical slots to free up."""
+    if len(steps) <= slots:
+        return max(steps, default=0)
+    steps = sorted(steps, reverse=True)
+    if steps[0] == steps[-1]:
+        return -(-len(steps) // slots) * steps[0]
+    loads = steps[:slots]
+    heapq.heapify(loads)
+    for s in steps[slots:]:
+        heapq.heapreplace(loads, loads[0] + s)
+    return max(loads)
 
 
 def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | list[int], num_kv_heads: int,
-                     num_heads: int, head_dim: int, partition_size: int, waves_per_group: int = 1) -> float:
-    """Modelled time (us) of a multi-row launch: the longer of its longest workgroup and its
-    total work spread over every workgroup slot (a lower bound of any schedule, which the
-    longest-first order nearly reaches), in chunk steps; plus, with partitions, writing and
-    reading back the partials of rows that span several, and the reduce launch."""
+                     num_heads: int, head_dim: int, partition_size: int, waves_per_group: int = 1,
+                     context_bytes: int = 0) -> float:
+    """Modelled time (us) of a multi-row launch.
+
+    Its workgroups (one per tile, partition and key/value head) start longest first, each
+    in the first of the GPU's workgroup slots to free up (:func:`_dispatch_makespan`), at
+    :data:`PREFILL_CHUNK_US_BY_WAVES` per 64-position chunk, but the launch takes no less
+    than streaming the requests' K and V once (``context_bytes``).
+    With partitions, writing and reading back the partials of rows that span several and
+    the reduce launch are added.
+    """
     slots = COMPUTE_UNITS * PREFILL_WORKGROUPS_PER_CU
-    longest, total = 0, 0
+    steps = []
     for length in group_lengths:
         if partition_size:
             full, rest = divmod(length, partition_size)
             pieces = [partition_size] * full + ([rest] if rest else [])
         else:
             pieces = [length]
-        for piece in pieces or [0]:
-            steps = -(-piece // PREFILL_CHUNK)
-            longest = max(longest, steps)
-            total += steps * num_kv_heads
-    t = max(longest, -(-total // slots)) * PREFILL_CHUNK_US_BY_WAVES[waves_per_group]
+        steps.extend([-(-piece // PREFILL_CHUNK) for piece in pieces or [0]] * num_kv_heads)
+    t = _dispatch_makespan(steps, slots) * PREFILL_CHUNK_US_BY_WAVES[waves_per_group]
+    t = max(t, context_bytes / PREFILL_STREAM_BYTES_PER_US)
     if partition_size:
         parts = sum(-(-n // partition_size) for n in row_lengths if n > partition_size)
         t += 2 * parts * num_heads * (head_dim + 2) * 4 / PREFILL_PARTIALS_BYTES_PER_US + PREFILL_REDUCE_US
@@ -520,7 +560,8 @@ def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | li
 
 
 def choose_prefill_partition(group_lengths: list[int], row_lengths: tuple[int, ...] | list[int],
-                             num_kv_heads: int, num_heads: int, head_dim: int, waves_per_group: int = 1) -> int:
+                             num_kv_heads: int, num_heads: int, head_dim: int, waves_per_group: int = 1,
+                             context_bytes: int = 0) -> int:
     """Partition size of a multi-row launch (0: none) for groups of rows with these context
     lengths: the candidate with the smallest :func:`prefill_model_us`, considered only when
     the unsplit grid fills at most two rounds of the GPU (beyond that the partials' traffic
@@ -530,11 +571,13 @@ def choose_prefill_partition(group_lengths: list[int], row_lengths: tuple[int, .
         return 0
     longest = max(group_lengths)
     model = functools.partial(prefill_model_us, group_lengths, row_lengths, num_kv_heads, num_heads, head_dim,
-                              waves_per_group=waves_per_group)
+                              waves_per_group=waves_per_group, context_bytes=context_bytes)
     best = (model(0), 0)
     for size in PREFILL_PARTITION_CANDIDATES:
         if size >= longest:
             break
+        if sum(-(-n // size) for n in group_lengths) * num_kv_heads > 8 * slots:
+            continue  # more than 8 rounds of partitions: their partials outweigh any balance
         t = model(size)
         if t < best[0]:
             best = (t, size)
@@ -632,7 +675,7 @@ def attend_with(
     partitions of that size (a multiple of 64) merged by the reduce kernel, and ``None``
     for both lets :func:`choose_prefill_partition` decide; ``tile_pairs`` forces the tile
     capacity (:data:`PREFILL_PAIRS`, or a half or a quarter of it; ``None``:
-    :func:`prefill_tile_pairs`).
+    :meth:`HipAttentionPlan.prefill_launch`).
     Benchmarks and tests use them to time and check every kernel on one step.
     """
     op = "attention.attend"
@@ -702,7 +745,8 @@ def attend_with(
     if prefill:
         if not isinstance(step, HipAttentionPlan):
             raise BackendError(f"{op}: the multi-row kernel needs a planned step", context={"op": op})
-        pairs = tile_pairs or prefill_tile_pairs(step.rows, heads // kv_heads, buffers.head_dim)
+        pairs = tile_pairs or step.prefill_launch(kv_heads, heads // kv_heads, buffers.head_dim,
+                                                  1 if buffers.codec == FP8_E4M3_CODEC else 2)[0]
         if heads // kv_heads > pairs:
             raise BackendError(
                 f"{op}: {heads // kv_heads} query heads per key/value head exceed the multi-row "
@@ -710,12 +754,13 @@ def attend_with(
                 context={"op": op, "argument": "q"},
             )
         group = heads // kv_heads
+        kv_bytes = 1 if buffers.codec == FP8_E4M3_CODEC else 2
         if partitions == 0:
             size = 0
         elif partition_size is not None:
             size = partition_size
         else:
-            size = step.prefill_split(kv_heads, group, pairs, buffers.head_dim)
+            size = step.prefill_split(kv_heads, group, pairs, buffers.head_dim, kv_bytes)
         tiles = step.prefill_tiles(group, pairs, size, device)
         scratch, nbytes = None, 0
         if size:

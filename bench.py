@@ -182,8 +182,7 @@ def multi_row(args) -> int:
         scale = dim ** -0.5
         kernel = time_calls(lambda: hip_attention.attend_with(q, buffers, meta, out, scale=scale, partitions=None,
                                                               prefill=True), args.steps, args.warmup)
-        pairs = hip_attention.prefill_tile_pairs(meta.plan.rows, heads // kv_heads, dim)
-        size = meta.plan.prefill_split(kv_heads, heads // kv_heads, pairs, dim)
+        pairs, size = meta.plan.prefill_launch(kv_heads, heads // kv_heads, dim)
         unsplit = kernel if not size else time_calls(
             lambda: hip_attention.attend_with(q, buffers, meta, per_row, scale=scale, partitions=0, prefill=True),
             args.steps, args.warmup)

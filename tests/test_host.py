@@ -173,6 +173,38 @@ def test_multi_row_partition_choice() -> None:
             assert model([1024] * 16, rows, 8, 32, 128, size) <= model([1024] * 16, rows, 8, 32, 128, other)
 
 
+def test_dispatch_makespan() -> None:
+    makespan = hip_attention._dispatch_makespan
+    assert makespan([5, 3, 9], 4) == 9                      # every item starts at once
+    assert makespan([7] * 9, 4) == 21                       # equal items: three rounds
+    assert makespan([10, 10, 2, 2, 2, 2, 2], 2) == 16        # the short ones share the slots
+    # against every order-respecting assignment on tiny cases: greedy longest-first dispatch
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        steps = [int(x) for x in rng.integers(1, 20, size=int(rng.integers(1, 9)))]
+        slots = int(rng.integers(1, 4))
+        loads = [0] * slots
+        for s in sorted(steps, reverse=True):
+            loads[loads.index(min(loads))] += s
+        assert makespan(steps, slots) == max(loads)
+
+
+def test_multi_row_launch_choice() -> None:
+    def launch(rows: list[int], lengths: list[int]) -> tuple[int, int]:
+        table = torch.ones(len(rows), max(lengths) // 16 + 1, dtype=torch.int32)
+        step = hip_attention.plan(ForwardMode.MIXED, _ints(*rows), _ints(*lengths), table, 16).plan
+        return step.prefill_launch(8, 4, 128)
+    # long chunks that fill the GPU: full tiles, no partitions
+    assert launch([512] * 4, [4096] * 4) == (128, 0)
+    # short verify windows: small tiles; few of them: partitions as well
+    assert launch([2] * 64, [2048] * 64)[0] < 128
+    pairs, size = launch([8] * 16, [1024] * 16)
+    assert pairs < 128 and size > 0
+    # decode rows beside one chunk: small tiles, split (they would stream alone otherwise)
+    pairs, size = launch([1] * 64 + [64], [4096] * 65)
+    assert pairs < 128 and size > 0
+
+
 def _cpu_buffers(**changes: object) -> KVBuffers:
     k = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16)
     buffers = KVBuffers(k, k.clone(), KVLayoutKind.NHD, RAW_CODEC)
