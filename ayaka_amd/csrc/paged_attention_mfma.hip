@@ -65,10 +65,12 @@ __device__ __forceinline__ void wave_lds_sync() {
 template <int D, int GC, bool BF16, bool SPLIT, bool KV8>
 __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel(const AttnParams p) {
   constexpr int MT = 16;            // tokens per MFMA tile
-  // Tiles per chunk: fp8 loads carry half the bytes of a 16-bit load, so a chunk
-  // of two tiles keeps as many bytes in flight per wave as the 16-bit kernel; at
-  // head_dim 256 two tiles' loads do not fit the registers (they spilled), one does.
-  constexpr int SUB = KV8 && D <= 128 ? 2 : 1;
+  // Tiles per chunk, so that a wave keeps about as many bytes in flight as a
+  // 16-bit tile of head_dim 128: fp8 loads and head_dim 64 carry half of that per
+  // tile (two tiles), fp8 at head_dim 64 a quarter (four); at head_dim 256 two fp8
+  // tiles' loads do not fit the registers (they spilled), one does. Measured: C2
+  // (fp16, head_dim 64) 26.2 -> 25.2 us with two tiles.
+  constexpr int SUB = D == 64 ? (KV8 ? 4 : 2) : (KV8 && D <= 128 ? 2 : 1);
   constexpr int CH = MT * SUB;      // tokens per chunk
   constexpr int KS = D / 32;        // MFMA k-steps over head_dim
   constexpr int CPT = D / 8;        // 8-element pieces per token (= value lanes per token)
