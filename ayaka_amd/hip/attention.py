@@ -191,14 +191,23 @@ class HipAttentionPlan:
             self.splits[key] = found
         return found
 
-    def prefill_tiles(self, group: int, pairs: int, partition_size: int, device: torch.device) -> torch.Tensor:
+    def prefill_tiles(self, group: int, pairs: int, partition_size: int, device: torch.device,
+                      capture: bool = False) -> torch.Tensor:
         """(first row, row count, request, partition) quadruples for the multi-row kernel.
 
         Without partitions (``partition_size`` 0) one tile per group of rows, heaviest
         first; with them, one per partition the group's last row sees, longest first.
+        Built once per step and launch shape; building copies it to the device, which a
+        graph capture cannot record (``capture``: raise instead).
         """
         key = (-group, pairs, partition_size)
         found = self.work.get(key)
+        if found is None and capture:
+            raise BackendError(
+                "attention.attend: the multi-row tile list of this step is built on its first "
+                "call; run the step once eagerly before capturing it",
+                context={"op": "attention.attend"},
+            )
         if found is None:
             tiles = []
             for length, row, n, request in self.prefill_groups(group, pairs):
@@ -761,7 +770,7 @@ def attend_with(
             size = partition_size
         else:
             size = step.prefill_split(kv_heads, group, pairs, buffers.head_dim, kv_bytes)
-        tiles = step.prefill_tiles(group, pairs, size, device)
+        tiles = step.prefill_tiles(group, pairs, size, device, capturing(q))
         scratch, nbytes = None, 0
         if size:
             max_partitions = -(-table.shape[1] * block_size // size)

@@ -233,6 +233,36 @@ def test_multi_row_partitions_across_table_segments(block_size: int) -> None:
         assert_parity(run_attention(s, prefill=True, **launch), expected, "bf16", f"bs{block_size}/{size}")
 
 
+@pytest.mark.parametrize("launch", [dict(partitions=0), dict(partitions=None, partition_size=128)],
+                         ids=["whole", "partitions"])
+def test_multi_row_step_in_a_captured_graph(launch: dict) -> None:
+    # an eagerly planned multi-row step captures once it has run eagerly (its tile list and
+    # workspace exist); every replay, with eager work between, matches the eager call
+    s = build_scenario([(40, 600), (3, 3), (7, 300)], heads=8, kv_heads=2, head_dim=128, block_size=16,
+                       mode="mixed", seed=46)
+    buffers, meta = scenario_buffers(s), plan_scenario(s)
+    q = to_device(s.q_bits, s.dtype)
+    eager, out = torch.full_like(q, 7.0), torch.full_like(q, 7.0)
+    hip_attention.attend_with(q, buffers, meta, eager, scale=s.scale, prefill=True, **launch)
+    torch.cuda.synchronize()
+    assert_parity(eager, s.expected(np.float64), "bf16", "eager")
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        hip_attention.attend_with(q, buffers, meta, out, scale=s.scale, prefill=True, **launch)
+    for _ in range(3):
+        out.fill_(7.0)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    # a step never run eagerly has no tile list yet: capture refuses it before any launch
+    fresh = plan_scenario(s)
+    with pytest.raises(BackendError, match="run the step once eagerly before capturing it"):
+        with torch.cuda.graph(torch.cuda.CUDAGraph()):
+            hip_attention.attend_with(q, buffers, fresh, out, scale=s.scale, prefill=True, **launch)
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("block_size", [1, 4, 8, 16, 32, 64])
 @pytest.mark.parametrize("qk", QK)
 def test_block_sizes(block_size: int, qk: str) -> None:
