@@ -157,15 +157,12 @@ int compute_units() {
 // Whether v2 merges its partitions inside the partition kernel (rather than in
 // a reduce kernel) for a grid of `workgroups`. Measured on MI355X: the in-kernel
 // merge costs each workgroup a device-scope release (an L2 write-back) and the
-// last one of a row the merge; when the whole grid runs in one round of the GPU
-// (C2, C3, C4 at up to 256 workgroups) these land together in the kernel's tail
-// and cost more (~10 us) than the reduce launch (~5 us), while past one round
-// (C5) they overlap the streaming of later workgroups. A grid of a few dozen
-// workgroups is latency-bound, and there the second launch is the larger cost.
-bool merge_in_kernel(int64_t workgroups) {
-  const int64_t cus = compute_units();
-  return workgroups > cus || workgroups <= cus / 4;
-}
+// last one of a row the merge; with the reduce kernel merging several heads per
+// workgroup (a few hundred workgroups for C3) the second launch costs less on
+// every benchmark grid (C3 161.4 vs 170.8 us, fp8 C5 228.0 vs 236.9, C5 a tie) but
+// a tiny one: a grid of a few dozen workgroups is latency-bound, and there the
+// second launch is the larger cost (C1 15.9 vs 18.9 us).
+bool merge_in_kernel(int64_t workgroups) { return workgroups <= compute_units() / 4; }
 
 // Heads per wave from which the library picks the matrix-core q.k kernel.
 constexpr int kMfmaMinHeads = 3;

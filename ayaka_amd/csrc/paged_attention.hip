@@ -285,50 +285,48 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
   }
 }
 
-// Merge the partitions of one (row, head): o = sum_p w_p o_p / sum_p w_p with
-// w_p = l_p * 2^(m_p - max m). Thread t owns 4 elements (t % (D/4)) of every
-// SLOTS-th partition from t / (D/4) on and merges them online (its own running
-// max), so all partial loads are independent; the SLOTS partial merges then
-// meet in LDS with the same log-sum-exp rule. A row with one partition copies
-// it, so v2 with a single partition rounds exactly the value v1 rounds.
+// Merge the partitions of (row, head) pairs: o = sum_p w_p o_p / sum_p w_p with
+// w_p = l_p * 2^(m_p - max m). A workgroup serves HEADS = 256 / (S * D/4)
+// consecutive (row, head) pairs, S * D/4 threads each: thread t of a pair owns 4
+// elements (t % (D/4)) of every S-th partition from t / (D/4) on and merges them
+// online (its own running max), so its partial loads are independent; the S
+// partial merges then meet in LDS with the same log-sum-exp rule. The host
+// takes S = 1 for a few partitions per row (one workgroup then merges 8 heads
+// at D 128: a step's grid is a few hundred workgroups, not one per head) and
+// more for long rows, whose serial folds would otherwise be long. A row with
+// one partition was written by the partition kernel, so v2 with a single
+// partition rounds exactly the value v1 rounds; a row without context gets zeros.
 constexpr int kReduceThreads = 256;
 
-template <int D, bool BF16>
+template <int D, bool BF16, int S>
 __global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const AttnParams p) {
   using E = Elem<BF16>;
-  constexpr int QUADS = D / 4;                     // float4 groups of a row
-  constexpr int SLOTS = kReduceThreads / QUADS;    // partitions merged side by side
-  __shared__ f32x4 s_acc[SLOTS][QUADS];
-  __shared__ float s_m[SLOTS];
-  __shared__ float s_l[SLOTS];
+  constexpr int QUADS = D / 4;                // float4 groups of a row
+  constexpr int HEADS = kReduceThreads / (S * QUADS);
+  static_assert(HEADS >= 1 && HEADS * S * QUADS == kReduceThreads, "reduce shape");
+  __shared__ f32x4 s_acc[HEADS][S][QUADS];
+  __shared__ float s_m[HEADS][S];
+  __shared__ float s_l[HEADS][S];
 
-  const int h = blockIdx.x % p.num_heads;
-  const int row = blockIdx.x / p.num_heads;
   const int tid = threadIdx.x;
+  const int hl = tid / (S * QUADS);
   const int quad = tid % QUADS;
-  const int slot = tid / QUADS;
+  const int slot = (tid / QUADS) % S;
+  const int64_t pair = (int64_t)blockIdx.x * HEADS + hl;  // (row, head) over n_rows x num_heads
+  const bool valid = pair < (int64_t)p.n_rows * p.num_heads;
+  const int row = valid ? (int)(pair / p.num_heads) : 0;
   int req, len;
   row_context(p, row, req, len);
-  const int64_t head_row = (int64_t)row * p.num_heads + h;
-  uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D;
-  const int np = len > 0 ? (len - 1) / p.partition_size + 1 : 0;
-  const float* ml = p.part_ml + head_row * p.max_partitions * 2;
-  const f32x4* po = reinterpret_cast<const f32x4*>(p.part_o + head_row * p.max_partitions * D);
+  const int np = valid ? (len > 0 ? (len - 1) / p.partition_size + 1 : 0) : 1;
+  uint16_t* out = static_cast<uint16_t*>(p.out) + pair * D;
+  const float* ml = p.part_ml + pair * p.max_partitions * 2;
+  const f32x4* po = reinterpret_cast<const f32x4*>(p.part_o + pair * p.max_partitions * D);
 
-  if (np == 1) return;  // the partition kernel wrote the row's output itself
-  if (np == 0) {
-    if (slot == 0) {
-      const f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      uint32_t* o32 = reinterpret_cast<uint32_t*>(out) + quad * 2;
-      o32[0] = E::round(v.x) | (E::round(v.y) << 16);
-      o32[1] = E::round(v.z) | (E::round(v.w) << 16);
-    }
-    return;
-  }
   float m = kNoScore, l = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int nfold = np > 1 ? np : 0;  // rows of one partition (or none) fold nothing
 #pragma unroll 4
-  for (int i = slot; i < np; i += SLOTS) {
+  for (int i = slot; i < nfold; i += S) {
     const float mi = ml[2 * i];
     const float wi = ml[2 * i + 1];
     const f32x4 v = po[(int64_t)i * QUADS + quad];
@@ -339,29 +337,34 @@ __global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const 
     acc = acc * a + v * b;
     m = mn;
   }
-  s_acc[slot][quad] = acc;
-  if (quad == 0) {
-    s_m[slot] = m;
-    s_l[slot] = l;
-  }
-  __syncthreads();
-  if (slot == 0) {
-    float mn = s_m[0];
-#pragma unroll
-    for (int s = 1; s < SLOTS; ++s) mn = fmaxf(mn, s_m[s]);
-    f32x4 total = {0.f, 0.f, 0.f, 0.f};
-    float L = 0.f;
-#pragma unroll
-    for (int s = 0; s < SLOTS; ++s) {
-      const float w = fast_exp2(s_m[s] - mn);
-      L += s_l[s] * w;
-      total += s_acc[s][quad] * w;
+  if constexpr (S > 1) {
+    s_acc[hl][slot][quad] = acc;
+    if (quad == 0) {
+      s_m[hl][slot] = m;
+      s_l[hl][slot] = l;
     }
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
-    uint32_t* o32 = reinterpret_cast<uint32_t*>(out) + quad * 2;
-    o32[0] = E::round(total.x * inv) | (E::round(total.y * inv) << 16);
-    o32[1] = E::round(total.z * inv) | (E::round(total.w * inv) << 16);
+    __syncthreads();
   }
+  if (slot != 0 || np == 1) return;
+  float mn = m, L = l;
+  f32x4 total = acc;
+  if constexpr (S > 1) {
+    mn = s_m[hl][0];
+#pragma unroll
+    for (int k = 1; k < S; ++k) mn = fmaxf(mn, s_m[hl][k]);
+    total = f32x4{0.f, 0.f, 0.f, 0.f};
+    L = 0.f;
+#pragma unroll
+    for (int k = 0; k < S; ++k) {
+      const float w = fast_exp2(s_m[hl][k] - mn);
+      L += s_l[hl][k] * w;
+      total += s_acc[hl][k][quad] * w;
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;  // np == 0: zeros
+  uint32_t* o32 = reinterpret_cast<uint32_t*>(out) + quad * 2;
+  o32[0] = E::round(total.x * inv) | (E::round(total.y * inv) << 16);
+  o32[1] = E::round(total.z * inv) | (E::round(total.w * inv) << 16);
 }
 
 // ---------------------------------------------------------------------------
@@ -452,24 +455,29 @@ hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipSt
   return hipGetLastError();
 }
 
+template <int D, bool BF16>
+static hipError_t launch_reduce_typed(const AttnParams& p, hipStream_t stream) {
+  // Partition slots per (row, head): one for up to 4 partitions per row, then 4, then
+  // as many as one workgroup holds for a single head.
+  constexpr int QUADS = D / 4;
+  constexpr int S_MAX = kReduceThreads / QUADS;
+  const int s = p.max_partitions <= 4 ? 1 : p.max_partitions <= 16 ? (S_MAX < 4 ? S_MAX : 4) : S_MAX;
+  const int64_t pairs = (int64_t)p.n_rows * p.num_heads;
+  const dim3 block(kReduceThreads);
+  auto grid = [&](int heads) { return dim3((unsigned)((pairs + heads - 1) / heads)); };
+  if (s == 1) hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, 1>), grid(S_MAX), block, 0, stream, p);
+  else if (s == 4) hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, 4>), grid(S_MAX / 4), block, 0, stream, p);
+  else hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, S_MAX>), grid(1), block, 0, stream, p);
+  return hipGetLastError();
+}
+
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream) {
-  const dim3 grid((unsigned)((int64_t)p.num_heads * p.n_rows)), block(kReduceThreads);
   switch (head_dim) {
-    case 64:
-      if (bf16) hipLaunchKernelGGL((partition_reduce_kernel<64, true>), grid, block, 0, stream, p);
-      else hipLaunchKernelGGL((partition_reduce_kernel<64, false>), grid, block, 0, stream, p);
-      break;
-    case 128:
-      if (bf16) hipLaunchKernelGGL((partition_reduce_kernel<128, true>), grid, block, 0, stream, p);
-      else hipLaunchKernelGGL((partition_reduce_kernel<128, false>), grid, block, 0, stream, p);
-      break;
-    case 256:
-      if (bf16) hipLaunchKernelGGL((partition_reduce_kernel<256, true>), grid, block, 0, stream, p);
-      else hipLaunchKernelGGL((partition_reduce_kernel<256, false>), grid, block, 0, stream, p);
-      break;
+    case 64: return bf16 ? launch_reduce_typed<64, true>(p, stream) : launch_reduce_typed<64, false>(p, stream);
+    case 128: return bf16 ? launch_reduce_typed<128, true>(p, stream) : launch_reduce_typed<128, false>(p, stream);
+    case 256: return bf16 ? launch_reduce_typed<256, true>(p, stream) : launch_reduce_typed<256, false>(p, stream);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace ayk

@@ -384,9 +384,9 @@ def uses_matrix_cores(group: int) -> bool:
 
 def merge_site_for(workgroups: int) -> str:
     """Where the library merges the v2 partitions of a grid of ``workgroups``: ``"in-kernel"``
-    above one round of the compute units or at a quarter round at most, ``"reduce-kernel"``
-    otherwise (the rule of ``merge_in_kernel`` in ``api.hip``)."""
-    return "in-kernel" if workgroups > COMPUTE_UNITS or workgroups <= COMPUTE_UNITS // 4 else "reduce-kernel"
+    for a quarter round of the compute units at most, ``"reduce-kernel"`` otherwise (the rule
+    of ``merge_in_kernel`` in ``api.hip``)."""
+    return "in-kernel" if workgroups <= COMPUTE_UNITS // 4 else "reduce-kernel"
 
 
 def merge_site(num_kv_heads: int, group: int, step: "HipAttentionPlan", partition_size: int) -> str:

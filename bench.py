@@ -35,19 +35,19 @@ HBM_PEAK_GBS = 8000.0
 # the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
 PROFILED_TRAFFIC = {
     (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 1024):
-        (1_082_094_921, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
+        (1_082_046_730, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
     (4, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 704):
-        (668_902_704, 4_054_832, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
-    (5, "paged_attention_mfma_kernel (v2, merge in-kernel)", 3072):
-        (2_605_291_206, 11_375_312, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
+        (668_966_255, 4_054_864, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
+    (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 3072):
+        (2_598_575_834, 10_319_248, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
     (2, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 320):
-        (148_554_886, 2_128_464, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
+        (148_558_725, 2_128_480, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
     (1, "paged_attention_mfma_kernel (v2, merge in-kernel)", 64):
         (1_749_850, 86_080, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
     (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1024):
-        (546_022_135, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
-    (5, "paged_attention_mfma_kernel (v2, merge in-kernel, fp8 cache)", 1280):
-        (1_333_681_658, 21_571_136, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
+        (546_016_631, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
+    (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1280):
+        (1_318_304_460, 20_069_216, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
 }
 
 

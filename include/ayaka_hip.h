@@ -131,8 +131,8 @@ size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads,
  * that finishes a row's partitions last merges them, and leaves its counter at
  * zero again, so the buffer stays ready for the next call. It must not be
  * shared by calls that overlap in time. The library takes the single launch
- * when the grid spans more than one round of the GPU's compute units or is
- * tiny, and a second (reduce) kernel otherwise; AYK_FLAG_SINGLE_LAUNCH and
+ * for a tiny grid (a quarter of the GPU's compute units at most), and a second
+ * (reduce) kernel otherwise; AYK_FLAG_SINGLE_LAUNCH and
  * AYK_FLAG_SEPARATE_REDUCE force one. With NULL arrivals the reduce kernel
  * merges. Either way the merge folds the partitions in partition order,
  * so results do not depend on scheduling. Same arguments and semantics
