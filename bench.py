@@ -149,6 +149,8 @@ MULTI_ROW_WORKLOADS = [
     (64, 2, 2048, 32, 8),     # verify windows of 2 draft tokens over 2K
     (4, 512, 4096, 32, 8, 128, "fp16"),  # the first workload with an fp16 model (one P.V MFMA per step)
     (4, 512, 4096, 32, 8, 64, "fp16"),   # Llama-3.2-1B shape (D 64, fp16)
+    (4, 512, 4096, 32, 8, 128, "bf16", "fp8_e4m3"),  # the first workload over fp8 caches
+    (32, 4, 4096, 32, 8, 128, "bf16", "fp8_e4m3"),   # verify windows over fp8 caches
 ]
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
@@ -160,12 +162,12 @@ def multi_row(args) -> int:
     from ayaka_amd.enums import ForwardMode, KVLayoutKind
     from ayaka_amd.hip import _lib
     from ayaka_amd.hip import attention as hip_attention
-    from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+    from ayaka_amd.kvcache import FP8_E4M3_CODEC, KVBuffers
 
     _lib.lib()
     dev = torch.device("cuda:0")
     for requests, rows, context, heads, kv_heads, *shape in MULTI_ROW_WORKLOADS:
-        dim, dtype_name = shape or (128, "bf16")
+        dim, dtype_name, codec = (*shape, "raw")[:3] if shape else (128, "bf16", "raw")
         dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[dtype_name]
         bs = 16
         blocks = requests * (context // bs) + 1
@@ -178,11 +180,13 @@ def multi_row(args) -> int:
                                   torch.full((requests,), context, dtype=torch.int32, device=dev), table, bs)
         q = torch.randn((requests * rows, heads, dim), generator=gen, device=dev).to(dtype)
         out, per_row = torch.empty_like(q), torch.empty_like(q)
-        buffers = KVBuffers(k, v, KVLayoutKind.NHD, RAW_CODEC)
+        if codec == FP8_E4M3_CODEC:
+            k, v = k.to(torch.float8_e4m3fn), v.to(torch.float8_e4m3fn)
+        buffers = KVBuffers(k, v, KVLayoutKind.NHD, codec)
         scale = dim ** -0.5
         kernel = time_calls(lambda: hip_attention.attend_with(q, buffers, meta, out, scale=scale, partitions=None,
                                                               prefill=True), args.steps, args.warmup)
-        pairs, size = meta.plan.prefill_launch(kv_heads, heads // kv_heads, dim)
+        pairs, size = meta.plan.prefill_launch(kv_heads, heads // kv_heads, dim, 1 if codec == FP8_E4M3_CODEC else 2)
         unsplit = kernel if not size else time_calls(
             lambda: hip_attention.attend_with(q, buffers, meta, per_row, scale=scale, partitions=0, prefill=True),
             args.steps, args.warmup)
@@ -192,11 +196,11 @@ def multi_row(args) -> int:
         # positions each row sees (causal within the chunk), and the flops of q.k and p.v on them
         visible = requests * sum(context - rows + j + 1 for j in range(rows))
         flops = 4 * heads * dim * visible
-        kv_bytes = requests * context * kv_heads * dim * 2 * 2
+        kv_bytes = requests * context * kv_heads * dim * 2 * (1 if codec == FP8_E4M3_CODEC else 2)
         us = kernel["median_us"]
         print(json.dumps({
             "workload": f"{requests} requests x {rows} rows over {context} positions, Hq {heads}, Hkv {kv_heads}, "
-                        f"D {dim}, {dtype_name}, block {bs}",
+                        f"D {dim}, {dtype_name}, block {bs}" + (", fp8 e4m3 cache" if codec == FP8_E4M3_CODEC else ""),
             "us_per_call": round(us, 2),
             "tile_pairs": pairs,
             "partition_size": size,
