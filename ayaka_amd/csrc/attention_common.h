@@ -503,6 +503,15 @@ __device__ __forceinline__ void split_weights4(const float (&w)[4], u32x2& hi, u
   lo = u32x2{r[0], r[1]};
 }
 
+// 4 elements of a 16-lane group's rows, transposed: lane o of each group of 16
+// receives element o % 4 of the 8-byte rows read by lanes o / 4, o / 4 + 4,
+// o / 4 + 8 and o / 4 + 12 of its group (ds_read_b64_tr_b16, measured).
+__device__ __forceinline__ u32x2 lds_read_transposed(const uint16_t* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p)));
+}
+
 // Element offset of position t within its block: (t mod block size) x token
 // stride on the full-rate 24-bit multiplier (both factors are below 2^24: the
 // host refuses larger token strides).

@@ -24,14 +24,14 @@
 //  * O^T += V^T P^T, per 16-element slice of head_dim and 32 positions:
 //    v_mfma_f32_16x16x32 with P^T taken straight from the lane's scores (its
 //    8 k-slots are positions 4*(l/16)+i of two adjacent 16-position tiles) and
-//    V^T read from a transposed LDS tile in that same position order. A bf16 P is
+//    V^T read in that same position order from a token-major LDS tile through
+//    ds_read_b64_tr_b16 (two 4-position reads per operand). A bf16 P is
 //    split by truncation into a 16-bit high part and the 16-bit remainder, two
 //    MFMAs, which keeps the product at fp32-level accuracy (one bf16 P would cost
 //    ~2e-3 relative); an fp16 P rounded to nearest is within 2^-12 and takes one.
-//  * The transposed value tile is written with 32-bit LDS stores: each thread
-//    carries the same 8 elements of two adjacent positions. Its row stride and the
-//    threads' value-load mapping keep stores and reads nearly free of bank
-//    conflicts with plain additive addresses.
+//  * Keys and values are staged with 16-byte LDS stores, values token-major in
+//    rows D + 16 elements apart, which keeps the transposing reads of a 16-lane
+//    group spread over the banks.
 #include "attention_common.h"
 
 namespace ayk {
@@ -85,16 +85,9 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   constexpr int PIECES = CH * CPT;              // pieces per chunk of K (or V)
   constexpr int PER_THREAD = PIECES / THREADS;  // 2 (D 64), 4 (D 128), 8 (D 256): even
   constexpr int POS_STEP = 2 * THREADS / CPT;   // positions covered by one pair of a thread's pieces
-  // Transposed value tile: row d holds the 32 position pairs of element d as 32-bit
-  // words, rows 34 words apart. The odd half of 34 spreads the 16 rows one read
-  // instruction touches over the banks (at most 3 words per bank) while the reads
-  // stay 8-byte aligned and every offset is a per-lane base plus a constant.
-  constexpr int VT2 = CH / 2 + 2;
-  // Value loads: a wave covers VSW slices of VNP position pairs per instruction, so the
-  // transposed stores of one instruction (rows 8 apart per slice, consecutive pairs)
-  // hit distinct banks under that stride.
-  constexpr int VSW = CPT / 4;                  // value slices per wave
-  constexpr int VNP = kWave / VSW;              // value position pairs per wave instruction
+  // Values in LDS token-major, rows VP elements apart: the transposing reads of the
+  // P.V operand (16 rows of one 16-lane group, 8 bytes each) then cover the banks evenly.
+  constexpr int VP = D + 16;
   static_assert(PER_THREAD % 2 == 0 && PIECES % THREADS == 0, "piece split");
   static_assert(PS == 1 || PS == 2 || PS == 4, "waves per pair group");
 
@@ -102,7 +95,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   // group with ps > 0 hand to its first wave: o of each lane, m and l per pair.
   struct Stage {
     u32x4 k[2][PIECES];
-    uint32_t vt[2][D * VT2];
+    uint16_t v[2][CH * VP];
   };
   constexpr int MERGE_WAVES = PS > 1 ? (PS - 1) * PGROUPS : 1;
   union Lds {
@@ -114,7 +107,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   __shared__ Lds lds;
   __shared__ float s_ml[MERGE_WAVES][PT][2][16];
   auto& s_k = lds.st.k;
-  auto& s_vt = lds.st.vt;
+  auto& s_v = lds.st.v;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -200,15 +193,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride);
   const uint16_t* vbase = kv_at<KV8>(p.v_cache, (int64_t)kvh * p.head_stride);
   auto key_slot = [](int token, int piece) { return token * CPT + (piece ^ (token & (CPT - 1))); };
-  auto vt_word = [](int d, int c2) { return d * VT2 + c2; };
   // Piece u of this thread: position piece_pos(u) (pieces 2v and 2v + 1 are adjacent
   // positions), 8-element slice piece_c of it; consecutive threads read consecutive
   // slices of one position.
   const int piece_c = tid % CPT;
   auto piece_pos = [&](int u) { return (u >> 1) * POS_STEP + 2 * (tid / CPT) + (u & 1); };
-  // Value piece u of this thread: position vpiece_pos(u) (again pairs 2v, 2v + 1), slice vpiece_c.
-  const int vpiece_c = wave * VSW + lane / VNP;
-  auto vpiece_pos = [&](int u) { return (u >> 1) * (2 * VNP) + 2 * (lane % VNP) + (u & 1); };
 
   // This workgroup's positions: the tile's whole context, or one partition of it.
   const int t_begin = split ? part * p.partition_size : 0;
@@ -232,13 +221,13 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
     auto load_chunk = [&](int ci) {
 #pragma unroll
       for (int u = 0; u < PER_THREAD; u += 2) {
-        uint32_t k0, k1, v0, v1;
-        pair_offsets(s0 + ci * CH + piece_pos(u), k0, k1);
-        pair_offsets(s0 + ci * CH + vpiece_pos(u), v0, v1);
-        kr[u] = load_kv_raw<KV8, false>(kbase, k0 + piece_c * 8);
-        kr[u + 1] = load_kv_raw<KV8, false>(kbase, k1 + piece_c * 8);
-        vr[u] = load_kv_raw<KV8, false>(vbase, v0 + vpiece_c * 8);
-        vr[u + 1] = load_kv_raw<KV8, false>(vbase, v1 + vpiece_c * 8);
+        // K and V pieces of the same two positions share their offsets
+        uint32_t o0, o1;
+        pair_offsets(s0 + ci * CH + piece_pos(u), o0, o1);
+        kr[u] = load_kv_raw<KV8, false>(kbase, o0 + piece_c * 8);
+        kr[u + 1] = load_kv_raw<KV8, false>(kbase, o1 + piece_c * 8);
+        vr[u] = load_kv_raw<KV8, false>(vbase, o0 + piece_c * 8);
+        vr[u + 1] = load_kv_raw<KV8, false>(vbase, o1 + piece_c * 8);
       }
     };
     auto stage_chunk = [&](int buf) {
@@ -247,15 +236,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
         const int pos = piece_pos(u);
         s_k[buf][key_slot(pos, piece_c)] = kv_pairs<KV8, BF16>(kr[u]);
         s_k[buf][key_slot(pos + 1, piece_c)] = kv_pairs<KV8, BF16>(kr[u + 1]);
-        const int vpos = vpiece_pos(u);
-        const u32x4 a = kv_pairs<KV8, BF16>(vr[u]), b = kv_pairs<KV8, BF16>(vr[u + 1]);
-        const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // elements 2e and 2e + 1 of the slice, each as (position vpos, vpos + 1)
-          s_vt[buf][vt_word(vpiece_c * 8 + 2 * e, vpos >> 1)] = (wa[e] & 0xffffu) | (wb[e] << 16);
-          s_vt[buf][vt_word(vpiece_c * 8 + 2 * e + 1, vpos >> 1)] = (wa[e] >> 16) | (wb[e] & 0xffff0000u);
-        }
+        *reinterpret_cast<u32x4*>(&s_v[buf][pos * VP + piece_c * 8]) = kv_pairs<KV8, BF16>(vr[u]);
+        *reinterpret_cast<u32x4*>(&s_v[buf][(pos + 1) * VP + piece_c * 8]) = kv_pairs<KV8, BF16>(vr[u + 1]);
       }
     };
 
@@ -337,9 +319,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
           }
 #pragma unroll
           for (int t = 0; t < DT; ++t) {
-            const uint32_t* vrow = &s_vt[buf][vt_word(t * 16 + mt, ks * 16 + 2 * mq)];
-            const u32x2 lo4 = *reinterpret_cast<const u32x2*>(vrow);
-            const u32x2 hi4 = *reinterpret_cast<const u32x2*>(vrow + 8);
+            // lane (mq, mt) gets element t*16 + mt of positions ks*32 + 4*mq + i (lo4)
+            // and ks*32 + 16 + 4*mq + i (hi4): the order of its weights
+            const uint16_t* vrow = &s_v[buf][(ks * 32 + 4 * mq + (mt >> 2)) * VP + t * 16 + 4 * (mt & 3)];
+            const u32x2 lo4 = lds_read_transposed(vrow);
+            const u32x2 hi4 = lds_read_transposed(vrow + 16 * VP);
             const u32x4 va = u32x4{lo4.x, lo4.y, hi4.x, hi4.y};
 #pragma unroll
             for (int j = 0; j < PT; ++j) {
@@ -359,7 +343,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
         }
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-          const u32x2 va = *reinterpret_cast<const u32x2*>(&s_vt[buf][vt_word(t * 16 + mt, ps * 8 + 2 * mq)]);
+          const u32x2 va = lds_read_transposed(&s_v[buf][(ps * 16 + 4 * mq + (mt >> 2)) * VP + t * 16 + 4 * (mt & 3)]);
 #pragma unroll
           for (int j = 0; j < PT; ++j) {
             o[j][t] = mfma_pv<BF16>(va, phi[j], o[j][t]);
