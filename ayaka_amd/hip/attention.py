@@ -511,12 +511,12 @@ PREFILL_WORKGROUPS_PER_CU = 2
 #: Positions one multi-row workgroup folds per step, and the time of a step by waves per
 #: pair group (tiles of the full capacity, a half, a quarter); with the streaming rate, the
 #: partials' rate and the reduce launch below, fitted to a sweep of 13 step shapes x 3 tile
-#: sizes x 5 partition sizes on MI355X (the model's choice averaged 1.4% and at worst 7%
+#: sizes x 5 partition sizes on MI355X (the model's choice averaged 2% and at worst 8%
 #: above the fastest measured launch).
 PREFILL_CHUNK = 64
-PREFILL_CHUNK_US_BY_WAVES = {1: 3.0, 2: 2.5, 4: 2.0}
-#: Rate (bytes per us) at which a launch streams K and V it reads once (about 6.5 TB/s).
-PREFILL_STREAM_BYTES_PER_US = 6.5e6
+PREFILL_CHUNK_US_BY_WAVES = {1: 2.5, 2: 1.75, 4: 1.5}
+#: Rate (bytes per us) at which a launch streams K and V it reads once (about 7 TB/s).
+PREFILL_STREAM_BYTES_PER_US = 7.0e6
 #: Rate (bytes per us) at which partials are written and read back, and the reduce launch.
 PREFILL_PARTIALS_BYTES_PER_US = 3.0e6
 PREFILL_REDUCE_US = 2.0
