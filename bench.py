@@ -69,6 +69,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-rows", type=int, default=8, help="rows of the CPU baseline sample")
     ap.add_argument("--access-probe", action="store_true",
                     help="only run the read-only access-pattern probes (ayaka_amd/lib/access_probe)")
+    ap.add_argument("--graph-step", action="store_true",
+                    help="time a 32-layer decode step (KV write + attention per layer) eagerly and as a "
+                         "captured graph replay, at the C1 and C3 shapes")
     ap.add_argument("--multi-row", action="store_true",
                     help="only time the multi-row (prefill / verify) kernel on its workloads, one JSON line each")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -215,6 +218,62 @@ def multi_row(args) -> int:
     return 0
 
 
+GRAPH_STEP_LAYERS = 32
+
+
+def graph_step(args) -> int:
+    """A decode step of GRAPH_STEP_LAYERS layers, each a KV write and an attention call over one
+    shared pool (every layer has the same shape, so one pool times them all), on graph metadata:
+    run eagerly (the Python ops per call) and as one captured graph replayed per step."""
+    import torch
+
+    from ayaka_amd import workloads
+    from ayaka_amd.hip import _lib
+    from ayaka_amd.hip import attention as hip_attention
+    from ayaka_amd.hip import kvcache as hip_kvcache
+    from ayaka_amd.enums import KVLayoutKind
+    from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    for index in (1, 3):
+        cfg = workloads.config(index)
+        step = workloads.build(cfg, dev, poison=False)
+        buffers = KVBuffers(step.k_cache, step.v_cache, KVLayoutKind.NHD, RAW_CODEC)
+        meta = hip_attention.graph_metadata(cfg.batch, step.table.shape[1], cfg.block_size, dev)
+        hip_attention.update_graph_metadata(meta, step.lengths.cpu(), step.table.cpu())
+        rows = step.k_new.shape[0]
+        k_new, v_new = step.k_new[:cfg.batch].contiguous(), step.v_new[:cfg.batch].contiguous()
+        if rows < cfg.batch:
+            raise RuntimeError("graph step: fewer new rows than sequences")
+        out = torch.empty_like(step.q)
+
+        def one_step() -> None:
+            for _ in range(GRAPH_STEP_LAYERS):
+                hip_kvcache.store(k_new, v_new, buffers, meta)
+                hip_attention.attend(step.q, buffers, meta, out, scale=cfg.scale)
+
+        eager = time_calls(one_step, max(3, args.steps // 20), 2, repeats=3)
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            one_step()
+        torch.cuda.current_stream().wait_stream(side)
+        with torch.cuda.graph(graph):
+            one_step()
+        replay = time_calls(graph.replay, max(3, args.steps // 20), 2, repeats=3)
+        print(json.dumps({
+            "workload": f"C{index} {cfg.name}: {GRAPH_STEP_LAYERS} layers of KV write + decode attention "
+                        f"(graph metadata, batch {cfg.batch})",
+            "eager_us_per_step": round(eager["median_us"], 1),
+            "graph_us_per_step": round(replay["median_us"], 1),
+            "eager_us_per_layer": round(eager["median_us"] / GRAPH_STEP_LAYERS, 2),
+            "graph_us_per_layer": round(replay["median_us"] / GRAPH_STEP_LAYERS, 2),
+        }), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -233,6 +292,8 @@ def main() -> int:
 
     if args.multi_row:
         return multi_row(args)
+    if args.graph_step:
+        return graph_step(args)
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
