@@ -261,18 +261,17 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 #pragma unroll
           for (int j = 0; j < PT; ++j) acc[w][j] = mfma32<BF16>(ka, qb[j][s], acc[w][j]);
         }
+      // the scale applied to a score in the exponent below (1 once the scores are scaled)
+      const float sc = whole ? scale_log2 : 1.f;
 #pragma unroll
       for (int j = 0; j < PT; ++j) {
         float mx = -INFINITY;
-        // the scale applied to a score in the exponent below (1 once the scores are scaled)
-        float sc = 1.f;
         if (whole) {
 #pragma unroll
           for (int w = 0; w < PTL_W; ++w)
 #pragma unroll
             for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[w][j][i]);
           mx *= scale_log2;
-          sc = scale_log2;
         } else {
           // position tb + pt*16 + 4*mq + i is visible iff pt*16 + i <= lim
           const int lim = min(my_pos[j], s1 - 1) - tb - 4 * mq;
@@ -295,6 +294,12 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
           for (int t = 0; t < DT; ++t) o[j][t] *= alpha;
           m[j] = mn;
         }
+      }
+      // Weights after every group's max and rescale: from here to the end of the chunk
+      // the code has no branch, so the scheduler can overlap one group's exponentials
+      // with the other's P.V MFMAs.
+#pragma unroll
+      for (int j = 0; j < PT; ++j)
 #pragma unroll
         for (int w = 0; w < PTL_W; ++w)
 #pragma unroll
@@ -303,7 +308,6 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
             acc[w][j][i] = e;
             l[j] += e;
           }
-      }
       if constexpr (PTL_W >= 2) {
         // O^T += V^T P^T over this wave's 32-position k-steps (16x16x32).
 #pragma unroll
