@@ -361,6 +361,11 @@ def test_fp8_attention_matches_the_oracle_on_decoded_values(dtype: str, layout: 
                 ("auto", dict(partitions=None))]
     if mode == "mixed":
         launches.append(("multi-row", dict(partitions=None, prefill=True)))
+        full = hip_attention.PREFILL_PAIRS[head_dim]
+        for waves in (2, 4):
+            if full // waves >= heads // kv_heads:
+                launches.append((f"multi-row/{waves} waves per group",
+                                 dict(partitions=None, partition_size=256, prefill=True, tile_pairs=full // waves)))
     for label, launch in launches:
         out = torch.full_like(q, 7.0)
         hip_attention.attend_with(q, buffers, meta, out, scale=s.scale, **launch)
