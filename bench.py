@@ -35,19 +35,19 @@ HBM_PEAK_GBS = 8000.0
 # the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
 PROFILED_TRAFFIC = {
     (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 1024):
-        (1_082_046_730, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
+        (1_081_374_743, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
     (4, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 704):
-        (668_966_255, 4_054_864, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
+        (668_338_845, 4_054_928, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
     (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 3072):
-        (2_598_575_834, 10_319_248, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
+        (2_597_999_291, 10_319_248, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
     (2, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 320):
-        (148_558_725, 2_128_480, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
+        (148_408_741, 2_128_752, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
     (1, "paged_attention_mfma_kernel (v2, merge in-kernel)", 64):
-        (1_749_850, 86_080, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
+        (1_749_849, 86_080, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
     (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1024):
-        (546_016_631, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
+        (545_693_884, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
     (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1280):
-        (1_318_304_460, 20_069_216, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
+        (1_317_813_532, 20_071_088, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
 }
 
 
