@@ -207,7 +207,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
 
 extern "C" {
 
-int ayk_abi_version(void) { return 9; }
+int ayk_abi_version(void) { return 10; }
 
 int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 
@@ -293,8 +293,9 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
                            int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
-                           const int32_t* work_items, int32_t n_work_items, void* workspace,
-                           size_t workspace_bytes, uint32_t* arrivals, int32_t flags, void* stream) {
+                           const int32_t* work_items, int32_t n_work_items, const int32_t* staged,
+                           void* workspace, size_t workspace_bytes, uint32_t* arrivals, int32_t flags,
+                           void* stream) {
   const char* op = "ayk_paged_attention_v2";
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
@@ -310,6 +311,8 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
     return fail(AYK_ERR_ARGUMENT, "%s: max_partitions %d is not in [1, 65535]", op, max_partitions);
   if (n_work_items < 0 || (n_work_items > 0 && !work_items))
     return fail(AYK_ERR_ARGUMENT, "%s: %d work items at %p", op, n_work_items, (const void*)work_items);
+  if (staged && n_work_items == 0)
+    return fail(AYK_ERR_ARGUMENT, "%s: staged parameters need a work list (the grid's capacity)", op);
   if (n_rows == 0) return ok();
   const size_t need =
       ayk_paged_attention_v2_workspace_bytes(n_rows, num_heads, head_dim, max_partitions);
@@ -325,6 +328,7 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
   p.max_partitions = max_partitions;
   p.work = n_work_items > 0 ? work_items : nullptr;
   p.n_work = n_work_items;
+  p.staged = staged;
   // The single launch merges in the partition kernel; without counters, or when
   // asked, a reduce kernel does (and PARTIALS_ONLY runs neither merge).
   p.arrivals = (flags & (AYK_FLAG_SEPARATE_REDUCE | AYK_FLAG_PARTIALS_ONLY)) ? nullptr : arrivals;

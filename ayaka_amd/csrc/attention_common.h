@@ -181,16 +181,24 @@ struct WgCoord {
   int part;
 };
 
+// A workgroup's (row, head group, partition). With staged parameters the grid is an
+// upper bound: workgroups past the staged item count get row -1 and do nothing.
 __device__ __forceinline__ WgCoord wg_coord(const AttnParams& p, int groups, bool split) {
   int id = blockIdx.x;
   if (split && p.work) {
     const int item = id / groups;
+    if (p.staged && item >= p.staged[1]) return WgCoord{-1, 0, 0};
     return WgCoord{p.work[2 * item], id % groups, p.work[2 * item + 1]};
   }
   const int parts = split ? p.max_partitions : 1;
   const int part = id % parts;
   id /= parts;
   return WgCoord{id / groups, id % groups, part};
+}
+
+// The v2 partition size: the launch's, or the one staged on the device for this step.
+__device__ __forceinline__ int partition_size_of(const AttnParams& p) {
+  return p.staged ? p.staged[0] : p.partition_size;
 }
 
 // Length of row `row`'s context and its request, clamped so no read leaves the table.

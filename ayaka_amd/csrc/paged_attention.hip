@@ -49,6 +49,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
   const int waves = threads / kWave;
   const int groups = (p.num_virtual_heads + waves - 1) / waves;
   const WgCoord wg = wg_coord(p, groups, SPLIT);
+  if (wg.row < 0) return;  // past the staged work items (uniform per workgroup)
   const int row = wg.row;
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
@@ -64,10 +65,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
   int req, len;
   row_context(p, row, req, len);
   int t_begin = 0, t_end = len;
-  const int np = SPLIT ? (len > 0 ? (len - 1) / p.partition_size + 1 : 0) : 1;  // partitions with tokens
+  const int psize = SPLIT ? partition_size_of(p) : 0;
+  const int np = SPLIT ? (len > 0 ? (len - 1) / psize + 1 : 0) : 1;  // partitions with tokens
   if constexpr (SPLIT) {
-    t_begin = wg.part * p.partition_size;
-    t_end = min(len, t_begin + p.partition_size);
+    t_begin = wg.part * psize;
+    t_end = min(len, t_begin + psize);
     if (t_begin >= t_end) {  // only partitions that hold tokens are merged
       if (len == 0 && wg.part == 0 && active) store_zero_rows<D, GC, kWave>(p, row, h0, lane);  // a padding row
       return;
@@ -317,7 +319,7 @@ __global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const 
   const int row = valid ? (int)(pair / p.num_heads) : 0;
   int req, len;
   row_context(p, row, req, len);
-  const int np = valid ? (len > 0 ? (len - 1) / p.partition_size + 1 : 0) : 1;
+  const int np = valid ? (len > 0 ? (len - 1) / partition_size_of(p) + 1 : 0) : 1;
   uint16_t* out = static_cast<uint16_t*>(p.out) + pair * D;
   const float* ml = p.part_ml + pair * p.max_partitions * 2;
   const f32x4* po = reinterpret_cast<const f32x4*>(p.part_o + pair * p.max_partitions * D);

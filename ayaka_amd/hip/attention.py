@@ -33,6 +33,7 @@ import functools
 import heapq
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from ayaka_amd.enums import ForwardMode, KVLayoutKind
@@ -65,6 +66,11 @@ __all__ = [
 
 #: Default positions per v2 partition (callers that force a v2 launch without a size).
 PARTITION_SIZE = 512
+#: Graph replays: the smallest partition, the most partitions per row of the table width,
+#: and the most work items of a bucket (the captured grid, by key/value head group).
+GRAPH_MIN_PARTITION = 256
+GRAPH_MAX_PARTITIONS = 64
+GRAPH_MAX_ITEMS = 8192
 #: Partition sizes an eagerly planned step chooses from (multiples of 64).
 PARTITION_CANDIDATES = (64, 128, 192, 256, 320, 384, 448, 512, 576, 640, 704, 768, 896, 1024, 1280, 1536,
                         2048, 3072, 4096, 8192, 16384)
@@ -223,37 +229,62 @@ class HipAttentionPlan:
         return found
 
     def work_items(self, partition_size: int, device: torch.device) -> torch.Tensor:
-        """The (row, partition) pairs of the step that hold tokens, longest first, on ``device``
-        (plus partition 0 of each row without context, last).
-
-        Every full partition comes before any partial one, so the last
-        workgroups to start are the short ones and consecutive workgroups land on
-        different XCDs.
-        """
+        """:func:`work_list` of the step's rows, on ``device``, built once per partition size."""
         found = self.work.get(partition_size)
         if found is None:
-            items = []
-            for row, length in enumerate(self.row_lengths):
-                # a row without context still gets partition 0, which writes its zeros
-                for part in range(max(1, -(-length // partition_size))):
-                    size = min(partition_size, length - part * partition_size)
-                    items.append((-size, row, part))
-            items.sort()
-            flat = [v for _, row, part in items for v in (row, part)]
-            found = torch.tensor(flat, dtype=torch.int32).to(device)
+            found = torch.from_numpy(work_list(self.row_lengths, partition_size)).to(device)
             self.work[partition_size] = found
         return found
 
 
+def work_list(row_lengths: "tuple[int, ...] | list[int] | np.ndarray", partition_size: int) -> np.ndarray:
+    """The v2 work list: the (row, partition) pairs that hold tokens, flattened to int32
+    ``[row0, part0, row1, part1, ...]``, longest partition first (ties by row, then
+    partition), plus partition 0 of each row without context, last (it writes the row's zeros).
+
+    Every full partition comes before any partial one, so the last workgroups to
+    start are the short ones and consecutive workgroups land on different XCDs.
+    """
+    lengths = np.asarray(row_lengths, dtype=np.int64).reshape(-1)
+    counts = np.maximum(1, -(-lengths // partition_size))
+    rows = np.repeat(np.arange(lengths.size, dtype=np.int64), counts)
+    starts = np.cumsum(counts) - counts
+    parts = np.arange(rows.size, dtype=np.int64) - np.repeat(starts, counts)
+    sizes = np.minimum(partition_size, lengths[rows] - parts * partition_size)
+    order = np.lexsort((parts, rows, -sizes))
+    return np.stack((rows[order], parts[order]), axis=1).reshape(-1).astype(np.int32)
+
+
 @dataclass(frozen=True, slots=True, eq=False)
 class HipGraphPlan:
-    """Pinned host staging of a graph bucket, and its fixed table width."""
+    """Pinned host staging of a graph bucket, its fixed table width, and the v2 launch
+    staged on the device for every step.
+
+    A captured v2 launch has a fixed grid of ``capacity`` work items over at most
+    ``partitions`` partitions of at least ``min_size`` positions. Each update
+    stages the step's own partition size (a multiple of 64, at least
+    ``min_size``) and work list into ``staged`` (device) as
+    ``[partition size, item count, row0, part0, ...]``; workgroups past the item
+    count return at once. ``head_shape`` holds the ``(num_kv_heads, group,
+    kv_bytes)`` of the first attend, which scores the staged split.
+    """
 
     positions: torch.Tensor
     slot_mapping: torch.Tensor
     kv_lengths: torch.Tensor
     block_table: torch.Tensor
     max_blocks: int
+    staged_host: torch.Tensor
+    staged: torch.Tensor
+    min_size: int
+    partitions: int
+    capacity: int
+    head_shape: list = field(default_factory=list)
+
+    @property
+    def staged_partition_size(self) -> int:
+        """The partition size the last update staged (the host copy)."""
+        return int(self.staged_host[0])
 
 
 def _host_ints(tensor: torch.Tensor) -> tuple[int, ...]:
@@ -446,11 +477,13 @@ def fits_schedule(lengths: list[int], size: int, groups: int = 1) -> bool:
     return items <= MAX_ROUNDS * COMPUTE_UNITS
 
 
-def _best_size(lengths: list[int], max_length: int, groups: int, kv_bytes: int = 2) -> int:
-    """The candidate partition size with the smallest :func:`schedule_makespan`."""
+def _best_size(lengths: list[int], max_length: int, groups: int, kv_bytes: int = 2, min_size: int = 0) -> int:
+    """The candidate partition size (of ``min_size`` or more) with the smallest
+    :func:`schedule_makespan`."""
+    candidates = [size for size in PARTITION_CANDIDATES if size >= min_size] or [min_size]
     best: tuple[int, int] | None = None
-    for size in PARTITION_CANDIDATES:
-        if not fits_schedule(lengths, size, groups) and size != PARTITION_CANDIDATES[-1]:
+    for size in candidates:
+        if not fits_schedule(lengths, size, groups) and size != candidates[-1]:
             continue
         cost = schedule_makespan(lengths, size, groups, WORKGROUP_COSTS[kv_bytes])
         if best is None or cost < best[0]:
@@ -469,6 +502,7 @@ def choose_split(
     total_length: int | None = None,
     row_lengths: tuple[int, ...] | None = None,
     kv_bytes: int = 2,
+    min_size: int = 0,
 ) -> Split:
     """Pick v1 or v2 and the partition size from the step's shape.
 
@@ -479,7 +513,8 @@ def choose_split(
     coarse signature of the lengths (row count, longest row to a power of two,
     total to 4 significant bits), which successive decode steps -- every length
     one longer than the step before -- keep hitting. ``kv_bytes`` is the cache's bytes
-    per element (2, or 1 for fp8), which sets the modelled workgroup cost.
+    per element (2, or 1 for fp8), which sets the modelled workgroup cost; ``min_size``
+    leaves out smaller partition sizes (a graph replay's grid is sized for it).
     """
     del total_length
     if max_length <= 0:
@@ -489,12 +524,12 @@ def choose_split(
     total = sum(lengths)
     # The total to 4 significant bits, the longest row to a power of two, the row count.
     top = max(total.bit_length() - 4, 0)
-    key = (groups, kv_bytes, len(lengths), max_length.bit_length(), total >> top, top)
+    key = (groups, kv_bytes, min_size, len(lengths), max_length.bit_length(), total >> top, top)
     size = _split_cache.get(key)
     if size is None:
         if len(_split_cache) > 4096:
             _split_cache.clear()
-        size = _best_size(lengths, max_length, groups, kv_bytes)
+        size = _best_size(lengths, max_length, groups, kv_bytes, min_size)
         _split_cache[key] = size
     if max_length <= size:
         return Split(0, 0)
@@ -815,10 +850,20 @@ def attend_with(
         _kv_code(buffers, q.dtype),
         float(scale),
     )
+    staged = None
     if partitions is None:
         kv_bytes = 1 if buffers.codec == FP8_E4M3_CODEC else 2
-        split = step.split_for(kv_heads, group, kv_bytes) if isinstance(step, HipAttentionPlan) else \
-            choose_split(n_rows, kv_heads, group, max_length, kv_bytes=kv_bytes)
+        if isinstance(step, HipAttentionPlan):
+            split = step.split_for(kv_heads, group, kv_bytes)
+        else:
+            if not step.head_shape:
+                step.head_shape.extend((kv_heads, group, kv_bytes))
+            # v2 over the staged split (rows of one partition write their output directly),
+            # or v1 when the table holds one partition at most
+            split = Split(0, 0)
+            if step.partitions > 1:
+                staged = step.staged
+                split = Split(step.min_size, step.partitions)
         partitions, partition_size = split.partitions, split.partition_size
     partition_size = partition_size or PARTITION_SIZE
     if partitions and partitions * partition_size < max_length:
@@ -833,17 +878,21 @@ def attend_with(
     nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, partitions)
     scratch = _workspace(op, device, nbytes, capturing(q))
     arrivals = _arrivals(op, device, n_rows * heads, capturing(q))
-    # An eager step runs only the partitions that hold tokens, longest first; graph
-    # metadata keeps the dense grid, whose shape does not depend on the lengths.
+    # A planned step runs only the partitions that hold tokens, longest first. Graph
+    # metadata's launch reads the same list and its partition size from the staged
+    # buffer, over a grid of the bucket's capacity; forced launches on graph metadata
+    # keep the dense grid.
     work, n_work = 0, 0
-    if isinstance(step, HipAttentionPlan) and not capturing(q):
+    if staged is not None:
+        work, n_work = staged.data_ptr() + 8, step.capacity
+    elif isinstance(step, HipAttentionPlan) and not capturing(q):
         items = step.work_items(partition_size, device)
         work, n_work = items.data_ptr(), items.numel() // 2
     _lib.check(
         op,
         lib.ayk_paged_attention_v2(
-            *common, partition_size, partitions, work, n_work, scratch.data_ptr(), scratch.numel(),
-            arrivals.data_ptr(), flags, stream,
+            *common, partition_size, partitions, work, n_work, staged.data_ptr() if staged is not None else 0,
+            scratch.data_ptr(), scratch.numel(), arrivals.data_ptr(), flags, stream,
         ),
     )
 
@@ -864,12 +913,28 @@ def graph_metadata(
     def host(shape: tuple[int, ...], dtype: torch.dtype) -> torch.Tensor:
         return torch.zeros(shape, dtype=dtype, pin_memory=pinned)
 
+    # Replays run v2 over partitions of at least min_size: 256 positions, or the share of
+    # the table width that keeps the captured grid within GRAPH_MAX_PARTITIONS items per
+    # row and GRAPH_MAX_ITEMS in all. Until the first update every row is one item.
+    max_length = max_blocks * block_size
+    per_row = max(1, min(GRAPH_MAX_PARTITIONS, GRAPH_MAX_ITEMS // num_requests))
+    min_size = max(GRAPH_MIN_PARTITION, -(-max_length // (64 * per_row)) * 64)
+    partitions = -(-max_length // min_size)
+    capacity = num_requests * partitions
+    staged_host = host((2 + 2 * capacity,), torch.int32)
+    staged_host[0], staged_host[1] = min_size, num_requests
+    staged_host[2:2 + 2 * num_requests:2] = torch.arange(num_requests, dtype=torch.int32)
     staging = HipGraphPlan(
         positions=host((num_requests,), torch.int32),
         slot_mapping=host((num_requests,), torch.int64),
         kv_lengths=host((num_requests,), torch.int32),
         block_table=host((num_requests, max_blocks), torch.int32),
         max_blocks=max_blocks,
+        staged_host=staged_host,
+        staged=staged_host.to(target),
+        min_size=min_size,
+        partitions=partitions,
+        capacity=capacity,
     )
     return AttentionMetadata(
         mode=ForwardMode.DECODE,
@@ -931,12 +996,31 @@ def update_graph_metadata(
     staging.slot_mapping.copy_(torch.where(real, block * block_size + positions % block_size, 0))
     staging.kv_lengths.copy_(kv_lengths)
     staging.block_table.copy_(block_rows)
+    used = _stage_split(staging, kv_lengths.numpy(), block_size)
     for device_tensor, host_tensor in (
         (meta.positions, staging.positions),
         (meta.slot_mapping, staging.slot_mapping),
         (meta.kv_lengths, staging.kv_lengths),
         (table, staging.block_table),
+        (staging.staged[:used], staging.staged_host[:used]),
     ):
         device_tensor.copy_(host_tensor, non_blocking=True)
+
+
+def _stage_split(staging: HipGraphPlan, lengths: np.ndarray, block_size: int) -> int:
+    """Fill ``staging.staged_host`` with this step's partition size and work list (the
+    eager plan's choice, from sizes of ``staging.min_size`` up); returns the int32 words used."""
+    kv_heads, group, kv_bytes = staging.head_shape or (8, 1, 2)
+    longest = int(lengths.max()) if lengths.size else 0
+    split = choose_split(lengths.size, kv_heads, group, max(longest, 1), row_lengths=tuple(lengths.tolist()),
+                         kv_bytes=kv_bytes, min_size=staging.min_size)
+    # one partition per row when the model prefers v1
+    size = split.partition_size or max(staging.min_size, -(-longest // 64) * 64)
+    items = work_list(lengths, size)
+    assert items.size <= 2 * staging.capacity and -(-longest // size) <= staging.partitions
+    host = staging.staged_host.numpy()
+    host[0], host[1] = size, items.size // 2
+    host[2:2 + items.size] = items
+    return 2 + items.size
 
 

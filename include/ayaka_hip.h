@@ -145,8 +145,12 @@ size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads,
  * cover every partition below ceil(length / partition_size) of every row,
  * each once (the arrival count relies on it), and partition 0 of every row
  * with no context (that workgroup writes the row's zeros). With
- * NULL the grid covers every (row, partition < max_partitions), which is what a
- * graph replay with fixed launch shape needs. The math the reference delegates
+ * NULL the grid covers every (row, partition < max_partitions). staged, if not
+ * NULL, is device memory holding two int32, {partition size, work items}, read by
+ * the kernels when they run: a graph replay then follows the split and the work
+ * list a host wrote there for this step (partition_size is the smallest such
+ * size, which max_partitions and the workspace must cover; n_work_items is the
+ * list's capacity and sizes the grid; the staged count must not exceed it). The math the reference delegates
  * to flashinfer's split-KV decode and its plan-time schedule
  * (python/ayaka/ops/backends/flashinfer/attention.py:221-251, :326).
  */
@@ -157,8 +161,9 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
                            int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
-                           const int32_t* work_items, int32_t n_work_items, void* workspace,
-                           size_t workspace_bytes, uint32_t* arrivals, int32_t flags, void* stream);
+                           const int32_t* work_items, int32_t n_work_items, const int32_t* staged,
+                           void* workspace, size_t workspace_bytes, uint32_t* arrivals, int32_t flags,
+                           void* stream);
 
 /*
  * Multi-row paged attention (prefill chunks, verify windows): the rows of each

@@ -78,14 +78,16 @@ def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, me
 def test_v2_and_store_refusals() -> None:
     lib = _lib.lib()
     base = [1, 1, 1, 1, 1, 4, 1, None, None, 1, 8, 2, 128, 10, 16, 4, 0, 1, 1, ctypes.c_float(1.0)]
-    assert lib.ayk_paged_attention_v2(*base, 100, 4, None, 0, 1, 1 << 20, None, 0, None) == 1
+    assert lib.ayk_paged_attention_v2(*base, 100, 4, None, 0, None, 1, 1 << 20, None, 0, None) == 1
     assert b"multiple of 64" in lib.ayk_last_error()
-    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 1, 16, None, 0, None) == 4
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, None, 1, 16, None, 0, None) == 4
     assert b"workspace" in lib.ayk_last_error()
-    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 3, 1, 1 << 20, None, 0, None) == 1
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 3, None, 1, 1 << 20, None, 0, None) == 1
     assert b"work items" in lib.ayk_last_error()
-    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 16, 1 << 20, None, 8 | 16, None) == 1
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, None, 16, 1 << 20, None, 8 | 16, None) == 1
     assert b"exclude each other" in lib.ayk_last_error()
+    assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, 1, 16, 1 << 20, None, 0, None) == 1
+    assert b"staged parameters need a work list" in lib.ayk_last_error()
     # the multi-row entry: tiles of the full capacity (128 at head_dim 128), a half or a
     # quarter; a partition size that is not a multiple of 64; the partitions' workspace
     def prefill(tile_pairs: int, size: int = 0, workspace: int = 0) -> int:

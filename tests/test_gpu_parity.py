@@ -531,9 +531,10 @@ def test_benchmark_configuration(index: int) -> None:
 # --- graph metadata and capture ---------------------------------------------------------------
 
 
-def test_graph_metadata_replays_match_eager_steps() -> None:
+@pytest.mark.parametrize("heads,kv_heads,max_blocks,bucket", [(8, 2, 80, 4), (32, 8, 512, 16)])
+def test_graph_metadata_replays_match_eager_steps(heads: int, kv_heads: int, max_blocks: int, bucket: int) -> None:
     rng = np.random.default_rng(61)
-    heads, kv_heads, dim, bs, max_blocks, bucket = 8, 2, 128, 16, 80, 4
+    dim, bs = 128, 16
     num_blocks = 1 + bucket * max_blocks
     k_cache = (torch.randn((num_blocks, bs, kv_heads, dim), device=DEV)).to(torch.bfloat16)
     v_cache = (torch.randn((num_blocks, bs, kv_heads, dim), device=DEV)).to(torch.bfloat16)
@@ -550,7 +551,7 @@ def test_graph_metadata_replays_match_eager_steps() -> None:
         hip_attention.attend(q, buffers, meta, out, scale=dim**-0.5)
 
     # one eager step sizes the scratch, then capture
-    lengths0 = torch.tensor([1, 1, 1, 1], dtype=torch.int32)
+    lengths0 = torch.ones(bucket, dtype=torch.int32)
     hip_attention.update_graph_metadata(meta, lengths0, torch.from_numpy(perm))
     step()
     torch.cuda.synchronize()
@@ -563,7 +564,13 @@ def test_graph_metadata_replays_match_eager_steps() -> None:
     with torch.cuda.graph(graph):
         step()
     torch.cuda.synchronize()
-    for trial, lens in enumerate([[5, 0, 1000, 17], [1280, 640, 0, 0], [33, 1, 2, 900]]):
+    if bucket == 4:
+        trials = [[5, 0, 1000, 17], [1280, 640, 0, 0], [33, 1, 2, 900]]
+    else:  # ragged batches: the staged partition size and work list change from step to step
+        cap = max_blocks * bs
+        trials = [[int(x) for x in rng.integers(0, cap + 1, size=bucket)] for _ in range(2)]
+        trials += [[cap] + [0] * (bucket - 1), [1] * bucket, [cap] * bucket]
+    for trial, lens in enumerate(trials):
         lengths = torch.tensor(lens, dtype=torch.int32)
         table = torch.from_numpy(perm.copy())
         q.copy_(torch.randn(q.shape, device=DEV).to(torch.bfloat16))
@@ -582,14 +589,20 @@ def test_graph_metadata_replays_match_eager_steps() -> None:
                                         lengths.to(DEV), table.to(DEV), bs)
         assert eager_meta.slot_mapping.tolist() == meta.slot_mapping.tolist()
         assert eager_meta.positions.tolist() == meta.positions.tolist()
-        graph_split = hip_attention.choose_split(bucket, kv_heads, heads // kv_heads, max_blocks * bs)
-        # the replay's dense grid and the eager work list differ in size, so the library may merge
-        # the partitions at different sites; the same site folds in the same order
-        site = hip_attention.graph_merge_site(bucket, kv_heads, heads // kv_heads, graph_split.partitions)
+        # a v2 replay runs the partition size the update staged, over a grid of the bucket's
+        # capacity and the bucket's partition count (which sets the reduce kernel's fold
+        # width), so the library may merge the partitions at another site than the eager
+        # work list's; the same site and partition count fold in the same order
+        staged_size = meta.plan.staged_partition_size
+        assert staged_size % 64 == 0 and staged_size >= meta.plan.min_size
+        site = hip_attention.graph_merge_site(bucket, kv_heads, heads // kv_heads, meta.plan.partitions)
         same_shape = torch.empty_like(out)
-        hip_attention.attend_with(q, buffers, eager_meta, same_shape, scale=dim**-0.5,
-                                  partitions=graph_split.partitions, partition_size=graph_split.partition_size or None,
-                                  merge=site if graph_split.partitions else None)
+        if meta.plan.partitions > 1:
+            hip_attention.attend_with(q, buffers, eager_meta, same_shape, scale=dim**-0.5,
+                                      partitions=meta.plan.partitions, partition_size=staged_size,
+                                      merge=site)
+        else:
+            hip_attention.attend_with(q, buffers, eager_meta, same_shape, scale=dim**-0.5, partitions=0)
         eager_out = torch.empty_like(out)
         hip_attention.attend(q, buffers, eager_meta, eager_out, scale=dim**-0.5)
         torch.cuda.synchronize()

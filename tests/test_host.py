@@ -93,6 +93,42 @@ def test_graph_metadata_starts_as_padding_and_updates_in_place() -> None:
     assert addresses == [t.data_ptr() for t in (meta.positions, meta.slot_mapping, meta.kv_lengths, meta.block_table)]
 
 
+def test_work_list_order_and_the_staged_graph_split() -> None:
+    # longest partition first, ties by row then partition; a row without context keeps partition 0
+    items = hip_attention.work_list([300, 0, 512, 40], 256).reshape(-1, 2).tolist()
+    assert items == [[0, 0], [2, 0], [2, 1], [0, 1], [3, 0], [1, 0]]
+    assert hip_attention.work_list([], 64).size == 0
+    # brute force over small cases: every partition with tokens once, sizes never rising
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        lengths = rng.integers(0, 700, size=int(rng.integers(1, 9)))
+        size = int(rng.choice([64, 128, 256]))
+        pairs = hip_attention.work_list(lengths, size).reshape(-1, 2)
+        want = {(r, p) for r, n in enumerate(lengths) for p in range(max(1, -(-int(n) // size)))}
+        assert {tuple(x) for x in pairs.tolist()} == want and len(pairs) == len(want)
+        sizes = [min(size, int(lengths[r]) - p * size) for r, p in pairs.tolist()]
+        assert sizes == sorted(sizes, reverse=True)
+    # a bucket of 8 requests x 1024 blocks of 16: at least 16384 / 64 = 256 positions a partition
+    meta = hip_attention.graph_metadata(8, 1024, 16, torch.device("cpu"))
+    plan = meta.plan
+    assert (plan.min_size, plan.partitions, plan.capacity) == (256, 64, 512)
+    assert plan.staged_host[:2].tolist() == [256, 8]
+    assert plan.staged_host[2:18:2].tolist() == list(range(8)) and plan.staged_host[3:18:2].tolist() == [0] * 8
+    table = torch.arange(8 * 1024, dtype=torch.int32).reshape(8, 1024)
+    lengths = [16384, 9000, 0, 1, 4096, 2048, 100, 16000]
+    hip_attention.update_graph_metadata(meta, _ints(*lengths), table)
+    size, count = plan.staged_partition_size, int(plan.staged_host[1])
+    assert size % 64 == 0 and size >= plan.min_size and -(-max(lengths) // size) <= plan.partitions
+    assert plan.staged_host[2:2 + 2 * count].tolist() == hip_attention.work_list(lengths, size).tolist()
+    # all rows empty: one item per row, the minimum size
+    hip_attention.update_graph_metadata(meta, _ints(*[0] * 8), table)
+    assert plan.staged_host[:2].tolist() == [256, 8]
+    # a short table: 256 positions at least; a large bucket: 8192 items at most
+    assert hip_attention.graph_metadata(2, 4, 16, torch.device("cpu")).plan.min_size == 256
+    big = hip_attention.graph_metadata(512, 2048, 16, torch.device("cpu")).plan
+    assert (big.min_size, big.partitions, big.capacity) == (2048, 16, 8192)
+
+
 def test_graph_metadata_update_refusals() -> None:
     meta = hip_attention.graph_metadata(2, 2, 4, torch.device("cpu"))
     with pytest.raises(BackendError, match=r"must be in \[0, 8\]"):
