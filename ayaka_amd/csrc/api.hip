@@ -199,7 +199,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   hipError_t err = mfma ? ayk::launch_attention_mfma(q, head_dim, gc, bf16, split, kv8, waves, s)
                         : ayk::launch_attention_dpp(q, head_dim, gc, bf16, split, waves, s);
   if (err == hipSuccess && split && !q.arrivals && !(flags & AYK_FLAG_PARTIALS_ONLY))
-    err = ayk::launch_partition_reduce(q, head_dim, bf16, s);
+    err = ayk::launch_partition_reduce(q, head_dim, bf16, compute_units(), s);
   return launched(err, op);
 }
 

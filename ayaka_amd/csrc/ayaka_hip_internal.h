@@ -56,8 +56,10 @@ hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int heads_pe
 int prefill_tile_pairs_for(int head_dim);
 hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16, bool kv8,
                           int waves_per_group, hipStream_t stream);
-// The v2 log-sum-exp merge of the partitions of every (row, head).
-hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);
+// The v2 log-sum-exp merge of the partitions of every (row, head); `compute_units` of the
+// device sets how many partition slots each pair gets.
+hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, int compute_units,
+                                   hipStream_t stream);
 hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);
 
 hipError_t launch_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,

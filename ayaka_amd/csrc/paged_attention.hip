@@ -458,26 +458,35 @@ hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipSt
 }
 
 template <int D, bool BF16>
-static hipError_t launch_reduce_typed(const AttnParams& p, hipStream_t stream) {
-  // Partition slots per (row, head): one for up to 4 partitions per row, then 4, then
-  // as many as one workgroup holds for a single head.
+static hipError_t launch_reduce_typed(const AttnParams& p, int compute_units, hipStream_t stream) {
+  // Partition slots per (row, head): one for up to 4 partitions per row, then 4, or as many
+  // as one workgroup holds for a single head when 4 would leave compute units without a
+  // workgroup (few rows of many partitions: C4's 8 x 32 pairs). A staged launch sizes
+  // max_partitions for its smallest partition size while its steps mostly run far fewer,
+  // so 4 slots serve it unless the grid is small.
   constexpr int QUADS = D / 4;
   constexpr int S_MAX = kReduceThreads / QUADS;
-  const int s = p.max_partitions <= 4 ? 1 : p.max_partitions <= 16 ? (S_MAX < 4 ? S_MAX : 4) : S_MAX;
+  constexpr int S4 = S_MAX < 4 ? S_MAX : 4;
   const int64_t pairs = (int64_t)p.n_rows * p.num_heads;
+  const int64_t groups4 = (pairs + S_MAX / S4 - 1) / (S_MAX / S4);
+  const int s = p.max_partitions <= 4 ? 1 : (p.max_partitions <= 16 || groups4 >= compute_units) ? S4 : S_MAX;
   const dim3 block(kReduceThreads);
   auto grid = [&](int heads) { return dim3((unsigned)((pairs + heads - 1) / heads)); };
   if (s == 1) hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, 1>), grid(S_MAX), block, 0, stream, p);
-  else if (s == 4) hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, 4>), grid(S_MAX / 4), block, 0, stream, p);
+  else if (s == S4) hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, S4>), grid(S_MAX / S4), block, 0, stream, p);
   else hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, S_MAX>), grid(1), block, 0, stream, p);
   return hipGetLastError();
 }
 
-hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream) {
+hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, int compute_units,
+                                   hipStream_t stream) {
+  const int cu = compute_units;
   switch (head_dim) {
-    case 64: return bf16 ? launch_reduce_typed<64, true>(p, stream) : launch_reduce_typed<64, false>(p, stream);
-    case 128: return bf16 ? launch_reduce_typed<128, true>(p, stream) : launch_reduce_typed<128, false>(p, stream);
-    case 256: return bf16 ? launch_reduce_typed<256, true>(p, stream) : launch_reduce_typed<256, false>(p, stream);
+    case 64: return bf16 ? launch_reduce_typed<64, true>(p, cu, stream) : launch_reduce_typed<64, false>(p, cu, stream);
+    case 128:
+      return bf16 ? launch_reduce_typed<128, true>(p, cu, stream) : launch_reduce_typed<128, false>(p, cu, stream);
+    case 256:
+      return bf16 ? launch_reduce_typed<256, true>(p, cu, stream) : launch_reduce_typed<256, false>(p, cu, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -68,9 +68,9 @@ __all__ = [
 PARTITION_SIZE = 512
 #: Graph replays: the smallest partition, the most partitions per row of the table width,
 #: and the most work items of a bucket (the captured grid, by key/value head group).
-GRAPH_MIN_PARTITION = 256
+GRAPH_MIN_PARTITION = 64
 GRAPH_MAX_PARTITIONS = 64
-GRAPH_MAX_ITEMS = 8192
+GRAPH_MAX_ITEMS = 2048
 #: Partition sizes an eagerly planned step chooses from (multiples of 64).
 PARTITION_CANDIDATES = (64, 128, 192, 256, 320, 384, 448, 512, 576, 640, 704, 768, 896, 1024, 1280, 1536,
                         2048, 3072, 4096, 8192, 16384)
@@ -913,7 +913,7 @@ def graph_metadata(
     def host(shape: tuple[int, ...], dtype: torch.dtype) -> torch.Tensor:
         return torch.zeros(shape, dtype=dtype, pin_memory=pinned)
 
-    # Replays run v2 over partitions of at least min_size: 256 positions, or the share of
+    # Replays run v2 over partitions of at least min_size: 64 positions, or the share of
     # the table width that keeps the captured grid within GRAPH_MAX_PARTITIONS items per
     # row and GRAPH_MAX_ITEMS in all. Until the first update every row is one item.
     max_length = max_blocks * block_size

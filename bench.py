@@ -71,7 +71,7 @@ def parse() -> argparse.Namespace:
                     help="only run the read-only access-pattern probes (ayaka_amd/lib/access_probe)")
     ap.add_argument("--graph-step", action="store_true",
                     help="time a 32-layer decode step (KV write + attention per layer) eagerly and as a "
-                         "captured graph replay, at the C1 and C3 shapes")
+                         "captured graph replay (and eagerly on a planned step), at the C1-C5 shapes")
     ap.add_argument("--multi-row", action="store_true",
                     help="only time the multi-row (prefill / verify) kernel on its workloads, one JSON line each")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -224,19 +224,20 @@ GRAPH_STEP_LAYERS = 32
 def graph_step(args) -> int:
     """A decode step of GRAPH_STEP_LAYERS layers, each a KV write and an attention call over one
     shared pool (every layer has the same shape, so one pool times them all), on graph metadata:
-    run eagerly (the Python ops per call) and as one captured graph replayed per step."""
+    run eagerly (the Python ops per call) and as one captured graph replayed per step; and, as
+    the reference point of a GPU-bound step, eagerly on a planned step (its own work list)."""
     import torch
 
     from ayaka_amd import workloads
     from ayaka_amd.hip import _lib
     from ayaka_amd.hip import attention as hip_attention
     from ayaka_amd.hip import kvcache as hip_kvcache
-    from ayaka_amd.enums import KVLayoutKind
+    from ayaka_amd.enums import ForwardMode, KVLayoutKind
     from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
 
     _lib.lib()
     dev = torch.device("cuda:0")
-    for index in (1, 3):
+    for index in (1, 2, 3, 4, 5):
         cfg = workloads.config(index)
         step = workloads.build(cfg, dev, poison=False)
         buffers = KVBuffers(step.k_cache, step.v_cache, KVLayoutKind.NHD, RAW_CODEC)
@@ -248,12 +249,16 @@ def graph_step(args) -> int:
             raise RuntimeError("graph step: fewer new rows than sequences")
         out = torch.empty_like(step.q)
 
-        def one_step() -> None:
+        planned = hip_attention.plan(ForwardMode.DECODE, torch.ones(cfg.batch, dtype=torch.int32, device=dev),
+                                     step.lengths, step.table, cfg.block_size)
+
+        def one_step(meta=meta) -> None:
             for _ in range(GRAPH_STEP_LAYERS):
                 hip_kvcache.store(k_new, v_new, buffers, meta)
                 hip_attention.attend(step.q, buffers, meta, out, scale=cfg.scale)
 
         eager = time_calls(one_step, max(3, args.steps // 20), 2, repeats=3)
+        eager_planned = time_calls(lambda: one_step(planned), max(3, args.steps // 20), 2, repeats=3)
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -266,8 +271,10 @@ def graph_step(args) -> int:
         print(json.dumps({
             "workload": f"C{index} {cfg.name}: {GRAPH_STEP_LAYERS} layers of KV write + decode attention "
                         f"(graph metadata, batch {cfg.batch})",
+            "planned_us_per_step": round(eager_planned["median_us"], 1),
             "eager_us_per_step": round(eager["median_us"], 1),
             "graph_us_per_step": round(replay["median_us"], 1),
+            "planned_us_per_layer": round(eager_planned["median_us"] / GRAPH_STEP_LAYERS, 2),
             "eager_us_per_layer": round(eager["median_us"] / GRAPH_STEP_LAYERS, 2),
             "graph_us_per_layer": round(replay["median_us"] / GRAPH_STEP_LAYERS, 2),
         }), flush=True)

@@ -123,10 +123,10 @@ def test_work_list_order_and_the_staged_graph_split() -> None:
     # all rows empty: one item per row, the minimum size
     hip_attention.update_graph_metadata(meta, _ints(*[0] * 8), table)
     assert plan.staged_host[:2].tolist() == [256, 8]
-    # a short table: 256 positions at least; a large bucket: 8192 items at most
-    assert hip_attention.graph_metadata(2, 4, 16, torch.device("cpu")).plan.min_size == 256
+    # a short table: 64 positions at least; a large bucket: 2048 items at most
+    assert hip_attention.graph_metadata(2, 4, 16, torch.device("cpu")).plan.min_size == 64
     big = hip_attention.graph_metadata(512, 2048, 16, torch.device("cpu")).plan
-    assert (big.min_size, big.partitions, big.capacity) == (2048, 16, 8192)
+    assert (big.min_size, big.partitions, big.capacity) == (8192, 4, 2048)
 
 
 def test_graph_metadata_update_refusals() -> None:
