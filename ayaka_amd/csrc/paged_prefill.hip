@@ -34,6 +34,7 @@
 //    group spread over the banks.
 #include "attention_common.h"
 
+
 namespace ayk {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -218,10 +219,11 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
       o0 = s_tbl[(t0 >> shift) - b0] + in_block(t0, bs_mask, token_stride);
       o1 = shift ? o0 + (t1 > t0 ? token_stride : 0u) : s_tbl[t1 - b0];
     };
+    // Chunk ci into registers kr and vr; K and V pieces of the same two positions share
+    // their offsets.
     auto load_chunk = [&](int ci) {
 #pragma unroll
       for (int u = 0; u < PER_THREAD; u += 2) {
-        // K and V pieces of the same two positions share their offsets
         uint32_t o0, o1;
         pair_offsets(s0 + ci * CH + piece_pos(u), o0, o1);
         kr[u] = load_kv_raw<KV8, false>(kbase, o0 + piece_c * 8);
@@ -230,24 +232,26 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
         vr[u + 1] = load_kv_raw<KV8, false>(vbase, o1 + piece_c * 8);
       }
     };
-    auto stage_chunk = [&](int buf) {
+    auto stage_keys = [&](int buf) {
 #pragma unroll
       for (int u = 0; u < PER_THREAD; u += 2) {
         const int pos = piece_pos(u);
         s_k[buf][key_slot(pos, piece_c)] = kv_pairs<KV8, BF16>(kr[u]);
         s_k[buf][key_slot(pos + 1, piece_c)] = kv_pairs<KV8, BF16>(kr[u + 1]);
+      }
+    };
+    auto stage_values = [&](int buf) {
+#pragma unroll
+      for (int u = 0; u < PER_THREAD; u += 2) {
+        const int pos = piece_pos(u);
         *reinterpret_cast<u32x4*>(&s_v[buf][pos * VP + piece_c * 8]) = kv_pairs<KV8, BF16>(vr[u]);
         *reinterpret_cast<u32x4*>(&s_v[buf][(pos + 1) * VP + piece_c * 8]) = kv_pairs<KV8, BF16>(vr[u + 1]);
       }
     };
 
-    // Fold chunk ci (in LDS buffer buf) into every pair's running state.
-    auto consume = [&](int ci, int buf) {
-      const int tb = s0 + ci * CH;
-      // uniform: no position masked (and, for folding the scale into the exponent,
-      // a scale >= 0, under which the largest raw score gives the largest scaled one)
-      const bool whole = tb + CH <= s1 && tb + CH - 1 <= wave_min_pos && scale_log2 >= 0.f;
-      f32x4 acc[PTL_W][PT];
+    typedef f32x4 Scores[PTL_W][PT];
+    // This wave's raw scores of the chunk whose keys sit in LDS buffer kb.
+    auto scores = [&](int kb, Scores& acc) {
 #pragma unroll
       for (int w = 0; w < PTL_W; ++w)
 #pragma unroll
@@ -257,10 +261,19 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 #pragma unroll
         for (int w = 0; w < PTL_W; ++w) {
           const int pt = ps * PTL_W + w;
-          const u32x4 ka = s_k[buf][key_slot(pt * 16 + mt, s * 4 + mq)];
+          const u32x4 ka = s_k[kb][key_slot(pt * 16 + mt, s * 4 + mq)];
 #pragma unroll
           for (int j = 0; j < PT; ++j) acc[w][j] = mfma32<BF16>(ka, qb[j][s], acc[w][j]);
         }
+    };
+    // Fold chunk ci's scores acc (its values in LDS buffer vb) into every pair's running
+    // state; mid() runs between the rescale and the weights.
+    auto fold = [&](int ci, int vb, Scores& acc, auto&& mid) {
+      const int buf = vb;
+      const int tb = s0 + ci * CH;
+      // uniform: no position masked (and, for folding the scale into the exponent,
+      // a scale >= 0, under which the largest raw score gives the largest scaled one)
+      const bool whole = tb + CH <= s1 && tb + CH - 1 <= wave_min_pos && scale_log2 >= 0.f;
       // the scale applied to a score in the exponent below (1 once the scores are scaled)
       const float sc = whole ? scale_log2 : 1.f;
 #pragma unroll
@@ -295,6 +308,7 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
           m[j] = mn;
         }
       }
+      mid();
       // Weights after every group's max and rescale: from here to the end of the chunk
       // the code has no branch, so the scheduler can overlap one group's exponentials
       // with the other's P.V MFMAs.
@@ -358,13 +372,26 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
     };
 
     load_chunk(0);
-    stage_chunk(0);
+    stage_keys(0);
+    stage_values(0);
     lds_barrier();
     for (int ci = 0; ci < nch; ++ci) {
       const int buf = ci & 1;
       if (ci + 1 < nch) load_chunk(ci + 1);
-      consume(ci, buf);
-      if (ci + 1 < nch) stage_chunk(buf ^ 1);
+      // The two waves a SIMD holds (one per workgroup) take turns: a wave raises its
+      // priority over its MFMA sections -- the q.k, and the weights with the P.V -- so
+      // that its matrix instructions issue ahead of the other wave's max and rescale
+      // VALU work, which fills the issue slots between them (5-6% on prefill chunks).
+      Scores acc;
+      __builtin_amdgcn_s_setprio(1);
+      scores(buf, acc);
+      __builtin_amdgcn_s_setprio(0);
+      fold(ci, buf, acc, [] { __builtin_amdgcn_s_setprio(1); });
+      __builtin_amdgcn_s_setprio(0);
+      if (ci + 1 < nch) {
+        stage_keys(buf ^ 1);
+        stage_values(buf ^ 1);
+      }
       lds_barrier();
     }
   }
