@@ -665,6 +665,51 @@ def test_c_abi_direct_call() -> None:
     assert rc == 2 and b"head_dim 96" in lib.ayk_last_error()
 
 
+@pytest.mark.parametrize("merge_flag", [8, 16], ids=["reduce-kernel", "in-kernel"])
+def test_c_abi_v2_follows_the_staged_split(merge_flag: int) -> None:
+    # ayk_paged_attention_v2 with staged parameters (as a graph replay calls it): the grid covers
+    # a capacity of work items, the partition size and the item list are read from device memory.
+    # The result equals, bit for bit, the same call given that size and list directly.
+    s = build_scenario([(1, 700), (1, 1), (1, 0), (1, 300)], heads=8, kv_heads=2, head_dim=128,
+                       block_size=16, mode="decode", seed=73)
+    k, v, q = to_device(s.k_bits, "bf16"), to_device(s.v_bits, "bf16"), to_device(s.q_bits, "bf16")
+    table = torch.from_numpy(s.table.astype(np.int32)).to(DEV)
+    lengths = torch.tensor(s.lengths, dtype=torch.int32, device=DEV)
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    n_rows, width = len(s.lengths), table.shape[1]
+    min_size = 64
+    max_partitions = -(-width * 16 // min_size)
+    capacity = n_rows * max_partitions
+    nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, 8, 128, max_partitions)
+    scratch = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    arrivals = torch.zeros(1024, dtype=torch.int32, device=DEV)
+    common = (q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), width, lengths.data_ptr(), None, None,
+              n_rows, 8, 2, 128, k.shape[0], 16, width, 0, 1, 1, ctypes.c_float(s.scale))
+    staged = torch.zeros(2 + 2 * capacity, dtype=torch.int32, device=DEV)
+    for size in (256, 128, 704):
+        items = hip_attention.work_list(s.lengths, size)
+        staged[:2 + items.size] = torch.tensor([size, items.size // 2, *items.tolist()], dtype=torch.int32)
+        direct = torch.from_numpy(items).to(DEV)
+        outs = []
+        for staged_call in (True, False):
+            out = torch.full_like(q, float("nan"))
+            if staged_call:
+                rc = lib.ayk_paged_attention_v2(out.data_ptr(), *common, min_size, max_partitions,
+                                                staged.data_ptr() + 8, capacity, staged.data_ptr(), scratch.data_ptr(),
+                                                nbytes, arrivals.data_ptr(), merge_flag, stream)
+            else:
+                rc = lib.ayk_paged_attention_v2(out.data_ptr(), *common, size, max_partitions, direct.data_ptr(),
+                                                items.size // 2, None, scratch.data_ptr(), nbytes,
+                                                arrivals.data_ptr(), merge_flag, stream)
+            assert rc == 0, lib.ayk_last_error()
+            torch.cuda.synchronize()
+            outs.append(out)
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16)), f"size {size}"
+        assert_parity(outs[0], s.expected(np.float64), "bf16", f"staged {size}")
+    assert int(arrivals.abs().sum()) == 0  # the in-kernel merge leaves its counters at zero
+
+
 def test_unsupported_shapes_are_refused_before_launch() -> None:
     s = build_scenario([(1, 10)], head_dim=64, block_size=16, mode="decode")
     buffers = scenario_buffers(s)
