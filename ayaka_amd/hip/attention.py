@@ -10,20 +10,20 @@ facts ``attend`` needs to pick a launch without reading the device.
 * v1 (``ayk_paged_attention_v1``): one workgroup per (row, key/value head)
   streams the row's whole context once;
 * v2 (``ayk_paged_attention_v2``): one workgroup per (row, key/value head,
-  partition of :data:`PARTITION_SIZE` positions), then a log-sum-exp merge.
+  partition) that holds tokens, longest first, then a log-sum-exp merge.
 
-:func:`choose_partitions` picks between them from the step's shape only, so a
-step computes the same thing eagerly and when replayed from a graph. Decode rows
-(one per request) and multi-row steps (prefill chunks, verify windows) use the
-same kernels: a multi-row step passes each row's request and position, and row
-``j`` attends to positions ``0 .. position_j`` (the reference's causal rule,
-``attention.py:209-234``).
+:func:`choose_split` picks between them, and the partition size, from the step's
+row lengths by a modelled schedule. Decode rows (one per request) use these kernels;
+steps of several rows per request (prefill chunks, verify windows) use the multi-row
+kernel (``ayk_paged_prefill``), where row ``j`` attends to positions
+``0 .. position_j`` (the reference's causal rule, ``attention.py:209-234``).
 
 ``graph_metadata`` / ``update_graph_metadata`` follow the reference's
 fixed-address record (``attention.py:274-374``): device tensors allocated once,
-host staging pinned, asynchronous copies on the current stream. ``attend`` on
-graph metadata reads nothing on the host that changes between replays: the
-launch shape comes from the bucket's table width.
+host staging pinned, asynchronous copies on the current stream. Each update also
+stages the step's v2 partition size and work list on the device, so ``attend`` on
+graph metadata reads nothing on the host that changes between replays: its
+captured launch covers the bucket's capacity and the kernels read the step's split.
 """
 
 from __future__ import annotations
@@ -428,7 +428,8 @@ def merge_site(num_kv_heads: int, group: int, step: "HipAttentionPlan", partitio
 
 
 def graph_merge_site(n_rows: int, num_kv_heads: int, group: int, partitions: int) -> str:
-    """Where the library merges the v2 partitions of a graph replay (the dense grid)."""
+    """Where the library merges the v2 partitions of a v2 launch over ``n_rows`` x ``partitions``
+    items (a graph replay's grid of the bucket's capacity, or a forced dense grid)."""
     return merge_site_for(n_rows * partitions * -(-num_kv_heads * head_chunks(group) // 8))
 
 
