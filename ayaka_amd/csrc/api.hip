@@ -314,14 +314,16 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
   if (staged && n_work_items == 0)
     return fail(AYK_ERR_ARGUMENT, "%s: staged parameters need a work list (the grid's capacity)", op);
   if (n_rows == 0) return ok();
-  const size_t need =
-      ayk_paged_attention_v2_workspace_bytes(n_rows, num_heads, head_dim, max_partitions);
+  // Staged parameters pack the rows' partials: at most one slot per work item.
+  const int32_t slot_rows = staged ? n_work_items : n_rows;
+  const int32_t slots_per_row = staged ? 1 : max_partitions;
+  const size_t need = ayk_paged_attention_v2_workspace_bytes(slot_rows, num_heads, head_dim, slots_per_row);
   if (!workspace || workspace_bytes < need)
     return fail(AYK_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", op, workspace_bytes,
                 need);
   if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
     return fail(AYK_ERR_ARGUMENT, "%s: workspace is not 16-byte aligned", op);
-  const size_t parts = (size_t)n_rows * num_heads * max_partitions;
+  const size_t parts = (size_t)slot_rows * num_heads * slots_per_row;
   p.part_o = static_cast<float*>(workspace);
   p.part_ml = p.part_o + parts * head_dim;
   p.partition_size = partition_size;

@@ -216,64 +216,14 @@ constexpr float kNoScore = -1.0e30f;
 // accumulators are rescaled: weights stay below 2^8, far inside fp32.
 constexpr float kRescaleSlack = 8.0f;
 
-// Per-wave partial results of one workgroup, merged by merge_waves_and_store.
-template <int D, int GC, int WAVES>
-struct WaveParts {
-  float o[WAVES][GC][D];  // unnormalised sums, relative to m
-  float m[WAVES][GC];     // running max (log2 domain)
-  float l[WAVES][GC];     // sum of weights
-};
-
-// Merge the waves' (m, l, o) of GC heads and write them: the rounded output
-// (v1) or the normalised partial and its (m, l) (v2 partition z). Call after a
-// __syncthreads() that follows the waves' writes; one thread per (head, 8 elements).
-template <int D, int GC, int WAVES, bool BF16, bool SPLIT>
-__device__ __forceinline__ void merge_waves_and_store(const AttnParams& p, const WaveParts<D, GC, WAVES>& parts,
-                                                      int row, int part, int h0, int tid) {
-  using E = Elem<BF16>;
-  constexpr int LPT = D / 8;
-  for (int it = tid; it < GC * LPT; it += WAVES * kWave) {
-    const int g = it / LPT, cc = it % LPT;
-    float mn = parts.m[0][g];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) mn = fmaxf(mn, parts.m[w][g]);
-    float wt[WAVES];
-    float L = 0.f;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      wt[w] = fast_exp2(parts.m[w][g] - mn);
-      L += parts.l[w][g] * wt[w];
-    }
-    float acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float a = 0.f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) a = fmaf(wt[w], parts.o[w][g][cc * 8 + e], a);
-      acc[e] = a;
-    }
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
-    const int64_t head_row = (int64_t)row * p.num_heads + h0 + g;
-    if constexpr (SPLIT) {
-      float* po = p.part_o + (head_row * p.max_partitions + part) * D + cc * 8;
-      *reinterpret_cast<f32x4*>(po) = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
-      *reinterpret_cast<f32x4*>(po + 4) =
-          f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
-      if (cc == 0) {
-        float* pml = p.part_ml + (head_row * p.max_partitions + part) * 2;
-        pml[0] = mn;
-        pml[1] = L;
-      }
-    } else {
-      uint16_t* out = static_cast<uint16_t*>(p.out) + head_row * D + cc * 8;
-      u32x4 w;
-      w.x = E::round(acc[0] * inv) | (E::round(acc[1] * inv) << 16);
-      w.y = E::round(acc[2] * inv) | (E::round(acc[3] * inv) << 16);
-      w.z = E::round(acc[4] * inv) | (E::round(acc[5] * inv) << 16);
-      w.w = E::round(acc[6] * inv) | (E::round(acc[7] * inv) << 16);
-      *reinterpret_cast<u32x4*>(out) = w;
-    }
-  }
+// Index of the first partial (partition 0) of (row, head), which has np partitions.
+// By default the partials are [n_rows, num_heads, max_partitions]; with staged
+// parameters the rows are packed: row r's partials start at slot staged[2 + r] (the
+// host's prefix sum of the rows' partition counts), head-major within the row, so a
+// launch needs as many slots as its work list holds items, not rows x max_partitions.
+__device__ __forceinline__ int64_t partial_index(const AttnParams& p, int row, int head, int np) {
+  return p.staged ? (int64_t)p.staged[2 + row] * p.num_heads + (int64_t)head * np
+                  : ((int64_t)row * p.num_heads + head) * p.max_partitions;
 }
 
 // Write one head's merged state from lane c (its 8 elements): the rounded
@@ -287,11 +237,12 @@ __device__ __forceinline__ void store_head(const AttnParams& p, int row, int par
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   const int64_t head_row = (int64_t)row * p.num_heads + head;
   if (SPLIT && np > 1) {
-    float* po = p.part_o + (head_row * p.max_partitions + part) * D + c * 8;
+    const int64_t slot = partial_index(p, row, head, np) + part;
+    float* po = p.part_o + slot * D + c * 8;
     *reinterpret_cast<f32x4*>(po) = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
     *reinterpret_cast<f32x4*>(po + 4) = f32x4{o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv};
     if (c == 0) {
-      float* pml = p.part_ml + (head_row * p.max_partitions + part) * 2;
+      float* pml = p.part_ml + slot * 2;
       pml[0] = m;
       pml[1] = l;
     }
@@ -315,11 +266,12 @@ __device__ __forceinline__ void store_head_t(const AttnParams& p, int row, int p
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   const int64_t head_row = (int64_t)row * p.num_heads + head;
   if (SPLIT && np > 1) {
-    float* po = p.part_o + (head_row * p.max_partitions + part) * D + 4 * g;
+    const int64_t slot = partial_index(p, row, head, np) + part;
+    float* po = p.part_o + slot * D + 4 * g;
 #pragma unroll
     for (int t = 0; t < D / 16; ++t) *reinterpret_cast<f32x4*>(po + 16 * t) = o[t] * inv;
     if (g == 0) {
-      float* pml = p.part_ml + (head_row * p.max_partitions + part) * 2;
+      float* pml = p.part_ml + slot * 2;
       pml[0] = m;
       pml[1] = l;
     }
@@ -346,7 +298,6 @@ __device__ __forceinline__ void merge_partitions(const AttnParams& p, int row, i
   using E = Elem<BF16>;
   constexpr int QUADS = D / 4;
   const int items = (head_hi - head_lo) * QUADS;
-  const int64_t stride = (int64_t)p.max_partitions;
   const float* ml[IPT];
   const f32x4* po[IPT];
   float m[IPT], l[IPT];
@@ -354,9 +305,9 @@ __device__ __forceinline__ void merge_partitions(const AttnParams& p, int row, i
 #pragma unroll
   for (int k = 0; k < IPT; ++k) {
     const int it = min(tid + k * threads, items - 1);  // spare slots repeat the last item, unstored
-    const int64_t head_row = (int64_t)row * p.num_heads + head_lo + it / QUADS;
-    ml[k] = p.part_ml + head_row * stride * 2;
-    po[k] = reinterpret_cast<const f32x4*>(p.part_o + head_row * stride * D) + it % QUADS;
+    const int64_t first = partial_index(p, row, head_lo + it / QUADS, np);
+    ml[k] = p.part_ml + first * 2;
+    po[k] = reinterpret_cast<const f32x4*>(p.part_o + first * D) + it % QUADS;
     m[k] = kNoScore;
     l[k] = 0.f;
     acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};

@@ -21,10 +21,12 @@ struct AttnParams {
   const int32_t* request_of_row;  // nullptr: row n is request n
   const int32_t* positions;       // nullptr: row n attends to its whole context
   const int32_t* work;            // v2 only, optional: n_work (row, partition) pairs to run
-  const int32_t* staged;          // v2 only, optional (graph replays): {partition size, work items}
-                                  // read on the device; the grid then covers n_work items at most
-  float* part_o;                  // v2 only: [n_rows, num_heads, max_partitions, head_dim]
-  float* part_ml;                 // v2 only: [n_rows, num_heads, max_partitions, 2] = (m, l)
+  const int32_t* staged;          // v2 only, optional (graph replays): {partition size, work items,
+                                  // n_rows partial offsets} read on the device; the grid then covers
+                                  // n_work items at most
+  float* part_o;                  // v2 only: [n_rows, num_heads, max_partitions, head_dim], or with
+                                  // staged parameters the rows packed (partial_index)
+  float* part_ml;                 // v2 only: the same slots' (m, l)
   uint32_t* arrivals;             // v2 single launch: [n_rows, head groups] counters, zero between calls;
                                   // nullptr: a separate reduce kernel merges the partitions
   int64_t table_stride;

@@ -321,8 +321,9 @@ __global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const 
   row_context(p, row, req, len);
   const int np = valid ? (len > 0 ? (len - 1) / partition_size_of(p) + 1 : 0) : 1;
   uint16_t* out = static_cast<uint16_t*>(p.out) + pair * D;
-  const float* ml = p.part_ml + pair * p.max_partitions * 2;
-  const f32x4* po = reinterpret_cast<const f32x4*>(p.part_o + pair * p.max_partitions * D);
+  const int64_t first = partial_index(p, row, (int)(pair % p.num_heads), np);
+  const float* ml = p.part_ml + first * 2;
+  const f32x4* po = reinterpret_cast<const f32x4*>(p.part_o + first * D);
 
   float m = kNoScore, l = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};

@@ -67,9 +67,10 @@ __all__ = [
 #: Default positions per v2 partition (callers that force a v2 launch without a size).
 PARTITION_SIZE = 512
 #: Graph replays: the smallest partition, the most partitions per row of the table width,
-#: and the most work items of a bucket (the captured grid, by key/value head group).
+#: and the work items of a bucket of fewer rows (the captured grid, by key/value head
+#: group, and the partial slots of its scratch).
 GRAPH_MIN_PARTITION = 64
-GRAPH_MAX_PARTITIONS = 64
+GRAPH_MAX_PARTITIONS = 256
 GRAPH_MAX_ITEMS = 2048
 #: Partition sizes an eagerly planned step chooses from (multiples of 64).
 PARTITION_CANDIDATES = (64, 128, 192, 256, 320, 384, 448, 512, 576, 640, 704, 768, 896, 1024, 1280, 1536,
@@ -263,10 +264,11 @@ class HipGraphPlan:
     A captured v2 launch has a fixed grid of ``capacity`` work items over at most
     ``partitions`` partitions of at least ``min_size`` positions. Each update
     stages the step's own partition size (a multiple of 64, at least
-    ``min_size``) and work list into ``staged`` (device) as
-    ``[partition size, item count, row0, part0, ...]``; workgroups past the item
-    count return at once. ``head_shape`` holds the ``(num_kv_heads, group,
-    kv_bytes)`` of the first attend, which scores the staged split.
+    ``min_size``, whose work list fits the capacity) into ``staged`` (device) as
+    ``[partition size, item count, first partial slot of each row, row0, part0,
+    ...]``; workgroups past the item count return at once, and the rows' partials
+    are packed into ``capacity`` slots. ``head_shape`` holds the ``(num_kv_heads,
+    group, kv_bytes)`` of the first attend, which scores the staged split.
     """
 
     positions: torch.Tensor
@@ -285,6 +287,11 @@ class HipGraphPlan:
     def staged_partition_size(self) -> int:
         """The partition size the last update staged (the host copy)."""
         return int(self.staged_host[0])
+
+    @property
+    def work_offset(self) -> int:
+        """Where the work list starts in ``staged``, in int32 words."""
+        return 2 + self.positions.shape[0]
 
 
 def _host_ints(tensor: torch.Tensor) -> tuple[int, ...]:
@@ -427,10 +434,10 @@ def merge_site(num_kv_heads: int, group: int, step: "HipAttentionPlan", partitio
     return merge_site_for(items * groups)
 
 
-def graph_merge_site(n_rows: int, num_kv_heads: int, group: int, partitions: int) -> str:
-    """Where the library merges the v2 partitions of a v2 launch over ``n_rows`` x ``partitions``
-    items (a graph replay's grid of the bucket's capacity, or a forced dense grid)."""
-    return merge_site_for(n_rows * partitions * -(-num_kv_heads * head_chunks(group) // 8))
+def graph_merge_site(items: int, num_kv_heads: int, group: int) -> str:
+    """Where the library merges the v2 partitions of a launch over a grid of ``items`` work
+    items (a graph replay's capacity, or the rows x partitions of a forced dense grid)."""
+    return merge_site_for(items * -(-num_kv_heads * head_chunks(group) // 8))
 
 
 @dataclass(frozen=True, slots=True)
@@ -478,10 +485,14 @@ def fits_schedule(lengths: list[int], size: int, groups: int = 1) -> bool:
     return items <= MAX_ROUNDS * COMPUTE_UNITS
 
 
-def _best_size(lengths: list[int], max_length: int, groups: int, kv_bytes: int = 2, min_size: int = 0) -> int:
-    """The candidate partition size (of ``min_size`` or more) with the smallest
-    :func:`schedule_makespan`."""
+def _best_size(lengths: list[int], max_length: int, groups: int, kv_bytes: int = 2, min_size: int = 0,
+               max_items: int = 0) -> int:
+    """The candidate partition size (of ``min_size`` or more, and with ``max_items`` work
+    items at most when that is positive) with the smallest :func:`schedule_makespan`."""
     candidates = [size for size in PARTITION_CANDIDATES if size >= min_size] or [min_size]
+    if max_items:
+        candidates = [size for size in candidates if sum(-(-n // size) for n in lengths) <= max_items] \
+            or [-(-max_length // 64) * 64]
     best: tuple[int, int] | None = None
     for size in candidates:
         if not fits_schedule(lengths, size, groups) and size != candidates[-1]:
@@ -504,6 +515,7 @@ def choose_split(
     row_lengths: tuple[int, ...] | None = None,
     kv_bytes: int = 2,
     min_size: int = 0,
+    max_items: int = 0,
 ) -> Split:
     """Pick v1 or v2 and the partition size from the step's shape.
 
@@ -515,7 +527,8 @@ def choose_split(
     total to 4 significant bits), which successive decode steps -- every length
     one longer than the step before -- keep hitting. ``kv_bytes`` is the cache's bytes
     per element (2, or 1 for fp8), which sets the modelled workgroup cost; ``min_size``
-    leaves out smaller partition sizes (a graph replay's grid is sized for it).
+    leaves out smaller partition sizes, and ``max_items`` sizes whose work list over the
+    rows with context is longer (a graph replay's grid and scratch are sized for both).
     """
     del total_length
     if max_length <= 0:
@@ -525,12 +538,12 @@ def choose_split(
     total = sum(lengths)
     # The total to 4 significant bits, the longest row to a power of two, the row count.
     top = max(total.bit_length() - 4, 0)
-    key = (groups, kv_bytes, min_size, len(lengths), max_length.bit_length(), total >> top, top)
+    key = (groups, kv_bytes, min_size, max_items, len(lengths), max_length.bit_length(), total >> top, top)
     size = _split_cache.get(key)
     if size is None:
         if len(_split_cache) > 4096:
             _split_cache.clear()
-        size = _best_size(lengths, max_length, groups, kv_bytes, min_size)
+        size = _best_size(lengths, max_length, groups, kv_bytes, min_size, max_items)
         _split_cache[key] = size
     if max_length <= size:
         return Split(0, 0)
@@ -876,7 +889,10 @@ def attend_with(
     if partitions == 0:
         _lib.check(op, lib.ayk_paged_attention_v1(*common, flags, stream))
         return
-    nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, partitions)
+    if staged is not None:  # the rows' partials packed into one slot per work item
+        nbytes = lib.ayk_paged_attention_v2_workspace_bytes(step.capacity, heads, buffers.head_dim, 1)
+    else:
+        nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, partitions)
     scratch = _workspace(op, device, nbytes, capturing(q))
     arrivals = _arrivals(op, device, n_rows * heads, capturing(q))
     # A planned step runs only the partitions that hold tokens, longest first. Graph
@@ -885,7 +901,7 @@ def attend_with(
     # keep the dense grid.
     work, n_work = 0, 0
     if staged is not None:
-        work, n_work = staged.data_ptr() + 8, step.capacity
+        work, n_work = staged.data_ptr() + 4 * step.work_offset, step.capacity
     elif isinstance(step, HipAttentionPlan) and not capturing(q):
         items = step.work_items(partition_size, device)
         work, n_work = items.data_ptr(), items.numel() // 2
@@ -914,17 +930,18 @@ def graph_metadata(
     def host(shape: tuple[int, ...], dtype: torch.dtype) -> torch.Tensor:
         return torch.zeros(shape, dtype=dtype, pin_memory=pinned)
 
-    # Replays run v2 over partitions of at least min_size: 64 positions, or the share of
-    # the table width that keeps the captured grid within GRAPH_MAX_PARTITIONS items per
-    # row and GRAPH_MAX_ITEMS in all. Until the first update every row is one item.
+    # Replays run v2 over partitions of at least min_size (64 positions, or the share of the
+    # table width that keeps a row within GRAPH_MAX_PARTITIONS of them) and a grid of
+    # `capacity` work items: GRAPH_MAX_ITEMS, or one per row for a larger bucket. Until the
+    # first update every row is one item.
     max_length = max_blocks * block_size
-    per_row = max(1, min(GRAPH_MAX_PARTITIONS, GRAPH_MAX_ITEMS // num_requests))
-    min_size = max(GRAPH_MIN_PARTITION, -(-max_length // (64 * per_row)) * 64)
+    min_size = max(GRAPH_MIN_PARTITION, -(-max_length // (64 * GRAPH_MAX_PARTITIONS)) * 64)
     partitions = -(-max_length // min_size)
-    capacity = num_requests * partitions
-    staged_host = host((2 + 2 * capacity,), torch.int32)
+    capacity = max(num_requests, GRAPH_MAX_ITEMS)
+    staged_host = host((2 + num_requests + 2 * capacity,), torch.int32)
     staged_host[0], staged_host[1] = min_size, num_requests
-    staged_host[2:2 + 2 * num_requests:2] = torch.arange(num_requests, dtype=torch.int32)
+    work = 2 + num_requests
+    staged_host[work:work + 2 * num_requests:2] = torch.arange(num_requests, dtype=torch.int32)
     staging = HipGraphPlan(
         positions=host((num_requests,), torch.int32),
         slot_mapping=host((num_requests,), torch.int64),
@@ -1009,19 +1026,28 @@ def update_graph_metadata(
 
 
 def _stage_split(staging: HipGraphPlan, lengths: np.ndarray, block_size: int) -> int:
-    """Fill ``staging.staged_host`` with this step's partition size and work list (the
-    eager plan's choice, from sizes of ``staging.min_size`` up); returns the int32 words used."""
+    """Fill ``staging.staged_host`` with this step's partition size, the rows' first partial
+    slots and the work list (the eager plan's choice among sizes of ``staging.min_size`` up
+    whose list fits the capacity); returns the int32 words used."""
     kv_heads, group, kv_bytes = staging.head_shape or (8, 1, 2)
+    lengths = lengths.astype(np.int64)
     longest = int(lengths.max()) if lengths.size else 0
+    empty = int((lengths == 0).sum())
     split = choose_split(lengths.size, kv_heads, group, max(longest, 1), row_lengths=tuple(lengths.tolist()),
-                         kv_bytes=kv_bytes, min_size=staging.min_size)
+                         kv_bytes=kv_bytes, min_size=staging.min_size, max_items=staging.capacity - empty)
     # one partition per row when the model prefers v1
     size = split.partition_size or max(staging.min_size, -(-longest // 64) * 64)
     items = work_list(lengths, size)
-    assert items.size <= 2 * staging.capacity and -(-longest // size) <= staging.partitions
+    if items.size > 2 * staging.capacity:  # cannot happen for sizes the model returns; stay safe
+        size = max(staging.min_size, -(-longest // 64) * 64)
+        items = work_list(lengths, size)
+    counts = -(-lengths // size)
+    assert items.size <= 2 * staging.capacity and int(counts.max(initial=0)) <= staging.partitions
     host = staging.staged_host.numpy()
+    work = staging.work_offset
     host[0], host[1] = size, items.size // 2
-    host[2:2 + items.size] = items
-    return 2 + items.size
+    host[2:work] = np.cumsum(counts) - counts  # each row's first partial slot
+    host[work:work + items.size] = items
+    return work + items.size
 
 

@@ -146,14 +146,17 @@ size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads,
  * each once (the arrival count relies on it), and partition 0 of every row
  * with no context (that workgroup writes the row's zeros). With
  * NULL the grid covers every (row, partition < max_partitions). staged, if not
- * NULL, is device memory holding two int32, {partition size, item count}, that
- * the kernels read when they run, with work_items then read up to that count: a
- * graph replay follows the split and the work list a host wrote for its step.
- * The staged size is a multiple of 64 of at least partition_size (which
- * max_partitions and the workspace are sized for); n_work_items is then the
+ * NULL, is device memory holding 2 + n_rows int32, {partition size, item count,
+ * then each row's first partial slot}, that the kernels read when they run, with
+ * work_items then read up to that count: a graph replay follows the split and the
+ * work list a host wrote for its step. The staged size is a multiple of 64 of at
+ * least partition_size (which max_partitions covers); n_work_items is then the
  * list's capacity, which sizes the grid, and the staged count must not exceed it;
- * workgroups past the count return at once. The math the reference delegates
- * to flashinfer's split-KV decode and its plan-time schedule
+ * workgroups past the count return at once. Row r's partials take the slots from
+ * its staged offset on, one per partition that holds tokens (offsets: a prefix sum
+ * of ceil(length / size) over the rows), and the workspace holds n_work_items
+ * slots: ayk_paged_attention_v2_workspace_bytes(n_work_items, num_heads, head_dim, 1).
+ * The math the reference delegates to flashinfer's split-KV decode and its plan-time schedule
  * (python/ayaka/ops/backends/flashinfer/attention.py:221-251, :326).
  */
 int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const void* v_cache,

@@ -598,7 +598,7 @@ def test_graph_metadata_replays_match_eager_steps(heads: int, kv_heads: int, max
         # work list's; the same site and partition count fold in the same order
         staged_size = meta.plan.staged_partition_size
         assert staged_size % 64 == 0 and staged_size >= meta.plan.min_size
-        site = hip_attention.graph_merge_site(bucket, kv_heads, heads // kv_heads, meta.plan.partitions)
+        site = hip_attention.graph_merge_site(meta.plan.capacity, kv_heads, heads // kv_heads)
         same_shape = torch.empty_like(out)
         if meta.plan.partitions > 1:
             hip_attention.attend_with(q, buffers, eager_meta, same_shape, scale=dim**-0.5,
@@ -668,8 +668,9 @@ def test_c_abi_direct_call() -> None:
 @pytest.mark.parametrize("merge_flag", [8, 16], ids=["reduce-kernel", "in-kernel"])
 def test_c_abi_v2_follows_the_staged_split(merge_flag: int) -> None:
     # ayk_paged_attention_v2 with staged parameters (as a graph replay calls it): the grid covers
-    # a capacity of work items, the partition size and the item list are read from device memory.
-    # The result equals, bit for bit, the same call given that size and list directly.
+    # a capacity of work items; the partition size, the rows' first partial slots and the item
+    # list are read from device memory, and the partials are packed. The result equals, bit for
+    # bit, the same call given that size and list directly (partials at (row, head, partition)).
     s = build_scenario([(1, 700), (1, 1), (1, 0), (1, 300)], heads=8, kv_heads=2, head_dim=128,
                        block_size=16, mode="decode", seed=73)
     k, v, q = to_device(s.k_bits, "bf16"), to_device(s.v_bits, "bf16"), to_device(s.q_bits, "bf16")
@@ -686,17 +687,22 @@ def test_c_abi_v2_follows_the_staged_split(merge_flag: int) -> None:
     arrivals = torch.zeros(1024, dtype=torch.int32, device=DEV)
     common = (q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), width, lengths.data_ptr(), None, None,
               n_rows, 8, 2, 128, k.shape[0], 16, width, 0, 1, 1, ctypes.c_float(s.scale))
-    staged = torch.zeros(2 + 2 * capacity, dtype=torch.int32, device=DEV)
+    staged = torch.zeros(2 + n_rows + 2 * capacity, dtype=torch.int32, device=DEV)
+    work = 2 + n_rows
     for size in (256, 128, 704):
         items = hip_attention.work_list(s.lengths, size)
-        staged[:2 + items.size] = torch.tensor([size, items.size // 2, *items.tolist()], dtype=torch.int32)
+        counts = [-(-n // size) for n in s.lengths]
+        first = [sum(counts[:r]) for r in range(n_rows)]
+        staged[:work + items.size] = torch.tensor([size, items.size // 2, *first, *items.tolist()],
+                                                  dtype=torch.int32)
         direct = torch.from_numpy(items).to(DEV)
         outs = []
         for staged_call in (True, False):
             out = torch.full_like(q, float("nan"))
             if staged_call:
                 rc = lib.ayk_paged_attention_v2(out.data_ptr(), *common, min_size, max_partitions,
-                                                staged.data_ptr() + 8, capacity, staged.data_ptr(), scratch.data_ptr(),
+                                                staged.data_ptr() + 4 * work, capacity, staged.data_ptr(),
+                                                scratch.data_ptr(),
                                                 nbytes, arrivals.data_ptr(), merge_flag, stream)
             else:
                 rc = lib.ayk_paged_attention_v2(out.data_ptr(), *common, size, max_partitions, direct.data_ptr(),

@@ -108,25 +108,39 @@ def test_work_list_order_and_the_staged_graph_split() -> None:
         assert {tuple(x) for x in pairs.tolist()} == want and len(pairs) == len(want)
         sizes = [min(size, int(lengths[r]) - p * size) for r, p in pairs.tolist()]
         assert sizes == sorted(sizes, reverse=True)
-    # a bucket of 8 requests x 1024 blocks of 16: at least 16384 / 64 = 256 positions a partition
+    # a bucket of 8 requests x 1024 blocks of 16: partitions of 64 positions at least (256 per
+    # row), a grid of 2048 work items whose partials the scratch packs
     meta = hip_attention.graph_metadata(8, 1024, 16, torch.device("cpu"))
     plan = meta.plan
-    assert (plan.min_size, plan.partitions, plan.capacity) == (256, 64, 512)
-    assert plan.staged_host[:2].tolist() == [256, 8]
-    assert plan.staged_host[2:18:2].tolist() == list(range(8)) and plan.staged_host[3:18:2].tolist() == [0] * 8
+    assert (plan.min_size, plan.partitions, plan.capacity, plan.work_offset) == (64, 256, 2048, 10)
+    assert plan.staged_host[:10].tolist() == [64, 8] + [0] * 8
+    assert plan.staged_host[10:26:2].tolist() == list(range(8)) and plan.staged_host[11:26:2].tolist() == [0] * 8
     table = torch.arange(8 * 1024, dtype=torch.int32).reshape(8, 1024)
-    lengths = [16384, 9000, 0, 1, 4096, 2048, 100, 16000]
-    hip_attention.update_graph_metadata(meta, _ints(*lengths), table)
-    size, count = plan.staged_partition_size, int(plan.staged_host[1])
-    assert size % 64 == 0 and size >= plan.min_size and -(-max(lengths) // size) <= plan.partitions
-    assert plan.staged_host[2:2 + 2 * count].tolist() == hip_attention.work_list(lengths, size).tolist()
+
+    def check(lengths: list[int]) -> int:
+        hip_attention.update_graph_metadata(meta, _ints(*lengths), table)
+        size, count = plan.staged_partition_size, int(plan.staged_host[1])
+        assert size % 64 == 0 and size >= plan.min_size and -(-max(lengths) // size) <= plan.partitions
+        assert count <= plan.capacity
+        counts = [-(-n // size) for n in lengths]
+        assert plan.staged_host[2:10].tolist() == [sum(counts[:r]) for r in range(8)]  # first partial slots
+        assert plan.staged_host[10:10 + 2 * count].tolist() == hip_attention.work_list(lengths, size).tolist()
+        return size
+
+    check([16384, 9000, 0, 1, 4096, 2048, 100, 16000])
+    # a few long rows split as finely as an eager plan splits them
+    size = check([16384, 16384, 0, 0, 0, 0, 0, 0])
+    eager = hip_attention.choose_split(8, 8, 1, 16384, row_lengths=(16384, 16384, 0, 0, 0, 0, 0, 0))
+    assert size == eager.partition_size
     # all rows empty: one item per row, the minimum size
     hip_attention.update_graph_metadata(meta, _ints(*[0] * 8), table)
-    assert plan.staged_host[:2].tolist() == [256, 8]
-    # a short table: 64 positions at least; a large bucket: 2048 items at most
-    assert hip_attention.graph_metadata(2, 4, 16, torch.device("cpu")).plan.min_size == 64
-    big = hip_attention.graph_metadata(512, 2048, 16, torch.device("cpu")).plan
-    assert (big.min_size, big.partitions, big.capacity) == (8192, 4, 2048)
+    assert plan.staged_host[:2].tolist() == [64, 8]
+    # a large bucket: one item per row at least; sizes whose list would overflow it are left out
+    big = hip_attention.graph_metadata(4096, 64, 16, torch.device("cpu"))
+    assert (big.plan.min_size, big.plan.partitions, big.plan.capacity) == (64, 16, 4096)
+    hip_attention.update_graph_metadata(big, torch.full((4096,), 1024, dtype=torch.int32),
+                                        torch.zeros((4096, 64), dtype=torch.int32))
+    assert int(big.plan.staged_host[1]) <= 4096 and big.plan.staged_partition_size == 1024
 
 
 def test_graph_metadata_update_refusals() -> None:
