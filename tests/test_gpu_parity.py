@@ -531,17 +531,20 @@ def test_benchmark_configuration(index: int) -> None:
 # --- graph metadata and capture ---------------------------------------------------------------
 
 
-@pytest.mark.parametrize("heads,kv_heads,max_blocks,bucket,fp8",
-                         [(8, 2, 80, 4, False), (32, 8, 512, 16, False), (32, 8, 512, 16, True)])
+@pytest.mark.parametrize("heads,kv_heads,max_blocks,bucket,fp8,layout",
+                         [(8, 2, 80, 4, False, "nhd"), (8, 2, 80, 4, False, "hnd"), (32, 8, 512, 16, False, "nhd"),
+                          (32, 8, 512, 16, True, "nhd")])
 def test_graph_metadata_replays_match_eager_steps(heads: int, kv_heads: int, max_blocks: int, bucket: int,
-                                                  fp8: bool) -> None:
+                                                  fp8: bool, layout: str) -> None:
     rng = np.random.default_rng(61)
     dim, bs = 128, 16
     num_blocks = 1 + bucket * max_blocks
     cache_dtype = torch.float8_e4m3fn if fp8 else torch.bfloat16
-    k_cache = (torch.randn((num_blocks, bs, kv_heads, dim), device=DEV)).to(cache_dtype)
-    v_cache = (torch.randn((num_blocks, bs, kv_heads, dim), device=DEV)).to(cache_dtype)
-    buffers = KVBuffers(k_cache, v_cache, KVLayoutKind.NHD, FP8_E4M3_CODEC if fp8 else RAW_CODEC)
+    shape = (num_blocks, bs, kv_heads, dim) if layout == "nhd" else (num_blocks, kv_heads, bs, dim)
+    k_cache = (torch.randn(shape, device=DEV)).to(cache_dtype)
+    v_cache = (torch.randn(shape, device=DEV)).to(cache_dtype)
+    kind = KVLayoutKind.NHD if layout == "nhd" else KVLayoutKind.HND
+    buffers = KVBuffers(k_cache, v_cache, kind, FP8_E4M3_CODEC if fp8 else RAW_CODEC)
     perm = rng.permutation(np.arange(1, num_blocks)).reshape(bucket, max_blocks).astype(np.int32)
     meta = hip_attention.graph_metadata(bucket, max_blocks, bs, DEV)
     q = torch.zeros((bucket, heads, dim), dtype=torch.bfloat16, device=DEV)
