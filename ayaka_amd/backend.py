@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import logging
 import sys
+from collections import Counter
 from collections.abc import Callable, Mapping, Sequence
 from dataclasses import dataclass
 from types import MappingProxyType
@@ -96,21 +97,71 @@ def available_backends() -> tuple[BackendCaps, ...]:
     return tuple(caps for caps, _ in _registry.values())
 
 
-def _rejection(caps: BackendCaps, family: str, device: str, dtype: DType, cuda_graph: bool) -> str | None:
-    if family not in caps.families:
-        return _NOT_IMPLEMENTED
-    problems: list[str] = []
-    if sys.platform not in caps.platforms:
-        problems.append(f"does not run on {sys.platform}")
-    if device not in caps.devices:
-        problems.append(f"has no {device} support")
-    if dtype not in caps.dtypes:
-        problems.append(f"has no {dtype.label} support")
-    if family == "attention" and not caps.multi_row_attention:
-        problems.append("serves only one query row per request")
-    if cuda_graph and family not in caps.graph_safe:
-        problems.append("cannot run inside a CUDA graph")
-    return ", ".join(problems) or None
+def _shortfalls(caps: BackendCaps, family: str, device: str, dtype: DType, cuda_graph: bool) -> list[str]:
+    """Why ``caps`` cannot serve ``family`` here, in the reference's words (empty: it can)."""
+    needs = (
+        (sys.platform in caps.platforms, f"does not run on {sys.platform}"),
+        (device in caps.devices, f"has no {device} support"),
+        (dtype in caps.dtypes, f"has no {dtype.label} support"),
+        (family != "attention" or caps.multi_row_attention, "serves only one query row per request"),
+        (not cuda_graph or family in caps.graph_safe, "cannot run inside a CUDA graph"),
+    )
+    return [why for met, why in needs if not met]
+
+
+class _Candidates:
+    """The listed backends of one :func:`load_backend` call. A loader runs the first time its
+    backend is the best fit for some family, and at most once; its result (the families, or
+    why the backend is unavailable) serves every later family."""
+
+    def __init__(self, device: str, dtype: DType, cuda_graph: bool) -> None:
+        self.device, self.dtype, self.cuda_graph = device, dtype, cuda_graph
+        self.families: dict[str, Mapping[str, object]] = {}
+        self.unavailable: dict[str, str] = {}
+
+    def _load(self, name: str) -> str | None:
+        if name in self.families or name in self.unavailable:
+            return self.unavailable.get(name)
+        caps, loader = _registry[name]
+        try:
+            families = loader()
+        except CapabilityError as exc:
+            self.unavailable[name] = f"is unavailable ({exc.detail}; {exc.remedy})"
+            logger.warning("ops backend %r %s", name, self.unavailable[name])
+            return self.unavailable[name]
+        absent = sorted(caps.families - set(families))
+        if absent:
+            raise BackendError(
+                f"ops backend {name!r} declares {absent} but its loader did not return them",
+                context={"backend": name, "families": absent},
+            )
+        self.families[name] = families
+        return None
+
+    def verdict(self, name: str, family: str) -> str | None:
+        """None if ``name`` serves ``family``, else the reason it does not."""
+        caps = _registry[name][0]
+        if family not in caps.families:
+            return _NOT_IMPLEMENTED
+        shortfalls = _shortfalls(caps, family, self.device, self.dtype, self.cuda_graph)
+        return ", ".join(shortfalls) if shortfalls else self._load(name)
+
+
+def _check_names(names: Sequence[str]) -> None:
+    if isinstance(names, str):
+        raise TypeError("names must be a sequence of backend names, not one string")
+    if not names:
+        raise ConfigError(_CONFIG_PATH, "BACKEND_LIST_EMPTY", "at least one backend must be listed")
+    repeated = sorted(name for name, count in Counter(names).items() if count > 1)
+    if repeated:
+        raise ConfigError(_CONFIG_PATH, "BACKEND_DUPLICATE", f"listed more than once: {repeated}")
+    unknown = [name for name in names if name not in _registry]
+    if unknown:
+        raise ConfigError(
+            _CONFIG_PATH,
+            "BACKEND_UNKNOWN",
+            f"not registered: {unknown}; registered backends: {sorted(_registry)}",
+        )
 
 
 def load_backend(
@@ -124,78 +175,35 @@ def load_backend(
             why each listed backend was rejected).
         BackendError: A loader did not return a family its record declares.
     """
-    if isinstance(names, str):
-        raise TypeError("names must be a sequence of backend names, not one string")
-    if not names:
-        raise ConfigError(_CONFIG_PATH, "BACKEND_LIST_EMPTY", "at least one backend must be listed")
-    repeated = sorted({name for name in names if list(names).count(name) > 1})
-    if repeated:
-        raise ConfigError(_CONFIG_PATH, "BACKEND_DUPLICATE", f"listed more than once: {repeated}")
-    unknown = [name for name in names if name not in _registry]
-    if unknown:
-        raise ConfigError(
-            _CONFIG_PATH,
-            "BACKEND_UNKNOWN",
-            f"not registered: {unknown}; registered backends: {sorted(_registry)}",
-        )
-
-    loaded: dict[str, Mapping[str, object]] = {}
-    unavailable: dict[str, str] = {}
-    chosen: dict[str, object] = {}
+    _check_names(names)
+    candidates = _Candidates(device, dtype, cuda_graph)
     providers: dict[str, str] = {}
-    missing: dict[str, tuple[str, ...]] = {}
+    refusals: dict[str, tuple[str, ...]] = {}
     for family in FAMILIES:
-        rejections: list[str] = []
+        verdicts: list[str] = []
         for name in names:
-            caps, loader = _registry[name]
-            reason = _rejection(caps, family, device, dtype, cuda_graph)
-            if reason is None and name not in loaded and name not in unavailable:
-                try:
-                    families = loader()
-                except CapabilityError as exc:
-                    unavailable[name] = f"is unavailable ({exc.detail}; {exc.remedy})"
-                    logger.warning("ops backend %r %s", name, unavailable[name])
-                else:
-                    absent = sorted(caps.families - set(families))
-                    if absent:
-                        raise BackendError(
-                            f"ops backend {name!r} declares {absent} but its loader did not "
-                            "return them",
-                            context={"backend": name, "families": absent},
-                        )
-                    loaded[name] = families
-            if reason is None:
-                reason = unavailable.get(name)
-            if reason is None:
-                chosen[family] = loaded[name][family]
+            why = candidates.verdict(name, family)
+            if why is None:
                 providers[family] = name
                 break
-            rejections.append(f"{name} {reason}")
-        else:
-            missing[family] = tuple(rejections)
+            verdicts.append(f"{name} {why}")
+        if family not in providers:
+            refusals[family] = tuple(verdicts)
 
-    if missing:
-        details = "".join(f"\n  {fam}: {'; '.join(why)}" for fam, why in missing.items())
-        graph = " inside a CUDA graph" if cuda_graph else ""
+    if refusals:
+        lines = "".join(f"\n  {family}: {'; '.join(why)}" for family, why in refusals.items())
+        inside = " inside a CUDA graph" if cuda_graph else ""
         raise ConfigError(
             _CONFIG_PATH,
             "BACKEND_CAPABILITY_MISSING",
-            f"no backend in {list(names)} provides {', '.join(missing)} "
-            f"for device {device!r} and dtype {dtype.label}{graph}:{details}",
-            context={"missing": missing},
+            f"no backend in {list(names)} provides {', '.join(refusals)} "
+            f"for device {device!r} and dtype {dtype.label}{inside}:{lines}",
+            context={"missing": refusals},
         )
-    logger.info(
-        "ops backends for %s %s: %s",
-        device,
-        dtype.label,
-        ", ".join(f"{family}={name}" for family, name in providers.items()),
-    )
-    return OpsBackend(
-        kvcache=chosen["kvcache"],
-        attention=chosen["attention"],
-        providers=MappingProxyType(providers),
-        graph_safe=cuda_graph,
-    )
+    logger.info("ops backends for %s %s: %s", device, dtype.label,
+                ", ".join(f"{family}={name}" for family, name in providers.items()))
+    ops = {family: candidates.families[name][family] for family, name in providers.items()}
+    return OpsBackend(providers=MappingProxyType(providers), graph_safe=cuda_graph, **ops)
 
 
 def _load_hip() -> Mapping[str, object]:

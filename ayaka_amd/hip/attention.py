@@ -925,10 +925,17 @@ def graph_metadata(
             context={"op": "attention.graph_metadata"},
         )
     target = torch.device(device)
-    pinned = target.type == "cuda"
-
-    def host(shape: tuple[int, ...], dtype: torch.dtype) -> torch.Tensor:
-        return torch.zeros(shape, dtype=dtype, pin_memory=pinned)
+    # The records a replay reads at fixed addresses, each with a pinned host twin that
+    # update_graph_metadata fills (a decode step: one row per request, row n is request n).
+    records = {
+        "positions": ((num_requests,), torch.int32),
+        "slot_mapping": ((num_requests,), torch.int64),
+        "kv_lengths": ((num_requests,), torch.int32),
+        "block_table": ((num_requests, max_blocks), torch.int32),
+    }
+    fixed = {name: torch.zeros(shape, dtype=dtype, device=target) for name, (shape, dtype) in records.items()}
+    twins = {name: torch.zeros(shape, dtype=dtype, pin_memory=target.type == "cuda")
+             for name, (shape, dtype) in records.items()}
 
     # Replays run v2 over partitions of at least min_size (64 positions, or the share of the
     # table width that keeps a row within GRAPH_MAX_PARTITIONS of them) and a grid of
@@ -936,22 +943,18 @@ def graph_metadata(
     # first update every row is one item.
     max_length = max_blocks * block_size
     min_size = max(GRAPH_MIN_PARTITION, -(-max_length // (64 * GRAPH_MAX_PARTITIONS)) * 64)
-    partitions = -(-max_length // min_size)
     capacity = max(num_requests, GRAPH_MAX_ITEMS)
-    staged_host = host((2 + num_requests + 2 * capacity,), torch.int32)
-    staged_host[0], staged_host[1] = min_size, num_requests
     work = 2 + num_requests
+    staged_host = torch.zeros(work + 2 * capacity, dtype=torch.int32, pin_memory=target.type == "cuda")
+    staged_host[0], staged_host[1] = min_size, num_requests
     staged_host[work:work + 2 * num_requests:2] = torch.arange(num_requests, dtype=torch.int32)
     staging = HipGraphPlan(
-        positions=host((num_requests,), torch.int32),
-        slot_mapping=host((num_requests,), torch.int64),
-        kv_lengths=host((num_requests,), torch.int32),
-        block_table=host((num_requests, max_blocks), torch.int32),
+        **twins,
         max_blocks=max_blocks,
         staged_host=staged_host,
         staged=staged_host.to(target),
         min_size=min_size,
-        partitions=partitions,
+        partitions=-(-max_length // min_size),
         capacity=capacity,
     )
     return AttentionMetadata(
@@ -959,12 +962,21 @@ def graph_metadata(
         block_size=block_size,
         rows_per_request=torch.ones(num_requests, dtype=torch.int32, device=target),
         request_of_row=torch.arange(num_requests, dtype=torch.int32, device=target),
-        positions=torch.zeros(num_requests, dtype=torch.int32, device=target),
-        slot_mapping=torch.zeros(num_requests, dtype=torch.int64, device=target),
-        kv_lengths=torch.zeros(num_requests, dtype=torch.int32, device=target),
-        block_table=torch.zeros((num_requests, max_blocks), dtype=torch.int32, device=target),
         plan=staging,
+        **fixed,
     )
+
+
+def _require_host_ints(op: str, name: str, tensor: torch.Tensor, shape: tuple[int, ...]) -> np.ndarray:
+    """``tensor`` as a numpy view, if it is an int32 CPU tensor of ``shape`` (the message is the
+    reference's, ``torch/attention.py:341-352``)."""
+    if tuple(tensor.shape) != shape or tensor.dtype != torch.int32 or tensor.device.type != "cpu":
+        raise BackendError(
+            f"{op}: {name} must be an int32 CPU tensor of shape {list(shape)}, got "
+            f"{tensor.dtype} {list(tensor.shape)} on {tensor.device}",
+            context={"op": op, "argument": name},
+        )
+    return tensor.numpy()
 
 
 def update_graph_metadata(
@@ -972,9 +984,12 @@ def update_graph_metadata(
 ) -> None:
     """Write the next decode step into ``meta`` without waiting on the device.
 
-    Reference ``attention.py:308-374``: checks the host inputs, derives positions
-    and slots on the host, fills the pinned staging and queues asynchronous
-    copies on the current stream.
+    The contract of the reference's update (``attention.py:308-374``): int32 CPU inputs,
+    every length within the table, each request's newest token at position
+    ``length - 1`` and its slot read from the table (a padding request, length 0,
+    gets position and slot 0). Everything is computed on the host into the pinned
+    staging, together with the step's v2 split, and copied to the fixed device
+    records with asynchronous copies on the current stream.
     """
     op = "attention.update_graph_metadata"
     staging = meta.plan
@@ -984,45 +999,26 @@ def update_graph_metadata(
             f"{op}: meta was not made by this backend's graph_metadata",
             context={"op": op, "argument": "meta"},
         )
-    requests, max_blocks = staging.block_table.shape
-    for name, tensor, shape in (
-        ("kv_lengths", kv_lengths, (requests,)),
-        ("block_rows", block_rows, (requests, max_blocks)),
-    ):
-        if (
-            tuple(tensor.shape) != shape
-            or tensor.dtype != torch.int32
-            or tensor.device.type != "cpu"
-        ):
-            raise BackendError(
-                f"{op}: {name} must be an int32 CPU tensor of shape {list(shape)}, got "
-                f"{tensor.dtype} {list(tensor.shape)} on {tensor.device}",
-                context={"op": op, "argument": name},
-            )
+    requests, width = staging.block_table.shape
+    lens = _require_host_ints(op, "kv_lengths", kv_lengths, (requests,)).astype(np.int64)
+    rows = _require_host_ints(op, "block_rows", block_rows, (requests, width))
     block_size = meta.block_size
-    lengths = kv_lengths.long()
-    if bool((lengths < 0).any()) or bool((lengths > max_blocks * block_size).any()):
+    limit = width * block_size
+    if lens.size and (int(lens.min()) < 0 or int(lens.max()) > limit):
         raise BackendError(
-            f"{op}: every length must be in [0, {max_blocks * block_size}] for a table of "
-            f"{max_blocks} blocks of {block_size}",
+            f"{op}: every length must be in [0, {limit}] for a table of {width} blocks of {block_size}",
             context={"op": op, "argument": "kv_lengths"},
         )
-    real = lengths > 0
-    positions = torch.where(real, lengths - 1, 0)
-    block = block_rows.long().gather(1, (positions // block_size)[:, None])[:, 0]
-    staging.positions.copy_(positions)
-    staging.slot_mapping.copy_(torch.where(real, block * block_size + positions % block_size, 0))
-    staging.kv_lengths.copy_(kv_lengths)
-    staging.block_table.copy_(block_rows)
-    used = _stage_split(staging, kv_lengths.numpy(), block_size)
-    for device_tensor, host_tensor in (
-        (meta.positions, staging.positions),
-        (meta.slot_mapping, staging.slot_mapping),
-        (meta.kv_lengths, staging.kv_lengths),
-        (table, staging.block_table),
-        (staging.staged[:used], staging.staged_host[:used]),
-    ):
-        device_tensor.copy_(host_tensor, non_blocking=True)
+    newest = np.maximum(lens - 1, 0)
+    block = rows[np.arange(requests), newest // block_size].astype(np.int64)
+    staging.positions.numpy()[:] = newest
+    staging.slot_mapping.numpy()[:] = np.where(lens > 0, block * block_size + newest % block_size, 0)
+    staging.kv_lengths.numpy()[:] = lens
+    staging.block_table.numpy()[:] = rows
+    used = _stage_split(staging, lens, block_size)
+    for name in ("positions", "slot_mapping", "kv_lengths", "block_table"):
+        getattr(meta, name).copy_(getattr(staging, name), non_blocking=True)
+    staging.staged[:used].copy_(staging.staged_host[:used], non_blocking=True)
 
 
 def _stage_split(staging: HipGraphPlan, lengths: np.ndarray, block_size: int) -> int:
