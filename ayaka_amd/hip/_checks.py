@@ -26,6 +26,7 @@ __all__ = [
     "require_device",
     "require_index_tensor",
     "require_like",
+    "stream_handle",
 ]
 
 HEAD_DIMS = frozenset({64, 128, 256})
@@ -49,7 +50,20 @@ def dtype_name(dtype: torch.dtype) -> str:
 
 def capturing(tensor: torch.Tensor) -> bool:
     """Whether ``tensor``'s device is capturing a graph on the current stream."""
-    return tensor.is_cuda and torch.cuda.is_current_stream_capturing()
+    return tensor.is_cuda and torch._C._cuda_isCurrentStreamCapturing()
+
+
+# torch's raw handle of the current stream, without building a Stream object per call
+# (about 3 us of host time each): the ops launch once per layer and per call.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def stream_handle(device: torch.device) -> int:
+    """The HIP stream behind torch's current stream on ``device``: the ops launch there."""
+    if _raw_stream is None:
+        return torch.cuda.current_stream(device).cuda_stream
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return _raw_stream(index)
 
 
 def require_like(

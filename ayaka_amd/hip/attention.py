@@ -48,6 +48,7 @@ from ayaka_amd.hip._checks import (
     require_device,
     require_index_tensor,
     require_like,
+    stream_handle,
 )
 from ayaka_amd.kvcache import FP8_E4M3_CODEC, KVBuffers
 
@@ -797,7 +798,7 @@ def attend_with(
         raise BackendError(f"{op}: meta.block_table must be a contiguous int32 [B, max_blocks] tensor")
 
     lib = _lib.lib()
-    stream = torch.cuda.current_stream(device).cuda_stream
+    stream = stream_handle(device)
     if prefill is None:
         prefill = not decode and _wants_prefill_kernel(step)
     if prefill:

@@ -23,6 +23,7 @@ from ayaka_amd.hip._checks import (
     require_device,
     require_index_tensor,
     require_like,
+    stream_handle,
 )
 from ayaka_amd.kvcache import FP8_E4M3_CODEC, KVBuffers
 
@@ -37,7 +38,7 @@ def layout() -> KVLayoutKind:
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    return stream_handle(device)
 
 
 def _block_bytes(buffers: KVBuffers) -> int:
