@@ -34,22 +34,41 @@ __device__ __forceinline__ u32x4 load16(const uint16_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
-// Flat stream over one pool: 4 independent 16-byte loads per lane per step.
-template <bool NT>
+// Flat stream over one pool: U independent 16-byte loads per lane per step.
+template <bool NT, int U = 4>
 __global__ __launch_bounds__(256) void stream_probe(const uint16_t* src, size_t n16, uint32_t* sink) {
   uint32_t acc = 0;
-  const size_t stride = (size_t)gridDim.x * 256 * 4;
-  for (size_t base = (size_t)blockIdx.x * 256 * 4 + threadIdx.x; base < n16; base += stride) {
-    u32x4 a[4];
+  const size_t stride = (size_t)gridDim.x * 256 * U;
+  for (size_t base = (size_t)blockIdx.x * 256 * U + threadIdx.x; base < n16; base += stride) {
+    u32x4 a[U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       const size_t i = base + (size_t)u * 256;
       a[u] = load16<NT>(src + (i < n16 ? i : 0) * 8);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc ^= a[u].x ^ a[u].y ^ a[u].z ^ a[u].w;
+    for (int u = 0; u < U; ++u) acc ^= a[u].x ^ a[u].y ^ a[u].z ^ a[u].w;
   }
   if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
+// Flat stream straight into LDS (global_load_lds, 16 bytes per lane): each wave fills its
+// own 1 KB slice per load, 4 loads per step, and waits for them before the next step.
+__global__ __launch_bounds__(256) void stream_lds_probe(const uint16_t* src, size_t n16, uint32_t* sink) {
+  constexpr int U = 4;
+  __shared__ u32x4 buf[4][U][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const size_t stride = (size_t)gridDim.x * 256 * U;
+  for (size_t base = (size_t)blockIdx.x * 256 * U + wave * 64 * U; base < n16; base += stride) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const size_t i = base + (size_t)u * 64 + lane;
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src + (i < n16 ? i : 0) * 8),
+                                       (__attribute__((address_space(3))) void*)&buf[wave][u][0], 16, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+  }
+  if (buf[wave][0][lane].x == 0x9e3779b9u) sink[0] = 1;
 }
 
 // Paged reads. A workgroup covers `part` positions of one row; HEADS_PER_WG
@@ -133,19 +152,19 @@ int main() {
   const double pool_bytes = (double)elems * 2 * 2;
 
   std::printf("%-58s %10s %10s\n", "pattern", "us", "GB/s");
-  for (int nt = 0; nt < 2; ++nt) {
+  auto flat = [&](const char* name, auto kernel, int grid) {
     const float us = time_us([&] {
-      if (nt) {
-        stream_probe<true><<<2048, 256>>>(k, elems / 8, sink);
-        stream_probe<true><<<2048, 256>>>(v, elems / 8, sink);
-      } else {
-        stream_probe<false><<<2048, 256>>>(k, elems / 8, sink);
-        stream_probe<false><<<2048, 256>>>(v, elems / 8, sink);
-      }
+      kernel<<<grid, 256>>>(k, elems / 8, sink);
+      kernel<<<grid, 256>>>(v, elems / 8, sink);
     });
-    std::printf("%-58s %10.1f %10.0f\n", nt ? "flat stream, nontemporal loads" : "flat stream, plain loads", us,
-                pool_bytes / us / 1e3);
-  }
+    std::printf("%-58s %10.1f %10.0f\n", name, us, pool_bytes / us / 1e3);
+  };
+  flat("flat stream, plain loads", stream_probe<false>, 2048);
+  flat("flat stream, nontemporal loads", stream_probe<true>, 2048);
+  flat("flat stream, nontemporal, 8 loads per lane", stream_probe<true, 8>, 2048);
+  flat("flat stream, nontemporal, 8 loads per lane, 8192 wgs", stream_probe<true, 8>, 8192);
+  flat("flat stream, nontemporal, 16 loads per lane", stream_probe<true, 16>, 2048);
+  flat("flat stream, straight to LDS (global_load_lds)", stream_lds_probe, 2048);
   struct Case {
     const char* name;
     bool hnd;
