@@ -533,9 +533,10 @@ def test_benchmark_configuration(index: int) -> None:
 
 @pytest.mark.parametrize("heads,kv_heads,max_blocks,bucket,fp8,layout",
                          [(8, 2, 80, 4, False, "nhd"), (8, 2, 80, 4, False, "hnd"), (32, 8, 512, 16, False, "nhd"),
-                          (32, 8, 512, 16, True, "nhd")])
+                          (32, 8, 512, 16, True, "nhd"), (16, 8, 512, 16, False, "nhd")])
 def test_graph_metadata_replays_match_eager_steps(heads: int, kv_heads: int, max_blocks: int, bucket: int,
                                                   fp8: bool, layout: str) -> None:
+    # (16, 8): two query heads per key/value head, which the DPP q.k kernel serves
     rng = np.random.default_rng(61)
     dim, bs = 128, 16
     num_blocks = 1 + bucket * max_blocks
@@ -668,13 +669,14 @@ def test_c_abi_direct_call() -> None:
     assert rc == 2 and b"head_dim 96" in lib.ayk_last_error()
 
 
+@pytest.mark.parametrize("heads", [8, 4], ids=["mfma", "dpp"])
 @pytest.mark.parametrize("merge_flag", [8, 16], ids=["reduce-kernel", "in-kernel"])
-def test_c_abi_v2_follows_the_staged_split(merge_flag: int) -> None:
+def test_c_abi_v2_follows_the_staged_split(merge_flag: int, heads: int) -> None:
     # ayk_paged_attention_v2 with staged parameters (as a graph replay calls it): the grid covers
     # a capacity of work items; the partition size, the rows' first partial slots and the item
     # list are read from device memory, and the partials are packed. The result equals, bit for
     # bit, the same call given that size and list directly (partials at (row, head, partition)).
-    s = build_scenario([(1, 700), (1, 1), (1, 0), (1, 300)], heads=8, kv_heads=2, head_dim=128,
+    s = build_scenario([(1, 700), (1, 1), (1, 0), (1, 300)], heads=heads, kv_heads=2, head_dim=128,
                        block_size=16, mode="decode", seed=73)
     k, v, q = to_device(s.k_bits, "bf16"), to_device(s.v_bits, "bf16"), to_device(s.q_bits, "bf16")
     table = torch.from_numpy(s.table.astype(np.int32)).to(DEV)
@@ -685,11 +687,11 @@ def test_c_abi_v2_follows_the_staged_split(merge_flag: int) -> None:
     min_size = 64
     max_partitions = -(-width * 16 // min_size)
     capacity = n_rows * max_partitions
-    nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, 8, 128, max_partitions)
+    nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, 128, max_partitions)
     scratch = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
     arrivals = torch.zeros(1024, dtype=torch.int32, device=DEV)
     common = (q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), width, lengths.data_ptr(), None, None,
-              n_rows, 8, 2, 128, k.shape[0], 16, width, 0, 1, 1, ctypes.c_float(s.scale))
+              n_rows, heads, 2, 128, k.shape[0], 16, width, 0, 1, 1, ctypes.c_float(s.scale))
     staged = torch.zeros(2 + n_rows + 2 * capacity, dtype=torch.int32, device=DEV)
     work = 2 + n_rows
     for size in (256, 128, 704):
