@@ -10,7 +10,8 @@
 // pairs of one request and one key/value head -- the TILE_PAIRS / G consecutive
 // rows of the request whose G query heads read that key/value head. Each wave
 // owns PT groups of 16 pairs. The context streams through LDS in chunks of 64
-// positions, loaded once per tile, cooperatively, one chunk ahead in registers.
+// positions (32 at head_dim 256 with 1 or 2 waves per pair group), loaded once
+// per tile, cooperatively, one chunk ahead in registers.
 // A launch with partitions (p.part_o set) gives each tile one workgroup per
 // partition of p.partition_size positions (a multiple of 64); a row's partitions
 // store v2 partials (the output itself when the row has one partition) for
@@ -77,7 +78,10 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   constexpr int PT = D == 256 ? 1 : 2;          // 16-pair groups per wave
   constexpr int PGROUPS = kPrefillWaves / PS;   // waves with distinct pairs
   constexpr int TILE_PAIRS = prefill_tile_pairs(D) / PS;
-  constexpr int CH = 64;                        // positions per chunk
+  // Positions per chunk: 64, or 32 at head_dim 256 with 1 or 2 waves per pair group, where a
+  // 64-position stage (133 KB of LDS) and its load registers left one wave per SIMD; 32 fit
+  // two workgroups per CU without spills (quarter tiles need 16 positions per wave: 64).
+  constexpr int CH = D == 256 && PS <= 2 ? 32 : 64;
   constexpr int PTL = CH / 16;                  // 16-position tiles per chunk
   constexpr int PTL_W = PTL / PS;               // 16-position tiles per chunk of one wave
   constexpr int KS = D / 32;                    // q.k k-steps

@@ -154,6 +154,7 @@ MULTI_ROW_WORKLOADS = [
     (4, 512, 4096, 32, 8, 64, "fp16"),   # Llama-3.2-1B shape (D 64, fp16)
     (4, 512, 4096, 32, 8, 128, "bf16", "fp8_e4m3"),  # the first workload over fp8 caches
     (32, 4, 4096, 32, 8, 128, "bf16", "fp8_e4m3"),   # verify windows over fp8 caches
+    (4, 512, 4096, 16, 8, 256, "bf16"),  # Gemma-2-9B shape (head_dim 256)
 ]
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
