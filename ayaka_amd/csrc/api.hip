@@ -207,7 +207,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
 
 extern "C" {
 
-int ayk_abi_version(void) { return 10; }
+int ayk_abi_version(void) { return 11; }
 
 int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 
@@ -397,6 +397,63 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   hipError_t err = ayk::launch_prefill(p, tiles, n_tiles, head_dim, dtype == AYK_DTYPE_BF16,
                                        kv_dtype == AYK_DTYPE_FP8_E4M3, waves_per_group, s);
   if (err == hipSuccess) err = ayk::launch_row_reduce(p, head_dim, dtype == AYK_DTYPE_BF16, s);
+  return launched(err, op);
+}
+
+int ayk_paged_attention_windows(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
+                                const int32_t* request_of_row, const int32_t* positions, const int32_t* tiles,
+                                int32_t n_tiles, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t max_blocks,
+                                int32_t layout, int32_t dtype, int32_t kv_dtype, float scale, int32_t partition_size,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  const char* op = "ayk_paged_attention_windows";
+  if (!request_of_row || !positions)
+    return fail(AYK_ERR_ARGUMENT, "%s: request_of_row and positions are required", op);
+  AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
+             kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
+             head_dim,  num_blocks, block_size, max_blocks, layout,      dtype,       kv_dtype, scale};
+  ayk::AttnParams p;
+  int gc = 0;
+  const int rc = prepare(op, c, p, gc);
+  if (rc != AYK_OK) return rc;
+  if (p.group > 16)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: %d query heads per key/value head exceed a window's 16 columns", op,
+                p.group);
+  if (n_tiles < 0 || (n_tiles > 0 && !tiles))
+    return fail(AYK_ERR_ARGUMENT, "%s: %d tiles at %p", op, n_tiles, (const void*)tiles);
+  if ((int64_t)n_tiles * num_kv_heads > INT32_MAX)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: %d tiles x %d key/value heads exceed one launch", op, n_tiles,
+                num_kv_heads);
+  if (partition_size < 0 || partition_size % 64 != 0)
+    return fail(AYK_ERR_ARGUMENT, "%s: partition_size %d is not 0 or a positive multiple of 64", op,
+                partition_size);
+  if (n_tiles == 0 || n_rows == 0) return ok();
+  // one wave per key/value head, its 16 columns the tile's (row, query head) pairs
+  p.head_chunks = 1;
+  p.num_virtual_heads = num_kv_heads;
+  p.work = tiles;
+  p.n_work = n_tiles;
+  p.arrivals = nullptr;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool bf16 = dtype == AYK_DTYPE_BF16, kv8 = kv_dtype == AYK_DTYPE_FP8_E4M3;
+  if (partition_size == 0) return launched(ayk::launch_window_mfma(p, head_dim, bf16, false, kv8, s), op);
+  const int64_t max_partitions = ((int64_t)p.max_len + partition_size - 1) / partition_size;
+  if (max_partitions < 1 || max_partitions > 65535)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: %lld partitions of %d positions per row are not in [1, 65535]", op,
+                (long long)max_partitions, partition_size);
+  const size_t need = ayk_paged_attention_v2_workspace_bytes(n_rows, num_heads, head_dim, (int32_t)max_partitions);
+  if (!workspace || workspace_bytes < need)
+    return fail(AYK_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", op, workspace_bytes, need);
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+    return fail(AYK_ERR_ARGUMENT, "%s: workspace is not 16-byte aligned", op);
+  const size_t parts = (size_t)n_rows * num_heads * max_partitions;
+  p.part_o = static_cast<float*>(workspace);
+  p.part_ml = p.part_o + parts * head_dim;
+  p.partition_size = partition_size;
+  p.max_partitions = (int32_t)max_partitions;
+  hipError_t err = ayk::launch_window_mfma(p, head_dim, bf16, true, kv8, s);
+  if (err == hipSuccess) err = ayk::launch_row_reduce(p, head_dim, bf16, s);
   return launched(err, op);
 }
 

@@ -58,6 +58,9 @@ hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int heads_pe
 int prefill_tile_pairs_for(int head_dim);
 hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool bf16, bool kv8,
                           int waves_per_group, hipStream_t stream);
+// Window launch of the decode kernel: p.work holds p.n_work tiles of the multi-row tile list
+// (first row, rows, request, partition) of at most 16 / group rows; p.head_chunks 1.
+hipError_t launch_window_mfma(const AttnParams& p, int head_dim, bool bf16, bool split, bool kv8, hipStream_t stream);
 // The v2 log-sum-exp merge of the partitions of every (row, head); `compute_units` of the
 // device sets how many partition slots each pair gets.
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, int compute_units,

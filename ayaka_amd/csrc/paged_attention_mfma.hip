@@ -54,7 +54,13 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int D, int GC, bool BF16, bool SPLIT, bool KV8>
+// WIN: a window launch (verify windows, short chunks). A work item is a tile of the
+// multi-row tile list, p.work[4 * item] = (first row, rows, request, partition), of at most
+// 16 / group rows of one request; a wave serves one key/value head and its 16 MFMA
+// columns are the tile's (row, query head) pairs, column mt = row mt / group, head
+// mt % group, each masked at its own row's position. The context is read once for all
+// the tile's rows. Partials (split launches) are merged per row by row_reduce_kernel.
+template <int D, int GC, bool BF16, bool SPLIT, bool KV8, bool WIN = false>
 __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel(const AttnParams p) {
   constexpr int MT = 16;            // tokens per MFMA tile
   // Tiles per chunk, so that a wave keeps about as many bytes in flight as a
@@ -84,9 +90,18 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   const int threads = blockDim.x;
   const int waves = threads / kWave;
   const int groups = (p.num_virtual_heads + waves - 1) / waves;
-  const WgCoord wg = wg_coord(p, groups, SPLIT);
-  if (wg.row < 0) return;  // past the staged work items (uniform per workgroup)
-  const int row = wg.row;
+  WgCoord wg;
+  int win_first = 0, win_rows = 0;  // WIN: the tile's rows
+  if constexpr (WIN) {
+    const int item = blockIdx.x / groups;
+    win_first = p.work[4 * item];
+    win_rows = p.work[4 * item + 1];
+    wg = WgCoord{p.work[4 * item + 2], (int)(blockIdx.x % groups), p.work[4 * item + 3]};
+  } else {
+    wg = wg_coord(p, groups, SPLIT);
+    if (wg.row < 0) return;  // past the staged work items (uniform per workgroup)
+  }
+  const int row = wg.row;  // WIN: the request
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
   const int vh = wg.group * waves + wave;
@@ -103,11 +118,41 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   auto key_slot = [](int token, int piece) { return token * CPT + (piece ^ (token & (CPT - 1))); };
 
   int req, len;
-  row_context(p, row, req, len);
+  int win_lim = 0;        // WIN: the last position column mt's row sees
+  bool win_col = false;   // WIN: column mt is a (row, head) pair of the tile
+  int win_row = 0, win_head = 0;
+  if constexpr (WIN) {
+    req = row;
+    len = max(0, min(p.kv_lengths[req], p.max_len));
+    const int rr = mt / p.group;
+    win_col = active && rr < win_rows;
+    win_row = win_first + min(rr, win_rows - 1);
+    win_head = kvh * p.group + mt % p.group;
+    win_lim = len > 0 ? min(p.positions[win_row], len - 1) : 0;
+    // the tile's last row sees the most; nothing past it is read
+    if (len > 0) len = min(len, p.positions[win_first + win_rows - 1] + 1);
+  } else {
+    row_context(p, row, req, len);
+  }
   int t_begin = 0, t_end = len;
   const int psize = SPLIT ? partition_size_of(p) : 0;
   const int np = SPLIT ? (len > 0 ? (len - 1) / psize + 1 : 0) : 1;  // partitions with tokens
-  if constexpr (SPLIT) {
+  if constexpr (WIN) {
+    if (len == 0 || (SPLIT && wg.part * psize >= len)) {
+      // a padding request's rows are zero (partition 0 writes them); an empty partition: nothing
+      if (len == 0 && (!SPLIT || wg.part == 0) && win_col) {
+        f32x4 zero[DT];
+#pragma unroll
+        for (int t = 0; t < DT; ++t) zero[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        store_head_t<D, BF16, false>(p, win_row, 0, 1, win_head, mq, zero, kNoScore, 0.f);
+      }
+      return;
+    }
+    if constexpr (SPLIT) {
+      t_begin = wg.part * psize;
+      t_end = min(len, t_begin + psize);
+    }
+  } else if constexpr (SPLIT) {
     t_begin = wg.part * psize;
     t_end = min(len, t_begin + psize);
     if (t_begin >= t_end) {  // only partitions that hold tokens are merged
@@ -121,11 +166,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
 
   // q as the MFMA B operand: head mt (zero columns past the group), k-slice mq of step s.
   u32x4 qb[KS];
+  const bool q_col = WIN ? win_col : (active && mt < GC);
+  const int64_t q_at = WIN ? (int64_t)win_row * p.num_heads + win_head : (int64_t)row * p.num_heads + h0 + mt;
 #pragma unroll
   for (int s = 0; s < KS; ++s)
-    qb[s] = (active && mt < GC)
-                ? *reinterpret_cast<const u32x4*>(p.q + ((int64_t)row * p.num_heads + h0 + mt) * D + s * 32 + mq * 8)
-                : u32x4{0u, 0u, 0u, 0u};
+    qb[s] = q_col ? *reinterpret_cast<const u32x4*>(p.q + q_at * D + s * 32 + mq * 8) : u32x4{0u, 0u, 0u, 0u};
 
   float m_h = kNoScore;  // running max of head mt (same in its 4 lanes)
   float l_h = 0.f;       // this lane's share of head mt's weight sum
@@ -175,7 +220,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           sc[i] = acc[i] * scale_log2;
-          if (mt >= GC || (tail && tb + 4 * mq + i >= s1)) sc[i] = -INFINITY;
+          if (WIN ? (!win_col || tb + 4 * mq + i > win_lim) : mt >= GC) sc[i] = -INFINITY;
+          if (tail && tb + 4 * mq + i >= s1) sc[i] = -INFINITY;
         }
         float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         mx = fmaxf(mx, __shfl_xor(mx, 16));
@@ -248,9 +294,16 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     // Head mt's weight sum over the wave's 4 token groups (its lanes share m_h).
     l_h += __shfl_xor(l_h, 16);
     l_h += __shfl_xor(l_h, 32);
-    if (mt < GC) store_head_t<D, BF16, SPLIT>(p, row, wg.part, np, h0 + mt, mq, o, m_h, l_h);
+    if constexpr (WIN) {
+      // the row sees positions [0, win_lim]: partitions past it hold nothing of it
+      const int np_row = SPLIT ? win_lim / psize + 1 : 1;
+      if (win_col && wg.part < np_row)
+        store_head_t<D, BF16, SPLIT>(p, win_row, wg.part, np_row, win_head, mq, o, m_h, l_h);
+    } else if (mt < GC) {
+      store_head_t<D, BF16, SPLIT>(p, row, wg.part, np, h0 + mt, mq, o, m_h, l_h);
+    }
   }
-  if constexpr (SPLIT) {
+  if constexpr (SPLIT && !WIN) {
     if (np > 1 && p.arrivals) {
       const int vh_lo = wg.group * waves;
       const int vh_hi = min(p.num_virtual_heads, vh_lo + waves);
@@ -294,6 +347,40 @@ static hipError_t launch_mfma_d(const AttnParams& p, int gc, bool bf16, bool spl
                        : launch_mfma_gc<D, false, true>(p, gc, split, stream);
   return bf16 ? launch_mfma_gc<D, true, false>(p, gc, split, stream)
               : launch_mfma_gc<D, false, false>(p, gc, split, stream);
+}
+
+template <int D, bool BF16, bool KV8>
+static hipError_t launch_window_typed(const AttnParams& p, bool split, hipStream_t stream) {
+  // one wave per key/value head, up to kMaxWaves per workgroup; 16 MFMA columns per wave
+  const int per_wg = p.num_virtual_heads < kMaxWaves ? p.num_virtual_heads : kMaxWaves;
+  const int groups = (p.num_virtual_heads + per_wg - 1) / per_wg;
+  const dim3 grid((unsigned)((int64_t)p.n_work * groups)), block(per_wg * kWave);
+  if (split)
+    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, 16, BF16, true, KV8, true>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((paged_attention_mfma_kernel<D, 16, BF16, false, KV8, true>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_window_mfma(const AttnParams& p, int head_dim, bool bf16, bool split, bool kv8, hipStream_t stream) {
+  switch (head_dim) {
+    case 64:
+      if (kv8) return bf16 ? launch_window_typed<64, true, true>(p, split, stream)
+                           : launch_window_typed<64, false, true>(p, split, stream);
+      return bf16 ? launch_window_typed<64, true, false>(p, split, stream)
+                  : launch_window_typed<64, false, false>(p, split, stream);
+    case 128:
+      if (kv8) return bf16 ? launch_window_typed<128, true, true>(p, split, stream)
+                           : launch_window_typed<128, false, true>(p, split, stream);
+      return bf16 ? launch_window_typed<128, true, false>(p, split, stream)
+                  : launch_window_typed<128, false, false>(p, split, stream);
+    case 256:
+      if (kv8) return bf16 ? launch_window_typed<256, true, true>(p, split, stream)
+                           : launch_window_typed<256, false, true>(p, split, stream);
+      return bf16 ? launch_window_typed<256, true, false>(p, split, stream)
+                  : launch_window_typed<256, false, false>(p, split, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_attention_mfma(const AttnParams& p, int head_dim, int gc, bool bf16, bool split, bool kv8,

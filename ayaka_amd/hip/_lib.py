@@ -17,7 +17,7 @@ from ayaka_amd.errors import BackendError, CapabilityError
 __all__ = ["ABI_VERSION", "EXPORTS", "LIB_PATH", "check", "lib"]
 
 LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libayaka_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -54,6 +54,11 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I32, _I32, _I32,
          _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P, _SZ, _P],
+    ),
+    "ayk_paged_attention_windows": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P,
+         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P, _SZ, _P],
     ),
     "ayk_gather_blocks": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I64, _I32, _I64, _P]),
     "ayk_copy_blocks": (ctypes.c_int, [_P, _P, _P, _P, _I32, _I64, _I32, _I64, _P]),

@@ -199,6 +199,28 @@ class HipAttentionPlan:
             self.splits[key] = found
         return found
 
+    def window_pairs(self, group: int) -> int:
+        """(row, query head) pairs of a window tile (:func:`attend_with`'s ``window``):
+        as many rows of a request as fit the decode kernel's 16 matrix-core columns, 0 when
+        a request's rows do not fit one tile (or a group is wider than 16)."""
+        if group > 16:
+            return 0
+        rows = 16 // group
+        return rows * group if all(count <= rows for count in self.rows) else 0
+
+    def window_split(self, num_kv_heads: int, group: int, kv_bytes: int = 2) -> int:
+        """Partition size (0: none) of the step's window launch: the decode kernel's split
+        model (:func:`choose_split`) over the tiles' contexts, one workgroup per tile,
+        partition and 8 key/value heads; chosen once for every layer."""
+        key = ("window", num_kv_heads, group, kv_bytes)
+        found = self.splits.get(key)
+        if found is None:
+            lengths = tuple(g[0] for g in self.prefill_groups(group, self.window_pairs(group)))
+            found = choose_split(len(lengths), num_kv_heads, 1, max(lengths, default=0), row_lengths=lengths,
+                                 kv_bytes=kv_bytes).partition_size
+            self.splits[key] = found
+        return found
+
     def prefill_tiles(self, group: int, pairs: int, partition_size: int, device: torch.device,
                       capture: bool = False) -> torch.Tensor:
         """(first row, row count, request, partition) quadruples for the multi-row kernel.
@@ -570,6 +592,9 @@ PREFILL_STREAM_BYTES_PER_US = 7.0e6
 #: Rate (bytes per us) at which partials are written and read back, and the reduce launch.
 PREFILL_PARTIALS_BYTES_PER_US = 3.0e6
 PREFILL_REDUCE_US = 2.0
+#: Whether steps whose requests' rows all fit one window tile run on the decode kernel's window
+#: launch (``ayk_paged_attention_windows``) rather than the multi-row kernel.
+WINDOWS = True
 #: Partition sizes a multi-row launch chooses from.
 PREFILL_PARTITION_CANDIDATES = (128, 256, 512, 1024, 2048, 4096)
 
@@ -717,6 +742,7 @@ def attend_with(
     prefill: bool | None = None,
     merge: str | None = None,
     tile_pairs: int | None = None,
+    window: bool | None = None,
 ) -> None:
     """:func:`attend` with the launch chosen by the caller.
 
@@ -801,6 +827,13 @@ def attend_with(
     stream = stream_handle(device)
     if prefill is None:
         prefill = not decode and _wants_prefill_kernel(step)
+    if prefill and isinstance(step, HipAttentionPlan):
+        group = heads // kv_heads
+        if window is None:
+            window = tile_pairs is None and WINDOWS and step.window_pairs(group) > 0
+        if window:
+            _attend_windows(op, q, buffers, meta, out, step, scale, partitions, partition_size, stream)
+            return
     if prefill:
         if not isinstance(step, HipAttentionPlan):
             raise BackendError(f"{op}: the multi-row kernel needs a planned step", context={"op": op})
@@ -911,6 +944,50 @@ def attend_with(
         lib.ayk_paged_attention_v2(
             *common, partition_size, partitions, work, n_work, staged.data_ptr() if staged is not None else 0,
             scratch.data_ptr(), scratch.numel(), arrivals.data_ptr(), flags, stream,
+        ),
+    )
+
+
+def _attend_windows(op: str, q: torch.Tensor, buffers: KVBuffers, meta: AttentionMetadata, out: torch.Tensor,
+                    step: HipAttentionPlan, scale: float, partitions: int | None, partition_size: int | None,
+                    stream: int) -> None:
+    """A step of few rows per request on the decode kernel (``ayk_paged_attention_windows``):
+    one tile per request, its (row, query head) pairs the kernel's 16 matrix-core columns."""
+    heads, kv_heads = q.shape[1], buffers.num_kv_heads
+    group = heads // kv_heads
+    pairs = step.window_pairs(group)
+    if not pairs:
+        raise BackendError(
+            f"{op}: a window tile holds 16 (row, query head) pairs; this step has a request of more "
+            f"rows than {16 // group if group <= 16 else 0} at {group} query heads per key/value head",
+            context={"op": op, "argument": "meta"},
+        )
+    kv_bytes = 1 if buffers.codec == FP8_E4M3_CODEC else 2
+    if partitions == 0:
+        size = 0
+    elif partition_size is not None:
+        size = partition_size
+    else:
+        size = step.window_split(kv_heads, group, kv_bytes)
+    device = buffers.k.device
+    tiles = step.prefill_tiles(group, pairs, size, device, capturing(q))
+    table = meta.block_table
+    n_rows = meta.request_of_row.shape[0]
+    lib = _lib.lib()
+    scratch, nbytes = None, 0
+    if size:
+        max_partitions = -(-table.shape[1] * buffers.block_size // size)
+        nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, max_partitions)
+        scratch = _workspace(op, device, nbytes, capturing(q))
+    _lib.check(
+        op,
+        lib.ayk_paged_attention_windows(
+            out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),
+            table.stride(0), meta.kv_lengths.data_ptr(), meta.request_of_row.data_ptr(), meta.positions.data_ptr(),
+            tiles.data_ptr(), tiles.numel() // 4, n_rows, heads, kv_heads, buffers.head_dim, buffers.num_blocks,
+            buffers.block_size, table.shape[1], _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype],
+            _kv_code(buffers, q.dtype), float(scale), size, scratch.data_ptr() if scratch is not None else 0,
+            scratch.numel() if scratch is not None else 0, stream,
         ),
     )
 

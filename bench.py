@@ -160,7 +160,9 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def multi_row(args) -> int:
-    """Time the multi-row kernel and, beside it, the same step through the per-row decode kernels."""
+    """Time a multi-row step as the library launches it (the multi-row kernel, or the decode kernel's
+    window launch when every request's rows fit one 16-column tile) and, beside it, the same
+    step through the per-row decode kernels and through the multi-row kernel."""
     import torch
 
     from ayaka_amd.enums import ForwardMode, KVLayoutKind
@@ -190,10 +192,19 @@ def multi_row(args) -> int:
         scale = dim ** -0.5
         kernel = time_calls(lambda: hip_attention.attend_with(q, buffers, meta, out, scale=scale, partitions=None,
                                                               prefill=True), args.steps, args.warmup)
-        pairs, size = meta.plan.prefill_launch(kv_heads, heads // kv_heads, dim, 1 if codec == FP8_E4M3_CODEC else 2)
+        kv_code = 1 if codec == FP8_E4M3_CODEC else 2
+        window = hip_attention.WINDOWS and meta.plan.window_pairs(heads // kv_heads) > 0
+        if window:
+            pairs, size = meta.plan.window_pairs(heads // kv_heads), meta.plan.window_split(kv_heads, heads // kv_heads,
+                                                                                           kv_code)
+        else:
+            pairs, size = meta.plan.prefill_launch(kv_heads, heads // kv_heads, dim, kv_code)
         unsplit = kernel if not size else time_calls(
             lambda: hip_attention.attend_with(q, buffers, meta, per_row, scale=scale, partitions=0, prefill=True),
             args.steps, args.warmup)
+        multi_row_kernel = kernel if not window else time_calls(
+            lambda: hip_attention.attend_with(q, buffers, meta, per_row, scale=scale, partitions=None, prefill=True,
+                                              window=False), args.steps, args.warmup)
         old = time_calls(lambda: hip_attention.attend_with(q, buffers, meta, per_row, scale=scale, partitions=None,
                                                            prefill=False), 3, 1, repeats=1)
         torch.cuda.synchronize()
@@ -206,9 +217,11 @@ def multi_row(args) -> int:
             "workload": f"{requests} requests x {rows} rows over {context} positions, Hq {heads}, Hkv {kv_heads}, "
                         f"D {dim}, {dtype_name}, block {bs}" + (", fp8 e4m3 cache" if codec == FP8_E4M3_CODEC else ""),
             "us_per_call": round(us, 2),
+            "launch": "windows" if window else "multi-row",
             "tile_pairs": pairs,
             "partition_size": size,
             "unsplit_us": round(unsplit["median_us"], 2),
+            "multi_row_kernel_us": round(multi_row_kernel["median_us"], 2),
             "tflops": round(flops / us / 1e6, 1),
             "mfma_fraction": round(flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4),
             "kv_gbs": round(kv_bytes / us / 1e3, 1),

@@ -211,6 +211,26 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
                       size_t workspace_bytes, void* stream);
 
 /*
+ * Attention for rows of few per request (verify windows, short chunks), on the decode
+ * kernel: each tile of the multi-row tile list (int32 quadruples (first row, rows,
+ * request, partition), as for ayk_paged_prefill, with at most 16 / (num_heads /
+ * num_kv_heads) rows each) is one work item; a wave serves one key/value head and its
+ * 16 matrix-core columns are the tile's (row, query head) pairs, each row masked at its
+ * own position, so a request's context is streamed once for all the tile's rows.
+ * partition_size 0 covers each tile's context in one workgroup; otherwise tiles carry
+ * partitions of that size (a multiple of 64) and the rows spanning several are merged as
+ * in ayk_paged_prefill (same workspace). The multi-row rule of the reference
+ * (python/ayaka/ops/backends/torch/attention.py:209-234), as ayk_paged_prefill.
+ */
+int ayk_paged_attention_windows(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
+                                const int32_t* request_of_row, const int32_t* positions, const int32_t* tiles,
+                                int32_t n_tiles, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t max_blocks,
+                                int32_t layout, int32_t dtype, int32_t kv_dtype, float scale, int32_t partition_size,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Whole-block copies of both caches; block_bytes is the size of one block of
  * one cache (block_size * num_kv_heads * head_dim * elem_bytes), the same in
  * either layout. Ids are int64 when ids_are_64bit, else int32.

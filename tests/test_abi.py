@@ -21,7 +21,7 @@ def declared() -> list[str]:
 
 def test_every_declared_function_is_exported_and_bound() -> None:
     names = declared()
-    assert len(names) == 12
+    assert len(names) == 13
     lib = _lib.lib()
     for name in names:
         assert hasattr(lib, name), name
@@ -95,6 +95,14 @@ def test_v2_and_store_refusals() -> None:
                                      ctypes.c_float(1.0), size, 1, workspace, None)
     assert prefill(100) == 1 and b"tile_pairs 100 is not 128, 64 or 32" in lib.ayk_last_error()
     assert prefill(16) == 1
+    # the window entry: positions required; more than 16 query heads per key/value head; a
+    # partition size that is not a multiple of 64
+    def windows(heads: int, positions: object = 1, size: int = 0) -> int:
+        return lib.ayk_paged_attention_windows(1, 1, 1, 1, 1, 4, 1, 1, positions, 1, 2, 3, heads, 1, 128, 10, 16, 4,
+                                               0, 1, 1, ctypes.c_float(1.0), size, None, 0, None)
+    assert windows(8, positions=None) == 1 and b"positions are required" in lib.ayk_last_error()
+    assert windows(32) == 2 and b"exceed a window's 16 columns" in lib.ayk_last_error()
+    assert windows(8, size=96) == 1 and b"multiple of 64" in lib.ayk_last_error()
     assert prefill(32, size=96) == 1 and b"multiple of 64" in lib.ayk_last_error()
     assert prefill(64, size=64, workspace=16) == 4 and b"workspace" in lib.ayk_last_error()
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 3, None) == 2

@@ -192,11 +192,31 @@ PREFILL_CASES = [
 def test_multi_row_kernel(dtype: str, heads: int, kv_heads: int, head_dim: int, name: str, steps: list) -> None:
     s = build_scenario(steps, dtype=dtype, heads=heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16,
                        mode="mixed", seed=67, spare_blocks=2)
-    out = run_attention(s, None, None, True)
+    out = run_attention(s, None, None, True, window=False)
     assert_parity(out, s.expected(np.float64), dtype, f"prefill/{name}")
     padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
     if padding_rows:
         assert torch.count_nonzero(out[padding_rows]) == 0
+
+
+@pytest.mark.parametrize("size", [0, 64, 512, None])
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(8, 2, 64), (32, 8, 128), (12, 4, 128), (4, 4, 256),
+                                                     (64, 8, 128), (16, 1, 64)])
+def test_window_kernel(size: int | None, dtype: str, heads: int, kv_heads: int, head_dim: int) -> None:
+    # steps of few rows per request on the decode kernel's window launch: a tile's (row, head)
+    # pairs are the 16 matrix-core columns, each row masked at its own position; rows of one
+    # to 16 / group per request, a padding request, contexts across partitions and blocks
+    rows = 16 // (heads // kv_heads)
+    steps = [(min(rows, 2), 900), (1, 17), (rows, rows), (1, 0), (min(rows, 3), 300), (rows, 1041)]
+    s = build_scenario(steps, dtype=dtype, heads=heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16,
+                       mode="mixed", seed=69, spare_blocks=2)
+    launch = dict(partitions=0) if size == 0 else dict(partition_size=size) if size else {}
+    assert plan_scenario(s).plan.window_pairs(heads // kv_heads) > 0
+    out = run_attention(s, prefill=True, window=True, **launch)
+    assert_parity(out, s.expected(np.float64), dtype, f"windows/{size}")
+    padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
+    assert torch.count_nonzero(out[padding_rows]) == 0
 
 
 @pytest.mark.parametrize("waves", [1, 2, 4])
@@ -268,9 +288,9 @@ def test_multi_row_step_in_a_captured_graph(launch: dict) -> None:
 def test_block_sizes(block_size: int, qk: str) -> None:
     s = build_scenario([(1, 1), (1, 63), (1, 130), (2, 70)], block_size=block_size, head_dim=128,
                        heads=8, kv_heads=2, seed=43)
-    for prefill in (False, True):
-        out = run_attention(s, None, qk, prefill)
-        assert_parity(out, s.expected(np.float64), "bf16", f"bs{block_size}/{prefill}")
+    for prefill, window in ((False, None), (True, False), (True, True)):
+        out = run_attention(s, None, qk, prefill, window=window)
+        assert_parity(out, s.expected(np.float64), "bf16", f"bs{block_size}/{prefill}/{window}")
 
 
 @pytest.mark.parametrize("block_size", [1, 2])
@@ -282,6 +302,12 @@ def test_table_segments(block_size: int) -> None:
     expected = s.expected(np.float64)
     for prefill in (False, True):
         assert_parity(run_attention(s, None, None, prefill), expected, "bf16", f"bs{block_size}/{prefill}")
+    # windows of 2-4 rows over contexts that span several segments
+    w = build_scenario([(2, 1300), (1, 1100), (4, 1400)], block_size=block_size, head_dim=128, heads=8,
+                       kv_heads=2, mode="mixed", seed=45)
+    for launch in (dict(partitions=0), dict(partition_size=512)):
+        assert_parity(run_attention(w, prefill=True, window=True, **launch), w.expected(np.float64), "bf16",
+                      f"bs{block_size}/windows/{launch}")
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
@@ -339,6 +365,7 @@ def test_fp8_store_is_bit_exact(dtype: str, layout: str, head_dim: int) -> None:
 FP8_CASES = [
     ("decode", [(1, 16), (1, 0), (1, 1300), (1, 33), (1, 517)], "decode"),
     ("mixed", [(7, 7), (1, 9), (40, 600), (2, 0), (3, 1100)], "mixed"),
+    ("windows", [(2, 700), (1, 0), (2, 1300), (1, 9)], "mixed"),
 ]
 
 
@@ -360,7 +387,10 @@ def test_fp8_attention_matches_the_oracle_on_decoded_values(dtype: str, layout: 
                 ("v2/reduce-kernel", dict(partitions=6, partition_size=256, merge="reduce-kernel", prefill=False)),
                 ("auto", dict(partitions=None))]
     if mode == "mixed":
-        launches.append(("multi-row", dict(partitions=None, prefill=True)))
+        launches.append(("multi-row", dict(partitions=None, prefill=True, window=False)))
+        if meta.plan.window_pairs(heads // kv_heads):
+            launches.append(("windows", dict(partitions=None, prefill=True, window=True)))
+            launches.append(("windows/256", dict(partitions=None, partition_size=256, prefill=True, window=True)))
         full = hip_attention.PREFILL_PAIRS[head_dim]
         for waves in (2, 4):
             if full // waves >= heads // kv_heads:

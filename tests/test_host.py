@@ -255,6 +255,22 @@ def test_multi_row_launch_choice() -> None:
     assert pairs < 128 and size > 0
 
 
+def test_window_tiles_and_split() -> None:
+    def step(rows: list[int], lengths: list[int]):
+        table = torch.ones(len(rows), max(lengths) // 16 + 1, dtype=torch.int32)
+        return hip_attention.plan(ForwardMode.MIXED, _ints(*rows), _ints(*lengths), table, 16).plan
+    # 16 columns: 4 rows at 4 query heads per key/value head, 2 at 8, 1 at 16, none past 16
+    assert step([2, 1, 4], [900, 17, 40]).window_pairs(4) == 16
+    assert step([2, 1, 5], [900, 17, 40]).window_pairs(4) == 0
+    assert step([2, 2], [900, 17]).window_pairs(8) == 16 and step([3], [40]).window_pairs(8) == 0
+    assert step([1, 1], [9, 9]).window_pairs(16) == 16 and step([1], [9]).window_pairs(32) == 0
+    assert step([3, 3], [100, 100]).window_pairs(3) == 15  # 5 rows x 3 heads
+    # the decode split model over the tiles: many long tiles stay whole-ish, few are split
+    few = step([4] * 8, [4096] * 8).window_split(8, 4)
+    assert few % 64 == 0 and 0 < few < 4096
+    assert step([4], [64]).window_split(8, 4) == 0
+
+
 def _cpu_buffers(**changes: object) -> KVBuffers:
     k = torch.zeros(4, 16, 2, 64, dtype=torch.bfloat16)
     buffers = KVBuffers(k, k.clone(), KVLayoutKind.NHD, RAW_CODEC)
