@@ -35,19 +35,19 @@ HBM_PEAK_GBS = 8000.0
 # the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
 PROFILED_TRAFFIC = {
     (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 1024):
-        (1_081_374_743, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
+        (1_081_377_096, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
     (4, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 704):
-        (668_338_845, 4_054_928, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
+        (668_259_684, 4_054_704, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
     (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 3072):
-        (2_597_999_291, 10_319_248, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
+        (2_597_973_216, 10_319_808, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
     (2, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 320):
-        (148_408_741, 2_128_752, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
+        (148_281_037, 2_128_256, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
     (1, "paged_attention_mfma_kernel (v2, merge in-kernel)", 64):
-        (1_749_849, 86_080, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
+        (1_738_582, 86_080, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
     (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1024):
-        (545_693_884, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
+        (545_397_811, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
     (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1280):
-        (1_317_813_532, 20_071_088, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
+        (1_317_549_585, 20_071_280, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
 }
 
 
