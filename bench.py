@@ -155,6 +155,7 @@ MULTI_ROW_WORKLOADS = [
     (4, 512, 4096, 32, 8, 128, "bf16", "fp8_e4m3"),  # the first workload over fp8 caches
     (32, 4, 4096, 32, 8, 128, "bf16", "fp8_e4m3"),   # verify windows over fp8 caches
     (4, 512, 4096, 16, 8, 256, "bf16"),  # Gemma-2-9B shape (head_dim 256)
+    (64, 2, 2048, 64, 8),     # verify windows of 2 draft tokens at GQA 8 (16 columns: 2 rows x 8 heads)
 ]
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 
