@@ -13,15 +13,12 @@ import sys
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
-__all__ = ["FLAGS", "LIB_PATH", "PROBE_PATH", "build_library", "hipcc_command"]
+__all__ = ["FLAGS", "LIB_PATH", "build_library", "hipcc_command"]
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_DIR = PACKAGE_DIR.parent
 SOURCES = ("api.hip", "paged_attention.hip", "paged_attention_mfma.hip", "paged_prefill.hip", "kv_cache.hip")
 LIB_PATH = PACKAGE_DIR / "lib" / "libayaka_hip.so"
-# A measurement tool built beside the library: read-only probes of the cache access patterns.
-PROBE_SOURCE = "access_probe.hip"
-PROBE_PATH = PACKAGE_DIR / "lib" / "access_probe"
 ARCH = "gfx950"
 
 
@@ -73,9 +70,6 @@ def build_library(*, verbose: bool = False, jobs: int | None = None) -> Path:
     tmp = LIB_PATH.with_suffix(".so.tmp")
     _run([_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)], verbose)
     os.replace(tmp, LIB_PATH)
-    probe_tmp = PROBE_PATH.with_suffix(".tmp")
-    _run([_hipcc(), *FLAGS, str(csrc / PROBE_SOURCE), "-o", str(probe_tmp)], verbose)
-    os.replace(probe_tmp, PROBE_PATH)
     return LIB_PATH
 
 

@@ -138,6 +138,7 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
   p.scale_log2 = c.scale * 1.4426950408889634f;
   p.partition_size = INT32_MAX;
   p.max_partitions = 1;
+  p.wave_split = 1;
   return AYK_OK;
 }
 
@@ -167,12 +168,33 @@ bool merge_in_kernel(int64_t workgroups) { return workgroups <= compute_units() 
 // Heads per wave from which the library picks the matrix-core q.k kernel.
 constexpr int kMfmaMinHeads = 3;
 
+constexpr int32_t kV1WaveFlags = AYK_FLAG_V1_WAVES_1 | AYK_FLAG_V1_WAVES_2 | AYK_FLAG_V1_WAVES_4 | AYK_FLAG_V1_WAVES_8;
+
+// Waves that share one virtual head's context in a v1 launch: the most (up to 8) that
+// keep rows x virtual heads x waves within one round of 8-wave workgroups on the GPU.
+// A workgroup per row covering every head (wave split 1) fills 64 of 256 compute units
+// at C3's 64 rows; splitting each context among 4 waves gives 256 workgroups of 2 heads.
+int v1_wave_split(const ayk::AttnParams& p, int32_t flags) {
+  if (flags & AYK_FLAG_V1_WAVES_1) return 1;
+  if (flags & AYK_FLAG_V1_WAVES_2) return 2;
+  if (flags & AYK_FLAG_V1_WAVES_4) return 4;
+  if (flags & AYK_FLAG_V1_WAVES_8) return 8;
+  const int64_t slots = (int64_t)compute_units() * ayk::kMaxWavesPerGroup;
+  int ws = 1;
+  while (ws < ayk::kMaxWavesPerGroup && (int64_t)p.n_rows * p.num_virtual_heads * ws * 2 <= slots) ws *= 2;
+  return ws;
+}
+
 // The q.k path and workgroup shape for a launch, then the kernel(s).
 int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool bf16, bool kv8, bool split,
            int32_t flags, void* stream) {
   if (flags & ~(AYK_FLAG_QK_DPP | AYK_FLAG_QK_MFMA | AYK_FLAG_PARTIALS_ONLY | AYK_FLAG_SEPARATE_REDUCE |
-                AYK_FLAG_SINGLE_LAUNCH))
+                AYK_FLAG_SINGLE_LAUNCH | kV1WaveFlags))
     return fail(AYK_ERR_ARGUMENT, "%s: unknown flags 0x%x", op, flags);
+  if (__builtin_popcount(flags & kV1WaveFlags) > 1)
+    return fail(AYK_ERR_ARGUMENT, "%s: at most one AYK_FLAG_V1_WAVES_* flag", op);
+  if ((flags & kV1WaveFlags) && split)
+    return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_V1_WAVES_* apply to v1 only", op);
   if ((flags & AYK_FLAG_QK_DPP) && (flags & AYK_FLAG_QK_MFMA))
     return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_QK_DPP and AYK_FLAG_QK_MFMA exclude each other", op);
   if ((flags & AYK_FLAG_SEPARATE_REDUCE) && (flags & AYK_FLAG_SINGLE_LAUNCH))
@@ -184,13 +206,19 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   // through LDS) streams faster than the DPP kernel, whose per-token dot2 and
   // butterfly work grows with the group; 1-2 heads stay on the DPP kernel.
   // fp8 caches are read by the matrix-core kernel only.
-  const bool mfma = kv8 || (flags & AYK_FLAG_QK_MFMA) || (!(flags & AYK_FLAG_QK_DPP) && gc >= kMfmaMinHeads);
+  ayk::AttnParams q = p;
+  // v1: split each context among waves of the matrix-core kernel when rows x heads leave the
+  // GPU idle (the DPP kernel, forced, streams each head's context in one wave)
+  q.wave_split = split || (flags & AYK_FLAG_QK_DPP) ? 1 : v1_wave_split(p, flags);
+  if ((flags & AYK_FLAG_QK_DPP) && (flags & kV1WaveFlags) && !(flags & AYK_FLAG_V1_WAVES_1))
+    return fail(AYK_ERR_UNSUPPORTED, "%s: the DPP kernel does not split a context among waves", op);
+  const bool mfma = kv8 || (flags & AYK_FLAG_QK_MFMA) || q.wave_split > 1 ||
+                    (!(flags & AYK_FLAG_QK_DPP) && gc >= kMfmaMinHeads);
   const int waves = 4;
   const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);
   const int64_t workgroups = items * p.num_virtual_heads;
   if (workgroups > INT32_MAX || (int64_t)p.n_rows * p.num_heads > INT32_MAX)
     return fail(AYK_ERR_UNSUPPORTED, "%s: %lld workgroups exceed one launch", op, (long long)workgroups);
-  ayk::AttnParams q = p;
   // The grid: one workgroup per item and group of up to kMaxWaves virtual heads.
   const int64_t grid = items * ((p.num_virtual_heads + ayk::kMaxWavesPerGroup - 1) / ayk::kMaxWavesPerGroup);
   if (split && q.arrivals && !(flags & AYK_FLAG_SINGLE_LAUNCH) && !merge_in_kernel(grid))
@@ -207,7 +235,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
 
 extern "C" {
 
-int ayk_abi_version(void) { return 11; }
+int ayk_abi_version(void) { return 12; }
 
 int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 

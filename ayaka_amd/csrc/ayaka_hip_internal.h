@@ -44,6 +44,8 @@ struct AttnParams {
   int32_t partition_size;
   int32_t max_partitions;
   int32_t n_work;
+  int32_t wave_split;   // v1, matrix-core kernel: waves sharing one virtual head's context
+                        // (1, 2, 4 or 8; a workgroup holds 8 / wave_split virtual heads)
   float scale_log2;     // scale * log2(e): scores live in the log2 domain
 };
 

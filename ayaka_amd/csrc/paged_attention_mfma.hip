@@ -85,11 +85,18 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   __shared__ __attribute__((aligned(16))) uint16_t s_v[kMaxWaves][MT * VP];  // a tile's values
   static_assert(SUB >= 1 && CH % TPL == 0 && NL == SUB * NL1, "chunk shape");
   __shared__ int s_last;
+  // v1 with a row's context split among waves: each slice's running max and weight sum
+  __shared__ float s_slice_m[kMaxWaves][16], s_slice_l[kMaxWaves][16];
 
   const int tid = threadIdx.x;
   const int threads = blockDim.x;
   const int waves = threads / kWave;
-  const int groups = (p.num_virtual_heads + waves - 1) / waves;
+  // v1 only: `ws` waves share one virtual head, each streaming every ws-th chunk of its
+  // context, and their states are merged in LDS at the end (fills the GPU when rows x
+  // heads alone leave compute units idle, and reads each context once).
+  const int ws = (SPLIT || WIN) ? 1 : p.wave_split;
+  const int heads_per_wg = waves / ws;
+  const int groups = (p.num_virtual_heads + heads_per_wg - 1) / heads_per_wg;
   WgCoord wg;
   int win_first = 0, win_rows = 0;  // WIN: the tile's rows
   if constexpr (WIN) {
@@ -104,7 +111,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   const int row = wg.row;  // WIN: the request
   const int lane = tid & (kWave - 1);
   const int wave = tid >> 6;
-  const int vh = wg.group * waves + wave;
+  const int vh = wg.group * heads_per_wg + wave / ws;
+  const int slice = wave % ws;
   const bool active = vh < p.num_virtual_heads;
   const int kvh = vh / p.head_chunks;
   const int h0 = kvh * p.group + (vh % p.head_chunks) * GC;
@@ -129,8 +137,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     win_row = win_first + min(rr, win_rows - 1);
     win_head = kvh * p.group + mt % p.group;
     win_lim = len > 0 ? min(p.positions[win_row], len - 1) : 0;
-    // the tile's last row sees the most; nothing past it is read
-    if (len > 0) len = min(len, p.positions[win_first + win_rows - 1] + 1);
+    // the tile's last row sees the most; nothing past it is read (a negative position
+    // leaves nothing to read: the tile's rows get zeros, as row_context gives them)
+    if (len > 0) len = max(0, min(len, p.positions[win_first + win_rows - 1] + 1));
   } else {
     row_context(p, row, req, len);
   }
@@ -160,7 +169,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
       return;
     }
   } else if (len == 0) {
-    if (active) store_zero_rows<D, GC, kWave>(p, row, h0, lane);
+    if (active && slice == 0) store_zero_rows<D, GC, kWave>(p, row, h0, lane);
     return;
   }
 
@@ -191,8 +200,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
     const int s1 = min(t_end, s0 + seg_len);
     const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, threads);
-    if (!active) continue;
     const int nch = (s1 - s0 + CH - 1) / CH;
+    if (!active || slice >= nch) continue;
+    // this wave's chunks: slice, slice + ws, ..., up to `last`
+    const int last = slice + (nch - 1 - slice) / ws * ws;
 
     auto offsets = [&](int ci, uint32_t(&dst)[NL]) {
 #pragma unroll
@@ -269,31 +280,72 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     // wait for everything).
     uint32_t offA[NL], offB[NL];
     Raw kA[NL], kB[NL], vc[NL];
-    int ci = 0;
-    offsets(0, offA);
+    int ci = slice;
+    offsets(ci, offA);
 #pragma unroll
     for (int j = 0; j < NL; ++j) kA[j] = load_kv_raw<KV8>(kbase, offA[j]);
-    while (ci < nch) {
+    while (ci <= last) {
 #pragma unroll
       for (int j = 0; j < NL; ++j) vc[j] = load_kv_raw<KV8>(vbase, offA[j]);
-      offsets(min(ci + 1, nch - 1), offB);
+      offsets(min(ci + ws, last), offB);
 #pragma unroll
       for (int j = 0; j < NL; ++j) kB[j] = load_kv_raw<KV8>(kbase, offB[j]);
       consume(ci, kA, vc);
-      if (++ci >= nch) break;
+      ci += ws;
+      if (ci > last) break;
 #pragma unroll
       for (int j = 0; j < NL; ++j) vc[j] = load_kv_raw<KV8>(vbase, offB[j]);
-      offsets(min(ci + 1, nch - 1), offA);
+      offsets(min(ci + ws, last), offA);
 #pragma unroll
       for (int j = 0; j < NL; ++j) kA[j] = load_kv_raw<KV8>(kbase, offA[j]);
       consume(ci, kB, vc);
-      ++ci;
+      ci += ws;
     }
   }
-  if (active) {
-    // Head mt's weight sum over the wave's 4 token groups (its lanes share m_h).
-    l_h += __shfl_xor(l_h, 16);
-    l_h += __shfl_xor(l_h, 32);
+  // Head mt's weight sum over the wave's 4 token groups (its lanes share m_h).
+  l_h += __shfl_xor(l_h, 16);
+  l_h += __shfl_xor(l_h, 32);
+  if constexpr (!SPLIT && !WIN) {
+    if (ws > 1) {
+      // Slices 1.. of a head hand (m, l, o) to slice 0 through their own LDS tiles (the
+      // keys' tile takes o[0, DT/2), the values' tile the rest: 4 * D 16-byte entries fit
+      // in 2 * D + (D + 16) / 4), which folds them in slice order: the result does not
+      // depend on the waves' timing.
+      constexpr int HALF = DT / 2;
+      u32x4* vt = reinterpret_cast<u32x4*>(&s_v[wave][0]);
+      if (active && slice > 0) {
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const u32x4 w = __builtin_bit_cast(u32x4, o[t]);
+          if (t < HALF) s_k[wave][t * kWave + lane] = w;
+          else vt[(t - HALF) * kWave + lane] = w;
+        }
+        if (lane < 16) {
+          s_slice_m[wave][lane] = m_h;
+          s_slice_l[wave][lane] = l_h;
+        }
+      }
+      __syncthreads();
+      if (active && slice == 0) {
+        for (int j = 1; j < ws; ++j) {
+          const int src = wave + j;
+          const float mj = s_slice_m[src][mt], lj = s_slice_l[src][mt];
+          const float mn = fmaxf(m_h, mj);
+          const float a = fast_exp2(m_h - mn), b = fast_exp2(mj - mn);
+          l_h = l_h * a + lj * b;
+          m_h = mn;
+          const u32x4* vs = reinterpret_cast<const u32x4*>(&s_v[src][0]);
+#pragma unroll
+          for (int t = 0; t < DT; ++t) {
+            const f32x4 oj = __builtin_bit_cast(f32x4, t < HALF ? s_k[src][t * kWave + lane]
+                                                                : vs[(t - HALF) * kWave + lane]);
+            o[t] = o[t] * a + oj * b;
+          }
+        }
+      }
+    }
+  }
+  if (active && slice == 0) {
     if constexpr (WIN) {
       // the row sees positions [0, win_lim]: partitions past it hold nothing of it
       const int np_row = SPLIT ? win_lim / psize + 1 : 1;
@@ -314,9 +366,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
 
 template <int D, int GC, bool BF16, bool KV8>
 static hipError_t launch_mfma_typed(const AttnParams& p, bool split, hipStream_t stream) {
-  // one wave per virtual head, up to kMaxWaves per workgroup
-  const int per_wg = p.num_virtual_heads < kMaxWaves ? p.num_virtual_heads : kMaxWaves;
-  const int groups = (p.num_virtual_heads + per_wg - 1) / per_wg;
+  // p.wave_split waves per virtual head (v1; 1 for v2), up to kMaxWaves per workgroup
+  const int ws = split ? 1 : p.wave_split;
+  const int heads = p.num_virtual_heads < kMaxWaves / ws ? p.num_virtual_heads : kMaxWaves / ws;
+  const int per_wg = heads * ws;
+  const int groups = (p.num_virtual_heads + heads - 1) / heads;
   const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);
   const dim3 grid((unsigned)(items * groups)), block(per_wg * kWave);
   if (split)

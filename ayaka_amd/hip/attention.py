@@ -7,13 +7,14 @@ facts ``attend`` needs to pick a launch without reading the device.
 
 ``attend`` launches one of two kernels through ``libayaka_hip.so``:
 
-* v1 (``ayk_paged_attention_v1``): one workgroup per (row, key/value head)
-  streams the row's whole context once;
+* v1 (``ayk_paged_attention_v1``): one launch, no scratch: a workgroup per row
+  and 8 / n of its key/value heads, n = 1-8 waves per head each streaming every
+  n-th chunk of the row's context, merged in LDS;
 * v2 (``ayk_paged_attention_v2``): one workgroup per (row, key/value head,
   partition) that holds tokens, longest first, then a log-sum-exp merge.
 
-:func:`choose_split` picks between them, and the partition size, from the step's
-row lengths by a modelled schedule. Decode rows (one per request) use these kernels;
+:func:`choose_split` picks between them, v1's wave count and v2's partition size,
+from the step's row lengths by a modelled schedule. Decode rows (one per request) use these kernels;
 steps of several rows per request (prefill chunks, verify windows) use the multi-row
 kernel (``ayk_paged_prefill``), where row ``j`` attends to positions
 ``0 .. position_j`` (the reference's causal rule, ``attention.py:209-234``).
@@ -84,6 +85,14 @@ PARTITION_CANDIDATES = (64, 128, 192, 256, 320, 384, 448, 512, 576, 640, 704, 76
 #: three shapes for both.
 WORKGROUP_COSTS = {2: 320, 1: 160}
 WORKGROUP_COST = WORKGROUP_COSTS[2]
+#: The same for a v1 workgroup, whose waves split each context among themselves and merge
+#: in LDS (no partials, no second launch): fitted so that the model prefers v1 where it
+#: measured faster than the best v2 launch (C3's 64 rows of 4096: 160.5 vs 162.8 us, with
+#: fp8 caches 90.7 vs 92.8; C1's four short rows: 12.1 vs 15.9 us, with fp8 caches 11.3 vs
+#: 15.7) and v2 where it is not (C2, C4, C5, both codecs).
+V1_WORKGROUP_COSTS = {2: 240, 1: 80}
+#: Waves a v1 workgroup may split each (row, key/value head)'s context among.
+V1_WAVE_SPLITS = (1, 2, 4, 8)
 #: XCDs of one MI355X; workgroups are dealt to them round-robin.
 XCDS = 8
 #: Heads per wave from which the library runs q.k on the matrix cores (mirrors the C library).
@@ -108,6 +117,8 @@ _QK_FLAGS = {None: 0, "dpp": 1, "mfma": 2}
 #: v2 flag: launch the partition kernel only (benchmarks time the dominant kernel with it).
 PARTIALS_ONLY = 4
 _MERGE_FLAGS = {None: 0, "reduce-kernel": 8, "in-kernel": 16}
+#: AYK_FLAG_V1_WAVES_*: waves sharing each (row, key/value head)'s context in a v1 launch
+_V1_WAVE_FLAGS = {None: 0, 1: 32, 2: 64, 4: 128, 8: 256}
 
 
 @dataclass(frozen=True, slots=True)
@@ -465,10 +476,13 @@ def graph_merge_site(items: int, num_kv_heads: int, group: int) -> str:
 
 @dataclass(frozen=True, slots=True)
 class Split:
-    """A launch: ``partitions == 0`` is v1, otherwise v2 over partitions of ``partition_size``."""
+    """A launch: ``partitions == 0`` is v1, otherwise v2 over partitions of ``partition_size``.
+    ``v1_waves`` (v1): waves sharing each (row, key/value head)'s context, 0 for the C
+    library's own rule."""
 
     partition_size: int
     partitions: int
+    v1_waves: int = 0
 
 
 def schedule_makespan(row_lengths: list[int], size: int, groups: int = 1, cost: int | None = None) -> int:
@@ -500,6 +514,16 @@ def schedule_makespan(row_lengths: list[int], size: int, groups: int = 1, cost: 
 _split_cache: dict[tuple, int] = {}
 #: Work lists longer than this many rounds of the GPU are not considered (start-up cost dominates).
 MAX_ROUNDS = 8
+
+
+def v1_makespan(row_lengths: list[int], waves: int, virtual_heads: int, cost: int) -> int:
+    """Modelled finish time, in positions, of v1 with each context split among ``waves`` waves:
+    a workgroup per row and ``8 / waves`` virtual heads, each wave streaming a ``1 / waves``
+    share of its row in 16-position chunks, scheduled as :func:`schedule_makespan` schedules
+    v2's workgroups."""
+    shares = [-(-n // (16 * waves)) * 16 for n in row_lengths]
+    groups = -(-virtual_heads * waves // 8)
+    return schedule_makespan(shares, max(shares, default=1) + 1, groups, cost)
 
 
 def fits_schedule(lengths: list[int], size: int, groups: int = 1) -> bool:
@@ -539,6 +563,7 @@ def choose_split(
     kv_bytes: int = 2,
     min_size: int = 0,
     max_items: int = 0,
+    v1: bool = True,
 ) -> Split:
     """Pick v1 or v2 and the partition size from the step's shape.
 
@@ -552,24 +577,43 @@ def choose_split(
     per element (2, or 1 for fp8), which sets the modelled workgroup cost; ``min_size``
     leaves out smaller partition sizes, and ``max_items`` sizes whose work list over the
     rows with context is longer (a graph replay's grid and scratch are sized for both).
+    An eagerly planned step also scores v1 with each context split among 1-8 waves
+    (:func:`v1_makespan`) and takes it, with its wave count, when it models faster than the
+    best v2 launch (``v1`` False leaves that out: the best v2 launch).
     """
     del total_length
     if max_length <= 0:
         return Split(0, 0)
-    groups = -(-num_kv_heads * head_chunks(group) // 8)
+    virtual_heads = num_kv_heads * head_chunks(group)
+    groups = -(-virtual_heads // 8)
     lengths = [n for n in row_lengths if n > 0] if row_lengths is not None else [max_length] * n_rows
     total = sum(lengths)
     # The total to 4 significant bits, the longest row to a power of two, the row count.
     top = max(total.bit_length() - 4, 0)
-    key = (groups, kv_bytes, min_size, max_items, len(lengths), max_length.bit_length(), total >> top, top)
-    size = _split_cache.get(key)
-    if size is None:
+    key = (virtual_heads, kv_bytes, min_size, max_items, v1, len(lengths), max_length.bit_length(), total >> top,
+           top)
+    found = _split_cache.get(key)
+    if found is None:
         if len(_split_cache) > 4096:
             _split_cache.clear()
         size = _best_size(lengths, max_length, groups, kv_bytes, min_size, max_items)
-        _split_cache[key] = size
+        waves = 0
+        # v1 with a wave split, scored by the same schedule: eager plans only (a graph replay's
+        # launch is the staged v2 split, sized by min_size and max_items)
+        if v1 and not min_size and not max_items and lengths:
+            v2 = schedule_makespan(lengths, size, groups, WORKGROUP_COSTS[kv_bytes]) if size < max_length else None
+            best = None
+            for ws in V1_WAVE_SPLITS:
+                t = v1_makespan(lengths, ws, virtual_heads, V1_WORKGROUP_COSTS[kv_bytes])
+                if best is None or t < best[0]:
+                    best = (t, ws)
+            if v2 is None or best[0] < v2:
+                size, waves = max_length, best[1]
+        found = (size, waves)
+        _split_cache[key] = found
+    size, waves = found
     if max_length <= size:
-        return Split(0, 0)
+        return Split(0, 0, waves)
     return Split(size, -(-max_length // size))
 
 
@@ -743,6 +787,7 @@ def attend_with(
     merge: str | None = None,
     tile_pairs: int | None = None,
     window: bool | None = None,
+    v1_waves: int | None = None,
 ) -> None:
     """:func:`attend` with the launch chosen by the caller.
 
@@ -760,7 +805,9 @@ def attend_with(
     partitions of that size (a multiple of 64) merged by the reduce kernel, and ``None``
     for both lets :func:`choose_prefill_partition` decide; ``tile_pairs`` forces the tile
     capacity (:data:`PREFILL_PAIRS`, or a half or a quarter of it; ``None``:
-    :meth:`HipAttentionPlan.prefill_launch`).
+    :meth:`HipAttentionPlan.prefill_launch`). ``v1_waves`` (1, 2, 4 or 8) forces how many
+    waves of a v1 launch share each (row, key/value head)'s context (``None``: the library's
+    choice, which fills the GPU).
     Benchmarks and tests use them to time and check every kernel on one step.
     """
     op = "attention.attend"
@@ -913,6 +960,7 @@ def attend_with(
                 staged = step.staged
                 split = Split(step.min_size, step.partitions)
         partitions, partition_size = split.partitions, split.partition_size
+        v1_waves = v1_waves or split.v1_waves or None
     partition_size = partition_size or PARTITION_SIZE
     if partitions and partitions * partition_size < max_length:
         raise BackendError(
@@ -921,7 +969,7 @@ def attend_with(
         )
     flags = _QK_FLAGS[qk] | (PARTIALS_ONLY if partials_only else 0) | _MERGE_FLAGS[merge]
     if partitions == 0:
-        _lib.check(op, lib.ayk_paged_attention_v1(*common, flags, stream))
+        _lib.check(op, lib.ayk_paged_attention_v1(*common, flags | _V1_WAVE_FLAGS[v1_waves], stream))
         return
     if staged is not None:  # the rows' partials packed into one slot per work item
         nbytes = lib.ayk_paged_attention_v2_workspace_bytes(step.capacity, heads, buffers.head_dim, 1)

@@ -30,7 +30,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 
 # HBM bytes per launch of the dominant kernel, measured with rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE on `bench.py --config C --only auto` and scaled by what the same counters read
+# WRITE_SIZE on `bench.py --config C --only` and scaled by what the same counters read
 # for a 1 GiB device copy (FETCH x2.0, WRITE x1.0). Reported only when this run's launch is
 # the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
 PROFILED_TRAFFIC = {
@@ -57,8 +57,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=3, help="benchmark configuration 1-5 (3 = headline)")
-    ap.add_argument("--only", choices=["auto", "auto/reduce-kernel", "auto/in-kernel", "v1", "v2"], default=None,
-                    help="time only this launch (for profiler runs)")
+    ap.add_argument("--only", action="store_true",
+                    help="time only the headline launch, on one pool (for profiler runs)")
     ap.add_argument("--layout", choices=["nhd", "hnd"], default=None,
                     help="cache layout (default: the one the hip backend asks the pool for)")
     ap.add_argument("--codec", choices=["raw", "fp8_e4m3"], default="raw",
@@ -66,9 +66,11 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--qk", choices=["dpp", "mfma"], default=None,
                     help="force the q.k implementation (default: the library's choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=8, help="rows of the CPU baseline sample")
-    ap.add_argument("--access-probe", action="store_true",
-                    help="only run the read-only access-pattern probes (ayaka_amd/lib/access_probe)")
+    ap.add_argument("--cpu-rows", type=int, default=64, help="rows of the CPU baseline sample")
+    ap.add_argument("--record", action="store_true",
+                    help="print only the record of --config (with --codec): µs per call, GB/s, kernel")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-configuration records (C1-C5, both codecs) of the default run")
     ap.add_argument("--graph-step", action="store_true",
                     help="time a 32-layer decode step (KV write + attention per layer) eagerly and as a "
                          "captured graph replay (and eagerly on a planned step), at the C1-C5 shapes")
@@ -108,35 +110,46 @@ def time_calls(fn, steps: int, warmup: int, repeats: int = 5) -> dict:
 
 
 def cpu_baseline(step, cfg, rows: int, kv_bytes: int = 2) -> dict:
-    """The oracle's restatement of the reference CPU decode, timed on a sample of the batch."""
-    import numpy as np
+    """The reference's CPU decode (``_attend_decode``, restated in torch by
+    ``oracle.torch_decode``) timed on this host over ``rows`` rows of the step: the padded
+    tables gathered from a bf16/fp16 cache, float32 matmuls and softmax, as the reference's
+    torch backend runs it, on as many threads as this process may use."""
+    import torch
 
     from ayaka_amd import workloads
-    from oracle import paged
+    from oracle.torch_decode import attend_decode
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
+    nproc = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(nproc, int(omp)) if omp.isdigit() and int(omp) > 0 else nproc
+    torch.set_num_threads(threads)
     rows = min(rows, cfg.batch)
     sample = workloads.sample_rows(step, list(range(rows)))
+    # the cache in its own dtype (fp8 caches: their decoded values, which the reference has no codec for)
+    keys = torch.from_numpy(sample["k"]).to(cfg.dtype)
+    values = torch.from_numpy(sample["v"]).to(cfg.dtype)
+    q = torch.from_numpy(sample["q"]).to(cfg.dtype)
+    table, lengths = torch.from_numpy(sample["table"]), torch.from_numpy(sample["lengths"])
     runs = []
     for _ in range(6):  # 1 warm-up + 5 timed
         t0 = time.perf_counter()
-        paged.attention(sample["q"], sample["k"], sample["v"], sample["table"], sample["lengths"],
-                        scale=cfg.scale, precision=np.float32)
+        attend_decode(q, keys, values, table, lengths, scale=cfg.scale)
         runs.append(time.perf_counter() - t0)
     seconds = statistics.median(runs[1:]) * cfg.batch / rows  # scaled to the whole batch
+    scaled = "all of them" if rows == cfg.batch else f"scaled by {cfg.batch}/{rows} to one call"
     return {
         "value": workloads.algorithmic_bytes(cfg, kv_bytes) / seconds / 1e9,
         "unit": "GB/s",
         "us_per_call": seconds * 1e6,
         "cores": threads,
+        "nproc": nproc,
+        "os_cpu_count": os.cpu_count(),
+        "torch_threads": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"{rows} of {cfg.batch} rows of the same step, fp32 gather-then-softmax (numpy), "
-                  f"median of 5 runs after 1 warm-up, scaled by {cfg.batch}/{rows} to one call",
+        "sample": f"{rows} of {cfg.batch} rows of the same step ({scaled}): the reference's _attend_decode "
+                  f"restated in torch "
+                  f"(oracle/torch_decode.py) on the CPU, bf16 cache gathered per padded table, float32 "
+                  f"matmuls and softmax; median of 5 runs after 1 warm-up, torch.set_num_threads({threads})",
     }
 
 
@@ -303,13 +316,6 @@ def main() -> int:
               "decode path on one MI355X (sequences and key/value heads shard across GPUs without a "
               "collective, so a multi-GPU figure would be N independent copies of this one)", file=sys.stderr)
         return 2
-    if args.access_probe:
-        import subprocess
-
-        from ayaka_amd._build import PROBE_PATH
-
-        return subprocess.run([str(PROBE_PATH)], check=False).returncode
-
     import torch
 
     if args.multi_row:
@@ -325,86 +331,170 @@ def main() -> int:
         print(json.dumps({"copy_calibration_bytes": src.numel()}))
         return 0
 
+    from ayaka_amd.hip import _lib
+
+    _lib.lib()
+    if args.record:
+        print(json.dumps(measure(args.config, args, args.codec, args.layout)), flush=True)
+        return 0
+    head = measure(args.config, args, args.codec, args.layout, headline=True)
+    line = head.pop("line")
+    if not args.only and not args.no_configs:
+        # every benchmark configuration, both codecs, as the library launches it (the
+        # headline's own record is the one above). Each runs in a child process of its
+        # own: a fresh allocator gives every pool the same placement a first run gets
+        # (in one process, after the rotated pools of C1/C2 came and went, the later
+        # configurations measured 5-10% slower).
+        for codec, key in (("raw", "configs"), ("fp8_e4m3", "configs_fp8")):
+            line[key] = {}
+            for index in (1, 2, 3, 4, 5):
+                if index == args.config and codec == args.codec:
+                    line[key][f"C{index}"] = head
+                    continue
+                line[key][f"C{index}"] = child_record(index, codec, args)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def child_record(index: int, codec: str, args) -> dict:
+    """One configuration's record, measured by ``bench.py --record`` in a child process."""
+    import subprocess
+
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--record", "--config", str(index), "--codec", codec,
+           "--steps", str(args.steps), "--warmup", str(args.warmup)]
+    if args.layout:
+        cmd += ["--layout", args.layout]
+    if args.qk:
+        cmd += ["--qk", args.qk]
+    done = subprocess.run(cmd, capture_output=True, text=True, timeout=300, check=False)
+    sys.stderr.write(done.stderr)
+    if done.returncode != 0:
+        return {"error": f"exit status {done.returncode}"}
+    return json.loads(done.stdout.strip().splitlines()[-1])
+
+
+# Caches whose K/V working set fits MI355X's 256 MB Infinity Cache are timed over rotating
+# copies of the pool, at least this many bytes of K/V in all, so that consecutive calls read
+# HBM rather than the last call's lines.
+ROTATION_BYTES = 1 << 30
+
+
+def kernel_label(mfma: bool, split, merge: str | None, kv_bytes: int) -> str:
+    """The dominant kernel of a launch, as the bench line and the profiles name it."""
+    name = "paged_attention_mfma_kernel" if mfma else "paged_attention_kernel"
+    what = f"v1, {split.v1_waves} waves per head" if not split.partitions else f"v2, merge {merge}"
+    return f"{name} ({what}{', fp8 cache' if kv_bytes == 1 else ''})"
+
+
+def measure(index: int, args, codec: str, layout_name: str | None, headline: bool = False) -> dict:
+    """Time configuration ``index`` as ``attend`` launches it: µs per call, GB/s, the HBM
+    fraction and the dominant kernel alone. The headline configuration also times v1 and
+    v2 (partition 512, the reference's) and the best v2 launch, the KV write, the
+    roofline record and the CPU baseline, and returns the bench line under "line"."""
+    import torch
+
     from ayaka_amd import workloads
     from ayaka_amd.enums import ForwardMode, KVLayoutKind
-    from ayaka_amd.hip import _lib
     from ayaka_amd.hip import attention as hip_attention
     from ayaka_amd.hip import kvcache as hip_kvcache
     from ayaka_amd.kvcache import KVBuffers
 
-    _lib.lib()
     dev = torch.device("cuda:0")
-    cfg = workloads.config(args.config)
-    layout = KVLayoutKind(args.layout) if args.layout else KVLayoutKind(hip_kvcache.layout())
-    step = workloads.build(cfg, dev, poison=False, layout=str(layout.value), codec=args.codec)
-    buffers = KVBuffers(step.k_cache, step.v_cache, layout, args.codec)
-    kv_bytes = 1 if args.codec == "fp8_e4m3" else 2
+    cfg = workloads.config(index)
+    group = cfg.heads // cfg.kv_heads
+    layout = KVLayoutKind(layout_name) if layout_name else KVLayoutKind(hip_kvcache.layout())
+    step = workloads.build(cfg, dev, poison=False, layout=str(layout.value), codec=codec)
+    buffers = KVBuffers(step.k_cache, step.v_cache, layout, codec)
+    kv_bytes = 1 if codec == "fp8_e4m3" else 2
     write = hip_attention.plan(ForwardMode.MIXED, step.rows_per_request, step.lengths, step.table, cfg.block_size)
     hip_kvcache.store(step.k_new, step.v_new, buffers, write)
     meta = hip_attention.plan(ForwardMode.DECODE, torch.ones(cfg.batch, dtype=torch.int32, device=dev),
                               step.lengths, step.table, cfg.block_size)
     out = torch.empty_like(step.q)
     nbytes = workloads.algorithmic_bytes(cfg, kv_bytes)
-    max_len = max(cfg.lengths)
-    auto = meta.plan.split_for(cfg.kv_heads, cfg.heads // cfg.kv_heads, kv_bytes)  # what attend will launch
-    # The headline ("auto", the launch attend picks) runs last, on a GPU warmed by the others.
-    # name: (partitions, partition size, where v2 merges: None = the library's choice)
-    launches = {
-        "v1": (0, 0, None),
-        "v2": (-(-max_len // hip_attention.PARTITION_SIZE), hip_attention.PARTITION_SIZE, None),
-        "auto/reduce-kernel": (None, auto.partition_size, "reduce-kernel"),
-        "auto/in-kernel": (None, auto.partition_size, "in-kernel"),
-        "auto": (None, auto.partition_size, None),
-    }
-    if args.only:
-        launches = {args.only: launches[args.only]}
+    kv_set = sum(cfg.lengths) * cfg.kv_heads * cfg.head_dim * 2 * kv_bytes
+    copies = 1 if headline and args.only else max(1, -(-ROTATION_BYTES // kv_set)) if kv_set < (256 << 20) else 1
+    pools = [buffers] + [KVBuffers(step.k_cache.clone(), step.v_cache.clone(), layout, codec)
+                         for _ in range(copies - 1)]
+    turn = [0]
 
-    results = {}
-    head_name = "auto" if "auto" in launches else next(iter(launches))
-    for name, (parts, size, merge) in launches.items():
-        def call(parts=parts, size=size, merge=merge):
-            hip_attention.attend_with(step.q, buffers, meta, out, scale=cfg.scale, partitions=parts, qk=args.qk,
-                                      partition_size=size or None, merge=merge)
-        # The headline launch times exactly K steps once; the others take the median of 3 regions.
-        results[name] = time_calls(call, args.steps, args.warmup, repeats=1 if name == head_name else 3)
-        results[name]["partitions"] = auto.partitions if parts is None else parts
-        results[name]["partition_size"] = size
-        results[name]["gbs"] = nbytes / (results[name]["median_us"] * 1e-6) / 1e9
-        print(f"[bench] {cfg.name} {name}: {results[name]['median_us']:.1f} us/call "
-              f"{results[name]['gbs']:.0f} GB/s", file=sys.stderr, flush=True)
+    def pool():
+        turn[0] += 1
+        return pools[turn[0] % len(pools)]
 
-    head = results[head_name]
-    store_us = time_calls(lambda: hip_kvcache.store(step.k_new, step.v_new, buffers, write), 50, 5)["median_us"]
-    # The dominant kernel: the attention kernel itself. v1 and a v2 that merges in
-    # its partition kernel are one kernel per call, so the call's time is the
-    # kernel's; with a reduce kernel, time the partition kernel alone with the
-    # same events.
-    mfma = args.qk == "mfma" or (args.qk is None and hip_attention.uses_matrix_cores(cfg.heads // cfg.kv_heads))
-    parts, size, merge = launches[head_name]
-    if merge is None and head["partitions"]:
-        merge = hip_attention.merge_site(cfg.kv_heads, cfg.heads // cfg.kv_heads, meta.plan, size)
-    kernel = ("paged_attention_mfma_kernel" if mfma else "paged_attention_kernel") + \
-        (" (v1" if head["partitions"] == 0 else f" (v2, merge {merge}") + \
-        (", fp8 cache)" if kv_bytes == 1 else ")")
-    if head["partitions"] == 0 or merge == "in-kernel":
-        kernel_us = head["median_us"]
-    else:
+    auto = meta.plan.split_for(cfg.kv_heads, group, kv_bytes)  # what attend will launch
+    mfma = args.qk == "mfma" or (args.qk is None and (hip_attention.uses_matrix_cores(group) or kv_bytes == 1
+                                                      or (auto.partitions == 0 and auto.v1_waves > 1)))
+    merge = None if not auto.partitions else \
+        hip_attention.merge_site(cfg.kv_heads, group, meta.plan, auto.partition_size)
+    kernel = kernel_label(mfma, auto, merge, kv_bytes)
+
+    def call():
+        hip_attention.attend(step.q, pool(), meta, out, scale=cfg.scale)
+
+    result = time_calls(call, args.steps, args.warmup, repeats=1 if headline else 3)
+    if auto.partitions and merge == "reduce-kernel":
         kernel_us = time_calls(
-            lambda: hip_attention.attend_with(step.q, buffers, meta, out, scale=cfg.scale, partitions=parts,
-                                              qk=args.qk, partition_size=size or None, partials_only=True),
-            args.steps, args.warmup)["median_us"]
-    kernel_gbs = nbytes / (kernel_us * 1e-6) / 1e9
-    profiled = PROFILED_TRAFFIC.get((cfg.index, kernel, head["partition_size"]))
+            lambda: hip_attention.attend_with(step.q, pool(), meta, out, scale=cfg.scale, partitions=None,
+                                              partials_only=True), args.steps, args.warmup)["median_us"]
+    else:
+        kernel_us = result["median_us"]
+    us = result["median_us"]
+    record = {
+        "us_per_call": round(us, 2),
+        "gbs": round(nbytes / us / 1e3, 1),
+        "hbm_fraction": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+        "launch": f"v1, {auto.v1_waves} waves per head" if not auto.partitions else
+                  f"v2 x{auto.partitions} partitions of {auto.partition_size}, merge {merge}",
+        "kernel": kernel,
+        "kernel_us": round(kernel_us, 2),
+        "kernel_gbs": round(nbytes / kernel_us / 1e3, 1),
+        "kernel_hbm_fraction": round(nbytes / kernel_us / 1e3 / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes": nbytes,
+        "pools": len(pools),
+    }
+    if len(pools) > 1:  # the same call over one pool: what the Infinity Cache serves
+        record["cache_resident_us"] = round(time_calls(
+            lambda: hip_attention.attend(step.q, buffers, meta, out, scale=cfg.scale), args.steps,
+            args.warmup)["median_us"], 2)
+    print(f"[bench] C{index} {cfg.name} {codec}: {us:.1f} us/call {nbytes / us / 1e3:.0f} GB/s "
+          f"({record['launch']}; kernel {kernel_us:.1f} us, {len(pools)} pools)", file=sys.stderr, flush=True)
+    if not headline:
+        del pools, step, buffers
+        torch.cuda.empty_cache()
+        return record
+
+    # The headline: the other launches of the same step, then the bench line.
+    max_len = max(cfg.lengths)
+    best_v2 = hip_attention.choose_split(cfg.batch, cfg.kv_heads, group, max_len, row_lengths=cfg.lengths,
+                                         kv_bytes=kv_bytes, v1=False)
+    launches = {
+        "v1": dict(partitions=0),
+        "v2": dict(partitions=-(-max_len // hip_attention.PARTITION_SIZE),
+                   partition_size=hip_attention.PARTITION_SIZE),
+        "v2-best": dict(partitions=best_v2.partitions, partition_size=best_v2.partition_size or None),
+    }
+    kernels = {"auto": {"us_per_call": record["us_per_call"], "gbs": record["gbs"], "launch": record["launch"]}}
+    if not args.only:
+        for name, launch in launches.items():
+            r = time_calls(lambda launch=launch: hip_attention.attend_with(step.q, pool(), meta, out, scale=cfg.scale,
+                                                                          qk=args.qk, **launch),
+                           args.steps, args.warmup, repeats=3)
+            kernels[name] = {"us_per_call": round(r["median_us"], 2), "gbs": round(nbytes / r["median_us"] / 1e3, 1),
+                             **{k: v for k, v in launch.items() if v is not None}}
+            print(f"[bench] {cfg.name} {name}: {r['median_us']:.1f} us/call", file=sys.stderr, flush=True)
+    store_us = time_calls(lambda: hip_kvcache.store(step.k_new, step.v_new, buffers, write), 50, 5)["median_us"]
+    profiled = PROFILED_TRAFFIC.get((cfg.index, kernel, auto.partition_size))
     line = {
         "metric": "decode-attention µs/call + achieved HBM GB/s (% of peak) at 1 MI355X",
-        "value": round(head["gbs"], 1),
+        "value": record["gbs"],
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(head["wall_ms_per_step"], 4),
-        "us_per_call": round(head["median_us"], 2),
-        "hbm_fraction": round(head["gbs"] / HBM_PEAK_GBS, 4),
+        "ms_per_step": round(result["wall_ms_per_step"], 4),
+        "us_per_call": record["us_per_call"],
+        "hbm_fraction": record["hbm_fraction"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -418,22 +508,19 @@ def main() -> int:
                         f"context {min(cfg.lengths)}-{max(cfg.lengths)} (sum {sum(cfg.lengths)}), "
                         f"pool {cfg.num_blocks} blocks",
             "algorithmic_bytes_per_call": nbytes,
-            "launch": "v1" if head["partitions"] == 0 else f"v2 x{head['partitions']} partitions of "
-                                                          f"{head['partition_size']}",
+            "launch": record["launch"],
         },
-        "kernels": {k: {"us_per_call": round(v["median_us"], 2), "gbs": round(v["gbs"], 1),
-                        "partitions": v["partitions"], "partition_size": v["partition_size"]}
-                    for k, v in results.items()},
+        "kernels": kernels,
         "kv_write": {"us_per_call": round(store_us, 2), "rows": int(step.k_new.shape[0]),
                      "bytes": workloads.store_bytes(cfg, kv_bytes)},
         "roofline": {
             "bound": "hbm",
             "kernel": kernel,
-            "kernel_us": round(kernel_us, 2),
-            "achieved": round(kernel_gbs, 1),
+            "kernel_us": record["kernel_us"],
+            "achieved": record["kernel_gbs"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+            "frac": record["kernel_hbm_fraction"],
             "traffic": None if profiled is None else profiled[0] + profiled[1],
             "traffic_read_write": None if profiled is None else [profiled[0], profiled[1]],
             "traffic_source": None if profiled is None else profiled[2],
@@ -441,8 +528,8 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(step, cfg, args.cpu_rows, kv_bytes)
-    print(json.dumps(line), flush=True)
-    return 0
+    record["line"] = line
+    return record
 
 
 if __name__ == "__main__":

@@ -51,7 +51,14 @@ enum {
   AYK_FLAG_PARTIALS_ONLY = 4, /* v2: run only the partition kernel (rows of several partitions are not
                                  written); for timing it */
   AYK_FLAG_SEPARATE_REDUCE = 8, /* v2: merge partitions in a second kernel even when arrivals is given */
-  AYK_FLAG_SINGLE_LAUNCH = 16   /* v2: merge partitions in the partition kernel (needs arrivals) */
+  AYK_FLAG_SINGLE_LAUNCH = 16,  /* v2: merge partitions in the partition kernel (needs arrivals) */
+  /* v1: how many waves share each (row, key/value head)'s context, each streaming every
+   * n-th chunk, merged in LDS at the end (at most one of these; none lets the library pick:
+   * the most, up to 8, that keep rows x heads x waves within one round of the GPU) */
+  AYK_FLAG_V1_WAVES_1 = 32,
+  AYK_FLAG_V1_WAVES_2 = 64,
+  AYK_FLAG_V1_WAVES_4 = 128,
+  AYK_FLAG_V1_WAVES_8 = 256
 };
 enum { AYK_LAYOUT_NHD = 0, AYK_LAYOUT_HND = 1 };
 
@@ -89,9 +96,13 @@ int ayk_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void
                                void* stream);
 
 /*
- * Paged attention, single pass ("v1"): one workgroup per (row, key/value head)
- * streams every page of that row's context once and serves the query heads of
- * the group from it. Replaces the reference's decode attention,
+ * Paged attention, single pass ("v1"): every page of a row's context is streamed
+ * once per key/value head, in one launch and with no scratch. A workgroup serves
+ * one row and 8 / n of its key/value heads, n waves per head (n = 1, 2, 4 or 8, see
+ * AYK_FLAG_V1_WAVES_*): each wave streams every n-th 16-position chunk and serves
+ * the head's query heads from it, and the waves' states are merged in LDS, in wave
+ * order. So the grid has rows x heads x n / 8 workgroups: C3's 64 rows fill the
+ * GPU's 256 compute units with n = 4. Replaces the reference's decode attention,
  * python/ayaka/ops/backends/torch/attention.py:237-271 (_attend_decode), and
  * the row-causal multi-row path of the same file, :209-234.
  *

@@ -66,7 +66,9 @@ def _v1(lib: ctypes.CDLL, **kw: object) -> int:
         ({"q": None}, 1, b"null"),
         ({"stride": 2}, 1, b"table_stride"),
         ({"flags": 3}, 1, b"exclude each other"),
-        ({"flags": 32}, 1, b"unknown flags"),
+        ({"flags": 1024}, 1, b"unknown flags"),
+        ({"flags": 32 | 64}, 1, b"at most one AYK_FLAG_V1_WAVES"),
+        ({"flags": 1 | 128}, 2, b"does not split a context"),
     ],
 )
 def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, message: bytes) -> None:

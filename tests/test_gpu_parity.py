@@ -326,6 +326,35 @@ def test_split_partitions_agree_with_the_oracle_and_v1(dtype: str, head_dim: int
     assert_parity(auto, expected, dtype, "auto")
 
 
+@pytest.mark.parametrize("waves", [1, 2, 4, 8])
+@pytest.mark.parametrize("heads,kv_heads,head_dim,dtype", [(8, 2, 64, "fp16"), (32, 8, 128, "bf16"),
+                                                           (4, 4, 256, "bf16"), (16, 1, 128, "fp16"),
+                                                           (40, 10, 128, "bf16"), (9, 3, 64, "bf16")])
+def test_v1_context_split_among_waves(waves: int, heads: int, kv_heads: int, head_dim: int, dtype: str) -> None:
+    # v1 with each (row, key/value head)'s context shared by 1-8 waves (every n-th chunk each,
+    # states merged in LDS in wave order): contexts shorter than one chunk per wave, ending
+    # inside blocks and chunks, a padding row, and a head count that leaves a workgroup's
+    # last head slots idle (10 heads at 8 / waves per workgroup)
+    s = build_scenario([(1, 1), (1, 17), (1, 0), (1, 2047), (1, 300), (1, 64), (1, 95)], dtype=dtype,
+                       heads=heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16, mode="decode", seed=93)
+    expected = s.expected(np.float64)
+    out = run_attention(s, 0, "mfma", v1_waves=waves)
+    assert_parity(out, expected, dtype, f"v1/{waves} waves")
+    assert torch.count_nonzero(out[2]) == 0
+    again = run_attention(s, 0, "mfma", v1_waves=waves)
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+
+
+@pytest.mark.parametrize("block_size", [1, 2])
+def test_v1_context_split_across_table_segments(block_size: int) -> None:
+    # one- and two-position blocks: each wave's chunks cross the staged table segments
+    s = build_scenario([(1, 1300), (1, 1100), (1, 3)], block_size=block_size, head_dim=128, heads=8,
+                       kv_heads=2, mode="decode", seed=94)
+    expected = s.expected(np.float64)
+    for waves in (2, 8):
+        assert_parity(run_attention(s, 0, "mfma", v1_waves=waves), expected, "bf16", f"bs{block_size}/{waves}")
+
+
 # --- fp8 e4m3 codec ---------------------------------------------------------------------------
 
 
@@ -383,6 +412,8 @@ def test_fp8_attention_matches_the_oracle_on_decoded_values(dtype: str, layout: 
     q = to_device(s.q_bits, dtype)
     padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
     launches = [("v1", dict(partitions=0, prefill=False)),
+                ("v1/1 wave", dict(partitions=0, prefill=False, v1_waves=1)),
+                ("v1/8 waves", dict(partitions=0, prefill=False, v1_waves=8)),
                 ("v2/in-kernel", dict(partitions=6, partition_size=256, merge="in-kernel", prefill=False)),
                 ("v2/reduce-kernel", dict(partitions=6, partition_size=256, merge="reduce-kernel", prefill=False)),
                 ("auto", dict(partitions=None))]
@@ -439,7 +470,7 @@ def test_single_launch_merge_agrees_with_the_reduce_kernel(qk: str, heads: int, 
 def test_one_partition_reproduces_v1_bit_for_bit(qk: str) -> None:
     s = build_scenario([(1, 300), (1, 17), (1, 512)], heads=8, kv_heads=2, head_dim=128, block_size=16,
                        mode="decode", seed=53)
-    v1 = run_attention(s, 0, qk)
+    v1 = run_attention(s, 0, qk, v1_waves=1)
     v2 = run_attention(s, 1, qk)
     assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
 

@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from ayaka_amd import backend as registry
+from ayaka_amd import workloads
 from ayaka_amd.enums import DType, ForwardMode, KVLayoutKind
 from ayaka_amd.errors import BackendError, CapabilityError, ConfigError
 from ayaka_amd.hip import attention as hip_attention
@@ -178,6 +179,26 @@ def test_the_split_covers_every_context_and_follows_the_modelled_schedule() -> N
     assert choose(64, 8, 4, 4096) == choose(64, 8, 4, 4096, row_lengths=(4096,) * 64)
     assert hip_attention.head_chunks(4) == 1 and hip_attention.head_chunks(12) == 2
     assert hip_attention.head_chunks(16) == 2 and hip_attention.head_chunks(11) == 11
+
+
+def test_v1_with_a_wave_split_is_chosen_where_it_models_faster() -> None:
+    choose = hip_attention.choose_split
+    hip_attention._split_cache.clear()
+    # C3: 64 rows of 4096 at 8 key/value heads: v1, each context split among 4 waves (256
+    # workgroups of 2 heads), which models (and measured) faster than any v2 launch
+    assert choose(64, 8, 4, 4096, row_lengths=(4096,) * 64) == hip_attention.Split(0, 0, 4)
+    assert choose(64, 8, 4, 4096, row_lengths=(4096,) * 64, kv_bytes=1) == hip_attention.Split(0, 0, 4)
+    # without v1, the best v2 launch: one round of 1024-position partitions
+    assert choose(64, 8, 4, 4096, row_lengths=(4096,) * 64, v1=False) == hip_attention.Split(1024, 4)
+    # a few long rows (C4) and a ragged batch stay on v2
+    assert choose(8, 8, 4, 32768, row_lengths=(8192, 16384, 24576, 32768, 32768, 32768, 12288, 2048)).partitions
+    lengths = workloads.config(5).lengths  # log-uniform in [16, 16384]
+    assert choose(256, 8, 8, max(lengths), row_lengths=lengths).partitions
+    # graph replays (a minimum partition size) never take the v1 candidate
+    assert choose(64, 8, 4, 4096, row_lengths=(4096,) * 64, min_size=64).partitions
+    # the model: a wave's share of its row, in 16-position chunks, plus the fixed cost
+    assert hip_attention.v1_makespan([4096] * 64, 4, 8, 240) == 1024 + 240
+    assert hip_attention.v1_makespan([4096] * 64, 8, 8, 240) == 2 * (512 + 240)
 
 
 def test_the_modelled_schedule() -> None:

@@ -199,6 +199,23 @@ def test_attention_matches_a_brute_force(name: str, steps: list, mode: str, head
     np.testing.assert_allclose(s.expected(np.float32), expected, rtol=0, atol=2e-6)
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(4, 4), (4, 2), (6, 1), (8, 4)])
+def test_torch_decode_restatement_matches_the_brute_force(heads: int, kv_heads: int) -> None:
+    # the CPU baseline's torch restatement of _attend_decode: whole padded tables (NaN in the
+    # unused slots and block 0), a padding request, lengths ending inside blocks
+    from oracle.torch_decode import attend_decode
+
+    s = build_scenario([(1, 6), (1, 0), (1, 2), (1, 9), (1, 4)], heads=heads, kv_heads=kv_heads, head_dim=8,
+                       mode="decode", seed=12)
+    expected = brute_force(s)
+    got = attend_decode(torch.from_numpy(s.q).double(), torch.from_numpy(paged.nhd(s.k, s.layout)).double(),
+                        torch.from_numpy(paged.nhd(s.v, s.layout)).double(), torch.from_numpy(s.table),
+                        torch.tensor(s.lengths), scale=s.scale)
+    assert torch.isfinite(got).all()
+    np.testing.assert_allclose(got.numpy(), expected, rtol=0, atol=2e-6)
+    assert not got[1].any()
+
+
 def test_attention_matches_torch_sdpa() -> None:
     steps = [(1, 70), (1, 17), (3, 40), (1, 1)]
     s = build_scenario(steps, heads=12, kv_heads=4, head_dim=64, block_size=16, seed=5)
