@@ -608,11 +608,11 @@ def choose_split(
                 if best is None or t < best[0]:
                     best = (t, ws)
             if v2 is None or best[0] < v2:
-                size, waves = max_length, best[1]
+                size, waves = 0, best[1]  # v1 (the key covers other lengths: no size is kept)
         found = (size, waves)
         _split_cache[key] = found
     size, waves = found
-    if max_length <= size:
+    if not size or max_length <= size:
         return Split(0, 0, waves)
     return Split(size, -(-max_length // size))
 
@@ -960,7 +960,8 @@ def attend_with(
                 staged = step.staged
                 split = Split(step.min_size, step.partitions)
         partitions, partition_size = split.partitions, split.partition_size
-        v1_waves = v1_waves or split.v1_waves or None
+        # a forced DPP q.k streams each head's context in one wave
+        v1_waves = v1_waves or (split.v1_waves if qk != "dpp" else None) or None
     partition_size = partition_size or PARTITION_SIZE
     if partitions and partitions * partition_size < max_length:
         raise BackendError(

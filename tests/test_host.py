@@ -194,6 +194,9 @@ def test_v1_with_a_wave_split_is_chosen_where_it_models_faster() -> None:
     assert choose(8, 8, 4, 32768, row_lengths=(8192, 16384, 24576, 32768, 32768, 32768, 12288, 2048)).partitions
     lengths = workloads.config(5).lengths  # log-uniform in [16, 16384]
     assert choose(256, 8, 8, max(lengths), row_lengths=lengths).partitions
+    # a cached v1 choice serves every step of the same signature (a longer one included)
+    assert choose(4, 3, 3, 121, row_lengths=(121, 100, 90, 64)) == choose(4, 3, 3, 127, row_lengths=(127, 100, 90, 64))
+    assert choose(4, 3, 3, 127, row_lengths=(127, 100, 90, 64)).partitions == 0
     # graph replays (a minimum partition size) never take the v1 candidate
     assert choose(64, 8, 4, 4096, row_lengths=(4096,) * 64, min_size=64).partitions
     # the model: a wave's share of its row, in 16-position chunks, plus the fixed cost
