@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
@@ -231,6 +232,39 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   return launched(err, op);
 }
 
+// Scratch of ayk_paged_attention_v2_static: one array per device, held until the process
+// ends; partials (and their (m, l)) first, then the arrival counters, which are zero when
+// the code object loads and which every call leaves at zero.
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+constexpr size_t kStaticCounterWords = size_t(1) << 18;  // 1 MiB of uint32 counters at the end
+constexpr size_t kStaticPartialBytes = kStaticScratchBytes - kStaticCounterWords * sizeof(uint32_t);
+static_assert(kStaticPartialBytes == AYK_V2_STATIC_SCRATCH_BYTES, "the header states the partials' capacity");
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+// The device address of `scratch` on the current device, looked up once per device
+// (hipGetSymbolAddress with that device current); nullptr with an error set on failure.
+// The array's name is a host-side stand-in: only this address may reach a kernel.
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+void* static_scratch(const char* op) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(AYK_ERR_LAUNCH, "%s: no current device (%s)", op, hipGetErrorString(err));
+    return nullptr;
+  }
+  void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr) return ptr;
+  err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (err != hipSuccess || !ptr) {
+    fail(AYK_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) on device %d: %s", op, dev, hipGetErrorString(err));
+    return nullptr;
+  }
+  g_scratch_ptr[dev].store(ptr, std::memory_order_release);  // two threads may race here: same address
+  return ptr;
+}
+
 }  // namespace
 
 extern "C" {
@@ -365,6 +399,41 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
   p.max_len = (int32_t)std::min<int64_t>(p.max_len, (int64_t)partition_size * max_partitions);
   return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, kv_dtype == AYK_DTYPE_FP8_E4M3, true, flags,
                 stream);
+}
+
+int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                  const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
+                                  const int32_t* request_of_row, const int32_t* positions, int32_t n_rows,
+                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                                  int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
+                                  int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
+                                  const int32_t* work_items, int32_t n_work_items, const int32_t* staged,
+                                  int32_t flags, void* stream) {
+  const char* op = "ayk_paged_attention_v2_static";
+  const int32_t slot_rows = staged ? n_work_items : n_rows;
+  const int32_t slots_per_row = staged ? 1 : max_partitions;
+  const size_t need = ayk_paged_attention_v2_workspace_bytes(slot_rows, num_heads, head_dim, slots_per_row);
+  if (need > kStaticPartialBytes)
+    return fail(AYK_ERR_WORKSPACE,
+                "%s: this call needs %zu bytes of scratch; the static scratch holds %zu (use ayk_paged_attention_v2 "
+                "with a workspace)",
+                op, need, kStaticPartialBytes);
+  if (n_rows <= 0 || num_heads <= 0) {  // nothing to launch: the checks of the allocating entry point apply
+    return ayk_paged_attention_v2(out, q, k_cache, v_cache, block_table, table_stride, kv_lengths, request_of_row,
+                                  positions, n_rows, num_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                                  max_blocks, layout, dtype, kv_dtype, scale, partition_size, max_partitions,
+                                  work_items, n_work_items, staged, nullptr, 0, nullptr, flags, stream);
+  }
+  unsigned char* base = static_cast<unsigned char*>(static_scratch(op));
+  if (!base) return AYK_ERR_LAUNCH;
+  // counters for the single launch only when every (row, head) has one
+  uint32_t* counters = (int64_t)n_rows * num_heads <= (int64_t)kStaticCounterWords
+                           ? reinterpret_cast<uint32_t*>(base + kStaticPartialBytes)
+                           : nullptr;
+  return ayk_paged_attention_v2(out, q, k_cache, v_cache, block_table, table_stride, kv_lengths, request_of_row,
+                                positions, n_rows, num_heads, num_kv_heads, head_dim, num_blocks, block_size,
+                                max_blocks, layout, dtype, kv_dtype, scale, partition_size, max_partitions, work_items,
+                                n_work_items, staged, base, kStaticPartialBytes, counters, flags, stream);
 }
 
 int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,

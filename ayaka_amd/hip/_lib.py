@@ -49,6 +49,12 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
          _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
          _I32, _I32, _P, _I32, _P, _P, _SZ, _P, _I32, _P],
     ),
+    "ayk_paged_attention_v2_static": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _P, _I64, _P, _P, _P,
+         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
+         _I32, _I32, _P, _I32, _P, _I32, _P],
+    ),
     "ayk_paged_prefill_tile_pairs": (ctypes.c_int, [_I32]),
     "ayk_paged_prefill": (
         ctypes.c_int,

@@ -182,6 +182,30 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            void* stream);
 
 /*
+ * ayk_paged_attention_v2 for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference:
+ * the same arguments, semantics and kernels as ayk_paged_attention_v2 without `workspace`,
+ * `workspace_bytes` and `arrivals`. The partials live in a static device array of the
+ * library (64 MiB per device, held from the first call on a device until the process
+ * ends): AYK_V2_STATIC_SCRATCH_BYTES of partials, then 2^18 arrival counters, zero when the
+ * library loads and left at zero by every call. A call whose partials need more (see
+ * ayk_paged_attention_v2_workspace_bytes) is refused with AYK_ERR_WORKSPACE; one of more
+ * than 2^18 (row, head) pairs merges in the reduce kernel. Nothing is allocated, freed or
+ * synchronised. Every call on a device shares that device's array: calls that overlap in
+ * time on one device (other streams, other threads) race, and must be serialised by the
+ * caller.
+ */
+#define AYK_V2_STATIC_SCRATCH_BYTES ((size_t)63 << 20)
+int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                  const int32_t* block_table, int64_t table_stride, const int32_t* kv_lengths,
+                                  const int32_t* request_of_row, const int32_t* positions, int32_t n_rows,
+                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
+                                  int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
+                                  int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
+                                  const int32_t* work_items, int32_t n_work_items, const int32_t* staged,
+                                  int32_t flags, void* stream);
+
+/*
  * Multi-row paged attention (prefill chunks, verify windows): the rows of each
  * request are its last rows, row i at position positions[i] attends to
  * [0, positions[i]] of its request's context; rows of a request with
