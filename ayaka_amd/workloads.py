@@ -203,13 +203,10 @@ def sample_rows(step: Step, rows: list[int]) -> dict[str, np.ndarray]:
     table = step.table[rows].cpu().numpy().astype(np.int64)
     lengths = step.lengths[rows].cpu().numpy().astype(np.int64)
     bs = step.config.block_size
-    ids = sorted({int(x) for b in range(len(rows)) for x in table[b, : -(-int(lengths[b]) // bs)]})
-    remap = {old: new + 1 for new, old in enumerate(ids)}
-    new_table = np.zeros_like(table)
-    for b in range(len(rows)):
-        n = -(-int(lengths[b]) // bs)
-        new_table[b, :n] = [remap[int(x)] for x in table[b, :n]]
-    index = torch.tensor(ids, dtype=torch.int64, device=step.k_cache.device)
+    used = np.arange(table.shape[1])[None, :] < -(-lengths[:, None] // bs)  # the table entries each row reads
+    ids = np.unique(table[used])
+    new_table = np.where(used, np.searchsorted(ids, table) + 1, 0)
+    index = torch.from_numpy(ids).to(step.k_cache.device)
     k_nhd, v_nhd = step.k_cache[index], step.v_cache[index]
     if k_nhd.shape[1] != bs:  # HND caches: back to [block, offset, head, dim]
         k_nhd, v_nhd = k_nhd.permute(0, 2, 1, 3), v_nhd.permute(0, 2, 1, 3)

@@ -157,3 +157,27 @@ def brute_force(s: Scenario) -> np.ndarray:
                             out[row, h, d] += weights[pos] / total * float(v[blk, off, kvh, d])
             row += 1
     return out
+
+
+def oracle_rows(step, rows: list[int], precision: type = np.float64, chunk: int = 16) -> np.ndarray:
+    """The oracle's output for decode rows ``rows`` of a ``workloads`` step.
+
+    Rows are taken ``chunk`` at a time in order of length, each chunk with its table cut to
+    the blocks its longest row reads: the oracle gathers a padded table per row, and on a
+    ragged batch the full width would multiply its work (same semantics: what lies past a
+    row's length is masked either way).
+    """
+    from ayaka_amd import workloads
+    from oracle import paged
+
+    sample = workloads.sample_rows(step, rows)
+    bs = step.config.block_size
+    order = np.argsort(sample["lengths"], kind="stable")
+    out = np.zeros((len(rows), *sample["q"].shape[1:]), dtype=precision)
+    for start in range(0, len(rows), chunk):
+        pick = order[start:start + chunk]
+        width = max(1, -(-int(sample["lengths"][pick].max()) // bs))
+        out[pick] = paged.attention(sample["q"][pick], sample["k"], sample["v"], sample["table"][pick, :width],
+                                    sample["lengths"][pick], scale=step.config.scale, precision=precision,
+                                    chunk=chunk)
+    return out

@@ -14,6 +14,8 @@ backend's ops, and once directly with ctypes). Bars:
 from __future__ import annotations
 
 import ctypes
+import json
+import os
 from pathlib import Path
 
 import numpy as np
@@ -29,7 +31,7 @@ from ayaka_amd.hip import kvcache as hip_kvcache
 from ayaka_amd.kvcache import FP8_E4M3_CODEC, RAW_CODEC, KVBuffers
 from oracle import paged
 from oracle.numerics import bits_to_f32, e4m3_to_f32, f32_to_bits, f32_to_e4m3, parity_report
-from tests._support import Scenario, build_scenario
+from tests._support import Scenario, build_scenario, oracle_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -255,12 +257,15 @@ def test_multi_row_partitions_across_table_segments(block_size: int) -> None:
 
 @pytest.mark.parametrize("launch", [dict(partitions=0), dict(partitions=None, partition_size=128)],
                          ids=["whole", "partitions"])
-def test_multi_row_step_in_a_captured_graph(launch: dict) -> None:
+@pytest.mark.parametrize("steps", [[(40, 600), (3, 3), (7, 300)], [(4, 600), (3, 3), (1, 300), (2, 0)]],
+                         ids=["multi-row-kernel", "window-launch"])
+def test_multi_row_step_in_a_captured_graph(launch: dict, steps: list) -> None:
     # an eagerly planned multi-row step captures once it has run eagerly (its tile list and
-    # workspace exist); every replay, with eager work between, matches the eager call
-    s = build_scenario([(40, 600), (3, 3), (7, 300)], heads=8, kv_heads=2, head_dim=128, block_size=16,
-                       mode="mixed", seed=46)
+    # workspace exist); every replay, with eager work between, matches the eager call. With at
+    # most 16 / G rows per request the step takes the decode kernel's window launch.
+    s = build_scenario(steps, heads=8, kv_heads=2, head_dim=128, block_size=16, mode="mixed", seed=46)
     buffers, meta = scenario_buffers(s), plan_scenario(s)
+    assert (meta.plan.window_pairs(4) > 0) == (max(rows for rows, _ in steps) <= 4)
     q = to_device(s.q_bits, s.dtype)
     eager, out = torch.full_like(q, 7.0), torch.full_like(q, 7.0)
     hip_attention.attend_with(q, buffers, meta, eager, scale=s.scale, prefill=True, **launch)
@@ -539,11 +544,20 @@ def test_golden_fixture() -> None:
 
 # --- benchmark configurations at full size --------------------------------------------------
 
-SAMPLES = {1: [0, 1, 2, 3], 2: list(range(32)), 3: [0, 21, 42, 63], 4: [0, 3, 7], 5: None}
+def _report(out: torch.Tensor, e32: np.ndarray, e64: np.ndarray, dtype: str) -> dict:
+    """The north star's raw figures against the float32 oracle (max-abs, relative L2), and the
+    net-of-rounding ones against the float64 oracle that the tests bound."""
+    got = out.float().cpu().numpy().astype(np.float64)
+    norm = float(np.linalg.norm(e32)) or 1.0
+    net = parity_report(got, e64, dtype)
+    return {"max_abs": float(np.abs(got - e32).max()), "rel_l2": float(np.linalg.norm(got - e32)) / norm,
+            "max_abs_excess_fp64": net["max_abs_excess"], "rel_l2_rounded_fp64": net["rel_l2"]}
 
 
 @pytest.mark.parametrize("index", [1, 2, 3, 4, 5])
 def test_benchmark_configuration(index: int) -> None:
+    # every row of every configuration against the oracle; the raw figures (ours, and the
+    # reference's own rounding of the float32 result) are written to $AYAKA_PARITY_DIR
     cfg = workloads.config(index)
     print(f"config {index} {cfg.name}", flush=True)
     step = workloads.build(cfg, DEV)
@@ -571,22 +585,52 @@ def test_benchmark_configuration(index: int) -> None:
                                   merge=merge)
         outs[name] = out
     torch.cuda.synchronize()
-    rows = SAMPLES[index]
-    if rows is None:  # the shortest, the longest and a spread between
-        order = np.argsort(cfg.lengths)
-        rows = sorted({int(order[0]), int(order[-1]), *[int(order[i]) for i in range(0, cfg.batch, 37)]})
-    sample = workloads.sample_rows(step, rows)
-    expected = paged.attention(sample["q"], sample["k"], sample["v"], sample["table"], sample["lengths"],
-                               scale=cfg.scale, precision=np.float64)
+    rows = list(range(cfg.batch))
+    expected = oracle_rows(step, rows, np.float64)
+    e32 = oracle_rows(step, rows, np.float32).astype(np.float64)
     for name, out in outs.items():
-        assert_parity(out[rows], expected, cfg.dtype_label, f"config {index} {name}")
-    # size-independent: v1 and v2 agree on every row, and every row is finite
-    for out in outs.values():
-        assert torch.isfinite(out.float()).all()
+        assert_parity(out, expected, cfg.dtype_label, f"config {index} {name}")
     assert counters_are_clear()
-    for name in ("v1-mfma", "v2-dpp", "v2-mfma", "v2-reduce-kernel", "v2-in-kernel"):
-        diff = (outs["v1-dpp"].float() - outs[name].float()).abs().max().item()
-        assert diff <= 4 * EPS[cfg.dtype_label] * outs["v1-dpp"].float().abs().max().item() + 1e-6, name
+    rounded = bits_to_f32(f32_to_bits(e32.astype(np.float32), cfg.dtype_label), cfg.dtype_label)
+    split = decode.plan.split_for(cfg.kv_heads, cfg.heads // cfg.kv_heads)
+    record = {
+        "config": f"C{index} {cfg.name}", "dtype": cfg.dtype_label, "rows": cfg.batch,
+        "auto_launch": f"v1, {split.v1_waves} waves" if not split.partitions else
+                       f"v2, {split.partitions} x {split.partition_size}",
+        "reference_rounding": _report(torch.from_numpy(rounded), e32, expected, cfg.dtype_label),
+        **{name: _report(outs[name], e32, expected, cfg.dtype_label) for name in ("auto", "v1-mfma", "v2-mfma")},
+    }
+    target = os.environ.get("AYAKA_PARITY_DIR")
+    if target:
+        Path(target).mkdir(parents=True, exist_ok=True)
+        (Path(target) / f"parity_c{index}.json").write_text(json.dumps(record, indent=1))
+
+
+def test_full_size_verify_windows() -> None:
+    # the benchmark's verify-window step (32 requests x 4 rows over 4K, Llama-3-8B shape) on the
+    # window launch, every row against the oracle
+    requests, rows, context, bs = 32, 4, 4096, 16
+    gen = torch.Generator(device=DEV).manual_seed(4)
+    blocks = requests * context // bs + 1
+    k = torch.randn((blocks, bs, 8, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    v = torch.randn((blocks, bs, 8, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    k[0], v[0] = float("nan"), float("nan")
+    ids = torch.randperm(blocks - 1, generator=gen, device=DEV) + 1
+    table = ids.view(requests, context // bs).to(torch.int32)
+    meta = hip_attention.plan(ForwardMode.MIXED, torch.full((requests,), rows, dtype=torch.int32, device=DEV),
+                              torch.full((requests,), context, dtype=torch.int32, device=DEV), table, bs)
+    assert meta.plan.window_pairs(4) > 0
+    q = torch.randn((requests * rows, 32, 128), generator=gen, device=DEV).to(torch.bfloat16)
+    buffers = KVBuffers(k, v, KVLayoutKind.NHD, RAW_CODEC)
+    for launch in (dict(partitions=None), dict(partitions=0)):
+        out = torch.full_like(q, 7.0)
+        hip_attention.attend_with(q, buffers, meta, out, scale=128 ** -0.5, prefill=True, window=True, **launch)
+        torch.cuda.synchronize()
+        expected = paged.attention(q.float().cpu().numpy(), k.float().cpu().numpy(), v.float().cpu().numpy(),
+                                   table.cpu().numpy(), np.full(requests, context),
+                                   request_of_row=meta.request_of_row.cpu().numpy(),
+                                   positions=meta.positions.cpu().numpy(), scale=128 ** -0.5, precision=np.float64)
+        assert_parity(out, expected, "bf16", f"windows {launch}")
 
 
 # --- graph metadata and capture ---------------------------------------------------------------
