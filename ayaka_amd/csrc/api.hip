@@ -40,11 +40,15 @@ int launched(hipError_t err, const char* what) {
   return ok();
 }
 
-int log2_exact(int32_t v) {
-  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+// The kernels' division of a position by the block size (block_of in attention_common.h):
+// shift l = ceil(log2 bs) and magic m = floor(2^32 (2^l - bs) / bs) + 1, exact for every
+// position below 2^31 (Granlund and Montgomery's round-up method; checked exhaustively on
+// the host for every block size up to 300 and sampled ones up to 65536).
+void block_divisor(int32_t bs, uint32_t& magic, int32_t& shift) {
   int s = 0;
-  while ((1 << s) < v) ++s;
-  return s;
+  while ((1 << s) < bs) ++s;
+  shift = s;
+  magic = (uint32_t)(((uint64_t)1 << 32) * (((uint64_t)1 << s) - (uint64_t)bs) / (uint64_t)bs + 1);
 }
 
 // Split a group of query heads into equal chunks of at most 8 heads (one workgroup each).
@@ -85,13 +89,13 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
     return fail(AYK_ERR_ARGUMENT,
                 "%s: %d query heads is not a positive multiple of %d key/value heads", op,
                 c.num_heads, c.num_kv_heads);
-  const int shift = log2_exact(c.block_size);
-  if (shift < 0 || shift > 16)
-    return fail(AYK_ERR_UNSUPPORTED, "%s: block_size %d is not a power of two up to 65536", op,
-                c.block_size);
+  if (c.block_size < 1 || c.block_size > 65536)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: block_size %d is not in [1, 65536]", op, c.block_size);
   if (c.num_blocks <= 0 || c.max_blocks < 0 || c.table_stride < c.max_blocks)
     return fail(AYK_ERR_ARGUMENT, "%s: num_blocks %d, max_blocks %d, table_stride %lld", op,
                 c.num_blocks, c.max_blocks, (long long)c.table_stride);
+  if (c.max_blocks >= (1 << 24))
+    return fail(AYK_ERR_UNSUPPORTED, "%s: a table of %d blocks per row exceeds 2^24", op, c.max_blocks);
   if ((c.request_of_row == nullptr) != (c.positions == nullptr))
     return fail(AYK_ERR_ARGUMENT, "%s: request_of_row and positions are given together or not at all",
                 op);
@@ -133,8 +137,9 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
   p.head_chunks = chunks;
   p.num_virtual_heads = c.num_kv_heads * chunks;
   p.num_blocks = c.num_blocks;
-  p.bs_shift = shift;
-  const int64_t table_len = (int64_t)c.max_blocks << shift;
+  p.block_size = c.block_size;
+  block_divisor(c.block_size, p.bs_magic, p.bs_shift);
+  const int64_t table_len = (int64_t)c.max_blocks * c.block_size;
   p.max_len = (int32_t)std::min<int64_t>(table_len, INT32_MAX);
   p.scale_log2 = c.scale * 1.4426950408889634f;
   p.partition_size = INT32_MAX;

@@ -401,14 +401,22 @@ __device__ __forceinline__ void store_zero_rows(const AttnParams& p, int row, in
   }
 }
 
+// Block of position t (0 <= t < 2^31) for any block size: a multiply-high division by the
+// host's magic number, q = (umulhi(t, m) + t) >> l with l = ceil(log2 bs) and
+// m = floor(2^32 (2^l - bs) / bs) + 1 (a power of two has m = 1: a shift). The sum stays
+// below 2^32 because umulhi(t, m) < t < 2^31.
+__device__ __forceinline__ int block_of(const AttnParams& p, int t) {
+  return (int)((__umulhi((uint32_t)t, p.bs_magic) + (uint32_t)t) >> p.bs_shift);
+}
+
 // Stage the block-table entries of positions [s0, s1) in LDS as element offsets
 // of their blocks (block id x block stride; ids outside the pool become the
 // padding block 0); returns the first staged block index. The host checks that
 // every offset in the pool fits 32 bits.
 __device__ __forceinline__ int stage_table(const AttnParams& p, const int32_t* tbl, uint32_t* s_tbl, int s0, int s1,
                                            int tid, int threads) {
-  const int b0 = s0 >> p.bs_shift;
-  const int nb = ((s1 - 1) >> p.bs_shift) - b0 + 1;
+  const int b0 = block_of(p, s0);
+  const int nb = block_of(p, s1 - 1) - b0 + 1;
   __syncthreads();  // the previous segment is done with s_tbl
   for (int i = tid; i < nb; i += threads) {
     const int b = tbl[b0 + i];
@@ -471,11 +479,15 @@ __device__ __forceinline__ u32x2 lds_read_transposed(const uint16_t* p) {
       u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p)));
 }
 
-// Element offset of position t within its block: (t mod block size) x token
-// stride on the full-rate 24-bit multiplier (both factors are below 2^24: the
-// host refuses larger token strides).
-__device__ __forceinline__ uint32_t in_block(int t, int bs_mask, uint32_t token_stride) {
-  return __umul24((uint32_t)(t & bs_mask), token_stride);
+// Element offset of position t in the cache, from the staged table segment that starts at
+// block b0: its block's offset plus (t mod block size) x token stride, the products on the
+// full-rate 24-bit multiplier (the block index is below the table width and the token
+// stride below 2^24: the host refuses wider tables and strides).
+__device__ __forceinline__ uint32_t kv_offset(const AttnParams& p, const uint32_t* s_tbl, int b0, int t,
+                                              uint32_t token_stride) {
+  const int b = block_of(p, t);
+  const uint32_t r = (uint32_t)t - __umul24((uint32_t)b, (uint32_t)p.block_size);
+  return s_tbl[b - b0] + __umul24(r, token_stride);
 }
 
 }  // namespace ayk

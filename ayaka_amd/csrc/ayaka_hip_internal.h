@@ -39,7 +39,9 @@ struct AttnParams {
   int32_t head_chunks;  // chunks one group's heads are split into (group / head_chunks each)
   int32_t num_virtual_heads;  // num_kv_heads * head_chunks: the unit one wave serves
   int32_t num_blocks;
-  int32_t bs_shift;     // log2(block_size)
+  int32_t block_size;
+  uint32_t bs_magic;    // position t -> block (umulhi(t, bs_magic) + t) >> bs_shift, for any block
+  int32_t bs_shift;     // size (a power of two: bs_magic 1, bs_shift its log2)
   int32_t max_len;      // no row reads positions at or past this
   int32_t partition_size;
   int32_t max_partitions;

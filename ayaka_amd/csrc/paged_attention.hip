@@ -99,9 +99,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
   }
 
   const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
-  const int shift = p.bs_shift;
-  const int bs_mask = (1 << shift) - 1;
-  const int seg_len = (((kTableCap - 1) << shift) / CH) * CH;
+  // positions per staged table segment: at most kTableCap blocks, whatever s0's offset
+  const int seg_len = ((kTableCap - 1) * p.block_size / CH) * CH;
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + c * 8;
@@ -119,7 +118,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
 #pragma unroll
       for (int j = 0; j < NLD; ++j) {
         const int t = min(s0 + ci * CH + j * TPL + r, s1 - 1);
-        dst[j] = s_tbl[(t >> shift) - b0] + in_block(t, bs_mask, token_stride);
+        dst[j] = kv_offset(p, s_tbl, b0, t, token_stride);
       }
     };
 

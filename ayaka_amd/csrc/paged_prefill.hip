@@ -190,9 +190,8 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
   }
 
   const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
-  const int shift = p.bs_shift;
-  const int bs_mask = (1 << shift) - 1;
-  const int seg_len = (((kTableCap - 1) << shift) / CH) * CH;
+  // positions per staged table segment: at most kTableCap blocks, whatever s0's offset
+  const int seg_len = ((kTableCap - 1) * p.block_size / CH) * CH;
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride);
@@ -214,14 +213,16 @@ __global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const
 
     typedef typename KvRaw<KV8>::T Raw;
     Raw kr[PER_THREAD], vr[PER_THREAD];
-    // Offsets of the pieces at positions t and t + 1 (t even: the chunk and segment
-    // starts are multiples of CH), clamped to the last position: past the end a
-    // real position is read, whose weight is 0. Both positions share a block
-    // unless blocks hold one position.
+    // Offsets of the pieces at positions t and t + 1, clamped to the last position:
+    // past the end a real position is read, whose weight is 0. The second position is
+    // the next token of the first one's block, or the first token of the next block.
+    const uint32_t bs = (uint32_t)p.block_size;
     auto pair_offsets = [&](int t, uint32_t& o0, uint32_t& o1) {
       const int t0 = min(t, s1 - 1), t1 = min(t + 1, s1 - 1);
-      o0 = s_tbl[(t0 >> shift) - b0] + in_block(t0, bs_mask, token_stride);
-      o1 = shift ? o0 + (t1 > t0 ? token_stride : 0u) : s_tbl[t1 - b0];
+      const int b = block_of(p, t0);
+      const uint32_t r = (uint32_t)t0 - __umul24((uint32_t)b, bs);
+      o0 = s_tbl[b - b0] + __umul24(r, token_stride);
+      o1 = t1 == t0 ? o0 : r + 1 < bs ? o0 + token_stride : s_tbl[b + 1 - b0];
     };
     // Chunk ci into registers kr and vr; K and V pieces of the same two positions share
     // their offsets.

@@ -3,7 +3,7 @@
 The messages follow the reference's (``python/ayaka/ops/backends/torch/_checks.py:21-59``,
 ``kvcache.py:39-62``) so that callers and tests read the same refusals. The
 hip backend computes in fp16 and bf16 only, on HIP devices, for head widths of
-64, 128 and 256 and power-of-two block sizes; it stores the ``"raw"`` codec
+64, 128 and 256 and block sizes of 1 to 65536 positions; it stores the ``"raw"`` codec
 (fp16/bf16 caches) and ``"fp8_e4m3"`` (``float8_e4m3fn`` caches).
 """
 

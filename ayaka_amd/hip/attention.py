@@ -302,7 +302,9 @@ class HipGraphPlan:
     ``[partition size, item count, first partial slot of each row, row0, part0,
     ...]``; workgroups past the item count return at once, and the rows' partials
     are packed into ``capacity`` slots. ``head_shape`` holds the ``(num_kv_heads,
-    group, kv_bytes)`` of the first attend, which scores the staged split.
+    group, kv_bytes)`` of the first attend, which scores the staged split;
+    ``staged_shape`` the shape the last staged split was scored for (an update before
+    the first attend scores a guess, and that attend re-stages the split).
     """
 
     positions: torch.Tensor
@@ -316,6 +318,7 @@ class HipGraphPlan:
     partitions: int
     capacity: int
     head_shape: list = field(default_factory=list)
+    staged_shape: list = field(default_factory=list)
 
     @property
     def staged_partition_size(self) -> int:
@@ -717,7 +720,28 @@ _workspaces: dict[torch.device, torch.Tensor] = {}
 _retired: list[torch.Tensor] = []
 
 
-def _workspace(op: str, device: torch.device, nbytes: int, capture: bool) -> torch.Tensor:
+#: The stream (raw handle) whose calls last used each device's shared scratch and counters.
+_scratch_streams: dict[torch.device, int] = {}
+
+
+def _order_scratch(device: torch.device, stream: int, capture: bool) -> None:
+    """Order this call's use of the device's shared v2 scratch and arrival counters after
+    every use already queued on another stream: an event recorded now on that stream, which
+    this one waits for (one per change of stream; nothing when the stream stays the same).
+    A capture is ordered after its stream's earlier work by the capture itself; replays of a
+    captured graph must not overlap calls on another stream (they share the buffers)."""
+    last = _scratch_streams.get(device)
+    if capture:
+        return
+    if last is not None and last != stream:
+        event = torch.cuda.Event()
+        event.record(torch.cuda.ExternalStream(last, device=device))
+        torch.cuda.ExternalStream(stream, device=device).wait_event(event)
+    _scratch_streams[device] = stream
+
+
+def _workspace(op: str, device: torch.device, nbytes: int, capture: bool, stream: int) -> torch.Tensor:
+    _order_scratch(device, stream, capture)
     found = _workspaces.get(device)
     if found is not None and found.numel() >= nbytes:
         return found
@@ -843,11 +867,6 @@ def attend_with(
             context={"op": op, "argument": "buffers"},
         )
     block_size = buffers.block_size
-    if block_size & (block_size - 1):
-        raise BackendError(
-            f"{op}: the hip kernels need a power-of-two block size, not {block_size}",
-            context={"op": op, "argument": "buffers"},
-        )
     device = buffers.k.device
     for name, tensor in (
         ("q", q),
@@ -905,7 +924,7 @@ def attend_with(
         if size:
             max_partitions = -(-table.shape[1] * block_size // size)
             nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, max_partitions)
-            scratch = _workspace(op, device, nbytes, capturing(q))
+            scratch = _workspace(op, device, nbytes, capturing(q), stream)
         _lib.check(
             op,
             lib.ayk_paged_prefill(
@@ -953,6 +972,10 @@ def attend_with(
         else:
             if not step.head_shape:
                 step.head_shape.extend((kv_heads, group, kv_bytes))
+                if step.staged_shape and step.staged_shape != step.head_shape and not capturing(q):
+                    # the last update scored a guessed head shape: re-stage its step's split
+                    used = _stage_split(step, step.kv_lengths.numpy(), block_size)
+                    step.staged[:used].copy_(step.staged_host[:used], non_blocking=True)
             # v2 over the staged split (rows of one partition write their output directly),
             # or v1 when the table holds one partition at most
             split = Split(0, 0)
@@ -976,7 +999,7 @@ def attend_with(
         nbytes = lib.ayk_paged_attention_v2_workspace_bytes(step.capacity, heads, buffers.head_dim, 1)
     else:
         nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, partitions)
-    scratch = _workspace(op, device, nbytes, capturing(q))
+    scratch = _workspace(op, device, nbytes, capturing(q), stream)
     arrivals = _arrivals(op, device, n_rows * heads, capturing(q))
     # A planned step runs only the partitions that hold tokens, longest first. Graph
     # metadata's launch reads the same list and its partition size from the staged
@@ -1027,7 +1050,7 @@ def _attend_windows(op: str, q: torch.Tensor, buffers: KVBuffers, meta: Attentio
     if size:
         max_partitions = -(-table.shape[1] * buffers.block_size // size)
         nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, max_partitions)
-        scratch = _workspace(op, device, nbytes, capturing(q))
+        scratch = _workspace(op, device, nbytes, capturing(q), stream)
     _lib.check(
         op,
         lib.ayk_paged_attention_windows(
@@ -1153,6 +1176,7 @@ def _stage_split(staging: HipGraphPlan, lengths: np.ndarray, block_size: int) ->
     slots and the work list (the eager plan's choice among sizes of ``staging.min_size`` up
     whose list fits the capacity); returns the int32 words used."""
     kv_heads, group, kv_bytes = staging.head_shape or (8, 1, 2)
+    staging.staged_shape[:] = [kv_heads, group, kv_bytes]
     lengths = lengths.astype(np.int64)
     longest = int(lengths.max()) if lengths.size else 0
     empty = int((lengths == 0).sum())

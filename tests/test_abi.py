@@ -61,7 +61,8 @@ def _v1(lib: ctypes.CDLL, **kw: object) -> int:
         ({"kv_dtype": 2, "flags": 1}, 2, b"16-bit caches only"),
         ({"layout": 3}, 2, b"layout 3"),
         ({"heads": 6, "kv_heads": 4}, 1, b"not a positive multiple"),
-        ({"block_size": 12}, 2, b"power of two"),
+        ({"block_size": 0}, 2, b"block_size 0 is not in [1, 65536]"),
+        ({"max_blocks": 1 << 24, "stride": 1 << 24}, 2, b"exceeds 2^24"),
         ({"ror": 1}, 1, b"together"),
         ({"q": None}, 1, b"null"),
         ({"stride": 2}, 1, b"table_stride"),

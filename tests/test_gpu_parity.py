@@ -288,17 +288,30 @@ def test_multi_row_step_in_a_captured_graph(launch: dict, steps: list) -> None:
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("block_size", [1, 4, 8, 16, 32, 64])
+@pytest.mark.parametrize("block_size", [1, 3, 4, 5, 8, 12, 16, 24, 32, 48, 64, 100])
 @pytest.mark.parametrize("qk", QK)
 def test_block_sizes(block_size: int, qk: str) -> None:
-    s = build_scenario([(1, 1), (1, 63), (1, 130), (2, 70)], block_size=block_size, head_dim=128,
+    # any block size (the reference's CacheConfig accepts every positive one): powers of two
+    # and others, odd ones included, whose positions the kernels divide by a magic number
+    s = build_scenario([(1, 1), (1, 63), (1, 130), (2, 70), (1, 301)], block_size=block_size, head_dim=128,
                        heads=8, kv_heads=2, seed=43)
+    expected = s.expected(np.float64)
     for prefill, window in ((False, None), (True, False), (True, True)):
         out = run_attention(s, None, qk, prefill, window=window)
-        assert_parity(out, s.expected(np.float64), "bf16", f"bs{block_size}/{prefill}/{window}")
+        assert_parity(out, expected, "bf16", f"bs{block_size}/{prefill}/{window}")
+    # v1 (one and several waves per head), v2 partitions that start inside a block, and the
+    # multi-row kernel's partitions and smaller tiles
+    launches = [dict(partitions=0, prefill=False), dict(partitions=3, partition_size=128, prefill=False),
+                dict(partitions=None, partition_size=64, prefill=True, window=False),
+                dict(partitions=None, partition_size=192, prefill=True, tile_pairs=32)]
+    if qk == "mfma":
+        launches.append(dict(partitions=0, prefill=False, v1_waves=8))
+    for launch in launches:
+        out = run_attention(s, qk=qk if not launch.get("prefill") else None, **launch)
+        assert_parity(out, expected, "bf16", f"bs{block_size}/{launch}")
 
 
-@pytest.mark.parametrize("block_size", [1, 2])
+@pytest.mark.parametrize("block_size", [1, 2, 3])
 def test_table_segments(block_size: int) -> None:
     # a workgroup stages at most 511 table entries at a time: with blocks of 1-2 positions these
     # contexts span several staged segments, and the rows end at positions in different ones
@@ -725,6 +738,57 @@ def test_graph_metadata_replays_match_eager_steps(heads: int, kv_heads: int, max
 
 
 # --- block ops ------------------------------------------------------------------------------
+
+
+def test_calls_on_two_streams_share_the_scratch_in_order() -> None:
+    # two v2 steps queued back to back on two streams with no synchronisation between them: the
+    # second stream waits for the first one's use of the shared scratch and counters, so both
+    # results are those of the steps run alone
+    s1 = build_scenario([(1, 3000), (1, 2500), (1, 4000)] * 6, heads=32, kv_heads=8, head_dim=128, block_size=16,
+                        mode="decode", seed=97)
+    s2 = build_scenario([(1, 1700), (1, 90), (1, 4000)] * 6, heads=32, kv_heads=8, head_dim=128, block_size=16,
+                        mode="decode", seed=98)
+    alone = [run_attention(s, 40, partition_size=128, merge="reduce-kernel") for s in (s1, s2)]
+    for merge in ("reduce-kernel", "in-kernel"):
+        setups = [(scenario_buffers(s), plan_scenario(s), to_device(s.q_bits, "bf16")) for s in (s1, s2)]
+        outs = [torch.full_like(q, 7.0) for _, _, q in setups]
+        torch.cuda.synchronize()
+        for (buffers, meta, q), out, stream in zip(setups, outs, (torch.cuda.Stream(), torch.cuda.Stream())):
+            with torch.cuda.stream(stream):
+                for _ in range(3):
+                    hip_attention.attend_with(q, buffers, meta, out, scale=s1.scale, partitions=40,
+                                              partition_size=128, merge=merge, prefill=False)
+        torch.cuda.synchronize()
+        for got, want in zip(outs, alone):
+            if merge == "reduce-kernel":
+                assert torch.equal(got.view(torch.int16), want.view(torch.int16)), merge
+        assert_parity(outs[0], s1.expected(np.float64), "bf16", f"stream 1 {merge}")
+        assert_parity(outs[1], s2.expected(np.float64), "bf16", f"stream 2 {merge}")
+    assert counters_are_clear()
+
+
+def test_graph_metadata_restages_the_split_for_the_real_head_shape() -> None:
+    # an update before the first attend scores the split for a guessed head shape; the first
+    # eager attend knows the real one (GQA 8 over fp8 caches here) and stages that split
+    bucket, max_blocks, bs = 8, 256, 16
+    meta = hip_attention.graph_metadata(bucket, max_blocks, bs, DEV)
+    lengths = torch.tensor([4096, 4096, 100, 0, 2000, 4096, 1, 3000], dtype=torch.int32)
+    table = torch.arange(1, 1 + bucket * max_blocks, dtype=torch.int32).view(bucket, max_blocks)
+    hip_attention.update_graph_metadata(meta, lengths, table)
+    assert meta.plan.staged_shape == [8, 1, 2]
+    k = torch.randn((1 + bucket * max_blocks, bs, 8, 128), device=DEV).to(torch.float8_e4m3fn)
+    buffers = KVBuffers(k, k.clone(), KVLayoutKind.NHD, FP8_E4M3_CODEC)
+    q = torch.randn((bucket, 64, 128), device=DEV).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    hip_attention.attend(q, buffers, meta, out, scale=128 ** -0.5)
+    torch.cuda.synchronize()
+    assert meta.plan.head_shape == meta.plan.staged_shape == [8, 8, 1]
+    expected = hip_attention.choose_split(bucket, 8, 8, max_blocks * bs, row_lengths=tuple(lengths.tolist()),
+                                          kv_bytes=1, min_size=meta.plan.min_size,
+                                          max_items=meta.plan.capacity - 1)
+    staged = meta.plan.staged.cpu()
+    assert int(staged[0]) == (expected.partition_size or int(staged[0]))
+    assert torch.equal(staged[:2], meta.plan.staged_host[:2])
 
 
 @pytest.mark.parametrize("layout", ["nhd", "hnd"])
