@@ -34,20 +34,20 @@ HBM_PEAK_GBS = 8000.0
 # for a 1 GiB device copy (FETCH x2.0, WRITE x1.0). Reported only when this run's launch is
 # the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
 PROFILED_TRAFFIC = {
-    (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 1024):
-        (1_081_377_096, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
+    (3, "paged_attention_mfma_kernel (v1, 4 waves per head)", 0):
+        (1_080_117_236, 524_288, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
+    (3, "paged_attention_mfma_kernel (v1, 4 waves per head, fp8 cache)", 0):
+        (544_005_220, 524_288, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
     (4, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 704):
-        (668_259_684, 4_054_704, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
+        (668_303_933, 4_054_912, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
     (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 3072):
-        (2_597_973_216, 10_319_808, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
+        (2_598_003_942, 10_319_152, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
     (2, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 320):
-        (148_281_037, 2_128_256, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
-    (1, "paged_attention_mfma_kernel (v2, merge in-kernel)", 64):
-        (1_738_582, 86_080, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
-    (3, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1024):
-        (545_397_811, 4_456_448, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
+        (148_252_492, 2_128_560, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
+    (1, "paged_attention_mfma_kernel (v1, 8 waves per head)", 0):
+        (1_634_780, 4_608, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
     (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1280):
-        (1_317_549_585, 20_071_280, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
+        (1_317_560_092, 20_072_720, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
 }
 
 
@@ -107,6 +107,29 @@ def time_calls(fn, steps: int, warmup: int, repeats: int = 5) -> dict:
         regions.append(start.elapsed_time(end) * 1000.0 / steps)  # µs per call
     return {"median_us": statistics.median(regions), "min_us": min(regions),
             "wall_ms_per_step": statistics.median(walls) * 1000.0 / steps}
+
+
+def settle(fn, steps: int, limit_s: float = 2.0) -> int:
+    """Run ``fn`` in regions of ``steps`` calls until two consecutive regions agree within 1%
+    (or ``limit_s`` passes); returns the calls made. A fresh pool reads slower for its first
+    100-200 calls on MI355X (fp8 C3 v1: ~108 then 90 µs), so the per-configuration records,
+    which are not the driver's headline step, are timed once that has passed."""
+    import torch
+
+    calls, last, t0 = 0, None, time.perf_counter()
+    while time.perf_counter() - t0 < limit_s:
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        calls += steps
+        us = start.elapsed_time(end)
+        if last is not None and abs(us - last) <= 0.01 * last:
+            break
+        last = us
+    return calls
 
 
 def cpu_baseline(step, cfg, rows: int, kv_bytes: int = 2) -> dict:
@@ -432,6 +455,7 @@ def measure(index: int, args, codec: str, layout_name: str | None, headline: boo
     def call():
         hip_attention.attend(step.q, pool(), meta, out, scale=cfg.scale)
 
+    settled = 0 if headline else settle(call, args.steps)
     result = time_calls(call, args.steps, args.warmup, repeats=1 if headline else 3)
     if auto.partitions and merge == "reduce-kernel":
         kernel_us = time_calls(
@@ -452,7 +476,12 @@ def measure(index: int, args, codec: str, layout_name: str | None, headline: boo
         "kernel_hbm_fraction": round(nbytes / kernel_us / 1e3 / HBM_PEAK_GBS, 4),
         "algorithmic_bytes": nbytes,
         "pools": len(pools),
+        "settling_calls": settled,
     }
+    profiled = PROFILED_TRAFFIC.get((cfg.index, kernel, auto.partition_size))
+    if profiled is not None:  # HBM bytes of the dominant kernel per launch (rocprofv3 counters)
+        record["traffic_read_write"] = [profiled[0], profiled[1]]
+        record["traffic_source"] = profiled[2]
     if len(pools) > 1:  # the same call over one pool: what the Infinity Cache serves
         record["cache_resident_us"] = round(time_calls(
             lambda: hip_attention.attend(step.q, buffers, meta, out, scale=cfg.scale), args.steps,
@@ -484,7 +513,6 @@ def measure(index: int, args, codec: str, layout_name: str | None, headline: boo
                              **{k: v for k, v in launch.items() if v is not None}}
             print(f"[bench] {cfg.name} {name}: {r['median_us']:.1f} us/call", file=sys.stderr, flush=True)
     store_us = time_calls(lambda: hip_kvcache.store(step.k_new, step.v_new, buffers, write), 50, 5)["median_us"]
-    profiled = PROFILED_TRAFFIC.get((cfg.index, kernel, auto.partition_size))
     line = {
         "metric": "decode-attention µs/call + achieved HBM GB/s (% of peak) at 1 MI355X",
         "value": record["gbs"],
