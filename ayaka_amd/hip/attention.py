@@ -40,7 +40,7 @@ import torch
 from ayaka_amd.enums import ForwardMode, KVLayoutKind
 from ayaka_amd.attention import AttentionMetadata
 from ayaka_amd.errors import BackendError
-from ayaka_amd.hip import _lib
+from ayaka_amd.hip import _fastpath, _lib
 from ayaka_amd.hip._checks import (
     compute_dtype,
     HEAD_DIMS,
@@ -137,6 +137,8 @@ class HipAttentionPlan:
     # v2 work lists built by the step's first attend, keyed by partition size, for the later layers
     work: dict[int, torch.Tensor] = field(default_factory=dict, compare=False, repr=False)
     splits: dict[tuple[int, int, int], Split] = field(default_factory=dict, compare=False, repr=False)
+    # library calls recorded by attend / store, replayed for the same objects (_fastpath)
+    launches: dict = field(default_factory=dict, compare=False, repr=False)
 
     def split_for(self, num_kv_heads: int, group: int, kv_bytes: int = 2) -> Split:
         """The step's launch for this head shape and cache element size, chosen once and
@@ -228,7 +230,7 @@ class HipAttentionPlan:
         if found is None:
             lengths = tuple(g[0] for g in self.prefill_groups(group, self.window_pairs(group)))
             found = choose_split(len(lengths), num_kv_heads, 1, max(lengths, default=0), row_lengths=lengths,
-                                 kv_bytes=kv_bytes).partition_size
+                                 kv_bytes=kv_bytes, v1=False).partition_size
             self.splits[key] = found
         return found
 
@@ -319,6 +321,7 @@ class HipGraphPlan:
     capacity: int
     head_shape: list = field(default_factory=list)
     staged_shape: list = field(default_factory=list)
+    launches: dict = field(default_factory=dict)
 
     @property
     def staged_partition_size(self) -> int:
@@ -784,6 +787,14 @@ def _arrivals(op: str, device: torch.device, words: int, capture: bool) -> torch
     return fresh
 
 
+def _call(op: str, fn, args: tuple, stream: int, device: torch.device, scratch: bool,
+          record: "_fastpath.Recorder | None") -> None:
+    """Make one library call (``stream`` last), and hand it to ``record`` for replays."""
+    if record is not None:
+        record(op, fn, args, device, scratch)
+    _lib.check(op, fn(*args, stream))
+
+
 def attend(
     q: torch.Tensor,
     buffers: KVBuffers,
@@ -792,8 +803,28 @@ def attend(
     *,
     scale: float,
 ) -> None:
-    """Write every query row's attention output into ``out`` (reference ``attention.py:167-234``)."""
-    attend_with(q, buffers, meta, out, scale=scale, partitions=None)
+    """Write every query row's attention output into ``out`` (reference ``attention.py:167-234``).
+
+    The first call with a combination of q, out, buffers and step metadata is checked in full;
+    its library call is recorded in the step's plan, and later calls with the same objects
+    (the engine's per-layer buffers, every layer of a step) replay it on the current stream.
+    """
+    cache = getattr(meta.plan, "launches", None)
+    if cache is None:
+        attend_with(q, buffers, meta, out, scale=scale, partitions=None)
+        return
+    key = ("attend", id(q), id(out), id(buffers), id(meta), scale)
+    tensors = (q, out, buffers.k, buffers.v)
+    found = _fastpath.lookup(cache, key, tensors)
+    if found is not None:
+        stream = stream_handle(found.device)
+        if found.scratch:
+            _order_scratch(found.device, stream, capturing(q))
+        _fastpath.run(found, stream)
+        return
+    record = _fastpath.Recorder()
+    attend_with(q, buffers, meta, out, scale=scale, partitions=None, _record=record)
+    _fastpath.remember(cache, key, tensors, (buffers, meta), record)
 
 
 def attend_with(
@@ -812,6 +843,7 @@ def attend_with(
     tile_pairs: int | None = None,
     window: bool | None = None,
     v1_waves: int | None = None,
+    _record: "_fastpath.Recorder | None" = None,
 ) -> None:
     """:func:`attend` with the launch chosen by the caller.
 
@@ -898,7 +930,7 @@ def attend_with(
         if window is None:
             window = tile_pairs is None and WINDOWS and step.window_pairs(group) > 0
         if window:
-            _attend_windows(op, q, buffers, meta, out, step, scale, partitions, partition_size, stream)
+            _attend_windows(op, q, buffers, meta, out, step, scale, partitions, partition_size, stream, _record)
             return
     if prefill:
         if not isinstance(step, HipAttentionPlan):
@@ -925,18 +957,15 @@ def attend_with(
             max_partitions = -(-table.shape[1] * block_size // size)
             nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, max_partitions)
             scratch = _workspace(op, device, nbytes, capturing(q), stream)
-        _lib.check(
-            op,
-            lib.ayk_paged_prefill(
-                out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),
-                table.stride(0), meta.kv_lengths.data_ptr(), meta.request_of_row.data_ptr(),
-                meta.positions.data_ptr(), tiles.data_ptr(), tiles.numel() // 4, pairs, n_rows, heads, kv_heads,
-                buffers.head_dim, buffers.num_blocks, block_size, table.shape[1],
-                _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype], _kv_code(buffers, q.dtype),
-                float(scale), size, scratch.data_ptr() if scratch is not None else 0,
-                scratch.numel() if scratch is not None else 0, stream,
-            ),
-        )
+        _call(op, lib.ayk_paged_prefill, (
+            out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),
+            table.stride(0), meta.kv_lengths.data_ptr(), meta.request_of_row.data_ptr(),
+            meta.positions.data_ptr(), tiles.data_ptr(), tiles.numel() // 4, pairs, n_rows, heads, kv_heads,
+            buffers.head_dim, buffers.num_blocks, block_size, table.shape[1],
+            _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype], _kv_code(buffers, q.dtype),
+            float(scale), size, scratch.data_ptr() if scratch is not None else 0,
+            scratch.numel() if scratch is not None else 0,
+        ), stream, device, scratch is not None, _record)
         return
     # Decode rows need no per-row indirection: row n is request n and sees its whole context.
     row_request = 0 if decode else meta.request_of_row.data_ptr()
@@ -993,7 +1022,8 @@ def attend_with(
         )
     flags = _QK_FLAGS[qk] | (PARTIALS_ONLY if partials_only else 0) | _MERGE_FLAGS[merge]
     if partitions == 0:
-        _lib.check(op, lib.ayk_paged_attention_v1(*common, flags | _V1_WAVE_FLAGS[v1_waves], stream))
+        _call(op, lib.ayk_paged_attention_v1, (*common, flags | _V1_WAVE_FLAGS[v1_waves]), stream, device, False,
+              _record)
         return
     if staged is not None:  # the rows' partials packed into one slot per work item
         nbytes = lib.ayk_paged_attention_v2_workspace_bytes(step.capacity, heads, buffers.head_dim, 1)
@@ -1011,18 +1041,15 @@ def attend_with(
     elif isinstance(step, HipAttentionPlan) and not capturing(q):
         items = step.work_items(partition_size, device)
         work, n_work = items.data_ptr(), items.numel() // 2
-    _lib.check(
-        op,
-        lib.ayk_paged_attention_v2(
-            *common, partition_size, partitions, work, n_work, staged.data_ptr() if staged is not None else 0,
-            scratch.data_ptr(), scratch.numel(), arrivals.data_ptr(), flags, stream,
-        ),
-    )
+    _call(op, lib.ayk_paged_attention_v2, (
+        *common, partition_size, partitions, work, n_work, staged.data_ptr() if staged is not None else 0,
+        scratch.data_ptr(), scratch.numel(), arrivals.data_ptr(), flags,
+    ), stream, device, True, _record)
 
 
 def _attend_windows(op: str, q: torch.Tensor, buffers: KVBuffers, meta: AttentionMetadata, out: torch.Tensor,
                     step: HipAttentionPlan, scale: float, partitions: int | None, partition_size: int | None,
-                    stream: int) -> None:
+                    stream: int, record: "_fastpath.Recorder | None" = None) -> None:
     """A step of few rows per request on the decode kernel (``ayk_paged_attention_windows``):
     one tile per request, its (row, query head) pairs the kernel's 16 matrix-core columns."""
     heads, kv_heads = q.shape[1], buffers.num_kv_heads
@@ -1051,17 +1078,14 @@ def _attend_windows(op: str, q: torch.Tensor, buffers: KVBuffers, meta: Attentio
         max_partitions = -(-table.shape[1] * buffers.block_size // size)
         nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, max_partitions)
         scratch = _workspace(op, device, nbytes, capturing(q), stream)
-    _lib.check(
-        op,
-        lib.ayk_paged_attention_windows(
-            out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),
-            table.stride(0), meta.kv_lengths.data_ptr(), meta.request_of_row.data_ptr(), meta.positions.data_ptr(),
-            tiles.data_ptr(), tiles.numel() // 4, n_rows, heads, kv_heads, buffers.head_dim, buffers.num_blocks,
-            buffers.block_size, table.shape[1], _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype],
-            _kv_code(buffers, q.dtype), float(scale), size, scratch.data_ptr() if scratch is not None else 0,
-            scratch.numel() if scratch is not None else 0, stream,
-        ),
-    )
+    _call(op, lib.ayk_paged_attention_windows, (
+        out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),
+        table.stride(0), meta.kv_lengths.data_ptr(), meta.request_of_row.data_ptr(), meta.positions.data_ptr(),
+        tiles.data_ptr(), tiles.numel() // 4, n_rows, heads, kv_heads, buffers.head_dim, buffers.num_blocks,
+        buffers.block_size, table.shape[1], _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype],
+        _kv_code(buffers, q.dtype), float(scale), size, scratch.data_ptr() if scratch is not None else 0,
+        scratch.numel() if scratch is not None else 0,
+    ), stream, device, scratch is not None, record)
 
 
 def graph_metadata(

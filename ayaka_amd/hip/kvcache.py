@@ -16,7 +16,7 @@ import torch
 from ayaka_amd.attention import AttentionMetadata
 from ayaka_amd.enums import KVLayoutKind
 from ayaka_amd.errors import BackendError
-from ayaka_amd.hip import _lib
+from ayaka_amd.hip import _fastpath, _lib
 from ayaka_amd.hip._checks import (
     compute_dtype,
     require_buffers,
@@ -53,6 +53,29 @@ def _ids(op: str, name: str, ids: torch.Tensor, device: torch.device) -> None:
 
 
 def store(k: torch.Tensor, v: torch.Tensor, buffers: KVBuffers, meta: AttentionMetadata) -> None:
+    """Write each row's k and v into its slot (reference ``torch/kvcache.py:65-80``).
+
+    As ``attend``: the first call with a combination of k, v, buffers and step metadata is
+    checked in full and recorded in the step's plan; later calls with the same objects replay
+    the library call on the current stream.
+    """
+    cache = getattr(meta.plan, "launches", None)
+    if cache is None:
+        _store(k, v, buffers, meta, None)
+        return
+    key = ("store", id(k), id(v), id(buffers), id(meta))
+    tensors = (k, v, buffers.k, buffers.v)
+    found = _fastpath.lookup(cache, key, tensors)
+    if found is not None:
+        _fastpath.run(found, _stream(found.device))
+        return
+    record = _fastpath.Recorder()
+    _store(k, v, buffers, meta, record)
+    _fastpath.remember(cache, key, tensors, (buffers, meta), record)
+
+
+def _store(k: torch.Tensor, v: torch.Tensor, buffers: KVBuffers, meta: AttentionMetadata,
+           record: "_fastpath.Recorder | None") -> None:
     op = "kvcache.store"
     require_buffers(op, buffers)
     if meta.block_size != buffers.block_size:
@@ -75,33 +98,18 @@ def store(k: torch.Tensor, v: torch.Tensor, buffers: KVBuffers, meta: AttentionM
     if rows == 0:
         return
     if buffers.codec == FP8_E4M3_CODEC:
-        _lib.check(
-            op,
-            _lib.lib().ayk_reshape_and_cache_e4m3(
-                k.data_ptr(), v.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), slots.data_ptr(), rows,
+        fn = _lib.lib().ayk_reshape_and_cache_e4m3
+        args = (k.data_ptr(), v.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), slots.data_ptr(), rows,
                 buffers.num_kv_heads, buffers.head_dim, buffers.num_blocks, buffers.block_size,
-                _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[dtype], _stream(device),
-            ),
-        )
-        return
-    _lib.check(
-        op,
-        _lib.lib().ayk_reshape_and_cache(
-            k.data_ptr(),
-            v.data_ptr(),
-            buffers.k.data_ptr(),
-            buffers.v.data_ptr(),
-            slots.data_ptr(),
-            rows,
-            buffers.num_kv_heads,
-            buffers.head_dim,
-            buffers.num_blocks,
-            buffers.block_size,
-            _LAYOUT_CODES[KVLayoutKind(buffers.layout)],
-            buffers.k.element_size(),
-            _stream(device),
-        ),
-    )
+                _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[dtype])
+    else:
+        fn = _lib.lib().ayk_reshape_and_cache
+        args = (k.data_ptr(), v.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), slots.data_ptr(), rows,
+                buffers.num_kv_heads, buffers.head_dim, buffers.num_blocks, buffers.block_size,
+                _LAYOUT_CODES[KVLayoutKind(buffers.layout)], buffers.k.element_size())
+    if record is not None:
+        record(op, fn, args, device, False)
+    _lib.check(op, fn(*args, _stream(device)))
 
 
 def gather(

@@ -740,6 +740,51 @@ def test_graph_metadata_replays_match_eager_steps(heads: int, kv_heads: int, max
 # --- block ops ------------------------------------------------------------------------------
 
 
+@pytest.mark.parametrize("mode,steps", [("decode", [(1, 900), (1, 0), (1, 5000)]),
+                                        ("mixed", [(40, 600), (3, 3), (7, 300)]),
+                                        ("mixed", [(4, 600), (3, 3), (1, 300)])], ids=["decode", "multi-row", "windows"])
+def test_repeated_calls_replay_the_recorded_launch(mode: str, steps: list) -> None:
+    # attend and store record their library call in the step's plan; later calls with the same
+    # objects replay it: new contents of the same tensors are read, other objects are checked anew
+    s = build_scenario(steps, heads=8, kv_heads=2, head_dim=128, block_size=16, mode=mode, seed=99)
+    buffers, meta = scenario_buffers(s), plan_scenario(s)
+    q = to_device(s.q_bits, "bf16")
+    out = torch.full_like(q, 7.0)
+    for _ in range(3):
+        hip_attention.attend(q, buffers, meta, out, scale=s.scale)
+    torch.cuda.synchronize()
+    assert len(meta.plan.launches) == 1
+    assert_parity(out, s.expected(np.float64), "bf16", "replayed")
+    first = out.clone()
+    q.mul_(-1.0)  # same tensor, new contents: the replay reads them
+    hip_attention.attend(q, buffers, meta, out, scale=s.scale)
+    fresh = torch.full_like(out, 7.0)
+    hip_attention.attend_with(q, buffers, meta, fresh, scale=s.scale, partitions=None)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), fresh.view(torch.int16))
+    assert not torch.equal(out, first)
+    other = torch.full_like(out, 7.0)  # another out: a second record
+    hip_attention.attend(q, buffers, meta, other, scale=s.scale)
+    assert len(meta.plan.launches) == 2
+    # a bad argument on a new object is still refused before any launch
+    with pytest.raises(BackendError):
+        hip_attention.attend(q, buffers, meta, torch.empty_like(out[:1]), scale=s.scale)
+    # store: the same rows twice, then new contents of the same k/v objects
+    rng = np.random.default_rng(3)
+    k_new = torch.from_numpy(rng.standard_normal((len(s.plan["slot_mapping"]), 2, 128)).astype(np.float32))
+    k_new = k_new.to(DEV).to(torch.bfloat16)
+    v_new = -k_new
+    for _ in range(2):
+        hip_kvcache.store(k_new, v_new, buffers, meta)
+    k_new.mul_(2.0)
+    hip_kvcache.store(k_new, v_new, buffers, meta)
+    torch.cuda.synchronize()
+    slots = meta.slot_mapping
+    real = slots != 0
+    got = buffers.k.view(-1, 2, 128)[slots[real]]
+    assert torch.equal(got.view(torch.int16), k_new[real].view(torch.int16))
+
+
 def test_calls_on_two_streams_share_the_scratch_in_order() -> None:
     # two v2 steps queued back to back on two streams with no synchronisation between them: the
     # second stream waits for the first one's use of the shared scratch and counters, so both
