@@ -112,7 +112,7 @@ int ayk_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void
  * (reference python/ayaka/ops/attention.py:12-30). A row whose request has
  * kv_lengths 0 is a padding row and gets zeros. Scores are scale * q.k in fp32,
  * the softmax and the value sum are fp32, and out is rounded once.
- * head_dim must be 64, 128 or 256 and block_size a power of two. `dtype` is
+ * head_dim must be 64, 128 or 256 and block_size in [1, 65536]. `dtype` is
  * the type of q and out; `kv_dtype` that of the caches: the same, or
  * AYK_DTYPE_FP8_E4M3 (decoded exactly to `dtype` as it is read; matrix-core
  * kernel only). `flags` (AYK_FLAG_QK_*) forces one q.k implementation; 0 picks
@@ -252,9 +252,12 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
  * num_kv_heads) rows each) is one work item; a wave serves one key/value head and its
  * 16 matrix-core columns are the tile's (row, query head) pairs, each row masked at its
  * own position, so a request's context is streamed once for all the tile's rows.
- * partition_size 0 covers each tile's context in one workgroup; otherwise tiles carry
- * partitions of that size (a multiple of 64) and the rows spanning several are merged as
- * in ayk_paged_prefill (same workspace). The multi-row rule of the reference
+ * The rows of a tile are consecutive rows of one request whose positions rise (the
+ * tile's last row sees the most: nothing past its position is read); a row whose position
+ * is negative sees nothing and gets zeros. partition_size 0 covers each tile's context in
+ * one workgroup; otherwise tiles carry partitions of that size (a multiple of 64) and the
+ * rows spanning several are merged as in ayk_paged_prefill (same workspace). The multi-row
+ * rule of the reference
  * (python/ayaka/ops/backends/torch/attention.py:209-234), as ayk_paged_prefill.
  */
 int ayk_paged_attention_windows(void* out, const void* q, const void* k_cache, const void* v_cache,
