@@ -355,3 +355,33 @@ def test_hip_backend_is_unavailable_without_a_device(monkeypatch: pytest.MonkeyP
         load()
     with pytest.raises(ConfigError, match="hip is unavailable"):
         registry.load_backend(["hip"], device="cuda", dtype=DType.BF16)
+
+
+def test_recorded_launches_replay_only_for_the_same_storage() -> None:
+    # the repeated-call record: found by identity, confirmed by data pointers and shapes, and
+    # dropped when a tensor's storage or shape changed
+    from ayaka_amd.hip import _fastpath
+
+    calls = []
+    cache: dict = {}
+    q, out = torch.zeros(4, 8), torch.zeros(4, 8)
+    key = ("attend", id(q), id(out))
+    assert _fastpath.lookup(cache, key, (q, out)) is None
+    record = _fastpath.Recorder()
+    record("op", lambda *args: calls.append(args) or 0, (1, 2), torch.device("cpu"), False)
+    _fastpath.remember(cache, key, (q, out), (), record)
+    found = _fastpath.lookup(cache, key, (q, out))
+    assert found is not None and found.keep[-2:] == (q, out)
+    _fastpath.run(found, 7)
+    assert calls == [(1, 2, 7)]
+    q.set_(torch.zeros(4, 8).untyped_storage())  # new storage behind the same object
+    assert _fastpath.lookup(cache, key, (q, out)) is None
+    out.resize_(2, 8)  # a new shape
+    _fastpath.remember(cache, key, (q, torch.zeros(1)), (), record)
+    assert _fastpath.lookup(cache, key, (q, out)) is None
+    # an empty recorder (a call that launched nothing) records nothing; the cache is bounded
+    _fastpath.remember(cache, ("none",), (q,), (), _fastpath.Recorder())
+    assert ("none",) not in cache
+    for i in range(_fastpath.MAX_RECORDS + 1):
+        _fastpath.remember(cache, ("k", i), (q,), (), record)
+    assert len(cache) <= _fastpath.MAX_RECORDS
