@@ -174,17 +174,19 @@ bool merge_in_kernel(int64_t workgroups) { return workgroups <= compute_units() 
 // Heads per wave from which the library picks the matrix-core q.k kernel.
 constexpr int kMfmaMinHeads = 3;
 
-constexpr int32_t kV1WaveFlags = AYK_FLAG_V1_WAVES_1 | AYK_FLAG_V1_WAVES_2 | AYK_FLAG_V1_WAVES_4 | AYK_FLAG_V1_WAVES_8;
+constexpr int32_t kWaveFlags = AYK_FLAG_WAVES_1 | AYK_FLAG_WAVES_2 | AYK_FLAG_WAVES_4 | AYK_FLAG_WAVES_8;
 
-// Waves that share one virtual head's context in a v1 launch: the most (up to 8) that
-// keep rows x virtual heads x waves within one round of 8-wave workgroups on the GPU.
-// A workgroup per row covering every head (wave split 1) fills 64 of 256 compute units
-// at C3's 64 rows; splitting each context among 4 waves gives 256 workgroups of 2 heads.
-int v1_wave_split(const ayk::AttnParams& p, int32_t flags) {
-  if (flags & AYK_FLAG_V1_WAVES_1) return 1;
-  if (flags & AYK_FLAG_V1_WAVES_2) return 2;
-  if (flags & AYK_FLAG_V1_WAVES_4) return 4;
-  if (flags & AYK_FLAG_V1_WAVES_8) return 8;
+// Waves that share one virtual head's positions: the AYK_FLAG_WAVES_* flag's count, else 1
+// for v2 and, for v1, the most (up to 8) that keep rows x virtual heads x waves within one
+// round of 8-wave workgroups on the GPU. A v1 workgroup per row covering every head (wave
+// split 1) fills 64 of 256 compute units at C3's 64 rows; splitting each context among 4
+// waves gives 256 workgroups of 2 heads.
+int wave_split_for(const ayk::AttnParams& p, bool split, int32_t flags) {
+  if (flags & AYK_FLAG_WAVES_1) return 1;
+  if (flags & AYK_FLAG_WAVES_2) return 2;
+  if (flags & AYK_FLAG_WAVES_4) return 4;
+  if (flags & AYK_FLAG_WAVES_8) return 8;
+  if (split) return 1;
   const int64_t slots = (int64_t)compute_units() * ayk::kMaxWavesPerGroup;
   int ws = 1;
   while (ws < ayk::kMaxWavesPerGroup && (int64_t)p.n_rows * p.num_virtual_heads * ws * 2 <= slots) ws *= 2;
@@ -195,12 +197,10 @@ int v1_wave_split(const ayk::AttnParams& p, int32_t flags) {
 int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool bf16, bool kv8, bool split,
            int32_t flags, void* stream) {
   if (flags & ~(AYK_FLAG_QK_DPP | AYK_FLAG_QK_MFMA | AYK_FLAG_PARTIALS_ONLY | AYK_FLAG_SEPARATE_REDUCE |
-                AYK_FLAG_SINGLE_LAUNCH | kV1WaveFlags))
+                AYK_FLAG_SINGLE_LAUNCH | kWaveFlags))
     return fail(AYK_ERR_ARGUMENT, "%s: unknown flags 0x%x", op, flags);
-  if (__builtin_popcount(flags & kV1WaveFlags) > 1)
-    return fail(AYK_ERR_ARGUMENT, "%s: at most one AYK_FLAG_V1_WAVES_* flag", op);
-  if ((flags & kV1WaveFlags) && split)
-    return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_V1_WAVES_* apply to v1 only", op);
+  if (__builtin_popcount(flags & kWaveFlags) > 1)
+    return fail(AYK_ERR_ARGUMENT, "%s: at most one AYK_FLAG_WAVES_* flag", op);
   if ((flags & AYK_FLAG_QK_DPP) && (flags & AYK_FLAG_QK_MFMA))
     return fail(AYK_ERR_ARGUMENT, "%s: AYK_FLAG_QK_DPP and AYK_FLAG_QK_MFMA exclude each other", op);
   if ((flags & AYK_FLAG_SEPARATE_REDUCE) && (flags & AYK_FLAG_SINGLE_LAUNCH))
@@ -213,10 +213,10 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   // butterfly work grows with the group; 1-2 heads stay on the DPP kernel.
   // fp8 caches are read by the matrix-core kernel only.
   ayk::AttnParams q = p;
-  // v1: split each context among waves of the matrix-core kernel when rows x heads leave the
-  // GPU idle (the DPP kernel, forced, streams each head's context in one wave)
-  q.wave_split = split || (flags & AYK_FLAG_QK_DPP) ? 1 : v1_wave_split(p, flags);
-  if ((flags & AYK_FLAG_QK_DPP) && (flags & kV1WaveFlags) && !(flags & AYK_FLAG_V1_WAVES_1))
+  // split each context (v1) or partition (v2) among waves of the matrix-core kernel (the DPP
+  // kernel, forced, streams each head's positions in one wave)
+  q.wave_split = (flags & AYK_FLAG_QK_DPP) ? 1 : wave_split_for(p, split, flags);
+  if ((flags & AYK_FLAG_QK_DPP) && (flags & kWaveFlags) && !(flags & AYK_FLAG_WAVES_1))
     return fail(AYK_ERR_UNSUPPORTED, "%s: the DPP kernel does not split a context among waves", op);
   const bool mfma = kv8 || (flags & AYK_FLAG_QK_MFMA) || q.wave_split > 1 ||
                     (!(flags & AYK_FLAG_QK_DPP) && gc >= kMfmaMinHeads);
@@ -225,8 +225,9 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   const int64_t workgroups = items * p.num_virtual_heads;
   if (workgroups > INT32_MAX || (int64_t)p.n_rows * p.num_heads > INT32_MAX)
     return fail(AYK_ERR_UNSUPPORTED, "%s: %lld workgroups exceed one launch", op, (long long)workgroups);
-  // The grid: one workgroup per item and group of up to kMaxWaves virtual heads.
-  const int64_t grid = items * ((p.num_virtual_heads + ayk::kMaxWavesPerGroup - 1) / ayk::kMaxWavesPerGroup);
+  // The grid: one workgroup per item and group of up to kMaxWaves / wave_split virtual heads.
+  const int heads_per_wg = ayk::kMaxWavesPerGroup / q.wave_split;
+  const int64_t grid = items * ((p.num_virtual_heads + heads_per_wg - 1) / heads_per_wg);
   if (split && q.arrivals && !(flags & AYK_FLAG_SINGLE_LAUNCH) && !merge_in_kernel(grid))
     q.arrivals = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);

@@ -91,10 +91,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   const int tid = threadIdx.x;
   const int threads = blockDim.x;
   const int waves = threads / kWave;
-  // v1 only: `ws` waves share one virtual head, each streaming every ws-th chunk of its
-  // context, and their states are merged in LDS at the end (fills the GPU when rows x
-  // heads alone leave compute units idle, and reads each context once).
-  const int ws = (SPLIT || WIN) ? 1 : p.wave_split;
+  // `ws` waves share one virtual head, each streaming every ws-th chunk of its context (v1)
+  // or partition (v2), and their states are merged in LDS at the end: v1 fills the GPU when
+  // rows x heads alone leave compute units idle, v2 covers a partition ws times as long
+  // with the same per-wave work, so a row has fewer partials to store and merge.
+  const int ws = WIN ? 1 : p.wave_split;
   const int heads_per_wg = waves / ws;
   const int groups = (p.num_virtual_heads + heads_per_wg - 1) / heads_per_wg;
   WgCoord wg;
@@ -165,7 +166,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     t_begin = wg.part * psize;
     t_end = min(len, t_begin + psize);
     if (t_begin >= t_end) {  // only partitions that hold tokens are merged
-      if (len == 0 && wg.part == 0 && active) store_zero_rows<D, GC, kWave>(p, row, h0, lane);  // a padding row
+      if (len == 0 && wg.part == 0 && active && slice == 0) store_zero_rows<D, GC, kWave>(p, row, h0, lane);
       return;
     }
   } else if (len == 0) {
@@ -304,7 +305,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   // Head mt's weight sum over the wave's 4 token groups (its lanes share m_h).
   l_h += __shfl_xor(l_h, 16);
   l_h += __shfl_xor(l_h, 32);
-  if constexpr (!SPLIT && !WIN) {
+  if constexpr (!WIN) {
     if (ws > 1) {
       // Slices 1.. of a head hand (m, l, o) to slice 0 through their own LDS tiles (the
       // keys' tile takes o[0, DT/2), the values' tile the rest: 4 * D 16-byte entries fit
@@ -356,8 +357,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   }
   if constexpr (SPLIT && !WIN) {
     if (np > 1 && p.arrivals) {
-      const int vh_lo = wg.group * waves;
-      const int vh_hi = min(p.num_virtual_heads, vh_lo + waves);
+      const int vh_lo = wg.group * heads_per_wg;
+      const int vh_hi = min(p.num_virtual_heads, vh_lo + heads_per_wg);
       arrive_and_merge<D, GC, BF16>(p, row, wg.group, groups, np, vh_lo * GC, vh_hi * GC, tid, threads, &s_last);
     }
   }
@@ -365,8 +366,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
 
 template <int D, int GC, bool BF16, bool KV8>
 static hipError_t launch_mfma_typed(const AttnParams& p, bool split, hipStream_t stream) {
-  // p.wave_split waves per virtual head (v1; 1 for v2), up to kMaxWaves per workgroup
-  const int ws = split ? 1 : p.wave_split;
+  // p.wave_split waves per virtual head, up to kMaxWaves per workgroup
+  const int ws = p.wave_split;
   const int heads = p.num_virtual_heads < kMaxWaves / ws ? p.num_virtual_heads : kMaxWaves / ws;
   const int per_wg = heads * ws;
   const int groups = (p.num_virtual_heads + heads - 1) / heads;

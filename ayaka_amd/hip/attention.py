@@ -117,8 +117,8 @@ _QK_FLAGS = {None: 0, "dpp": 1, "mfma": 2}
 #: v2 flag: launch the partition kernel only (benchmarks time the dominant kernel with it).
 PARTIALS_ONLY = 4
 _MERGE_FLAGS = {None: 0, "reduce-kernel": 8, "in-kernel": 16}
-#: AYK_FLAG_V1_WAVES_*: waves sharing each (row, key/value head)'s context in a v1 launch
-_V1_WAVE_FLAGS = {None: 0, 1: 32, 2: 64, 4: 128, 8: 256}
+#: AYK_FLAG_WAVES_*: waves sharing each (row, key/value head)'s context (v1) or partition (v2)
+_WAVE_FLAGS = {None: 0, 1: 32, 2: 64, 4: 128, 8: 256}
 
 
 @dataclass(frozen=True, slots=True)
@@ -483,12 +483,12 @@ def graph_merge_site(items: int, num_kv_heads: int, group: int) -> str:
 @dataclass(frozen=True, slots=True)
 class Split:
     """A launch: ``partitions == 0`` is v1, otherwise v2 over partitions of ``partition_size``.
-    ``v1_waves`` (v1): waves sharing each (row, key/value head)'s context, 0 for the C
+    ``waves`` (v1): waves sharing each (row, key/value head)'s context, 0 for the C
     library's own rule."""
 
     partition_size: int
     partitions: int
-    v1_waves: int = 0
+    waves: int = 0
 
 
 def schedule_makespan(row_lengths: list[int], size: int, groups: int = 1, cost: int | None = None) -> int:
@@ -842,7 +842,7 @@ def attend_with(
     merge: str | None = None,
     tile_pairs: int | None = None,
     window: bool | None = None,
-    v1_waves: int | None = None,
+    waves: int | None = None,
     _record: "_fastpath.Recorder | None" = None,
 ) -> None:
     """:func:`attend` with the launch chosen by the caller.
@@ -861,9 +861,9 @@ def attend_with(
     partitions of that size (a multiple of 64) merged by the reduce kernel, and ``None``
     for both lets :func:`choose_prefill_partition` decide; ``tile_pairs`` forces the tile
     capacity (:data:`PREFILL_PAIRS`, or a half or a quarter of it; ``None``:
-    :meth:`HipAttentionPlan.prefill_launch`). ``v1_waves`` (1, 2, 4 or 8) forces how many
-    waves of a v1 launch share each (row, key/value head)'s context (``None``: the library's
-    choice, which fills the GPU).
+    :meth:`HipAttentionPlan.prefill_launch`). ``waves`` (1, 2, 4 or 8) forces how many
+    waves share each (row, key/value head)'s context (v1) or partition (v2) (``None``: the
+    split model's choice, else the library's).
     Benchmarks and tests use them to time and check every kernel on one step.
     """
     op = "attention.attend"
@@ -1013,7 +1013,7 @@ def attend_with(
                 split = Split(step.min_size, step.partitions)
         partitions, partition_size = split.partitions, split.partition_size
         # a forced DPP q.k streams each head's context in one wave
-        v1_waves = v1_waves or (split.v1_waves if qk != "dpp" else None) or None
+        waves = waves or (split.waves if qk != "dpp" else None) or None
     partition_size = partition_size or PARTITION_SIZE
     if partitions and partitions * partition_size < max_length:
         raise BackendError(
@@ -1022,7 +1022,7 @@ def attend_with(
         )
     flags = _QK_FLAGS[qk] | (PARTIALS_ONLY if partials_only else 0) | _MERGE_FLAGS[merge]
     if partitions == 0:
-        _call(op, lib.ayk_paged_attention_v1, (*common, flags | _V1_WAVE_FLAGS[v1_waves]), stream, device, False,
+        _call(op, lib.ayk_paged_attention_v1, (*common, flags | _WAVE_FLAGS[waves]), stream, device, False,
               _record)
         return
     if staged is not None:  # the rows' partials packed into one slot per work item
@@ -1043,7 +1043,7 @@ def attend_with(
         work, n_work = items.data_ptr(), items.numel() // 2
     _call(op, lib.ayk_paged_attention_v2, (
         *common, partition_size, partitions, work, n_work, staged.data_ptr() if staged is not None else 0,
-        scratch.data_ptr(), scratch.numel(), arrivals.data_ptr(), flags,
+        scratch.data_ptr(), scratch.numel(), arrivals.data_ptr(), flags | _WAVE_FLAGS[waves],
     ), stream, device, True, _record)
 
 

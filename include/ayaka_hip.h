@@ -52,13 +52,14 @@ enum {
                                  written); for timing it */
   AYK_FLAG_SEPARATE_REDUCE = 8, /* v2: merge partitions in a second kernel even when arrivals is given */
   AYK_FLAG_SINGLE_LAUNCH = 16,  /* v2: merge partitions in the partition kernel (needs arrivals) */
-  /* v1: how many waves share each (row, key/value head)'s context, each streaming every
-   * n-th chunk, merged in LDS at the end (at most one of these; none lets the library pick:
-   * the most, up to 8, that keep rows x heads x waves within one round of the GPU) */
-  AYK_FLAG_V1_WAVES_1 = 32,
-  AYK_FLAG_V1_WAVES_2 = 64,
-  AYK_FLAG_V1_WAVES_4 = 128,
-  AYK_FLAG_V1_WAVES_8 = 256
+  /* how many waves share each (row, key/value head)'s context (v1) or partition (v2), each
+   * streaming every n-th 16-position chunk, their states merged in LDS at the end (at most
+   * one of these; none lets the library pick: 1 for v2, and for v1 the most, up to 8, that
+   * keep rows x heads x waves within one round of the GPU) */
+  AYK_FLAG_WAVES_1 = 32,
+  AYK_FLAG_WAVES_2 = 64,
+  AYK_FLAG_WAVES_4 = 128,
+  AYK_FLAG_WAVES_8 = 256
 };
 enum { AYK_LAYOUT_NHD = 0, AYK_LAYOUT_HND = 1 };
 
@@ -99,7 +100,7 @@ int ayk_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void
  * Paged attention, single pass ("v1"): every page of a row's context is streamed
  * once per key/value head, in one launch and with no scratch. A workgroup serves
  * one row and 8 / n of its key/value heads, n waves per head (n = 1, 2, 4 or 8, see
- * AYK_FLAG_V1_WAVES_*): each wave streams every n-th 16-position chunk and serves
+ * AYK_FLAG_WAVES_*): each wave streams every n-th 16-position chunk and serves
  * the head's query heads from it, and the waves' states are merged in LDS, in wave
  * order. So the grid has rows x heads x n / 8 workgroups: C3's 64 rows fill the
  * GPU's 256 compute units with n = 4. Replaces the reference's decode attention,

@@ -68,7 +68,7 @@ def _v1(lib: ctypes.CDLL, **kw: object) -> int:
         ({"stride": 2}, 1, b"table_stride"),
         ({"flags": 3}, 1, b"exclude each other"),
         ({"flags": 1024}, 1, b"unknown flags"),
-        ({"flags": 32 | 64}, 1, b"at most one AYK_FLAG_V1_WAVES"),
+        ({"flags": 32 | 64}, 1, b"at most one AYK_FLAG_WAVES"),
         ({"flags": 1 | 128}, 2, b"does not split a context"),
     ],
 )

@@ -305,7 +305,7 @@ def test_block_sizes(block_size: int, qk: str) -> None:
                 dict(partitions=None, partition_size=64, prefill=True, window=False),
                 dict(partitions=None, partition_size=192, prefill=True, tile_pairs=32)]
     if qk == "mfma":
-        launches.append(dict(partitions=0, prefill=False, v1_waves=8))
+        launches.append(dict(partitions=0, prefill=False, waves=8))
     for launch in launches:
         out = run_attention(s, qk=qk if not launch.get("prefill") else None, **launch)
         assert_parity(out, expected, "bf16", f"bs{block_size}/{launch}")
@@ -356,11 +356,17 @@ def test_v1_context_split_among_waves(waves: int, heads: int, kv_heads: int, hea
     s = build_scenario([(1, 1), (1, 17), (1, 0), (1, 2047), (1, 300), (1, 64), (1, 95)], dtype=dtype,
                        heads=heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16, mode="decode", seed=93)
     expected = s.expected(np.float64)
-    out = run_attention(s, 0, "mfma", v1_waves=waves)
+    out = run_attention(s, 0, "mfma", waves=waves)
     assert_parity(out, expected, dtype, f"v1/{waves} waves")
     assert torch.count_nonzero(out[2]) == 0
-    again = run_attention(s, 0, "mfma", v1_waves=waves)
+    again = run_attention(s, 0, "mfma", waves=waves)
     assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    # v2: each partition shared by the waves the same way, either merge site
+    for merge in ("reduce-kernel", "in-kernel"):
+        out = run_attention(s, 8, "mfma", waves=waves, partition_size=256, merge=merge)
+        assert_parity(out, expected, dtype, f"v2/{waves} waves/{merge}")
+        assert torch.count_nonzero(out[2]) == 0
+    assert counters_are_clear()
 
 
 @pytest.mark.parametrize("block_size", [1, 2])
@@ -370,7 +376,7 @@ def test_v1_context_split_across_table_segments(block_size: int) -> None:
                        kv_heads=2, mode="decode", seed=94)
     expected = s.expected(np.float64)
     for waves in (2, 8):
-        assert_parity(run_attention(s, 0, "mfma", v1_waves=waves), expected, "bf16", f"bs{block_size}/{waves}")
+        assert_parity(run_attention(s, 0, "mfma", waves=waves), expected, "bf16", f"bs{block_size}/{waves}")
 
 
 # --- fp8 e4m3 codec ---------------------------------------------------------------------------
@@ -430,8 +436,8 @@ def test_fp8_attention_matches_the_oracle_on_decoded_values(dtype: str, layout: 
     q = to_device(s.q_bits, dtype)
     padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]
     launches = [("v1", dict(partitions=0, prefill=False)),
-                ("v1/1 wave", dict(partitions=0, prefill=False, v1_waves=1)),
-                ("v1/8 waves", dict(partitions=0, prefill=False, v1_waves=8)),
+                ("v1/1 wave", dict(partitions=0, prefill=False, waves=1)),
+                ("v1/8 waves", dict(partitions=0, prefill=False, waves=8)),
                 ("v2/in-kernel", dict(partitions=6, partition_size=256, merge="in-kernel", prefill=False)),
                 ("v2/reduce-kernel", dict(partitions=6, partition_size=256, merge="reduce-kernel", prefill=False)),
                 ("auto", dict(partitions=None))]
@@ -488,7 +494,7 @@ def test_single_launch_merge_agrees_with_the_reduce_kernel(qk: str, heads: int, 
 def test_one_partition_reproduces_v1_bit_for_bit(qk: str) -> None:
     s = build_scenario([(1, 300), (1, 17), (1, 512)], heads=8, kv_heads=2, head_dim=128, block_size=16,
                        mode="decode", seed=53)
-    v1 = run_attention(s, 0, qk, v1_waves=1)
+    v1 = run_attention(s, 0, qk, waves=1)
     v2 = run_attention(s, 1, qk)
     assert torch.equal(v1.view(torch.int16), v2.view(torch.int16))
 
@@ -608,7 +614,7 @@ def test_benchmark_configuration(index: int) -> None:
     split = decode.plan.split_for(cfg.kv_heads, cfg.heads // cfg.kv_heads)
     record = {
         "config": f"C{index} {cfg.name}", "dtype": cfg.dtype_label, "rows": cfg.batch,
-        "auto_launch": f"v1, {split.v1_waves} waves" if not split.partitions else
+        "auto_launch": f"v1, {split.waves} waves" if not split.partitions else
                        f"v2, {split.partitions} x {split.partition_size}",
         "reference_rounding": _report(torch.from_numpy(rounded), e32, expected, cfg.dtype_label),
         **{name: _report(outs[name], e32, expected, cfg.dtype_label) for name in ("auto", "v1-mfma", "v2-mfma")},
