@@ -21,8 +21,9 @@ from ayaka_amd.hip import _lib
 
 __all__ = ["Launch", "Recorder", "lookup", "remember"]
 
-#: Most records one plan keeps (an engine has one per layer); past it the cache starts over.
-MAX_RECORDS = 256
+#: Most records one plan keeps (an engine has one or two per layer); past it the cache starts
+#: over. Large enough for a benchmark that rotates a step over hundreds of pool copies.
+MAX_RECORDS = 4096
 
 
 @dataclass(slots=True)
