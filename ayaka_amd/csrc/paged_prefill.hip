@@ -71,9 +71,15 @@ __device__ __forceinline__ void split_weights(const float (&w)[8], u32x4& hi, u3
   lo = u32x4{l0.x, l0.y, l1.x, l1.y};
 }
 
+// Workgroups per CU the register budget is set for: two, except quarter tiles at head_dim 256,
+// whose 64-position stage (133 KB of LDS) leaves room for one.
+__host__ __device__ constexpr int prefill_workgroups_per_cu(int head_dim, int waves_per_group) {
+  return head_dim == 256 && waves_per_group == 4 ? 1 : 2;
+}
+
 template <int D, bool BF16, bool KV8, int PS>
-__global__ __launch_bounds__(kPrefillThreads, 2) void paged_prefill_kernel(const AttnParams p, const int32_t* tiles) {
-  using E = Elem<BF16>;
+__global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) void paged_prefill_kernel(
+    const AttnParams p, const int32_t* tiles) {
   constexpr int THREADS = kPrefillThreads;
   constexpr int PT = D == 256 ? 1 : 2;          // 16-pair groups per wave
   constexpr int PGROUPS = kPrefillWaves / PS;   // waves with distinct pairs
