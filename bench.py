@@ -488,6 +488,15 @@ def measure(index: int, args, codec: str, layout_name: str | None, headline: boo
         record["cache_resident_us"] = round(time_calls(
             lambda: hip_attention.attend(step.q, buffers, meta, out, scale=cfg.scale), args.steps,
             args.warmup)["median_us"], 2)
+    if not headline and index != 1:
+        # v2 at the reference's partition size (512; C4: up to 64 partitions per row), as the
+        # configurations name it, beside the library's own launch
+        ref_split = dict(partitions=-(-max(cfg.lengths) // hip_attention.PARTITION_SIZE),
+                         partition_size=hip_attention.PARTITION_SIZE)
+        r = time_calls(lambda: hip_attention.attend_with(step.q, pool(), meta, out, scale=cfg.scale, qk=args.qk,
+                                                         **ref_split), args.steps, args.warmup, repeats=3)
+        record["v2_512"] = {"us_per_call": round(r["median_us"], 2), "gbs": round(nbytes / r["median_us"] / 1e3, 1),
+                            "hbm_fraction": round(nbytes / r["median_us"] / 1e3 / HBM_PEAK_GBS, 4), **ref_split}
     print(f"[bench] C{index} {cfg.name} {codec}: {us:.1f} us/call {nbytes / us / 1e3:.0f} GB/s "
           f"({record['launch']}; kernel {kernel_us:.1f} us, {len(pools)} pools)", file=sys.stderr, flush=True)
     if not headline:
