@@ -95,7 +95,6 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
   constexpr int CPT = D / 8;                    // 8-element pieces per position
   constexpr int PIECES = CH * CPT;              // pieces per chunk of K (or V)
   constexpr int PER_THREAD = PIECES / THREADS;  // 2 (D 64), 4 (D 128), 8 (D 256): even
-  constexpr int POS_STEP = 2 * THREADS / CPT;   // positions covered by one pair of a thread's pieces
   // Values in LDS token-major, rows VP elements apart: the transposing reads of the
   // P.V operand (16 rows of one 16-lane group, 8 bytes each) then cover the banks evenly.
   constexpr int VP = D + 16;
@@ -203,11 +202,13 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
   const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride);
   const uint16_t* vbase = kv_at<KV8>(p.v_cache, (int64_t)kvh * p.head_stride);
   auto key_slot = [](int token, int piece) { return token * CPT + (piece ^ (token & (CPT - 1))); };
-  // Piece u of this thread: position piece_pos(u) (pieces 2v and 2v + 1 are adjacent
-  // positions), 8-element slice piece_c of it; consecutive threads read consecutive
-  // slices of one position.
+  // Piece u of this thread: 8-element slice piece_c of the chunk's position
+  // first_pos + u; consecutive threads read consecutive slices of one position, and a
+  // thread's PER_THREAD positions are consecutive (one block when the block size is a
+  // multiple of PER_THREAD, so one table lookup serves them all).
   const int piece_c = tid % CPT;
-  auto piece_pos = [&](int u) { return (u >> 1) * POS_STEP + 2 * (tid / CPT) + (u & 1); };
+  const int first_pos = PER_THREAD * (tid / CPT);
+  static_assert(PER_THREAD * (THREADS / CPT) == CH, "a chunk's positions, PER_THREAD per thread");
 
   // This workgroup's positions: the tile's whole context, or one partition of it.
   const int t_begin = split ? part * p.partition_size : 0;
@@ -219,45 +220,46 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
 
     typedef typename KvRaw<KV8>::T Raw;
     Raw kr[PER_THREAD], vr[PER_THREAD];
-    // Offsets of the pieces at positions t and t + 1, clamped to the last position:
-    // past the end a real position is read, whose weight is 0. The second position is
-    // the next token of the first one's block, or the first token of the next block.
+    // Chunk ci into registers kr and vr (K and V pieces of a position share its offset).
+    // Positions past the segment's last one are read as that one (weight 0, finite
+    // values). Block sizes that are a multiple of PER_THREAD (uniform across the launch)
+    // take one table lookup per chunk for the thread's positions, the others one per
+    // position.
     const uint32_t bs = (uint32_t)p.block_size;
-    auto pair_offsets = [&](int t, uint32_t& o0, uint32_t& o1) {
-      const int t0 = min(t, s1 - 1), t1 = min(t + 1, s1 - 1);
-      const int b = block_of(p, t0);
-      const uint32_t r = (uint32_t)t0 - __umul24((uint32_t)b, bs);
-      o0 = s_tbl[b - b0] + __umul24(r, token_stride);
-      o1 = t1 == t0 ? o0 : r + 1 < bs ? o0 + token_stride : s_tbl[b + 1 - b0];
+    const bool one_block = bs % PER_THREAD == 0;
+    auto offset_of = [&](int t) {
+      const int b = block_of(p, t);
+      const uint32_t r = (uint32_t)t - __umul24((uint32_t)b, bs);
+      return s_tbl[b - b0] + __umul24(r, token_stride) + piece_c * 8;
     };
-    // Chunk ci into registers kr and vr; K and V pieces of the same two positions share
-    // their offsets.
     auto load_chunk = [&](int ci) {
+      const int t = s0 + ci * CH + first_pos;
+      uint32_t off[PER_THREAD];
+      if (one_block) {
+        // t is a multiple of PER_THREAD (s0 and CH are), so t .. t + PER_THREAD - 1 share a
+        // block; a thread past the end reads the last position for all its pieces
+        const int last = s1 - 1;
+        const uint32_t o0 = offset_of(min(t, last));
 #pragma unroll
-      for (int u = 0; u < PER_THREAD; u += 2) {
-        uint32_t o0, o1;
-        pair_offsets(s0 + ci * CH + piece_pos(u), o0, o1);
-        kr[u] = load_kv_raw<KV8, false>(kbase, o0 + piece_c * 8);
-        kr[u + 1] = load_kv_raw<KV8, false>(kbase, o1 + piece_c * 8);
-        vr[u] = load_kv_raw<KV8, false>(vbase, o0 + piece_c * 8);
-        vr[u + 1] = load_kv_raw<KV8, false>(vbase, o1 + piece_c * 8);
+        for (int u = 0; u < PER_THREAD; ++u) off[u] = o0 + (uint32_t)min(u, max(last - t, 0)) * token_stride;
+      } else {
+#pragma unroll
+        for (int u = 0; u < PER_THREAD; ++u) off[u] = offset_of(min(t + u, s1 - 1));
+      }
+#pragma unroll
+      for (int u = 0; u < PER_THREAD; ++u) {
+        kr[u] = load_kv_raw<KV8, false>(kbase, off[u]);
+        vr[u] = load_kv_raw<KV8, false>(vbase, off[u]);
       }
     };
     auto stage_keys = [&](int buf) {
 #pragma unroll
-      for (int u = 0; u < PER_THREAD; u += 2) {
-        const int pos = piece_pos(u);
-        s_k[buf][key_slot(pos, piece_c)] = kv_pairs<KV8, BF16>(kr[u]);
-        s_k[buf][key_slot(pos + 1, piece_c)] = kv_pairs<KV8, BF16>(kr[u + 1]);
-      }
+      for (int u = 0; u < PER_THREAD; ++u) s_k[buf][key_slot(first_pos + u, piece_c)] = kv_pairs<KV8, BF16>(kr[u]);
     };
     auto stage_values = [&](int buf) {
 #pragma unroll
-      for (int u = 0; u < PER_THREAD; u += 2) {
-        const int pos = piece_pos(u);
-        *reinterpret_cast<u32x4*>(&s_v[buf][pos * VP + piece_c * 8]) = kv_pairs<KV8, BF16>(vr[u]);
-        *reinterpret_cast<u32x4*>(&s_v[buf][(pos + 1) * VP + piece_c * 8]) = kv_pairs<KV8, BF16>(vr[u + 1]);
-      }
+      for (int u = 0; u < PER_THREAD; ++u)
+        *reinterpret_cast<u32x4*>(&s_v[buf][(first_pos + u) * VP + piece_c * 8]) = kv_pairs<KV8, BF16>(vr[u]);
     };
 
     typedef f32x4 Scores[PTL_W][PT];
