@@ -388,8 +388,9 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
     stage_keys(0);
     stage_values(0);
     lds_barrier();
-    for (int ci = 0; ci < nch; ++ci) {
-      const int buf = ci & 1;
+    // Two chunks per iteration, so that each body's LDS buffer is a constant (immediate
+    // address offsets instead of per-access arithmetic).
+    auto chunk_step = [&](int ci, int buf) {
       if (ci + 1 < nch) load_chunk(ci + 1);
       // The two waves a SIMD holds (one per workgroup) take turns: a wave raises its
       // priority over its MFMA sections -- the q.k, and the weights with the P.V -- so
@@ -406,6 +407,10 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
         stage_values(buf ^ 1);
       }
       lds_barrier();
+    };
+    for (int ci = 0; ci < nch; ci += 2) {
+      chunk_step(ci, 0);
+      if (ci + 1 < nch) chunk_step(ci + 1, 1);
     }
   }
 
