@@ -134,11 +134,13 @@ def settle(fn, steps: int, limit_s: float = 2.0, min_s: float = 0.3) -> int:
     return calls
 
 
-def cpu_baseline(step, cfg, rows: int, kv_bytes: int = 2) -> dict:
+def cpu_baseline(step, cfg, rows: int, kv_bytes: int = 2, chunk: int | None = None, runs: int = 5) -> dict:
     """The reference's CPU decode (``_attend_decode``, restated in torch by
     ``oracle.torch_decode``) timed on this host over ``rows`` rows of the step: the padded
     tables gathered from a bf16/fp16 cache, float32 matmuls and softmax, as the reference's
-    torch backend runs it, on as many threads as this process may use."""
+    torch backend runs it, on as many threads as this process may use. ``chunk`` runs the
+    requests in groups of that many (same padded width, same arithmetic per request: C5's
+    whole padded gather would need ~34 GB); ``runs`` timed runs follow one warm-up."""
     import torch
 
     from ayaka_amd import workloads
@@ -155,13 +157,18 @@ def cpu_baseline(step, cfg, rows: int, kv_bytes: int = 2) -> dict:
     values = torch.from_numpy(sample["v"]).to(cfg.dtype)
     q = torch.from_numpy(sample["q"]).to(cfg.dtype)
     table, lengths = torch.from_numpy(sample["table"]), torch.from_numpy(sample["lengths"])
-    runs = []
-    for _ in range(6):  # 1 warm-up + 5 timed
+    step_rows = chunk or rows
+    times = []
+    for _ in range(runs + 1):  # 1 warm-up + `runs` timed
         t0 = time.perf_counter()
-        attend_decode(q, keys, values, table, lengths, scale=cfg.scale)
-        runs.append(time.perf_counter() - t0)
-    seconds = statistics.median(runs[1:]) * cfg.batch / rows  # scaled to the whole batch
+        for r0 in range(0, rows, step_rows):
+            attend_decode(q[r0:r0 + step_rows], keys, values, table[r0:r0 + step_rows], lengths[r0:r0 + step_rows],
+                          scale=cfg.scale)
+        times.append(time.perf_counter() - t0)
+    seconds = statistics.median(times[1:]) * cfg.batch / rows  # scaled to the whole batch
     scaled = "all of them" if rows == cfg.batch else f"scaled by {cfg.batch}/{rows} to one call"
+    if chunk:
+        scaled += f", in groups of {chunk} requests"
     return {
         "value": workloads.algorithmic_bytes(cfg, kv_bytes) / seconds / 1e9,
         "unit": "GB/s",
@@ -174,7 +181,7 @@ def cpu_baseline(step, cfg, rows: int, kv_bytes: int = 2) -> dict:
         "sample": f"{rows} of {cfg.batch} rows of the same step ({scaled}): the reference's _attend_decode "
                   f"restated in torch "
                   f"(oracle/torch_decode.py) on the CPU, bf16 cache gathered per padded table, float32 "
-                  f"matmuls and softmax; median of 5 runs after 1 warm-up, torch.set_num_threads({threads})",
+                  f"matmuls and softmax; median of {runs} runs after 1 warm-up, torch.set_num_threads({threads})",
     }
 
 
@@ -391,6 +398,8 @@ def child_record(index: int, codec: str, args) -> dict:
         cmd += ["--layout", args.layout]
     if args.qk:
         cmd += ["--qk", args.qk]
+    if args.no_cpu_baseline:
+        cmd += ["--no-cpu-baseline"]
     done = subprocess.run(cmd, capture_output=True, text=True, timeout=300, check=False)
     sys.stderr.write(done.stderr)
     if done.returncode != 0:
@@ -497,6 +506,13 @@ def measure(index: int, args, codec: str, layout_name: str | None, headline: boo
                                                          **ref_split), args.steps, args.warmup, repeats=3)
         record["v2_512"] = {"us_per_call": round(r["median_us"], 2), "gbs": round(nbytes / r["median_us"] / 1e3, 1),
                             "hbm_fraction": round(nbytes / r["median_us"] / 1e3 / HBM_PEAK_GBS, 4), **ref_split}
+    if not headline and kv_bytes == 2 and not args.no_cpu_baseline:
+        # the reference's CPU path on the same step (it has no fp8 codec): every request,
+        # C5 in groups of 16 with 3 timed runs (its padded gather is 7x its context)
+        big = index == 5
+        base = cpu_baseline(step, cfg, cfg.batch, kv_bytes, chunk=16 if big else None, runs=3 if big else 5)
+        record["cpu_baseline"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in base.items()
+                                  if k in ("value", "unit", "us_per_call", "cores", "kind", "sample")}
     print(f"[bench] C{index} {cfg.name} {codec}: {us:.1f} us/call {nbytes / us / 1e3:.0f} GB/s "
           f"({record['launch']}; kernel {kernel_us:.1f} us, {len(pools)} pools)", file=sys.stderr, flush=True)
     if not headline:
