@@ -56,10 +56,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // WIN: a window launch (verify windows, short chunks). A work item is a tile of the
 // multi-row tile list, p.work[4 * item] = (first row, rows, request, partition), of at most
-// 16 / group rows of one request; a wave serves one key/value head and its 16 MFMA
-// columns are the tile's (row, query head) pairs, column mt = row mt / group, head
-// mt % group, each masked at its own row's position. The context is read once for all
-// the tile's rows. Partials (split launches) are merged per row by row_reduce_kernel.
+// 16 / group rows of one request; p.wave_split waves serve one key/value head (taking
+// every n-th chunk, merged in LDS as in v1) and their 16 MFMA columns are the tile's
+// (row, query head) pairs, column mt = row mt / group, head mt % group, each masked at its
+// own row's position. The context is read once for all the tile's rows. Partials (split
+// launches) are merged per row by row_reduce_kernel.
 template <int D, int GC, bool BF16, bool SPLIT, bool KV8, bool WIN = false>
 __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel(const AttnParams p) {
   constexpr int MT = 16;            // tokens per MFMA tile
@@ -95,7 +96,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   // or partition (v2), and their states are merged in LDS at the end: v1 fills the GPU when
   // rows x heads alone leave compute units idle, v2 covers a partition ws times as long
   // with the same per-wave work, so a row has fewer partials to store and merge.
-  const int ws = WIN ? 1 : p.wave_split;
+  const int ws = p.wave_split;
   const int heads_per_wg = waves / ws;
   const int groups = (p.num_virtual_heads + heads_per_wg - 1) / heads_per_wg;
   WgCoord wg;
@@ -305,42 +306,40 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   // Head mt's weight sum over the wave's 4 token groups (its lanes share m_h).
   l_h += __shfl_xor(l_h, 16);
   l_h += __shfl_xor(l_h, 32);
-  if constexpr (!WIN) {
-    if (ws > 1) {
-      // Slices 1.. of a head hand (m, l, o) to slice 0 through their own LDS tiles (the
-      // keys' tile takes o[0, DT/2), the values' tile the rest: 4 * D 16-byte entries fit
-      // in 2 * D + (D + 16) / 4), which folds them in slice order: the result does not
-      // depend on the waves' timing.
-      constexpr int HALF = DT / 2;
-      u32x4* vt = reinterpret_cast<u32x4*>(&s_v[wave][0]);
-      if (active && slice > 0) {
+  if (ws > 1) {
+    // Slices 1.. of a head hand (m, l, o) to slice 0 through their own LDS tiles (the
+    // keys' tile takes o[0, DT/2), the values' tile the rest: 4 * D 16-byte entries fit
+    // in 2 * D + (D + 16) / 4), which folds them in slice order: the result does not
+    // depend on the waves' timing.
+    constexpr int HALF = DT / 2;
+    u32x4* vt = reinterpret_cast<u32x4*>(&s_v[wave][0]);
+    if (active && slice > 0) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const u32x4 w = __builtin_bit_cast(u32x4, o[t]);
+        if (t < HALF) s_k[wave][t * kWave + lane] = w;
+        else vt[(t - HALF) * kWave + lane] = w;
+      }
+      if (lane < 16) {
+        s_slice_m[wave][lane] = m_h;
+        s_slice_l[wave][lane] = l_h;
+      }
+    }
+    __syncthreads();
+    if (active && slice == 0) {
+      for (int j = 1; j < ws; ++j) {
+        const int src = wave + j;
+        const float mj = s_slice_m[src][mt], lj = s_slice_l[src][mt];
+        const float mn = fmaxf(m_h, mj);
+        const float a = fast_exp2(m_h - mn), b = fast_exp2(mj - mn);
+        l_h = l_h * a + lj * b;
+        m_h = mn;
+        const u32x4* vs = reinterpret_cast<const u32x4*>(&s_v[src][0]);
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
-          const u32x4 w = __builtin_bit_cast(u32x4, o[t]);
-          if (t < HALF) s_k[wave][t * kWave + lane] = w;
-          else vt[(t - HALF) * kWave + lane] = w;
-        }
-        if (lane < 16) {
-          s_slice_m[wave][lane] = m_h;
-          s_slice_l[wave][lane] = l_h;
-        }
-      }
-      __syncthreads();
-      if (active && slice == 0) {
-        for (int j = 1; j < ws; ++j) {
-          const int src = wave + j;
-          const float mj = s_slice_m[src][mt], lj = s_slice_l[src][mt];
-          const float mn = fmaxf(m_h, mj);
-          const float a = fast_exp2(m_h - mn), b = fast_exp2(mj - mn);
-          l_h = l_h * a + lj * b;
-          m_h = mn;
-          const u32x4* vs = reinterpret_cast<const u32x4*>(&s_v[src][0]);
-#pragma unroll
-          for (int t = 0; t < DT; ++t) {
-            const f32x4 oj = __builtin_bit_cast(f32x4, t < HALF ? s_k[src][t * kWave + lane]
-                                                                : vs[(t - HALF) * kWave + lane]);
-            o[t] = o[t] * a + oj * b;
-          }
+          const f32x4 oj = __builtin_bit_cast(f32x4, t < HALF ? s_k[src][t * kWave + lane]
+                                                              : vs[(t - HALF) * kWave + lane]);
+          o[t] = o[t] * a + oj * b;
         }
       }
     }
@@ -405,9 +404,11 @@ static hipError_t launch_mfma_d(const AttnParams& p, int gc, bool bf16, bool spl
 
 template <int D, bool BF16, bool KV8>
 static hipError_t launch_window_typed(const AttnParams& p, bool split, hipStream_t stream) {
-  // one wave per key/value head, up to kMaxWaves per workgroup; 16 MFMA columns per wave
-  const int per_wg = p.num_virtual_heads < kMaxWaves ? p.num_virtual_heads : kMaxWaves;
-  const int groups = (p.num_virtual_heads + per_wg - 1) / per_wg;
+  // p.wave_split waves per key/value head, up to kMaxWaves per workgroup; 16 MFMA columns per wave
+  const int ws = p.wave_split;
+  const int heads = p.num_virtual_heads < kMaxWaves / ws ? p.num_virtual_heads : kMaxWaves / ws;
+  const int per_wg = heads * ws;
+  const int groups = (p.num_virtual_heads + heads - 1) / heads;
   const dim3 grid((unsigned)((int64_t)p.n_work * groups)), block(per_wg * kWave);
   if (split)
     hipLaunchKernelGGL((paged_attention_mfma_kernel<D, 16, BF16, true, KV8, true>), grid, block, 0, stream, p);

@@ -252,7 +252,10 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
  * request, partition), as for ayk_paged_prefill, with at most 16 / (num_heads /
  * num_kv_heads) rows each) is one work item; a wave serves one key/value head and its
  * 16 matrix-core columns are the tile's (row, query head) pairs, each row masked at its
- * own position, so a request's context is streamed once for all the tile's rows.
+ * own position, so a request's context is streamed once for all the tile's rows. When
+ * tiles x key/value heads leave compute units idle, the library gives each head up to 8
+ * waves that split its chunks and merge in LDS (the most that keep the launch within one
+ * round of 8-wave workgroups).
  * The rows of a tile are consecutive rows of one request whose positions rise (the
  * tile's last row sees the most: nothing past its position is read); a row whose position
  * is negative sees nothing and gets zeros. partition_size 0 covers each tile's context in
