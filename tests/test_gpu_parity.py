@@ -311,6 +311,35 @@ def test_block_sizes(block_size: int, qk: str) -> None:
         assert_parity(out, expected, "bf16", f"bs{block_size}/{launch}")
 
 
+EXTREME_CASES = [
+    # a 128K-position context (v2 up to 2048 partitions of 64, v1 at 8 waves per head)
+    ("long-context", dict(steps=[(1, 131072), (1, 5)], heads=8, kv_heads=1, head_dim=128, block_size=16)),
+    # 4096 short decode rows (grids of tens of thousands of workgroups, work lists of 4096 items)
+    ("many-rows", dict(steps=[(1, int(n)) for n in np.random.default_rng(7).integers(1, 40, size=4096)], heads=8,
+                       kv_heads=2, head_dim=64, block_size=16)),
+    # the largest block size the library takes, with a context spanning two blocks
+    ("block-65536", dict(steps=[(1, 70000), (1, 3), (3, 65537)], heads=4, kv_heads=1, head_dim=64,
+                         block_size=65536, mode="mixed")),
+]
+
+
+@pytest.mark.parametrize("name,shape", EXTREME_CASES, ids=[c[0] for c in EXTREME_CASES])
+def test_extreme_shapes(name: str, shape: dict) -> None:
+    shape = dict(shape)
+    steps = shape.pop("steps")
+    s = build_scenario(steps, seed=47, spare_blocks=1, **{"mode": "decode", **shape})
+    expected = s.expected(np.float64)
+    longest = max(n for _, n in steps)
+    launches = [dict(partitions=None), dict(partitions=0, prefill=False, waves=8),
+                dict(partitions=-(-longest // 64), partition_size=64, prefill=False)]
+    if s.mode == "mixed":
+        launches += [dict(partitions=None, prefill=True, window=False),
+                     dict(partitions=None, partition_size=4096, prefill=True, window=False)]
+    for launch in launches:
+        out = run_attention(s, **launch)
+        assert_parity(out, expected, s.dtype, f"{name}/{launch}")
+
+
 @pytest.mark.parametrize("block_size", [1, 2, 3])
 def test_table_segments(block_size: int) -> None:
     # a workgroup stages at most 511 table entries at a time: with blocks of 1-2 positions these
