@@ -293,6 +293,18 @@ def test_window_tiles_and_split() -> None:
     few = step([4] * 8, [4096] * 8).window_split(8, 4)
     assert few % 64 == 0 and 0 < few < 4096
     assert step([4], [64]).window_split(8, 4) == 0
+    # the waves the library gives each head: the most (up to 8) within one round of 8-wave
+    # workgroups on 256 CUs (items x heads x waves <= 1024)
+    assert [hip_attention.window_waves(n, 8) for n in (16, 32, 64, 128, 256)] == [8, 8, 4, 2, 1]
+    assert hip_attention.window_waves(4, 1) == 8 and hip_attention.window_waves(2048, 8) == 1
+    # measured on MI355X: many 4K tiles run unsplit at 8 waves per head (32 x 4-row windows
+    # 89.3 us, the best split 86.5), few long ones split into large partitions (8 x 8K:
+    # 2048, 52.0 us; 1024 measured fastest at 50.5, 256 63.0)
+    assert hip_attention.window_partition_size([4096] * 32, 8) == 0
+    assert hip_attention.window_partition_size([2048] * 64, 8) == 0
+    assert hip_attention.window_partition_size([8192] * 8, 8) in (1024, 2048)
+    assert hip_attention.window_partition_size([32768] * 2, 8) in (1024, 2048, 4096)
+    assert hip_attention.window_partition_size([], 8) == 0
 
 
 def _cpu_buffers(**changes: object) -> KVBuffers:
