@@ -94,7 +94,7 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
   constexpr int DT = D / 16;                    // 16-element slices of head_dim for P.V
   constexpr int CPT = D / 8;                    // 8-element pieces per position
   constexpr int PIECES = CH * CPT;              // pieces per chunk of K (or V)
-  constexpr int PER_THREAD = PIECES / THREADS;  // 2 (D 64), 4 (D 128), 8 (D 256): even
+  constexpr int PER_THREAD = PIECES / THREADS;  // 2 (D 64), 4 (D 128), 4 or 8 (D 256)
   // Values in LDS token-major, rows VP elements apart: the transposing reads of the
   // P.V operand (16 rows of one 16-lane group, 8 bytes each) then cover the banks evenly.
   constexpr int VP = D + 16;
