@@ -22,10 +22,12 @@ import torch
 from ayaka_amd.enums import KVLayoutKind
 from ayaka_amd.errors import BackendError
 from ayaka_amd.hip import attention as hip_attention
+from ayaka_amd.hip import kvcache as hip_kvcache
 from ayaka_amd.kvcache import FP8_E4M3_CODEC, RAW_CODEC, KVBuffers
-from oracle.numerics import e4m3_to_f32, f32_to_e4m3
+from oracle import paged
+from oracle.numerics import bits_to_f32, e4m3_to_f32, f32_to_bits, f32_to_e4m3
 from tests._support import build_scenario
-from tests.test_gpu_parity import DEV, assert_parity, plan_scenario, to_device
+from tests.test_gpu_parity import DEV, assert_parity, plan_scenario, to_bits, to_device
 
 pytestmark = pytest.mark.gpu
 
@@ -118,3 +120,80 @@ def test_sweep(case: int) -> None:
         assert_parity(out, expected, s.dtype, f"case {case} {label} {desc}")
         if padding_rows:
             assert torch.count_nonzero(out[padding_rows]) == 0, f"case {case} {label}: padding rows"
+
+
+# --- the bit-exact ops: KV write (both codecs) and block ops ------------------------------------
+
+OPS_CASES = 48
+
+
+@pytest.mark.parametrize("case", range(OPS_CASES))
+def test_sweep_bit_exact_ops(case: int) -> None:
+    """A seeded shape (``default_rng(7000 + case)``: head_dim 8-256, 1-8 key/value heads, block size
+    1-64, NHD/HND, fp16/bf16, 16-bit or fp8 caches, steps of prefill and decode rows with padding
+    requests), then the step's KV write and, on 16-bit caches, gather / copy_blocks / zero_blocks
+    with int32 or int64 ids: every cache byte against the oracle's, except block 0 (padding rows'
+    slot, written in an unspecified order)."""
+    rng = np.random.default_rng(7000 + case)
+    head_dim = int([8, 12, 16, 64, 128, 256][rng.integers(6)])
+    kv_heads = int(rng.integers(1, 9))
+    bs = int(BLOCK_SIZES[rng.integers(len(BLOCK_SIZES))])
+    dtype = ["bf16", "fp16"][rng.integers(2)]
+    layout = ["nhd", "hnd"][rng.integers(2)]
+    fp8 = rng.random() < 0.4
+    steps = []
+    for _ in range(int(rng.integers(1, 6))):
+        length = 0 if rng.random() < 0.15 else int(rng.integers(1, 300))
+        steps.append((max(1, min(int(rng.integers(1, 40)), length)) if length else int(rng.integers(1, 3)), length))
+    s = build_scenario(steps, dtype=dtype, layout=layout, heads=kv_heads, kv_heads=kv_heads, head_dim=head_dim,
+                       block_size=bs, mode="mixed", seed=int(rng.integers(1 << 30)), spare_blocks=8)
+    desc = dict(head_dim=head_dim, kv_heads=kv_heads, block_size=bs, dtype=dtype, layout=layout, fp8=fp8,
+                steps=steps)
+    print(f"case {case}: {desc}", flush=True)
+    n = len(s.plan["slot_mapping"])
+    rows = rng.standard_normal((2, n, kv_heads, head_dim)) * np.exp2(rng.uniform(-10, 8, (2, n, kv_heads, 1)))
+    bits = f32_to_bits(rows.astype(np.float32), dtype)
+    meta = plan_scenario(s)
+    kind = KVLayoutKind.NHD if layout == "nhd" else KVLayoutKind.HND
+    if fp8:
+        kc, vc = f32_to_e4m3(s.k), f32_to_e4m3(s.v)
+        buffers = KVBuffers(torch.from_numpy(kc).view(torch.float8_e4m3fn).to(DEV),
+                            torch.from_numpy(vc).view(torch.float8_e4m3fn).to(DEV), kind, FP8_E4M3_CODEC)
+        hip_kvcache.store(to_device(bits[0], dtype), to_device(bits[1], dtype), buffers, meta)
+        torch.cuda.synchronize()
+        decoded = bits_to_f32(bits, dtype)
+        paged.store(kc, vc, f32_to_e4m3(decoded[0]), f32_to_e4m3(decoded[1]), s.plan["slot_mapping"], layout)
+        got_k, got_v = buffers.k.view(torch.uint8).cpu().numpy(), buffers.v.view(torch.uint8).cpu().numpy()
+        assert np.array_equal(got_k[1:], kc[1:]) and np.array_equal(got_v[1:], vc[1:]), f"case {case}: {desc}"
+        return
+    buffers = KVBuffers(to_device(s.k_bits, dtype), to_device(s.v_bits, dtype), kind, RAW_CODEC)
+    hip_kvcache.store(to_device(bits[0], dtype), to_device(bits[1], dtype), buffers, meta)
+    torch.cuda.synchronize()
+    want_k, want_v = s.k_bits.copy(), s.v_bits.copy()
+    paged.store(want_k, want_v, bits[0], bits[1], s.plan["slot_mapping"], layout)
+    got_k, got_v = to_bits(buffers.k), to_bits(buffers.v)
+    assert np.array_equal(got_k[1:], want_k[1:]) and np.array_equal(got_v[1:], want_v[1:]), f"case {case}: {desc}"
+    # block ops on the written caches (block 0 included now: made deterministic first)
+    buffers.k[0].zero_()
+    buffers.v[0].zero_()
+    torch.cuda.synchronize()
+    cur_k, cur_v = to_bits(buffers.k), to_bits(buffers.v)
+    blocks = buffers.k.shape[0]
+    ids_dtype = [torch.int32, torch.int64][rng.integers(2)]
+    picks = rng.integers(0, blocks, size=int(rng.integers(1, 2 * blocks)))
+    out_k = torch.empty((len(picks), *buffers.k.shape[1:]), dtype=buffers.k.dtype, device=DEV)
+    out_v = torch.empty_like(out_k)
+    hip_kvcache.gather(buffers, torch.tensor(picks, dtype=ids_dtype, device=DEV), out_k, out_v)
+    perm = rng.permutation(blocks)
+    pairs = int(rng.integers(1, blocks // 2 + 1))
+    src, dst = perm[:pairs], perm[pairs:2 * pairs]  # disjoint, so the result does not depend on order
+    hip_kvcache.copy_blocks(buffers, torch.tensor(src, dtype=ids_dtype, device=DEV),
+                            torch.tensor(dst, dtype=ids_dtype, device=DEV))
+    zero = rng.choice(blocks, size=int(rng.integers(1, blocks + 1)), replace=False)
+    hip_kvcache.zero_blocks(buffers, torch.tensor(zero, dtype=ids_dtype, device=DEV))
+    torch.cuda.synchronize()
+    want_gk, want_gv = paged.gather(cur_k, cur_v, picks)
+    assert np.array_equal(to_bits(out_k), want_gk) and np.array_equal(to_bits(out_v), want_gv), f"case {case}"
+    paged.copy_blocks(cur_k, cur_v, src, dst)
+    paged.zero_blocks(cur_k, cur_v, zero)
+    assert np.array_equal(to_bits(buffers.k), cur_k) and np.array_equal(to_bits(buffers.v), cur_v), f"case {case}"
