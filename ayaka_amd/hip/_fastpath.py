@@ -12,6 +12,7 @@ eager steps.
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import Any
 
@@ -28,12 +29,15 @@ MAX_RECORDS = 4096
 
 @dataclass(slots=True)
 class Launch:
-    """One library call: ``fn(*args, stream)``; ``keep`` are the tensors its pointers come
+    """One library call: ``fn(*args, stream)``, kept as a pointer to the same export with no
+    declared argument types and the arguments converted once to the declared ones, so that a
+    replay skips ctypes' per-argument conversion; ``keep`` are the tensors its pointers come
     from, ``ptrs`` their data pointers and shapes when it was recorded."""
 
     op: str
     fn: Any
     args: tuple
+    stream_arg: Any  # the stream handle's conversion: ctypes.c_void_p for a library export
     keep: tuple
     ptrs: tuple
     device: torch.device
@@ -53,7 +57,26 @@ class Recorder:
 
 
 def _signature(tensors: tuple) -> tuple:
-    return tuple((t.data_ptr(), t.shape) for t in tensors)
+    if len(tensors) == 4:  # every call site of the library: unrolled, a few hundred ns cheaper
+        a, b, c, d = tensors
+        return (a.data_ptr(), b.data_ptr(), c.data_ptr(), d.data_ptr(), a.shape, b.shape, c.shape, d.shape)
+    return tuple(t.data_ptr() for t in tensors) + tuple(t.shape for t in tensors)
+
+
+def convert(types: list, args: tuple) -> tuple:
+    """``args`` as instances of the ctypes ``types`` a library export declares (the same values
+    ctypes would pass for them; numpy scalars included)."""
+    out = []
+    for t, a in zip(types, args, strict=True):
+        if isinstance(a, t):
+            out.append(a)
+        elif t is ctypes.c_float:
+            out.append(t(float(a)))
+        elif t is ctypes.c_void_p:
+            out.append(t(None if a is None else int(a)))
+        else:
+            out.append(t(int(a)))
+    return tuple(out)
 
 
 def lookup(cache: dict, key: tuple, tensors: tuple) -> Launch | None:
@@ -70,8 +93,14 @@ def remember(cache: dict, key: tuple, tensors: tuple, keep: tuple, recorder: Rec
     if len(cache) >= MAX_RECORDS:
         cache.clear()
     op, fn, args, device, scratch = recorder.launch
-    cache[key] = Launch(op, fn, args, keep + tensors, _signature(tensors), device, scratch)
+    stream_arg: Any = int
+    types = getattr(fn, "argtypes", None)
+    if types is not None:  # a library export (its last argument is the stream)
+        untyped = _lib.lib()[fn.__name__]  # a new function object: fn keeps its declared types
+        untyped.restype = fn.restype
+        fn, args, stream_arg = untyped, convert(types[:-1], args), ctypes.c_void_p
+    cache[key] = Launch(op, fn, args, stream_arg, keep + tensors, _signature(tensors), device, scratch)
 
 
 def run(launch: Launch, stream: int) -> None:
-    _lib.check(launch.op, launch.fn(*launch.args, stream))
+    _lib.check(launch.op, launch.fn(*launch.args, launch.stream_arg(stream)))

@@ -397,3 +397,25 @@ def test_recorded_launches_replay_only_for_the_same_storage() -> None:
     for i in range(_fastpath.MAX_RECORDS + 1):
         _fastpath.remember(cache, ("k", i), (q,), (), record)
     assert len(cache) <= _fastpath.MAX_RECORDS
+
+
+def test_recorded_library_arguments_keep_their_values() -> None:
+    # a recorded library call converts its arguments once to the export's declared types;
+    # the values (pointers, sizes, numpy scalars, the float scale) must come through unchanged
+    import ctypes
+
+    import numpy as np
+
+    from ayaka_amd.hip import _fastpath, _lib
+
+    types = _lib.EXPORTS["ayk_paged_attention_v1"][1][:-1]
+    args = tuple(range(1000, 1000 + len(types)))
+    args = args[:5] + (np.int64(64),) + (None,) + args[7:19] + (np.float32(0.125),) + args[20:]
+    converted = _fastpath.convert(types, args)
+    assert [type(c) for c in converted] == types
+    assert converted[6].value is None and converted[5].value == 64 and converted[19].value == 0.125
+    assert [c.value for i, c in enumerate(converted) if i not in (5, 6, 19)] == \
+        [a for i, a in enumerate(args) if i not in (5, 6, 19)]
+    with pytest.raises(ValueError):
+        _fastpath.convert(types, args[:-1])
+    assert isinstance(_fastpath.convert([ctypes.c_int32], (ctypes.c_int32(3),))[0], ctypes.c_int32)
