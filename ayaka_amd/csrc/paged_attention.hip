@@ -459,17 +459,22 @@ hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipSt
 
 template <int D, bool BF16>
 static hipError_t launch_reduce_typed(const AttnParams& p, int compute_units, hipStream_t stream) {
-  // Partition slots per (row, head): one for up to 4 partitions per row, then 4, or as many
-  // as one workgroup holds for a single head when 4 would leave compute units without a
-  // workgroup (few rows of many partitions: C4's 8 x 32 pairs). A staged launch sizes
-  // max_partitions for its smallest partition size while its steps mostly run far fewer,
-  // so 4 slots serve it unless the grid is small.
+  // Partition slots per (row, head): one for up to 4 partitions per row, and up to 16 when
+  // one slot still gives every compute unit a workgroup (many pairs, most of whose rows often
+  // hold one partition and merge nothing: a ragged batch's grid of 2-pair workgroups spent
+  // ~4 us more in residency rounds); then 4, or as many as one workgroup holds for a single
+  // head when 4 would leave compute units without a workgroup (few rows of many partitions:
+  // 8 rows x 32 heads over 32K). A staged launch sizes max_partitions for its smallest
+  // partition size while its steps mostly run far fewer, so 4 slots serve it unless the grid
+  // is small.
   constexpr int QUADS = D / 4;
   constexpr int S_MAX = kReduceThreads / QUADS;
   constexpr int S4 = S_MAX < 4 ? S_MAX : 4;
   const int64_t pairs = (int64_t)p.n_rows * p.num_heads;
+  const int64_t groups1 = (pairs + S_MAX - 1) / S_MAX;
   const int64_t groups4 = (pairs + S_MAX / S4 - 1) / (S_MAX / S4);
-  const int s = p.max_partitions <= 4 ? 1 : (p.max_partitions <= 16 || groups4 >= compute_units) ? S4 : S_MAX;
+  const bool one_slot = p.max_partitions <= 4 || (p.max_partitions <= 16 && groups1 >= compute_units);
+  const int s = one_slot ? 1 : (p.max_partitions <= 16 || groups4 >= compute_units) ? S4 : S_MAX;
   const dim3 block(kReduceThreads);
   auto grid = [&](int heads) { return dim3((unsigned)((pairs + heads - 1) / heads)); };
   if (s == 1) hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, 1>), grid(S_MAX), block, 0, stream, p);
