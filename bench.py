@@ -35,19 +35,19 @@ HBM_PEAK_GBS = 8000.0
 # the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
 PROFILED_TRAFFIC = {
     (3, "paged_attention_mfma_kernel (v1, 4 waves per head)", 0):
-        (1_080_117_236, 524_288, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
+        (1_080_070_645, 524_288, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
     (3, "paged_attention_mfma_kernel (v1, 4 waves per head, fp8 cache)", 0):
-        (544_005_220, 524_288, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
+        (544_024_803, 524_288, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
     (4, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 704):
-        (668_303_933, 4_054_912, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
+        (668_605_302, 4_054_928, "profiles/paged_attention_mfma_kernel_c4_long_context.md"),
     (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 3072):
-        (2_598_003_942, 10_319_152, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
+        (2_598_158_371, 10_319_456, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8.md"),
     (2, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 320):
-        (148_252_492, 2_128_560, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
+        (148_332_170, 2_128_368, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
     (1, "paged_attention_mfma_kernel (v1, 8 waves per head)", 0):
         (1_634_780, 4_608, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
     (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1280):
-        (1_317_560_092, 20_072_720, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
+        (1_316_632_688, 20_077_328, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
 }
 
 
