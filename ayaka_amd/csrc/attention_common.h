@@ -202,10 +202,15 @@ __device__ __forceinline__ int partition_size_of(const AttnParams& p) {
 }
 
 // Length of row `row`'s context and its request, clamped so no read leaves the table.
+// The row's position and request are read unconditionally (from a valid stand-in address
+// when a table is absent) and ahead of the request's length, so the lookups overlap instead
+// of each waiting behind a branch.
 __device__ __forceinline__ void row_context(const AttnParams& p, int row, int& req, int& len) {
-  req = p.request_of_row ? p.request_of_row[row] : row;
+  const int pos = *(p.positions ? p.positions + row : p.kv_lengths);
+  const int r = *(p.request_of_row ? p.request_of_row + row : p.kv_lengths);
+  req = p.request_of_row ? r : row;
   len = p.kv_lengths[req];
-  if (len > 0 && p.positions) len = min(len, p.positions[row] + 1);
+  if (len > 0 && p.positions) len = min(len, pos + 1);
   len = max(0, min(len, p.max_len));
 }
 

@@ -315,29 +315,57 @@ __global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const 
   const int slot = (tid / QUADS) % S;
   const int64_t pair = (int64_t)blockIdx.x * HEADS + hl;  // (row, head) over n_rows x num_heads
   const bool valid = pair < (int64_t)p.n_rows * p.num_heads;
-  const int row = valid ? (int)(pair / p.num_heads) : 0;
+  // 32-bit division: the host refuses n_rows x num_heads above INT32_MAX
+  const int pair32 = valid ? (int)pair : 0;
+  const int row = pair32 / p.num_heads;
+  const int head = pair32 - row * p.num_heads;
+  // the row's first partial slot of a staged launch, read with the row's context
+  const int staged_first = *(p.staged ? p.staged + 2 + row : p.kv_lengths);
   int req, len;
   row_context(p, row, req, len);
   const int np = valid ? (len > 0 ? (len - 1) / partition_size_of(p) + 1 : 0) : 1;
   uint16_t* out = static_cast<uint16_t*>(p.out) + pair * D;
-  const int64_t first = partial_index(p, row, (int)(pair % p.num_heads), np);
+  // partial_index, with the staged slot read above
+  const int64_t first = p.staged ? (int64_t)staged_first * p.num_heads + (int64_t)head * np
+                                 : ((int64_t)row * p.num_heads + head) * p.max_partitions;
   const float* ml = p.part_ml + first * 2;
   const f32x4* po = reinterpret_cast<const f32x4*>(p.part_o + first * D);
 
   float m = kNoScore, l = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int nfold = np > 1 ? np : 0;  // rows of one partition (or none) fold nothing
-#pragma unroll 4
-  for (int i = slot; i < nfold; i += S) {
-    const float mi = ml[2 * i];
-    const float wi = ml[2 * i + 1];
-    const f32x4 v = po[(int64_t)i * QUADS + quad];
-    const float mn = fmaxf(m, mi);
+  auto fold = [&](float mi, float wi, f32x4 v, bool real) {
+    const float mn = real ? fmaxf(m, mi) : m;
     const float a = fast_exp2(m - mn);
-    const float b = wi * fast_exp2(mi - mn);
+    const float b = real ? wi * fast_exp2(mi - mn) : 0.f;
     l = l * a + b;
     acc = acc * a + v * b;
     m = mn;
+  };
+  if constexpr (S == 1) {
+    // One slot: the thread folds its pair's partitions one by one (with one slot the
+    // grid is wide and the rows hold few partitions; batched loads measured no faster).
+#pragma unroll 4
+    for (int i = 0; i < nfold; ++i) fold(ml[2 * i], ml[2 * i + 1], po[(int64_t)i * QUADS + quad], true);
+  } else {
+    // 8 partitions per thread per batch, all loaded before the first is folded (indices
+    // past the last partition read the last one, folded with weight 0), so a batch costs
+    // one memory round trip, not one per partition; the fold order is the thread's
+    // partitions in order, as one at a time.
+    constexpr int B = 8;
+    for (int base = 0; base < nfold; base += B * S) {
+      float mi[B], wi[B];
+      f32x4 vi[B];
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        const int i = min(base + slot + k * S, nfold - 1);
+        mi[k] = ml[2 * i];
+        wi[k] = ml[2 * i + 1];
+        vi[k] = po[(int64_t)i * QUADS + quad];
+      }
+#pragma unroll
+      for (int k = 0; k < B; ++k) fold(mi[k], wi[k], vi[k], base + slot + k * S < nfold);
+    }
   }
   if constexpr (S > 1) {
     s_acc[hl][slot][quad] = acc;
