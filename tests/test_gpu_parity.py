@@ -494,6 +494,27 @@ def counters_are_clear() -> bool:
     return all(int(c.abs().max()) == 0 for c in hip_attention._counters.values())
 
 
+@pytest.mark.parametrize("shape", ["8 slots, 3 batches", "4 slots, 2 batches", "1 slot"])
+def test_reduce_kernel_slot_shapes(shape: str) -> None:
+    # the reduce kernel's three shapes, chosen by partitions per row and the grid: 8 slots per
+    # (row, head) pair for few pairs of many partitions (here 133 partitions of 64: three
+    # batches of 8 per slot), 4 slots for many pairs of many partitions (41: two batches),
+    # one slot for many pairs of at most 16 (most rows here hold one partition)
+    rng = np.random.default_rng(71)
+    if shape == "8 slots, 3 batches":
+        lengths = [8500, 4100, 0, 64, 65]
+    elif shape == "4 slots, 2 batches":
+        lengths = [2600, 0, 1] + rng.integers(1, 2600, 61).tolist()
+    else:
+        lengths = [1000, 0] + rng.integers(1, 64, 200).tolist() + rng.integers(64, 1000, 54).tolist()
+    s = build_scenario([(1, n) for n in lengths], heads=8, kv_heads=2, head_dim=128, block_size=16,
+                       mode="decode", seed=72)
+    parts = -(-max(lengths) // 64)
+    out = run_attention(s, parts, "mfma", partition_size=64, merge="reduce-kernel")
+    assert_parity(out, s.expected(np.float64), "bf16", shape)
+    assert torch.count_nonzero(out[lengths.index(0)]) == 0
+
+
 @pytest.mark.parametrize("qk", QK)
 @pytest.mark.parametrize("heads,kv_heads", [(8, 2), (40, 10), (96, 12), (12, 12)])
 def test_single_launch_merge_agrees_with_the_reduce_kernel(qk: str, heads: int, kv_heads: int) -> None:
