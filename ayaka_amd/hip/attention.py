@@ -335,10 +335,6 @@ class HipGraphPlan:
         return 2 + self.positions.shape[0]
 
 
-def _host_ints(tensor: torch.Tensor) -> tuple[int, ...]:
-    return tuple(int(x) for x in tensor.tolist())
-
-
 def plan(
     mode: ForwardMode,
     rows_per_request: torch.Tensor,
@@ -360,8 +356,14 @@ def plan(
         )
     if block_size < 1:
         raise BackendError(f"{op}: block_size must be positive, got {block_size}", context={"op": op})
-    rows, lengths = _host_ints(rows_per_request), _host_ints(kv_lengths)
-    for index, (count, length) in enumerate(zip(rows, lengths)):
+    rows_np = rows_per_request.to(device="cpu", dtype=torch.int64).numpy()
+    lengths_np = kv_lengths.to(device="cpu", dtype=torch.int64).numpy()
+    # the checks over all requests at once; the first failing request names the refusal
+    bad = np.flatnonzero((rows_np < 0) | (lengths_np < 0) | ((lengths_np > 0) & (rows_np > lengths_np))
+                         | ((rows_np != 1) if mode == ForwardMode.DECODE else False))
+    if bad.size:
+        index = int(bad[0])
+        count, length = int(rows_np[index]), int(lengths_np[index])
         if count < 0 or length < 0:
             raise BackendError(
                 f"{op}: request {index} has {count} rows and {length} tokens; neither can be "
@@ -374,66 +376,59 @@ def plan(
                 "keys after this step; kv_lengths counts this step's rows",
                 context={"op": op, "request": index},
             )
-        if mode == ForwardMode.DECODE and count != 1:
-            raise BackendError(
-                f"{op}: a DECODE step has one row per request, request {index} has {count}",
-                context={"op": op, "request": index},
-            )
-    total = sum(rows)
+        raise BackendError(
+            f"{op}: a DECODE step has one row per request, request {index} has {count}",
+            context={"op": op, "request": index},
+        )
+    rows, lengths = tuple(rows_np.tolist()), tuple(lengths_np.tolist())
+    total = int(rows_np.sum())
     if mode == ForwardMode.IDLE and total:
         raise BackendError(f"{op}: an IDLE step has no rows, got {total}", context={"op": op})
 
     # The table: long enough for every request, and no padding block inside a used range.
     table_host = block_rows.to(device="cpu", dtype=torch.int64)
     max_blocks = table_host.shape[1]
-    needed = [-(-length // block_size) for length in lengths]
-    longest = max(needed, default=0)
+    needed = -(-lengths_np // block_size)
+    longest = int(needed.max(initial=0))
     if longest > max_blocks or (total > 0 and max_blocks == 0):
         raise BackendError(
             f"{op}: block_rows has {max_blocks} column(s) but the longest request needs "
             f"{longest} blocks of {block_size}",
             context={"op": op, "argument": "block_rows"},
         )
+    table_np = table_host.numpy()
     if batch and max_blocks:
-        used = torch.arange(max_blocks)[None, :] < torch.tensor(needed, dtype=torch.int64)[:, None]
-        if bool((used & (table_host == 0)).any()):
+        used = np.arange(max_blocks)[None, :] < needed[:, None]
+        if bool((used & (table_np == 0)).any()):
             raise BackendError(
                 f"{op}: block_rows has the padding block 0 inside a request's blocks",
                 context={"op": op, "argument": "block_rows"},
             )
 
-    request_of_row: list[int] = []
-    positions: list[int] = []
-    slots: list[int] = []
-    row_lengths: list[int] = []
-    table_list = table_host.tolist()
-    for request, (count, length) in enumerate(zip(rows, lengths)):
-        for j in range(count):
-            request_of_row.append(request)
-            if length == 0:
-                positions.append(0)
-                slots.append(0)
-                row_lengths.append(0)
-            else:
-                position = length - count + j
-                positions.append(position)
-                row_lengths.append(position + 1)
-                slots.append(
-                    table_list[request][position // block_size] * block_size
-                    + position % block_size
-                )
+    # Row j of a request of `count` rows and `length` tokens sits at position
+    # length - count + j, in slot table[request][position // bs] * bs + position % bs; a
+    # request without tokens (padding) gets position 0, slot 0 and no context.
+    request_of_row = np.repeat(np.arange(batch, dtype=np.int64), rows_np)
+    first = np.cumsum(rows_np) - rows_np
+    j = np.arange(total, dtype=np.int64) - np.repeat(first, rows_np)
+    row_length = lengths_np[request_of_row]
+    live = row_length > 0
+    positions_np = np.where(live, row_length - rows_np[request_of_row] + j, 0)
+    blocks = table_np[request_of_row, positions_np // block_size] if total else np.zeros(0, dtype=np.int64)
+    slots_np = np.where(live, blocks * block_size + positions_np % block_size, 0)
+    row_lengths = tuple(np.where(live, positions_np + 1, 0).tolist())
 
     device = rows_per_request.device
     return AttentionMetadata(
         mode=mode,
         block_size=block_size,
-        rows_per_request=torch.tensor(rows, dtype=torch.int32, device=device),
-        request_of_row=torch.tensor(request_of_row, dtype=torch.int32, device=device),
-        positions=torch.tensor(positions, dtype=torch.int32, device=device),
-        slot_mapping=torch.tensor(slots, dtype=torch.int64, device=device),
-        kv_lengths=torch.tensor(lengths, dtype=torch.int32, device=device),
+        rows_per_request=torch.from_numpy(rows_np.astype(np.int32)).to(device),
+        request_of_row=torch.from_numpy(request_of_row.astype(np.int32)).to(device),
+        positions=torch.from_numpy(positions_np.astype(np.int32)).to(device),
+        slot_mapping=torch.from_numpy(slots_np).to(device),
+        kv_lengths=torch.from_numpy(lengths_np.astype(np.int32)).to(device),
         block_table=block_rows.to(device=device, dtype=torch.int32).contiguous(),
-        plan=HipAttentionPlan(rows, lengths, max(lengths, default=0), sum(row_lengths), tuple(row_lengths)),
+        plan=HipAttentionPlan(rows, lengths, max(lengths, default=0), sum(row_lengths), row_lengths),
     )
 
 

@@ -64,6 +64,21 @@ def test_plan_matches_the_oracle_on_random_steps() -> None:
         for key in ("request_of_row", "positions", "slot_mapping"):
             assert getattr(meta, key).tolist() == want[key].tolist()
         assert meta.plan.max_length == max(lengths)
+        # the host record the split model reads: plain ints, each row's visible context
+        assert meta.plan.rows == tuple(rows) and meta.plan.kv_lengths == tuple(lengths)
+        assert meta.plan.row_lengths == tuple(p + 1 if lengths[r] else 0
+                                              for r, p in zip(want["request_of_row"].tolist(),
+                                                              want["positions"].tolist()))
+        assert all(type(x) is int for x in meta.plan.row_lengths + meta.plan.rows + meta.plan.kv_lengths)
+    for _ in range(10):  # decode steps: one row per request, padding requests among them
+        batch, bs = int(rng.integers(1, 40)), int(rng.choice([1, 16, 32]))
+        lengths = [int(x) for x in rng.integers(0, 300, size=batch)]
+        width = max(max(-(-n // bs) for n in lengths), 1)
+        table = rng.integers(1, 999, size=(batch, width + 2))
+        meta = hip_attention.plan(ForwardMode.DECODE, _ints(*[1] * batch), _ints(*lengths), torch.from_numpy(table), bs)
+        want = paged.plan("decode", [1] * batch, lengths, table, bs)
+        for key in ("request_of_row", "positions", "slot_mapping"):
+            assert getattr(meta, key).tolist() == want[key].tolist()
 
 
 def test_plan_rejects_mismatched_batches_and_bad_types() -> None:
