@@ -292,9 +292,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
 // elements (t % (D/4)) of every S-th partition from t / (D/4) on and merges them
 // online (its own running max), so its partial loads are independent; the S
 // partial merges then meet in LDS with the same log-sum-exp rule. The host
-// takes S = 1 for a few partitions per row (one workgroup then merges 8 heads
-// at D 128: a step's grid is a few hundred workgroups, not one per head) and
-// more for long rows, whose serial folds would otherwise be long. A row with
+// takes S = 1 for up to 4 partitions per row, or up to 16 when the grid still
+// gives every compute unit a workgroup (one workgroup then merges 8 heads at
+// D 128), and more slots for long rows, whose serial folds would otherwise be
+// long. A row with
 // one partition was written by the partition kernel, so v2 with a single
 // partition rounds exactly the value v1 rounds; a row without context gets zeros.
 constexpr int kReduceThreads = 256;
