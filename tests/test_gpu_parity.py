@@ -991,6 +991,29 @@ def test_c_abi_v2_follows_the_staged_split(merge_flag: int, heads: int) -> None:
     assert int(arrivals.abs().sum()) == 0  # the in-kernel merge leaves its counters at zero
 
 
+def test_attend_refuses_what_the_reference_contract_refuses() -> None:
+    # the reference contract's refusals (tests/ops/test_attention_contract.py:252-391)
+    import dataclasses
+
+    s = build_scenario([(1, 10), (1, 7)], heads=4, kv_heads=2, head_dim=64, block_size=16, mode="decode")
+    buffers = scenario_buffers(s)
+    meta = plan_scenario(s)
+    q = to_device(s.q_bits, s.dtype)
+    foreign = dataclasses.replace(meta, plan=object())
+    with pytest.raises(BackendError, match="planned by another backend"):
+        hip_attention.attend(q, buffers, foreign, torch.empty_like(q), scale=1.0)
+    small = dataclasses.replace(meta, block_size=8)
+    with pytest.raises(BackendError, match="planned for blocks of 8 positions but the cache has blocks of 16"):
+        hip_attention.attend(q, buffers, small, torch.empty_like(q), scale=1.0)
+    with pytest.raises(BackendError, match=r"q must be bfloat16 \[2, 4, 64\]"):
+        hip_attention.attend(q[:1], buffers, meta, torch.empty_like(q[:1]), scale=1.0)
+    with pytest.raises(BackendError, match=r"out must be bfloat16 \[2, 4, 64\]"):
+        hip_attention.attend(q, buffers, meta, torch.empty_like(q, dtype=torch.float32), scale=1.0)  # never cast into
+    q3 = q[:, :3].contiguous()
+    with pytest.raises(BackendError, match="not a positive multiple of the cache's 2 key/value heads"):
+        hip_attention.attend(q3, buffers, meta, torch.empty_like(q3), scale=1.0)
+
+
 def test_unsupported_shapes_are_refused_before_launch() -> None:
     s = build_scenario([(1, 10)], head_dim=64, block_size=16, mode="decode")
     buffers = scenario_buffers(s)

@@ -434,3 +434,14 @@ def test_recorded_library_arguments_keep_their_values() -> None:
     with pytest.raises(ValueError):
         _fastpath.convert(types, args[:-1])
     assert isinstance(_fastpath.convert([ctypes.c_int32], (ctypes.c_int32(3),))[0], ctypes.c_int32)
+
+
+def test_plan_accepts_int64_inputs() -> None:
+    # tests/ops/test_attention_contract.py:414-423: int64 step tensors plan as int32 do
+    as32 = hip_attention.plan(ForwardMode.MIXED, _ints(2, 1), _ints(5, 3), torch.tensor([[3, 4], [7, 0]]), 4)
+    as64 = hip_attention.plan(ForwardMode.MIXED, torch.tensor([2, 1]), torch.tensor([5, 3]),
+                              torch.tensor([[3, 4], [7, 0]], dtype=torch.int64), 4)
+    for key in ("rows_per_request", "request_of_row", "positions", "slot_mapping", "kv_lengths", "block_table"):
+        a, b = getattr(as32, key), getattr(as64, key)
+        assert a.dtype == b.dtype and a.tolist() == b.tolist(), key
+    assert as64.positions.tolist() == [3, 4, 2] and as64.slot_mapping.tolist() == [15, 16, 30]
