@@ -1014,6 +1014,35 @@ def test_attend_refuses_what_the_reference_contract_refuses() -> None:
         hip_attention.attend(q3, buffers, meta, torch.empty_like(q3), scale=1.0)
 
 
+def test_kvcache_refuses_what_the_reference_contract_refuses() -> None:
+    # the reference contract's refusals (tests/ops/test_kvcache_contract.py:200-296), raised
+    # before a launch; nothing in the cache changes
+    s = build_scenario([(2, 9), (1, 4)], heads=4, kv_heads=2, head_dim=64, block_size=16, seed=5)
+    buffers = scenario_buffers(s)
+    meta = plan_scenario(s)
+    before = (buffers.k.clone(), buffers.v.clone())
+    rows = sum(s.rows)
+    k = torch.zeros((rows, 2, 64), dtype=torch.bfloat16, device=buffers.k.device)
+    with pytest.raises(BackendError, match=r"k must be bfloat16 \[3, 2, 64\]"):
+        hip_kvcache.store(k[:2], k[:2], buffers, meta)  # one row short of the slot mapping
+    with pytest.raises(BackendError, match=r"v must be bfloat16 \[3, 2, 64\]"):
+        hip_kvcache.store(k, k.half(), buffers, meta)
+    with pytest.raises(BackendError, match="planned for blocks of 8 positions but the cache has blocks of 16"):
+        import dataclasses
+        hip_kvcache.store(k, k, buffers, dataclasses.replace(meta, block_size=8))
+    ids = torch.tensor([1, 2], dtype=torch.int32, device=buffers.k.device)
+    with pytest.raises(BackendError, match="src has 2 blocks but dst has 1"):
+        hip_kvcache.copy_blocks(buffers, ids, ids[:1])
+    with pytest.raises(BackendError, match="int32 or int64 tensor"):
+        hip_kvcache.zero_blocks(buffers, ids.float())
+    out = torch.empty((1, *buffers.k.shape[1:]), dtype=buffers.k.dtype, device=buffers.k.device)
+    with pytest.raises(BackendError, match="out_k must be bfloat16"):
+        hip_kvcache.gather(buffers, ids, out, out)  # one block of output for two ids
+    torch.cuda.synchronize()
+    for now, then in zip((buffers.k, buffers.v), before):  # the caches hold NaN padding: compare bits
+        assert torch.equal(now.view(torch.int16), then.view(torch.int16))
+
+
 def test_unsupported_shapes_are_refused_before_launch() -> None:
     s = build_scenario([(1, 10)], head_dim=64, block_size=16, mode="decode")
     buffers = scenario_buffers(s)
