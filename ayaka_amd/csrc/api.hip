@@ -139,8 +139,15 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
   p.num_blocks = c.num_blocks;
   p.block_size = c.block_size;
   block_divisor(c.block_size, p.bs_magic, p.bs_shift);
+  // The kernels walk a context in 32-bit positions, a staged table segment (up to
+  // kTableCap blocks) and a chunk past the current one at a time; a table whose positions
+  // come within that reach of INT32_MAX could overflow those sums, so it is refused.
   const int64_t table_len = (int64_t)c.max_blocks * c.block_size;
-  p.max_len = (int32_t)std::min<int64_t>(table_len, INT32_MAX);
+  const int64_t max_table_len = INT32_MAX - (int64_t)(ayk::kTableCap + 1) * c.block_size - 4096;
+  if (table_len > max_table_len)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: a table of %d blocks of %d positions exceeds %lld positions per row", op,
+                c.max_blocks, c.block_size, (long long)max_table_len);
+  p.max_len = (int32_t)table_len;
   p.scale_log2 = c.scale * 1.4426950408889634f;
   p.partition_size = INT32_MAX;
   p.max_partitions = 1;
@@ -253,12 +260,26 @@ static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 constexpr int kMaxDevices = 64;
 std::atomic<void*> g_scratch_ptr[kMaxDevices];
 
-void* static_scratch(const char* op) {
+void* static_scratch(const char* op, void* stream) {
   int dev = -1;
   hipError_t err = hipGetDevice(&dev);
   if (err != hipSuccess || dev < 0 || dev >= kMaxDevices) {
     fail(AYK_ERR_LAUNCH, "%s: no current device (%s)", op, hipGetErrorString(err));
     return nullptr;
+  }
+  // The array is looked up on the current device; a stream of another device would run the
+  // kernels there with this device's address, so the two must agree.
+  if (stream) {
+    int stream_dev = -1;
+    err = hipStreamGetDevice(static_cast<hipStream_t>(stream), &stream_dev);
+    if (err != hipSuccess) {
+      fail(AYK_ERR_LAUNCH, "%s: hipStreamGetDevice: %s", op, hipGetErrorString(err));
+      return nullptr;
+    }
+    if (stream_dev != dev) {
+      fail(AYK_ERR_ARGUMENT, "%s: the stream belongs to device %d but device %d is current", op, stream_dev, dev);
+      return nullptr;
+    }
   }
   void* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
   if (ptr) return ptr;
@@ -275,7 +296,7 @@ void* static_scratch(const char* op) {
 
 extern "C" {
 
-int ayk_abi_version(void) { return 12; }
+int ayk_abi_version(void) { return 13; }
 
 int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 
@@ -430,7 +451,7 @@ int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache,
                                   max_blocks, layout, dtype, kv_dtype, scale, partition_size, max_partitions,
                                   work_items, n_work_items, staged, nullptr, 0, nullptr, flags, stream);
   }
-  unsigned char* base = static_cast<unsigned char*>(static_scratch(op));
+  unsigned char* base = static_cast<unsigned char*>(static_scratch(op, stream));
   if (!base) return AYK_ERR_LAUNCH;
   // counters for the single launch only when every (row, head) has one
   uint32_t* counters = (int64_t)n_rows * num_heads <= (int64_t)kStaticCounterWords
@@ -440,6 +461,16 @@ int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache,
                                 positions, n_rows, num_heads, num_kv_heads, head_dim, num_blocks, block_size,
                                 max_blocks, layout, dtype, kv_dtype, scale, partition_size, max_partitions, work_items,
                                 n_work_items, staged, base, kStaticPartialBytes, counters, flags, stream);
+}
+
+int ayk_paged_attention_v2_static_counters(void** counters, int64_t* words) {
+  const char* op = "ayk_paged_attention_v2_static_counters";
+  if (!counters || !words) return fail(AYK_ERR_ARGUMENT, "%s: a required pointer is null", op);
+  unsigned char* base = static_cast<unsigned char*>(static_scratch(op, nullptr));
+  if (!base) return AYK_ERR_LAUNCH;
+  *counters = base + kStaticPartialBytes;
+  *words = (int64_t)kStaticCounterWords;
+  return ok();
 }
 
 int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,

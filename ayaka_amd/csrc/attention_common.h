@@ -18,8 +18,6 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
-// Block-table entries staged in LDS per segment of a row's context.
-constexpr int kTableCap = 512;
 // Most waves in one workgroup (one per virtual head).
 constexpr int kMaxWaves = kMaxWavesPerGroup;
 

@@ -9,6 +9,8 @@ namespace ayk {
 
 // Most waves (one per virtual head) in one decode workgroup.
 constexpr int kMaxWavesPerGroup = 8;
+// Block-table entries staged in LDS per segment of a row's context.
+constexpr int kTableCap = 512;
 
 // Everything one paged-attention launch reads. Strides are in elements.
 struct AttnParams {

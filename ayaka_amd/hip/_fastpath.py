@@ -3,11 +3,15 @@
 An engine calls ``attend`` and ``store`` once per layer per step with the same tensors every
 time (its per-layer q/out buffers and caches, one step's metadata). The first call of a
 combination checks everything and records the library call it made; later calls with the same
-objects -- found by identity, confirmed by their data pointers and shapes -- replay that call on
-the current stream. The record holds the tensors it points into, so their ids cannot be reused
-while it lives; it lives in the step's plan (a planned step, or a graph bucket's fixed record)
-and goes with it. This cuts the host time of a decode layer's two calls, which bounds small
-eager steps.
+objects replay that call on the current stream. A record is found by the identity of the
+long-lived objects (the KV buffers and the step metadata, which it holds, so their ids cannot be
+reused while it lives) and by the data pointer, shape, strides and dtype of every tensor the call
+reads or writes: everything the first call's checks depended on. It holds no activation tensor,
+so an engine that allocates fresh q/out (or k/v) per layer keeps nothing alive by calling; the
+caching allocator hands such tensors the same addresses from step to step, so those calls still
+hit. The records live in the step's plan (a planned step, or a graph bucket's fixed record) and
+go with it. This cuts the host time of a decode layer's two calls, which bounds small eager
+steps.
 """
 
 from __future__ import annotations
@@ -32,14 +36,13 @@ class Launch:
     """One library call: ``fn(*args, stream)``, kept as a pointer to the same export with no
     declared argument types and the arguments converted once to the declared ones, so that a
     replay skips ctypes' per-argument conversion; ``keep`` are the tensors its pointers come
-    from, ``ptrs`` their data pointers and shapes when it was recorded."""
+    and metadata objects its arguments were checked against."""
 
     op: str
     fn: Any
     args: tuple
     stream_arg: Any  # the stream handle's conversion: ctypes.c_void_p for a library export
     keep: tuple
-    ptrs: tuple
     device: torch.device
     scratch: bool  # it uses the device's shared v2 scratch, ordered across streams
 
@@ -56,11 +59,15 @@ class Recorder:
         self.launch = (op, fn, args, device, scratch)
 
 
-def _signature(tensors: tuple) -> tuple:
+def signature(tensors: tuple) -> tuple:
+    """Where and how each tensor lies: data pointer, shape, strides and dtype."""
     if len(tensors) == 4:  # every call site of the library: unrolled, a few hundred ns cheaper
         a, b, c, d = tensors
-        return (a.data_ptr(), b.data_ptr(), c.data_ptr(), d.data_ptr(), a.shape, b.shape, c.shape, d.shape)
-    return tuple(t.data_ptr() for t in tensors) + tuple(t.shape for t in tensors)
+        return (a.data_ptr(), b.data_ptr(), c.data_ptr(), d.data_ptr(), a.shape, b.shape, c.shape,
+                d.shape, a.stride(), b.stride(), c.stride(), d.stride(), a.dtype, b.dtype, c.dtype,
+                d.dtype)
+    return (tuple(t.data_ptr() for t in tensors) + tuple(t.shape for t in tensors)
+            + tuple(t.stride() for t in tensors) + tuple(t.dtype for t in tensors))
 
 
 def convert(types: list, args: tuple) -> tuple:
@@ -79,15 +86,12 @@ def convert(types: list, args: tuple) -> tuple:
     return tuple(out)
 
 
-def lookup(cache: dict, key: tuple, tensors: tuple) -> Launch | None:
-    """The recorded launch for ``key`` if the tensors still are where it recorded them."""
-    found = cache.get(key)
-    if found is None or found.ptrs != _signature(tensors):
-        return None
-    return found
+def lookup(cache: dict, key: tuple) -> Launch | None:
+    """The recorded launch for ``key`` (the objects' ids plus :func:`signature` of the tensors)."""
+    return cache.get(key)
 
 
-def remember(cache: dict, key: tuple, tensors: tuple, keep: tuple, recorder: Recorder) -> None:
+def remember(cache: dict, key: tuple, keep: tuple, recorder: Recorder) -> None:
     if recorder.launch is None:
         return
     if len(cache) >= MAX_RECORDS:
@@ -99,7 +103,7 @@ def remember(cache: dict, key: tuple, tensors: tuple, keep: tuple, recorder: Rec
         untyped = _lib.lib()[fn.__name__]  # a new function object: fn keeps its declared types
         untyped.restype = fn.restype
         fn, args, stream_arg = untyped, convert(types[:-1], args), ctypes.c_void_p
-    cache[key] = Launch(op, fn, args, stream_arg, keep + tensors, _signature(tensors), device, scratch)
+    cache[key] = Launch(op, fn, args, stream_arg, keep, device, scratch)
 
 
 def run(launch: Launch, stream: int) -> None:

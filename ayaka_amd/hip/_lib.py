@@ -17,7 +17,7 @@ from ayaka_amd.errors import BackendError, CapabilityError
 __all__ = ["ABI_VERSION", "EXPORTS", "LIB_PATH", "check", "lib"]
 
 LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libayaka_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -55,6 +55,7 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
          _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
          _I32, _I32, _P, _I32, _P, _I32, _P],
     ),
+    "ayk_paged_attention_v2_static_counters": (ctypes.c_int, [ctypes.POINTER(_P), ctypes.POINTER(_I64)]),
     "ayk_paged_prefill_tile_pairs": (ctypes.c_int, [_I32]),
     "ayk_paged_prefill": (
         ctypes.c_int,

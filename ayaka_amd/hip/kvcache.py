@@ -56,22 +56,22 @@ def store(k: torch.Tensor, v: torch.Tensor, buffers: KVBuffers, meta: AttentionM
     """Write each row's k and v into its slot (reference ``torch/kvcache.py:65-80``).
 
     As ``attend``: the first call with a combination of k, v, buffers and step metadata is
-    checked in full and recorded in the step's plan; later calls with the same objects replay
-    the library call on the current stream.
+    checked in full and recorded in the step's plan; later calls with the same buffers and
+    metadata, and k and v at the same addresses, shapes, strides and dtype, replay the library
+    call on the current stream.
     """
     cache = getattr(meta.plan, "launches", None)
     if cache is None:
         _store(k, v, buffers, meta, None)
         return
-    key = ("store", id(k), id(v), id(buffers), id(meta))
-    tensors = (k, v, buffers.k, buffers.v)
-    found = _fastpath.lookup(cache, key, tensors)
+    key = ("store", id(buffers), id(meta), _fastpath.signature((k, v, buffers.k, buffers.v)))
+    found = _fastpath.lookup(cache, key)
     if found is not None:
         _fastpath.run(found, _stream(found.device))
         return
     record = _fastpath.Recorder()
     _store(k, v, buffers, meta, record)
-    _fastpath.remember(cache, key, tensors, (buffers, meta), record)
+    _fastpath.remember(cache, key, (buffers, meta), record)
 
 
 def _store(k: torch.Tensor, v: torch.Tensor, buffers: KVBuffers, meta: AttentionMetadata,

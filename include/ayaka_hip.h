@@ -187,14 +187,19 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference:
  * the same arguments, semantics and kernels as ayk_paged_attention_v2 without `workspace`,
  * `workspace_bytes` and `arrivals`. The partials live in a static device array of the
- * library (64 MiB per device, held from the first call on a device until the process
- * ends): AYK_V2_STATIC_SCRATCH_BYTES of partials, then 2^18 arrival counters, zero when the
- * library loads and left at zero by every call. A call whose partials need more (see
+ * library, a code-object global of 64 MiB: it is allocated on each device when the library's
+ * code object loads there (the runtime loads it on a device's first use by this library,
+ * whichever entry point that is), and held until the process ends, whether or not this entry
+ * point is ever called. An engine's memory ledger should count it as memory a library takes
+ * on its own (the reference's `runtime` owner, python/ayaka/memory/budget.py:43-48). It holds
+ * AYK_V2_STATIC_SCRATCH_BYTES of partials, then 2^18 arrival counters, zero when the code
+ * object loads and left at zero by every call. A call whose partials need more (see
  * ayk_paged_attention_v2_workspace_bytes) is refused with AYK_ERR_WORKSPACE; one of more
  * than 2^18 (row, head) pairs merges in the reduce kernel. Nothing is allocated, freed or
- * synchronised. Every call on a device shares that device's array: calls that overlap in
- * time on one device (other streams, other threads) race, and must be serialised by the
- * caller.
+ * synchronised. The array is the current device's: `stream` must belong to the current device
+ * (a stream of another device is refused with AYK_ERR_ARGUMENT). Every call on a device
+ * shares that device's array: calls that overlap in time on one device (other streams, other
+ * threads) race, and must be serialised by the caller.
  */
 #define AYK_V2_STATIC_SCRATCH_BYTES ((size_t)63 << 20)
 int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache, const void* v_cache,
@@ -205,6 +210,14 @@ int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache,
                                   int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
                                   const int32_t* work_items, int32_t n_work_items, const int32_t* staged,
                                   int32_t flags, void* stream);
+
+/*
+ * Diagnostic, no counterpart in the reference: the current device's address of the arrival
+ * counters of ayk_paged_attention_v2_static (`*counters`, uint32 words) and their number
+ * (`*words`), so a test can read them back and check that every call left them at zero.
+ * Looks the array up as the entry point does; launches, allocates and synchronises nothing.
+ */
+int ayk_paged_attention_v2_static_counters(void** counters, int64_t* words);
 
 /*
  * Multi-row paged attention (prefill chunks, verify windows): the rows of each

@@ -6,14 +6,19 @@ The reference runs its tiny models through the engine for this (``tests/e2e/test
 not part of this build, so the test drives the ops contract the way the engine's attention layer
 does (``layers/attention/dense.py:122,124``): per layer, ``kvcache.store`` then
 ``attention.attend``, with one plan per step. A 4-layer attention-only decoder (RMSNorm, q/k/v/o
-projections, residual, tied embedding head) with seeded weights:
+projections, residual, an untied output head, so the next token depends on what attention
+returned rather than echoing the input embedding) with seeded weights:
 
 * prefills its prompts through the multi-row kernel, then decodes greedily, eagerly planned;
 * decodes the same prompts from one decode step captured in a graph on graph metadata, every
   step staged with ``update_graph_metadata`` and replayed under torch's sync debug mode set to
   "error": staging and replay never wait on the device (the token read after it is the step's
   one declared wait, as in the reference's sync-guard test);
-* is checked against the same model in plain torch float32 over contiguous K/V.
+* every replay is bit-identical to the same step run eagerly on the same graph metadata (the
+  same kernels and launch shapes), and within bf16 rounding of the eagerly planned step;
+* is checked against the same model in plain torch float32 over contiguous K/V: every hidden
+  state within bf16 model error while the tokens agree, and a token may differ only where the
+  float32 model's own choice was a near-tie.
 """
 
 from __future__ import annotations
@@ -46,15 +51,17 @@ class Model:
 
         self.embed = w(VOCAB, HIDDEN, scale=1.0)
         s = 1 / math.sqrt(HIDDEN)
+        self.head = w(HIDDEN, VOCAB, scale=s)
         self.layers = [
             dict(wq=w(HIDDEN, HEADS * DIM, scale=s), wk=w(HIDDEN, KV_HEADS * DIM, scale=s),
-                 wv=w(HIDDEN, KV_HEADS * DIM, scale=s), wo=w(HEADS * DIM, HIDDEN, scale=s / 2))
+                 wv=w(HIDDEN, KV_HEADS * DIM, scale=s), wo=w(HEADS * DIM, HIDDEN, scale=s))
             for _ in range(LAYERS)
         ]
 
     def cast(self, dtype: torch.dtype) -> "Model":
         out = Model.__new__(Model)
         out.embed = self.embed.to(dtype)
+        out.head = self.head.to(dtype)
         out.layers = [{k: v.to(dtype) for k, v in layer.items()} for layer in self.layers]
         return out
 
@@ -80,16 +87,21 @@ def forward_hip(model: Model, x: torch.Tensor, caches: list[KVBuffers], meta) ->
 
 
 def logits(model: Model, x: torch.Tensor) -> torch.Tensor:
-    return rms(x).float() @ model.embed.float().T
+    return rms(x).float() @ model.head.float()
 
 
-def reference_generate(model: Model, prompts: list[torch.Tensor], steps: int) -> tuple[list[list[int]], list]:
-    """Greedy decoding in plain torch float32, recomputing every sequence from scratch."""
+def reference_generate(model: Model, prompts: list[torch.Tensor], steps: int, forced: list[list[int]]
+                       ) -> tuple[list[list[int]], list, list]:
+    """Greedy decoding in plain torch float32, recomputing every sequence from scratch.
+
+    The sequence is continued with ``forced`` (the tokens under test) so that every step's hidden
+    state and logits describe the same prefix as the step under test; the returned tokens are the
+    float32 model's own choices at each step."""
     m = model.cast(torch.float32)
-    tokens_out, last_hidden = [], []
-    for prompt in prompts:
+    tokens_out, last_hidden, all_logits = [], [], []
+    for prompt, follow in zip(prompts, forced):
         seq = prompt.tolist()
-        hiddens = []
+        hiddens, chosen, step_logits = [], [], []
         for _ in range(steps + 1):
             x = m.embed[torch.tensor(seq, device=DEV)]
             length = x.shape[0]
@@ -106,10 +118,14 @@ def reference_generate(model: Model, prompts: list[torch.Tensor], steps: int) ->
                 o = (att @ v).transpose(0, 1).reshape(length, HEADS * DIM)
                 x = x + o @ layer["wo"]
             hiddens.append(x[-1])
-            seq.append(int(logits(m, x[-1:]).argmax()))
-        tokens_out.append(seq[len(prompt):])
+            row = logits(m, x[-1:])[0]
+            step_logits.append(row)
+            chosen.append(int(row.argmax()))
+            seq.append(follow[len(chosen) - 1])
+        tokens_out.append(chosen)
         last_hidden.append(hiddens)
-    return tokens_out, last_hidden
+        all_logits.append(step_logits)
+    return tokens_out, last_hidden, all_logits
 
 
 def new_caches(num_blocks: int) -> list[KVBuffers]:
@@ -199,24 +215,38 @@ def test_greedy_decode_eager_and_from_a_captured_graph_agree_with_a_torch_model(
             tokens = logits(model, static_out).argmax(-1)
         finally:
             torch.cuda.set_sync_debug_mode("default")
-        out = static_out.float()
+        replayed = static_out.clone()
+        # the same step eagerly on the same graph metadata (same kernels, same launch shapes);
+        # its KV writes store the same values in the same slots
+        step()
+        assert torch.equal(static_out.view(torch.int16), replayed.view(torch.int16)), \
+            f"step {i}: the replay differs from the same step run eagerly on the graph metadata"
+        out = replayed.float()
         diff = (out[: len(PROMPTS)] - eager_hidden[i]).abs().max().item()
         scale = eager_hidden[i].abs().max().item()
-        assert diff <= 2e-2 * scale, f"step {i}: graph vs eager hidden {diff} (max {scale})"
+        assert diff <= 1e-2 * scale, f"step {i}: graph vs planned eager hidden {diff} (max {scale})"
         graph_tokens.append(tokens[: len(PROMPTS)].tolist())
 
-    ref_tokens, ref_hidden = reference_generate(base, prompts, STEPS)
     eager_by_seq = [[step_tokens[b] for step_tokens in eager_tokens] for b in range(len(PROMPTS))]
     graph_by_seq = [[step_tokens[b] for step_tokens in graph_tokens] for b in range(len(PROMPTS))]
     assert graph_by_seq == eager_by_seq
-    # the bf16 model follows the float32 one until a near-tie flips a token; compare the hidden
-    # states while the tokens agree
+    ref_tokens, ref_hidden, ref_logits = reference_generate(base, prompts, STEPS, eager_by_seq)
+    # Along our own tokens, the float32 model at every step: the hidden states agree within the
+    # bf16 model's error (about 0.6% relative, simulated on the CPU for these weights), and where
+    # the float32 model would choose another token its own top two logits are a near-tie (the
+    # bf16 model's logits are within about 0.03 of the float32 ones; logits here are ~N(0, 1)).
+    agreed = 0
     for b in range(len(PROMPTS)):
-        agree = 0
-        while agree < STEPS + 1 and eager_by_seq[b][agree] == ref_tokens[b][agree]:
-            agree += 1
-        assert agree >= 1, f"sequence {b}: the prefill token differs from the float32 model's"
-        for i in range(min(agree, STEPS)):
-            ours, ref = eager_hidden[i][b], ref_hidden[b][i + 1]
-            rel = ((ours - ref).norm() / ref.norm()).item()
-            assert rel < 3e-2, f"sequence {b} step {i}: relative error {rel} against float32"
+        for i in range(STEPS + 1):
+            if i >= 1:
+                ours, ref = eager_hidden[i - 1][b], ref_hidden[b][i]
+                rel = ((ours - ref).norm() / ref.norm()).item()
+                assert rel < 1.5e-2, f"sequence {b} step {i}: relative error {rel} against float32"
+            if eager_by_seq[b][i] == ref_tokens[b][i]:
+                agreed += 1
+                continue
+            row = ref_logits[b][i]
+            margin = (row.max() - row[eager_by_seq[b][i]]).item()
+            assert margin < 0.1, (f"sequence {b} step {i}: token {eager_by_seq[b][i]} where the float32 model "
+                                  f"chooses {ref_tokens[b][i]} by a margin of {margin}")
+    assert agreed >= (STEPS + 1) * len(PROMPTS) * 3 // 4, f"only {agreed} tokens agree with float32"

@@ -385,32 +385,51 @@ def test_hip_backend_is_unavailable_without_a_device(monkeypatch: pytest.MonkeyP
 
 
 def test_recorded_launches_replay_only_for_the_same_storage() -> None:
-    # the repeated-call record: found by identity, confirmed by data pointers and shapes, and
-    # dropped when a tensor's storage or shape changed
+    # the repeated-call record: keyed by the long-lived objects' ids and by every tensor's data
+    # pointer, shape, strides and dtype; it holds no activation tensor
+    import gc
+    import weakref
+
     from ayaka_amd.hip import _fastpath
 
     calls = []
     cache: dict = {}
+    owner = object()  # stands in for the buffers and metadata a record keeps
     q, out = torch.zeros(4, 8), torch.zeros(4, 8)
-    key = ("attend", id(q), id(out))
-    assert _fastpath.lookup(cache, key, (q, out)) is None
+
+    def key_of(*tensors):
+        return ("attend", id(owner), _fastpath.signature(tensors))
+
+    assert _fastpath.lookup(cache, key_of(q, out)) is None
     record = _fastpath.Recorder()
     record("op", lambda *args: calls.append(args) or 0, (1, 2), torch.device("cpu"), False)
-    _fastpath.remember(cache, key, (q, out), (), record)
-    found = _fastpath.lookup(cache, key, (q, out))
-    assert found is not None and found.keep[-2:] == (q, out)
+    _fastpath.remember(cache, key_of(q, out), (owner,), record)
+    found = _fastpath.lookup(cache, key_of(q, out))
+    assert found is not None and found.keep == (owner,)
     _fastpath.run(found, 7)
     assert calls == [(1, 2, 7)]
-    q.set_(torch.zeros(4, 8).untyped_storage())  # new storage behind the same object
-    assert _fastpath.lookup(cache, key, (q, out)) is None
-    out.resize_(2, 8)  # a new shape
-    _fastpath.remember(cache, key, (q, torch.zeros(1)), (), record)
-    assert _fastpath.lookup(cache, key, (q, out)) is None
+    # the record does not keep q or out alive
+    dead = weakref.ref(q)
+    del q, found
+    gc.collect()
+    assert dead() is None
+    q = torch.zeros(4, 8)
+    # new storage, a new shape, new strides or a new dtype behind the same object miss
+    base = key_of(q, out)
+    _fastpath.remember(cache, base, (owner,), record)
+    q.set_(torch.zeros(4, 8).untyped_storage())
+    assert _fastpath.lookup(cache, key_of(q, out)) is None
+    same = torch.zeros(8, 4)
+    _fastpath.remember(cache, key_of(same, out), (owner,), record)
+    assert _fastpath.lookup(cache, key_of(same.t(), out)) is None  # same address, other strides
+    assert _fastpath.lookup(cache, key_of(same.view(torch.int32), out)) is None
+    assert _fastpath.lookup(cache, key_of(same.view(32), out)) is None
+    assert _fastpath.lookup(cache, key_of(same, out)) is not None
     # an empty recorder (a call that launched nothing) records nothing; the cache is bounded
-    _fastpath.remember(cache, ("none",), (q,), (), _fastpath.Recorder())
+    _fastpath.remember(cache, ("none",), (), _fastpath.Recorder())
     assert ("none",) not in cache
     for i in range(_fastpath.MAX_RECORDS + 1):
-        _fastpath.remember(cache, ("k", i), (q,), (), record)
+        _fastpath.remember(cache, ("k", i), (), record)
     assert len(cache) <= _fastpath.MAX_RECORDS
 
 

@@ -216,6 +216,30 @@ def test_torch_decode_restatement_matches_the_brute_force(heads: int, kv_heads: 
     assert not got[1].any()
 
 
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+def test_attention_of_requests_matches_attention(layout: str) -> None:
+    # the shared-gather form used for full-size prefill chunks: the same outputs as attention()
+    # (itself pinned by the brute force) on mixed steps with padding requests, rows ending
+    # inside blocks, passes of rows that split a request, and NaN in every unused slot
+    steps = [(5, 23), (1, 0), (9, 9), (3, 40), (1, 1), (2, 0), (17, 64)]
+    for heads, kv_heads in ((8, 2), (6, 1), (4, 4)):
+        s = build_scenario(steps, heads=heads, kv_heads=kv_heads, head_dim=16, block_size=8, layout=layout,
+                           mode="mixed", seed=13)
+        expected = s.expected(np.float64)
+        for rows_per_pass in (1, 4, 64):
+            got = paged.attention_of_requests(s.q, s.k, s.v, s.table, np.asarray(s.lengths), scale=s.scale,
+                                              request_of_row=s.plan["request_of_row"],
+                                              positions=s.plan["positions"], layout=layout,
+                                              rows_per_pass=rows_per_pass)
+            assert np.isfinite(got).all()
+            np.testing.assert_allclose(got, expected, rtol=0, atol=1e-12)
+    tiny = build_scenario([(4, 4), (2, 0), (3, 11)], heads=4, kv_heads=2, head_dim=8, mode="mixed", seed=11)
+    got = paged.attention_of_requests(tiny.q, tiny.k, tiny.v, tiny.table, np.asarray(tiny.lengths),
+                                      scale=tiny.scale, request_of_row=tiny.plan["request_of_row"],
+                                      positions=tiny.plan["positions"])
+    np.testing.assert_allclose(got, brute_force(tiny), rtol=0, atol=1e-12)
+
+
 def test_attention_matches_torch_sdpa() -> None:
     steps = [(1, 70), (1, 17), (3, 40), (1, 1)]
     s = build_scenario(steps, heads=12, kv_heads=4, head_dim=64, block_size=16, seed=5)

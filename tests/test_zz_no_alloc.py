@@ -44,6 +44,19 @@ def _call(lib, static: bool, out, s, tensors, size: int, parts: int, work, n_wor
                                       stream)
 
 
+def _static_counters(lib) -> torch.Tensor:
+    """The static array's arrival counters on this device, viewed in place as int32."""
+    ptr, words = ctypes.c_void_p(), ctypes.c_int64()
+    assert lib.ayk_paged_attention_v2_static_counters(ctypes.byref(ptr), ctypes.byref(words)) == 0
+    assert ptr.value and words.value == 1 << 18
+
+    class _View:
+        __cuda_array_interface__ = {"shape": (words.value,), "typestr": "<i4", "data": (ptr.value, False),
+                                    "version": 3, "strides": None}
+
+    return torch.as_tensor(_View(), device=DEV)
+
+
 def _scenario(steps, heads: int, seed: int):
     s = build_scenario(steps, heads=heads, kv_heads=2, head_dim=128, block_size=16, mode="decode", seed=seed)
     table = torch.from_numpy(s.table.astype(np.int32)).to(DEV)
@@ -81,6 +94,35 @@ def test_static_scratch_matches_the_workspace_entry_point(flags: int, heads: int
         rep = parity_report(got, expected, "bf16")
         assert rep["max_abs_excess"] <= 2e-3 and rep["rel_l2"] <= 1e-3, rep
         assert int(arrivals.abs().sum()) == 0
+        assert int(torch.count_nonzero(_static_counters(lib))) == 0
+
+
+def test_static_counters_stay_zero_when_a_larger_call_follows() -> None:
+    # the in-kernel merge counts finished partitions in the static array's counters; a call over
+    # more (row, head) pairs than the one before it reads counters the earlier call never
+    # touched, so each call must leave every counter at zero, read back from the array itself
+    lib = _lib.lib()
+    counters = _static_counters(lib)
+    assert int(torch.count_nonzero(counters)) == 0
+    for steps, size, seed in (([(1, 300), (1, 40)], 64, 85),
+                              ([(1, 900), (1, 1), (1, 0), (1, 700), (1, 350)] * 3, 128, 86)):
+        s, tensors = _scenario(steps, 8, seed)
+        print(f"static v2 counters: rows {len(s.lengths)} size {size}", flush=True)
+        parts = -(-tensors[3].shape[1] * s.block_size // size)
+        items = torch.from_numpy(hip_attention.work_list(s.lengths, size)).to(DEV)
+        nbytes = lib.ayk_paged_attention_v2_workspace_bytes(len(s.lengths), 8, 128, parts)
+        scratch = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+        arrivals = torch.zeros(len(s.lengths) * 8, dtype=torch.int32, device=DEV)
+        outs = []
+        for static in (True, False):
+            out = torch.full_like(tensors[0], float("nan"))
+            rc = _call(lib, static, out, s, tensors, size, parts, items.data_ptr(), items.numel() // 2, None, 16,
+                       scratch, arrivals)
+            assert rc == 0, lib.ayk_last_error()
+            torch.cuda.synchronize()
+            outs.append(out)
+        assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+        assert int(torch.count_nonzero(counters)) == 0
 
 
 def test_static_scratch_follows_a_staged_split() -> None:
