@@ -29,9 +29,10 @@ captured launch covers the bucket's capacity and the kernels read the step's spl
 
 from __future__ import annotations
 
+import ctypes
 import functools
-
 import heapq
+import math
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -281,16 +282,16 @@ def work_list(row_lengths: "tuple[int, ...] | list[int] | np.ndarray", partition
     partition), plus partition 0 of each row without context, last (it writes the row's zeros).
 
     Every full partition comes before any partial one, so the last workgroups to
-    start are the short ones and consecutive workgroups land on different XCDs.
+    start are the short ones and consecutive workgroups land on different XCDs. Built by the
+    library's host code (``ayk_work_list``).
     """
-    lengths = np.asarray(row_lengths, dtype=np.int64).reshape(-1)
-    counts = np.maximum(1, -(-lengths // partition_size))
-    rows = np.repeat(np.arange(lengths.size, dtype=np.int64), counts)
-    starts = np.cumsum(counts) - counts
-    parts = np.arange(rows.size, dtype=np.int64) - np.repeat(starts, counts)
-    sizes = np.minimum(partition_size, lengths[rows] - parts * partition_size)
-    order = np.lexsort((parts, rows, -sizes))
-    return np.stack((rows[order], parts[order]), axis=1).reshape(-1).astype(np.int32)
+    lengths = np.ascontiguousarray(row_lengths, dtype=np.int64).reshape(-1)
+    count = int(np.maximum(1, -(-lengths // max(partition_size, 1))).sum())
+    out = np.empty(2 * count, dtype=np.int32)
+    if _lib.lib().ayk_work_list(lengths.ctypes.data, lengths.size, partition_size, out.ctypes.data) != count:
+        raise BackendError(f"attention.work_list: bad lengths or partition size {partition_size}",
+                           context={"op": "attention.work_list"})
+    return out
 
 
 @dataclass(frozen=True, slots=True, eq=False)
@@ -320,6 +321,9 @@ class HipGraphPlan:
     min_size: int
     partitions: int
     capacity: int
+    host_all: torch.Tensor  # the pinned buffer every host record above is a view of
+    device_all: torch.Tensor  # its device twin, holding the fixed records and `staged`
+    staged_offset: int  # where `staged` starts in both, in bytes (it comes last)
     head_shape: list = field(default_factory=list)
     staged_shape: list = field(default_factory=list)
     launches: dict = field(default_factory=dict)
@@ -487,30 +491,34 @@ class Split:
     waves: int = 0
 
 
-def schedule_makespan(row_lengths: list[int], size: int, groups: int = 1, cost: int | None = None) -> int:
-    """Modelled finish time, in positions, of v2 over partitions of ``size``.
+def schedule_makespans(row_lengths: "list[int] | np.ndarray", sizes: "list[int] | tuple[int, ...]",
+                       groups: int = 1, cost: int | None = None) -> tuple[np.ndarray, np.ndarray]:
+    """Modelled finish times, in positions, of v2 over partitions of each of ``sizes``, and
+    the work items per key/value head group at each size.
 
     Workgroups start in work-list order (longest partition first); the GPU hands
     workgroup i to XCD i mod 8 and each XCD to whichever of its 32 CUs frees up
     first, one 8-wave workgroup per CU at a time. A workgroup costs its
     positions plus ``cost`` (default :data:`WORKGROUP_COST`: start-up, the final
-    merge, writing the partial).
+    merge, writing the partial). Computed by the library's host code
+    (``ayk_split_model``), one call for every size.
     """
     cost = WORKGROUP_COST if cost is None else cost
-    items: list[int] = []
-    for length in row_lengths:
-        full, rest = divmod(length, size)
-        items.extend([size] * full)
-        if rest:
-            items.append(rest)
-    items.sort(reverse=True)
-    items = [item for item in items for _ in range(groups)]
-    per_xcd = COMPUTE_UNITS // XCDS
-    loads = [[0] * per_xcd for _ in range(XCDS)]
-    for index, item in enumerate(items):
-        heap = loads[index % XCDS]
-        heapq.heapreplace(heap, heap[0] + item + cost)
-    return max(max(heap) for heap in loads)
+    lengths = np.ascontiguousarray(row_lengths, dtype=np.int64).reshape(-1)
+    sizes = np.ascontiguousarray(sizes, dtype=np.int32).reshape(-1)
+    makespans = np.empty(sizes.size, dtype=np.int64)
+    items = np.empty(sizes.size, dtype=np.int64)
+    rc = _lib.lib().ayk_split_model(lengths.ctypes.data, lengths.size, sizes.ctypes.data, sizes.size, groups, cost,
+                                    COMPUTE_UNITS, XCDS, makespans.ctypes.data, items.ctypes.data)
+    if rc != 0:
+        raise BackendError(f"attention.schedule_makespans: bad sizes {sizes.tolist()}, groups {groups} or cost {cost}",
+                           context={"op": "attention.schedule_makespans"})
+    return makespans, items
+
+
+def schedule_makespan(row_lengths: list[int], size: int, groups: int = 1, cost: int | None = None) -> int:
+    """:func:`schedule_makespans` at one partition size."""
+    return int(schedule_makespans(row_lengths, (size,), groups, cost)[0][0])
 
 
 _split_cache: dict[tuple, int] = {}
@@ -523,9 +531,9 @@ def v1_makespan(row_lengths: list[int], waves: int, virtual_heads: int, cost: in
     a workgroup per row and ``8 / waves`` virtual heads, each wave streaming a ``1 / waves``
     share of its row in 16-position chunks, scheduled as :func:`schedule_makespan` schedules
     v2's workgroups."""
-    shares = [-(-n // (16 * waves)) * 16 for n in row_lengths]
+    shares = -(-np.asarray(row_lengths, dtype=np.int64) // (16 * waves)) * 16
     groups = -(-virtual_heads * waves // 8)
-    return schedule_makespan(shares, max(shares, default=1) + 1, groups, cost)
+    return schedule_makespan(shares, int(shares.max(initial=0)) + 1, groups, cost)
 
 
 def window_waves(n_items: int, num_kv_heads: int) -> int:
@@ -569,22 +577,26 @@ def fits_schedule(lengths: list[int], size: int, groups: int = 1) -> bool:
 def _best_size(lengths: list[int], max_length: int, groups: int, kv_bytes: int = 2, min_size: int = 0,
                max_items: int = 0) -> int:
     """The candidate partition size (of ``min_size`` or more, and with ``max_items`` work
-    items at most when that is positive) with the smallest :func:`schedule_makespan`."""
+    items at most when that is positive) with the smallest :func:`schedule_makespan`; sizes
+    whose work list exceeds :data:`MAX_ROUNDS` rounds are left out unless none is left, and
+    no size past the first that covers ``max_length`` is scored."""
     candidates = [size for size in PARTITION_CANDIDATES if size >= min_size] or [min_size]
-    if max_items:
-        candidates = [size for size in candidates if sum(-(-n // size) for n in lengths) <= max_items] \
-            or [-(-max_length // 64) * 64]
-    best: tuple[int, int] | None = None
-    for size in candidates:
-        if not fits_schedule(lengths, size, groups) and size != candidates[-1]:
-            continue
-        cost = schedule_makespan(lengths, size, groups, WORKGROUP_COSTS[kv_bytes])
-        if best is None or cost < best[0]:
-            best = (cost, size)
+    for i, size in enumerate(candidates):
         if size >= max_length:
+            candidates = candidates[:i + 1]
             break
-    assert best is not None
-    return best[1]
+    lengths = np.ascontiguousarray(lengths, dtype=np.int64)
+    sizes = np.ascontiguousarray(candidates, dtype=np.int32)
+    best = ctypes.c_int32(-1)
+    rc = _lib.lib().ayk_best_split(lengths.ctypes.data, lengths.size, sizes.ctypes.data, sizes.size, groups,
+                                   WORKGROUP_COSTS[kv_bytes], COMPUTE_UNITS, XCDS, max_items,
+                                   MAX_ROUNDS * COMPUTE_UNITS, ctypes.byref(best))
+    if rc != 0:
+        raise BackendError(f"attention.choose_split: bad sizes {candidates} or groups {groups}",
+                           context={"op": "attention.choose_split"})
+    if best.value < 0:  # no size keeps the work list within max_items: one partition per row
+        return -(-max_length // 64) * 64
+    return candidates[best.value]
 
 
 def choose_split(
@@ -593,7 +605,7 @@ def choose_split(
     group: int,
     max_length: int,
     total_length: int | None = None,
-    row_lengths: tuple[int, ...] | None = None,
+    row_lengths: "tuple[int, ...] | np.ndarray | None" = None,
     kv_bytes: int = 2,
     min_size: int = 0,
     max_items: int = 0,
@@ -620,11 +632,15 @@ def choose_split(
         return Split(0, 0)
     virtual_heads = num_kv_heads * head_chunks(group)
     groups = -(-virtual_heads // 8)
-    lengths = [n for n in row_lengths if n > 0] if row_lengths is not None else [max_length] * n_rows
-    total = sum(lengths)
+    if row_lengths is not None:
+        lengths = np.asarray(row_lengths, dtype=np.int64)
+        lengths = lengths[lengths > 0]
+    else:
+        lengths = np.full(n_rows, max_length, dtype=np.int64)
+    total = int(lengths.sum())
     # The total to 4 significant bits, the longest row to a power of two, the row count.
     top = max(total.bit_length() - 4, 0)
-    key = (virtual_heads, kv_bytes, min_size, max_items, v1, len(lengths), max_length.bit_length(), total >> top,
+    key = (virtual_heads, kv_bytes, min_size, max_items, v1, lengths.size, max_length.bit_length(), total >> top,
            top)
     found = _split_cache.get(key)
     if found is None:
@@ -634,7 +650,7 @@ def choose_split(
         waves = 0
         # v1 with a wave split, scored by the same schedule: eager plans only (a graph replay's
         # launch is the staged v2 split, sized by min_size and max_items)
-        if v1 and not min_size and not max_items and lengths:
+        if v1 and not min_size and not max_items and lengths.size:
             v2 = schedule_makespan(lengths, size, groups, WORKGROUP_COSTS[kv_bytes]) if size < max_length else None
             best = None
             for ws in V1_WAVE_SPLITS:
@@ -1127,37 +1143,56 @@ def graph_metadata(
             context={"op": "attention.graph_metadata"},
         )
     target = torch.device(device)
-    # The records a replay reads at fixed addresses, each with a pinned host twin that
-    # update_graph_metadata fills (a decode step: one row per request, row n is request n).
-    records = {
-        "positions": ((num_requests,), torch.int32),
-        "slot_mapping": ((num_requests,), torch.int64),
-        "kv_lengths": ((num_requests,), torch.int32),
-        "block_table": ((num_requests, max_blocks), torch.int32),
-    }
-    fixed = {name: torch.zeros(shape, dtype=dtype, device=target) for name, (shape, dtype) in records.items()}
-    twins = {name: torch.zeros(shape, dtype=dtype, pin_memory=target.type == "cuda")
-             for name, (shape, dtype) in records.items()}
-
     # Replays run v2 over partitions of at least min_size (64 positions, or the share of the
     # table width that keeps a row within GRAPH_MAX_PARTITIONS of them) and a grid of
-    # `capacity` work items: GRAPH_MAX_ITEMS, or one per row for a larger bucket. Until the
-    # first update every row is one item.
+    # `capacity` work items: GRAPH_MAX_ITEMS, or one per row for a larger bucket.
     max_length = max_blocks * block_size
     min_size = max(GRAPH_MIN_PARTITION, -(-max_length // (64 * GRAPH_MAX_PARTITIONS)) * 64)
     capacity = max(num_requests, GRAPH_MAX_ITEMS)
     work = 2 + num_requests
-    staged_host = torch.zeros(work + 2 * capacity, dtype=torch.int32, pin_memory=target.type == "cuda")
+    # The records a replay reads at fixed addresses (a decode step: one row per request, row n
+    # is request n), then the staged split, laid out in one device buffer with a pinned host
+    # twin that update_graph_metadata fills, so each update is one asynchronous copy (of
+    # everything up to the end of the step's work list).
+    records = {
+        "block_table": ((num_requests, max_blocks), torch.int32),
+        "positions": ((num_requests,), torch.int32),
+        "slot_mapping": ((num_requests,), torch.int64),
+        "kv_lengths": ((num_requests,), torch.int32),
+        "staged": ((work + 2 * capacity,), torch.int32),
+    }
+    offsets, total = {}, 0
+    for name, (shape, dtype) in records.items():
+        offsets[name] = total
+        nbytes = math.prod(shape) * torch.tensor([], dtype=dtype).element_size()
+        total += -(-nbytes // 256) * 256
+    host_all = torch.zeros(total, dtype=torch.uint8, pin_memory=target.type == "cuda")
+    device_all = torch.zeros(total, dtype=torch.uint8, device=target)
+
+    def view(buffer: torch.Tensor, name: str) -> torch.Tensor:
+        shape, dtype = records[name]
+        nbytes = math.prod(shape) * torch.tensor([], dtype=dtype).element_size()
+        return buffer[offsets[name]:offsets[name] + nbytes].view(dtype).view(shape)
+
+    fixed = {name: view(device_all, name) for name in records if name != "staged"}
+    twins = {name: view(host_all, name) for name in records if name != "staged"}
+    # Until the first update every row is one item.
+    staged_host = view(host_all, "staged")
     staged_host[0], staged_host[1] = min_size, num_requests
     staged_host[work:work + 2 * num_requests:2] = torch.arange(num_requests, dtype=torch.int32)
+    staged = view(device_all, "staged")
+    staged.copy_(staged_host)
     staging = HipGraphPlan(
         **twins,
         max_blocks=max_blocks,
         staged_host=staged_host,
-        staged=staged_host.to(target),
+        staged=staged,
         min_size=min_size,
         partitions=-(-max_length // min_size),
         capacity=capacity,
+        host_all=host_all,
+        device_all=device_all,
+        staged_offset=offsets["staged"],
     )
     return AttentionMetadata(
         mode=ForwardMode.DECODE,
@@ -1218,9 +1253,8 @@ def update_graph_metadata(
     staging.kv_lengths.numpy()[:] = lens
     staging.block_table.numpy()[:] = rows
     used = _stage_split(staging, lens, block_size)
-    for name in ("positions", "slot_mapping", "kv_lengths", "block_table"):
-        getattr(meta, name).copy_(getattr(staging, name), non_blocking=True)
-    staging.staged[:used].copy_(staging.staged_host[:used], non_blocking=True)
+    end = staging.staged_offset + 4 * used
+    staging.device_all[:end].copy_(staging.host_all[:end], non_blocking=True)
 
 
 def _stage_split(staging: HipGraphPlan, lengths: np.ndarray, block_size: int) -> int:
@@ -1232,7 +1266,7 @@ def _stage_split(staging: HipGraphPlan, lengths: np.ndarray, block_size: int) ->
     lengths = lengths.astype(np.int64)
     longest = int(lengths.max()) if lengths.size else 0
     empty = int((lengths == 0).sum())
-    split = choose_split(lengths.size, kv_heads, group, max(longest, 1), row_lengths=tuple(lengths.tolist()),
+    split = choose_split(lengths.size, kv_heads, group, max(longest, 1), row_lengths=lengths,
                          kv_bytes=kv_bytes, min_size=staging.min_size, max_items=staging.capacity - empty)
     # one partition per row when the model prefers v1
     size = split.partition_size or max(staging.min_size, -(-longest // 64) * 64)

@@ -78,6 +78,9 @@ def parse() -> argparse.Namespace:
                     help="only time the multi-row (prefill / verify) kernel on its workloads, one JSON line each")
     ap.add_argument("--block-ops", action="store_true",
                     help="only time the block ops (gather / copy_blocks / zero_blocks) at the C3 pool shape")
+    ap.add_argument("--host-trace", action="store_true",
+                    help="only time the host side of decode steps (update_graph_metadata, and plan plus the "
+                         "split choice of an eager step) over a continuous-batching trace at the C5 shape")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 5 plain device copies of MIB MiB (scales profiler byte counters)")
     return ap.parse_args()
@@ -381,6 +384,95 @@ def block_ops(args) -> int:
     return 0
 
 
+HOST_TRACE_STEPS = 3000
+
+
+def continuous_batching_trace(steps: int, bucket: int, capacity: int, seed: int = 5) -> list:
+    """Per-step int32 lengths of a decode bucket under continuous batching, C5-like: prompts
+    log-uniform in [16, 16384]; every step each running request grows by one; every 4 steps
+    0-3 requests finish (their rows go vacant, length 0) and 0-3 new ones take vacant rows,
+    keeping 200-256 running. The row count of running requests changes at most steps, which
+    is what defeats a choice cached under the step's shape."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+
+    def draw(n: int):
+        return np.minimum(np.exp(rng.uniform(np.log(16), np.log(16384), n)).astype(np.int64), capacity - steps - 1)
+
+    lengths, out = draw(bucket), []
+    for step in range(steps):
+        lengths = np.where(lengths > 0, lengths + 1, 0)
+        if step % 4 == 0:
+            busy, free = np.flatnonzero(lengths > 0), np.flatnonzero(lengths == 0)
+            k = int(rng.integers(0, 4))
+            if k and busy.size > 200:
+                lengths[rng.choice(busy, k, replace=False)] = 0
+            k = min(int(rng.integers(0, 4)), free.size)
+            if k:
+                lengths[rng.choice(free, k, replace=False)] = draw(k)
+        out.append(lengths.astype(np.int32))
+    return out
+
+
+def host_trace(args) -> int:
+    """Host time per decode step over :func:`continuous_batching_trace` (C5 head shape: 64
+    query heads over 8 key/value heads, block 32, a bucket of 256 rows by 512 blocks): the
+    graph path's ``update_graph_metadata`` (positions, slots, table and the staged v2 split,
+    one asynchronous copy), and the eager path's ``plan`` plus the split choice its first
+    ``attend`` makes. Percentiles in µs over the trace; the split model's cache misses are
+    counted."""
+    import numpy as np
+    import torch
+
+    from ayaka_amd.enums import ForwardMode
+    from ayaka_amd.hip import _lib
+    from ayaka_amd.hip import attention as hip_attention
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    bucket, width, bs = 256, 512, 32
+    trace = continuous_batching_trace(HOST_TRACE_STEPS, bucket, width * bs)
+    rng = np.random.default_rng(6)
+    table = torch.from_numpy(rng.integers(1, 100_000, (bucket, width)).astype(np.int32))
+    meta = hip_attention.graph_metadata(bucket, width, bs, dev)
+    meta.plan.head_shape.extend((8, 8, 2))
+    hip_attention._split_cache.clear()
+    misses, graph_us = 0, []
+    for lengths in trace:
+        host = torch.from_numpy(lengths)
+        before = len(hip_attention._split_cache)
+        t0 = time.perf_counter()
+        hip_attention.update_graph_metadata(meta, host, table)
+        graph_us.append((time.perf_counter() - t0) * 1e6)
+        misses += len(hip_attention._split_cache) != before
+    torch.cuda.synchronize()
+    device_table = table.to(dev)
+    ones = torch.ones(bucket, dtype=torch.int32, device=dev)
+    eager_us = []
+    hip_attention._split_cache.clear()
+    for lengths in trace[:1000]:
+        device_lengths = torch.from_numpy(lengths).to(dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step = hip_attention.plan(ForwardMode.DECODE, ones, device_lengths, device_table, bs)
+        step.plan.split_for(8, 8, 2)
+        eager_us.append((time.perf_counter() - t0) * 1e6)
+
+    def pct(values: list) -> dict:
+        return {f"p{q}": round(float(np.percentile(values, q)), 1) for q in (50, 90, 99)} | \
+               {"max": round(max(values), 1)}
+
+    print(json.dumps({"workload": "continuous-batching decode trace: 256-row bucket x 512 blocks of 32, "
+                                  "64/8 heads, lengths log-uniform in [16, 16384], requests joining and "
+                                  "leaving every 4 steps",
+                      "steps": len(trace), "split_model_misses": misses,
+                      "update_graph_metadata_us": pct(graph_us),
+                      "eager_plan_and_split_us": pct(eager_us),
+                      "host_cpus": os.cpu_count()}), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse()
     if args.gpus != 1:
@@ -396,6 +488,8 @@ def main() -> int:
         return graph_step(args)
     if args.block_ops:
         return block_ops(args)
+    if args.host_trace:
+        return host_trace(args)
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)

@@ -306,6 +306,40 @@ int ayk_copy_blocks(void* k_cache, void* v_cache, const void* src, const void* d
 int ayk_zero_blocks(void* k_cache, void* v_cache, const void* block_ids, int32_t ids_are_64bit,
                     int64_t n, int32_t num_blocks, int64_t block_bytes, void* stream);
 
+/*
+ * Host-side launch model (no device work; callable without a GPU). No counterpart in the
+ * reference, whose split-KV scheduling happens inside flashinfer's plan
+ * (python/ayaka/ops/backends/flashinfer/attention.py:221-251).
+ *
+ * ayk_split_model: for each of `n_sizes` partition sizes, the modelled finish time (in
+ * positions) of a v2 launch over the rows' `lengths` (rows of length <= 0 hold no work): each
+ * row split into partitions of the size, the work items ordered longest first, each repeated
+ * `groups` times (workgroups per item), dealt to XCD i mod `xcds`, each XCD handing its next
+ * item to whichever of its `compute_units / xcds` units frees first, an item costing its
+ * positions plus `cost`. Writes `makespans[c]` and, if `item_counts` is not null, the work
+ * items per group at each size. Returns AYK_OK, or AYK_ERR_ARGUMENT for bad sizes or pointers.
+ *
+ * ayk_work_list: the v2 work list of rows of `lengths` at `partition_size`, as int32
+ * (row, partition) pairs into `out` (2 words per item): full partitions by row then partition,
+ * then each row's partial last partition, longest first (ties by row), then partition 0 of
+ * every row without context. Returns the item count (with `out` null: the count only), or -1
+ * for bad arguments.
+ */
+int ayk_split_model(const int64_t* lengths, int32_t n_lengths, const int32_t* sizes, int32_t n_sizes,
+                    int32_t groups, int32_t cost, int32_t compute_units, int32_t xcds, int64_t* makespans,
+                    int64_t* item_counts);
+int64_t ayk_work_list(const int64_t* lengths, int32_t n_lengths, int32_t partition_size, int32_t* out);
+/*
+ * ayk_best_split: the index (`*best`) of the candidate size with the smallest
+ * ayk_split_model finish time (the first of equal ones), among those with at most `max_items`
+ * work items when `max_items` > 0 (-1 if none has), leaving out those whose items x `groups`
+ * exceed `round_items` unless it is the last such candidate. Only candidates whose lower bound
+ * can still beat the best found are scheduled in full.
+ */
+int ayk_best_split(const int64_t* lengths, int32_t n_lengths, const int32_t* sizes, int32_t n_sizes, int32_t groups,
+                   int32_t cost, int32_t compute_units, int32_t xcds, int64_t max_items, int64_t round_items,
+                   int32_t* best);
+
 #ifdef __cplusplus
 }
 #endif

@@ -181,3 +181,47 @@ def oracle_rows(step, rows: list[int], precision: type = np.float64, chunk: int 
                                     sample["lengths"][pick], scale=step.config.scale, precision=precision,
                                     chunk=chunk)
     return out
+
+
+# --- the host launch model, stated in plain Python -------------------------------------------
+# The library computes these in C++ (ayk_split_model, ayk_work_list); the tests check that its
+# answers are these, on random and edge-case inputs.
+
+
+def python_schedule_makespan(row_lengths, size: int, groups: int = 1, cost: int = 320,
+                             compute_units: int = 256, xcds: int = 8) -> int:
+    """Finish time of v2 over partitions of ``size``: work items longest first, each repeated
+    ``groups`` times, dealt to XCD i mod ``xcds``; each XCD hands its next item to whichever
+    of its units frees first; an item costs its positions plus ``cost``."""
+    import heapq
+
+    items: list[int] = []
+    for length in row_lengths:
+        if length <= 0:
+            continue
+        full, rest = divmod(int(length), size)
+        items.extend([size] * full)
+        if rest:
+            items.append(rest)
+    items.sort(reverse=True)
+    items = [item for item in items for _ in range(groups)]
+    loads = [[0] * (compute_units // xcds) for _ in range(xcds)]
+    for index, item in enumerate(items):
+        heap = loads[index % xcds]
+        heapq.heapreplace(heap, heap[0] + item + cost)
+    return max(max(heap) for heap in loads)
+
+
+def python_work_list(row_lengths, partition_size: int) -> np.ndarray:
+    """(row, partition) pairs holding tokens, longest partition first (ties by row, then
+    partition), then partition 0 of each row without context; flattened int32."""
+    entries = []
+    for row, length in enumerate(row_lengths):
+        length = int(length)
+        if length <= 0:
+            entries.append((0, row, 0))
+            continue
+        for part in range(-(-length // partition_size)):
+            entries.append((-min(partition_size, length - part * partition_size), row, part))
+    entries.sort()
+    return np.array([x for _, row, part in entries for x in (row, part)], dtype=np.int32)

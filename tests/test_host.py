@@ -225,6 +225,43 @@ def test_the_modelled_schedule() -> None:
     assert hip_attention.schedule_makespan([1024] * 257, 1024) == 2 * (1024 + hip_attention.WORKGROUP_COST)
 
 
+def test_the_native_launch_model_is_the_python_statement() -> None:
+    # ayk_split_model and ayk_work_list (C++, host) against the plain-Python statement of the
+    # same schedule and order, on random ragged steps, edge lengths and every group count
+    from tests._support import python_schedule_makespan, python_work_list
+
+    rng = np.random.default_rng(17)
+    cases = [[0], [1], [64], [65], [4096] * 64, [1024] * 257, [0, 0, 3], list(range(0, 3000, 7))]
+    for _ in range(120):
+        n = int(rng.integers(1, 400))
+        cases.append([int(x) for x in np.exp(rng.uniform(0, np.log(40000), n)).astype(int) * (rng.random(n) > 0.1)])
+    for lengths in cases:
+        sizes = [int(x) for x in rng.choice(hip_attention.PARTITION_CANDIDATES, size=4)] + [max(lengths) + 1]
+        groups, cost = int(rng.integers(1, 4)), int(rng.choice([0, 80, 160, 240, 320]))
+        makespans, items = hip_attention.schedule_makespans(lengths, sizes, groups, cost)
+        for size, got, count in zip(sizes, makespans, items):
+            assert got == python_schedule_makespan(lengths, size, groups, cost), (lengths, size, groups, cost)
+            assert count == sum(-(-n // size) for n in lengths if n > 0)
+        size = int(rng.choice([64, 128, 320, 512, 4096]))
+        assert hip_attention.work_list(lengths, size).tolist() == python_work_list(lengths, size).tolist()
+    with pytest.raises(BackendError):
+        hip_attention.schedule_makespans([10], [0])
+
+
+@pytest.mark.parametrize("index,kv_bytes,expected", [
+    (1, 2, (0, 8)), (1, 1, (0, 8)), (2, 2, (320, 0)), (2, 1, (320, 0)), (3, 2, (0, 4)), (3, 1, (0, 4)),
+    (4, 2, (704, 0)), (4, 1, (704, 0)), (5, 2, (3072, 0)), (5, 1, (1280, 0))])
+def test_the_launches_chosen_for_the_benchmark_steps(index: int, kv_bytes: int, expected: tuple) -> None:
+    # the library's launch for each benchmark configuration: (partition size, v1 waves per head),
+    # (0, n) being v1 with each context split among n waves (measured choices: C3 v1 at 4 waves,
+    # C1 v1 at 8, C2 v2 at 320, C4 v2 at 704, C5 v2 at 3072, or 1280 over fp8 caches)
+    cfg = workloads.config(index)
+    hip_attention._split_cache.clear()
+    split = hip_attention.choose_split(cfg.batch, cfg.kv_heads, cfg.heads // cfg.kv_heads, max(cfg.lengths),
+                                       row_lengths=tuple(cfg.lengths), kv_bytes=kv_bytes)
+    assert (split.partition_size, split.waves) == expected
+
+
 def test_multi_row_tiles_list_every_partition_a_group_sees_once() -> None:
     rows, lengths = [37, 5, 1, 8, 0], [37, 900, 2, 130, 0]
     table = torch.ones(len(rows), 64, dtype=torch.int32)
@@ -464,3 +501,38 @@ def test_plan_accepts_int64_inputs() -> None:
         a, b = getattr(as32, key), getattr(as64, key)
         assert a.dtype == b.dtype and a.tolist() == b.tolist(), key
     assert as64.positions.tolist() == [3, 4, 2] and as64.slot_mapping.tolist() == [15, 16, 30]
+
+
+def test_the_pruned_best_split_is_the_exhaustive_one() -> None:
+    # ayk_best_split schedules only candidates whose lower bound can still win; its choice must
+    # be the first smallest exact finish time among the eligible candidates, as an exhaustive
+    # scoring of every candidate (the plain-Python schedule) picks it
+    from tests._support import python_schedule_makespan
+
+    rng = np.random.default_rng(23)
+    sizes = list(hip_attention.PARTITION_CANDIDATES)
+    for trial in range(150):
+        n = int(rng.integers(1, 300))
+        lengths = [int(x) for x in np.exp(rng.uniform(0, np.log(40000), n)).astype(int)]
+        if trial % 3 == 0:
+            lengths = [int(rng.choice([512, 1024, 4096]))] * n  # equal rows: ties between sizes
+        groups = int(rng.integers(1, 3))
+        kv_bytes = int(rng.choice([1, 2]))
+        max_items = int(rng.choice([0, 0, 64, 2048]))
+        cost = hip_attention.WORKGROUP_COSTS[kv_bytes]
+        got = hip_attention._best_size(lengths, max(lengths), groups, kv_bytes, 0, max_items)
+        cands = sizes
+        for i, size in enumerate(sizes):
+            if size >= max(lengths):
+                cands = sizes[:i + 1]
+                break
+        counts = [sum(-(-x // size) for x in lengths) for size in cands]
+        eligible = [i for i, c in enumerate(counts) if not max_items or c <= max_items]
+        if not eligible:
+            assert got == -(-max(lengths) // 64) * 64
+            continue
+        scored = [i for k, i in enumerate(eligible)
+                  if k == len(eligible) - 1 or counts[i] * groups <= hip_attention.MAX_ROUNDS * 256]
+        times = {i: python_schedule_makespan(lengths, cands[i], groups, cost) for i in scored}
+        want = min(scored, key=lambda i: (times[i], i))
+        assert got == cands[want], (trial, got, cands[want])
