@@ -175,8 +175,15 @@ int compute_units() {
 // workgroup (a few hundred workgroups for C3) the second launch costs less on
 // every benchmark grid (C3 161.4 vs 170.8 us, fp8 C5 228.0 vs 236.9, C5 a tie) but
 // a tiny one: a grid of a few dozen workgroups is latency-bound, and there the
-// second launch is the larger cost (C1 15.9 vs 18.9 us).
-bool merge_in_kernel(int64_t workgroups) { return workgroups <= compute_units() / 4; }
+// second launch is the larger cost (C1 15.9 vs 18.9 us). The merging workgroup folds
+// a row's partitions one round trip per two of them, so it only pays for rows of a
+// few partitions: at one row of 2048 positions (32 x 4 heads of 64) the in-kernel
+// merge over 32 partitions took 16.1 us per call in a graph replay, the reduce
+// kernel 9.2; over 2-4 partitions the two sites measured within 0.1 us.
+constexpr int kInKernelMaxPartitions = 4;
+bool merge_in_kernel(int64_t workgroups, int max_partitions) {
+  return workgroups <= compute_units() / 4 && max_partitions <= kInKernelMaxPartitions;
+}
 
 // Heads per wave from which the library picks the matrix-core q.k kernel.
 constexpr int kMfmaMinHeads = 3;
@@ -235,7 +242,7 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   // The grid: one workgroup per item and group of up to kMaxWaves / wave_split virtual heads.
   const int heads_per_wg = ayk::kMaxWavesPerGroup / q.wave_split;
   const int64_t grid = items * ((p.num_virtual_heads + heads_per_wg - 1) / heads_per_wg);
-  if (split && q.arrivals && !(flags & AYK_FLAG_SINGLE_LAUNCH) && !merge_in_kernel(grid))
+  if (split && q.arrivals && !(flags & AYK_FLAG_SINGLE_LAUNCH) && !merge_in_kernel(grid, p.max_partitions))
     q.arrivals = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err = mfma ? ayk::launch_attention_mfma(q, head_dim, gc, bf16, split, kv8, waves, s)

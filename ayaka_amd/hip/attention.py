@@ -460,24 +460,31 @@ def uses_matrix_cores(group: int) -> bool:
     return group // head_chunks(group) >= MFMA_MIN_HEADS
 
 
-def merge_site_for(workgroups: int) -> str:
-    """Where the library merges the v2 partitions of a grid of ``workgroups``: ``"in-kernel"``
-    for a quarter round of the compute units at most, ``"reduce-kernel"`` otherwise (the rule
-    of ``merge_in_kernel`` in ``api.hip``)."""
-    return "in-kernel" if workgroups <= COMPUTE_UNITS // 4 else "reduce-kernel"
+#: Most partitions per row the in-kernel merge serves (``kInKernelMaxPartitions`` in ``api.hip``).
+IN_KERNEL_MAX_PARTITIONS = 4
+
+
+def merge_site_for(workgroups: int, partitions: int) -> str:
+    """Where the library merges the v2 partitions of a grid of ``workgroups`` whose rows hold up
+    to ``partitions`` partitions: ``"in-kernel"`` for a quarter round of the compute units at
+    most and a few partitions per row, ``"reduce-kernel"`` otherwise (the rule of
+    ``merge_in_kernel`` in ``api.hip``)."""
+    small = workgroups <= COMPUTE_UNITS // 4 and partitions <= IN_KERNEL_MAX_PARTITIONS
+    return "in-kernel" if small else "reduce-kernel"
 
 
 def merge_site(num_kv_heads: int, group: int, step: "HipAttentionPlan", partition_size: int) -> str:
     """Where the library merges the v2 partitions of an eagerly planned step (its work list)."""
     groups = -(-num_kv_heads * head_chunks(group) // 8)
     items = sum(max(1, -(-n // partition_size)) for n in step.row_lengths)
-    return merge_site_for(items * groups)
+    return merge_site_for(items * groups, -(-step.max_length // partition_size))
 
 
-def graph_merge_site(items: int, num_kv_heads: int, group: int) -> str:
+def graph_merge_site(items: int, num_kv_heads: int, group: int, partitions: int) -> str:
     """Where the library merges the v2 partitions of a launch over a grid of ``items`` work
-    items (a graph replay's capacity, or the rows x partitions of a forced dense grid)."""
-    return merge_site_for(items * -(-num_kv_heads * head_chunks(group) // 8))
+    items (a graph replay's capacity, or the rows x partitions of a forced dense grid) whose
+    rows hold up to ``partitions`` partitions."""
+    return merge_site_for(items * -(-num_kv_heads * head_chunks(group) // 8), partitions)
 
 
 @dataclass(frozen=True, slots=True)

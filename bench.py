@@ -78,6 +78,9 @@ def parse() -> argparse.Namespace:
                     help="only time the multi-row (prefill / verify) kernel on its workloads, one JSON line each")
     ap.add_argument("--block-ops", action="store_true",
                     help="only time the block ops (gather / copy_blocks / zero_blocks) at the C3 pool shape")
+    ap.add_argument("--reference-shapes", action="store_true",
+                    help="only time the reference's own op-benchmark matrix (TinyLlama 32/4/64 and SmolLM2 "
+                         "9/3/64, fp16: five decode and two prefill steps), one JSON line per step")
     ap.add_argument("--host-trace", action="store_true",
                     help="only time the host side of decode steps (update_graph_metadata, and plan plus the "
                          "split choice of an eager step) over a continuous-batching trace at the C5 shape")
@@ -384,6 +387,114 @@ def block_ops(args) -> int:
     return 0
 
 
+#: The reference's op benchmark (benchmarks/ops/attention.py:33-36): (query heads, key/value
+#: heads, head width) of TinyLlama-1.1B and SmolLM2-135M; decode (batch, context) and prefill
+#: (rows, context) steps of one request; block 16.
+REFERENCE_SHAPES = {"tinyllama": (32, 4, 64), "smollm2-135m": (9, 3, 64)}
+REFERENCE_DECODE = [(1, 512), (1, 2048), (1, 8192), (4, 2048), (8, 2048)]
+REFERENCE_PREFILL = [(512, 512), (256, 2048)]
+
+
+def reference_shapes(args) -> int:
+    """The reference's op-benchmark matrix on this backend, fp16 as its default. Each step's
+    requests hold contiguous blocks, as the reference lays them out; the step is planned over
+    many disjoint copies of its blocks in one pool of about 1 GiB, and consecutive calls take
+    consecutive copies, so every call reads its K/V from HBM rather than from the last call's
+    cache lines (these steps hold 0.3-8 MB of K/V, well inside the 256 MB Infinity Cache). The
+    time is the mean over back-to-back calls between two HIP events (median of 5 regions);
+    ``us_one_pool_event`` is the reference's own method (one call per event pair, the median,
+    always the same copy) for comparison. GB/s counts K/V read, q read and output written."""
+    import numpy as np
+    import torch
+
+    from ayaka_amd.enums import ForwardMode, KVLayoutKind
+    from ayaka_amd.hip import _lib
+    from ayaka_amd.hip import attention as hip_attention
+    from ayaka_amd.kvcache import RAW_CODEC, KVBuffers
+
+    _lib.lib()
+    dev, bs, dtype = torch.device("cuda:0"), 16, torch.float16
+    for shape, (heads, kv_heads, dim) in REFERENCE_SHAPES.items():
+        group = heads // kv_heads
+        steps = [("decode", [1] * b, [n] * b) for b, n in REFERENCE_DECODE]
+        steps += [("prefill", [rows], [n]) for rows, n in REFERENCE_PREFILL]
+        for kind, rows, lengths in steps:
+            need = [-(-n // bs) for n in lengths]
+            per_copy = sum(need)
+            block_bytes = bs * kv_heads * dim * 2
+            copies = max(1, min(4096, (1 << 30) // (2 * block_bytes * per_copy)))
+            gen = torch.Generator(device=dev).manual_seed(sum(lengths) + len(rows))
+            k = torch.randn((copies * per_copy + 1, bs, kv_heads, dim), generator=gen, device=dev).to(dtype)
+            v = torch.randn(k.shape, generator=gen, device=dev).to(dtype)
+            buffers = KVBuffers(k, v, KVLayoutKind.NHD, RAW_CODEC)
+            width = max(need)
+            mode = ForwardMode.DECODE if kind == "decode" else ForwardMode.PREFILL
+            rows_t = torch.tensor(rows, dtype=torch.int32, device=dev)
+            lengths_t = torch.tensor(lengths, dtype=torch.int32, device=dev)
+            metas = []
+            for c in range(copies):
+                table = np.zeros((len(lengths), width), dtype=np.int32)
+                first = 1 + c * per_copy
+                for r, n in enumerate(need):
+                    table[r, :n] = np.arange(first, first + n)
+                    first += n
+                metas.append(hip_attention.plan(mode, rows_t, lengths_t, torch.from_numpy(table).to(dev), bs))
+            q = torch.randn((sum(rows), heads, dim), generator=gen, device=dev).to(dtype)
+            out = torch.empty_like(q)
+            scale = dim ** -0.5
+            turn = [0]
+
+            def call() -> None:
+                meta = metas[turn[0]]
+                turn[0] = (turn[0] + 1) % copies
+                hip_attention.attend(q, buffers, meta, out, scale=scale)
+
+            for meta in metas:  # plan each copy's launch (work list, tiles) before timing
+                hip_attention.attend(q, buffers, meta, out, scale=scale)
+            timed = time_calls(call, max(args.steps, copies), args.warmup)
+
+            def one() -> None:
+                hip_attention.attend(q, buffers, metas[0], out, scale=scale)
+
+            for _ in range(args.warmup):
+                one()
+            torch.cuda.synchronize()
+            single = []
+            for _ in range(50):
+                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                one()
+                stop.record()
+                stop.synchronize()
+                single.append(start.elapsed_time(stop) * 1000.0)
+            plan = metas[0].plan
+            if kind == "decode":
+                split = plan.split_for(kv_heads, group, 2)
+                if split.partitions:
+                    merge = hip_attention.merge_site(kv_heads, group, plan, split.partition_size)
+                    launch = f"v2, {split.partitions} x {split.partition_size}, merge {merge}"
+                else:
+                    launch = f"v1, {split.waves or 'library'} waves per head"
+            elif hip_attention.WINDOWS and plan.window_pairs(group) > 0:
+                launch = f"windows, partition {plan.window_split(kv_heads, group, 2)}"
+            else:
+                pairs, size = plan.prefill_launch(kv_heads, group, dim, 2)
+                launch = f"multi-row, tiles of {pairs} pairs, partition {size}"
+            nbytes = sum(lengths) * kv_heads * dim * 2 * 2 + 2 * q.numel() * 2
+            us = timed["median_us"]
+            record = {"shape": shape, "heads": [heads, kv_heads, dim], "kind": kind, "dtype": "fp16",
+                      "batch": len(rows), "rows": sum(rows), "context": lengths[0], "us_per_call": round(us, 2),
+                      "gbs": round(nbytes / us / 1e3, 1), "launch": launch, "copies": copies,
+                      "us_one_pool_event": round(statistics.median(single), 2)}
+            if kind == "prefill":
+                visible = sum(n - rows[0] + j + 1 for j in range(rows[0]) for n in lengths)
+                record["tflops"] = round(4 * heads * dim * visible / us / 1e6, 1)
+            print(json.dumps(record), flush=True)
+            del metas, k, v, buffers
+            torch.cuda.empty_cache()
+    return 0
+
+
 HOST_TRACE_STEPS = 3000
 
 
@@ -437,6 +548,8 @@ def host_trace(args) -> int:
     table = torch.from_numpy(rng.integers(1, 100_000, (bucket, width)).astype(np.int32))
     meta = hip_attention.graph_metadata(bucket, width, bs, dev)
     meta.plan.head_shape.extend((8, 8, 2))
+    hip_attention.update_graph_metadata(meta, torch.from_numpy(trace[0]), table)  # first-use costs
+    torch.cuda.synchronize()
     hip_attention._split_cache.clear()
     misses, graph_us = 0, []
     for lengths in trace:
@@ -446,10 +559,12 @@ def host_trace(args) -> int:
         hip_attention.update_graph_metadata(meta, host, table)
         graph_us.append((time.perf_counter() - t0) * 1e6)
         misses += len(hip_attention._split_cache) != before
+        torch.cuda.synchronize()  # the step's replay and token read would wait here
     torch.cuda.synchronize()
     device_table = table.to(dev)
     ones = torch.ones(bucket, dtype=torch.int32, device=dev)
     eager_us = []
+    hip_attention.plan(ForwardMode.DECODE, ones, torch.from_numpy(trace[0]).to(dev), device_table, bs)
     hip_attention._split_cache.clear()
     for lengths in trace[:1000]:
         device_lengths = torch.from_numpy(lengths).to(dev)
@@ -461,7 +576,7 @@ def host_trace(args) -> int:
 
     def pct(values: list) -> dict:
         return {f"p{q}": round(float(np.percentile(values, q)), 1) for q in (50, 90, 99)} | \
-               {"max": round(max(values), 1)}
+               {"max": round(max(values), 1), "max_at_step": int(np.argmax(values))}
 
     print(json.dumps({"workload": "continuous-batching decode trace: 256-row bucket x 512 blocks of 32, "
                                   "64/8 heads, lengths log-uniform in [16, 16384], requests joining and "
@@ -490,6 +605,8 @@ def main() -> int:
         return block_ops(args)
     if args.host_trace:
         return host_trace(args)
+    if args.reference_shapes:
+        return reference_shapes(args)
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)

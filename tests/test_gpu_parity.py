@@ -809,7 +809,8 @@ def test_graph_metadata_replays_match_eager_steps(heads: int, kv_heads: int, max
         # work list's; the same site and partition count fold in the same order
         staged_size = meta.plan.staged_partition_size
         assert staged_size % 64 == 0 and staged_size >= meta.plan.min_size
-        site = hip_attention.graph_merge_site(meta.plan.capacity, kv_heads, heads // kv_heads)
+        site = hip_attention.graph_merge_site(meta.plan.capacity, kv_heads, heads // kv_heads,
+                                              meta.plan.partitions)
         same_shape = torch.empty_like(out)
         if meta.plan.partitions > 1:
             hip_attention.attend_with(q, buffers, eager_meta, same_shape, scale=dim**-0.5,
