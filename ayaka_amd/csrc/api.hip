@@ -244,6 +244,10 @@ int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool 
   const int64_t grid = items * ((p.num_virtual_heads + heads_per_wg - 1) / heads_per_wg);
   if (split && q.arrivals && !(flags & AYK_FLAG_SINGLE_LAUNCH) && !merge_in_kernel(grid, p.max_partitions))
     q.arrivals = nullptr;
+  if (ayk::walking()) {  // the host address walk: the launch's loads, no launch
+    ayk::walk_decode(q, head_dim, mfma, kv8, split, false);
+    return ok();
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err = mfma ? ayk::launch_attention_mfma(q, head_dim, gc, bf16, split, kv8, waves, s)
                         : ayk::launch_attention_dpp(q, head_dim, gc, bf16, split, waves, s);
@@ -303,7 +307,7 @@ void* static_scratch(const char* op, void* stream) {
 
 extern "C" {
 
-int ayk_abi_version(void) { return 14; }
+int ayk_abi_version(void) { return 15; }
 
 int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 
@@ -517,6 +521,11 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
                 partition_size);
   if (n_tiles == 0 || n_rows == 0) return ok();
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool walk = ayk::walking();  // the host address walk: the launch's loads, no launch
+  if (partition_size == 0 && walk) {
+    ayk::walk_prefill(p, tiles, n_tiles, head_dim, kv_dtype == AYK_DTYPE_FP8_E4M3, waves_per_group);
+    return ok();
+  }
   if (partition_size == 0)
     return launched(ayk::launch_prefill(p, tiles, n_tiles, head_dim, dtype == AYK_DTYPE_BF16,
                                         kv_dtype == AYK_DTYPE_FP8_E4M3, waves_per_group, s),
@@ -535,6 +544,10 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   p.part_ml = p.part_o + parts * head_dim;
   p.partition_size = partition_size;
   p.max_partitions = (int32_t)max_partitions;
+  if (walk) {
+    ayk::walk_prefill(p, tiles, n_tiles, head_dim, kv_dtype == AYK_DTYPE_FP8_E4M3, waves_per_group);
+    return ok();
+  }
   hipError_t err = ayk::launch_prefill(p, tiles, n_tiles, head_dim, dtype == AYK_DTYPE_BF16,
                                        kv_dtype == AYK_DTYPE_FP8_E4M3, waves_per_group, s);
   if (err == hipSuccess) err = ayk::launch_row_reduce(p, head_dim, dtype == AYK_DTYPE_BF16, s);
@@ -589,6 +602,11 @@ int ayk_paged_attention_windows(void* out, const void* q, const void* k_cache, c
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf16 = dtype == AYK_DTYPE_BF16, kv8 = kv_dtype == AYK_DTYPE_FP8_E4M3;
+  const bool walk = ayk::walking();  // the host address walk: the launch's loads, no launch
+  if (partition_size == 0 && walk) {
+    ayk::walk_decode(p, head_dim, true, kv8, false, true);
+    return ok();
+  }
   if (partition_size == 0) return launched(ayk::launch_window_mfma(p, head_dim, bf16, false, kv8, s), op);
   const int64_t max_partitions = ((int64_t)p.max_len + partition_size - 1) / partition_size;
   if (max_partitions < 1 || max_partitions > 65535)
@@ -604,6 +622,10 @@ int ayk_paged_attention_windows(void* out, const void* q, const void* k_cache, c
   p.part_ml = p.part_o + parts * head_dim;
   p.partition_size = partition_size;
   p.max_partitions = (int32_t)max_partitions;
+  if (walk) {
+    ayk::walk_decode(p, head_dim, true, kv8, true, true);
+    return ok();
+  }
   hipError_t err = ayk::launch_window_mfma(p, head_dim, bf16, true, kv8, s);
   if (err == hipSuccess) err = ayk::launch_row_reduce(p, head_dim, bf16, s);
   return launched(err, op);

@@ -7,6 +7,7 @@
 #include <cstdint>
 
 #include "ayaka_hip_internal.h"
+#include "kv_address.h"
 
 namespace ayk {
 
@@ -108,8 +109,7 @@ __device__ __forceinline__ uint32_t e4m3_pair(uint32_t word) {
 // Address of element `elem` of a cache: 2-byte elements, or 1-byte fp8 codes.
 template <bool KV8>
 __device__ __forceinline__ const uint16_t* kv_at(const uint16_t* base, int64_t elem) {
-  if constexpr (KV8) return reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(base) + elem);
-  return base + elem;
+  return reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(base) + kv_bytes_of<KV8>(elem));
 }
 
 // Raw loads and decoding are separate, so prefetched chunks stay in flight: a
@@ -129,7 +129,7 @@ struct KvRaw<true> {
 
 template <bool KV8, bool STREAM = true>
 __device__ __forceinline__ typename KvRaw<KV8>::T load_kv_raw(const uint16_t* base, uint32_t off) {
-  const auto* p8 = reinterpret_cast<const uint8_t*>(base) + (KV8 ? off : 2 * (size_t)off);
+  const auto* p8 = reinterpret_cast<const uint8_t*>(base) + kv_bytes_of<KV8>(off);
   typedef typename KvRaw<KV8>::T T;
   if constexpr (STREAM) return __builtin_nontemporal_load(reinterpret_cast<const T*>(p8));
   else return *reinterpret_cast<const T*>(p8);
@@ -404,14 +404,6 @@ __device__ __forceinline__ void store_zero_rows(const AttnParams& p, int row, in
   }
 }
 
-// Block of position t (0 <= t < 2^31) for any block size: a multiply-high division by the
-// host's magic number, q = (umulhi(t, m) + t) >> l with l = ceil(log2 bs) and
-// m = floor(2^32 (2^l - bs) / bs) + 1 (a power of two has m = 1: a shift). The sum stays
-// below 2^32 because umulhi(t, m) < t < 2^31.
-__device__ __forceinline__ int block_of(const AttnParams& p, int t) {
-  return (int)((__umulhi((uint32_t)t, p.bs_magic) + (uint32_t)t) >> p.bs_shift);
-}
-
 // Stage the block-table entries of positions [s0, s1) in LDS as element offsets
 // of their blocks (block id x block stride; ids outside the pool become the
 // padding block 0); returns the first staged block index. The host checks that
@@ -421,10 +413,7 @@ __device__ __forceinline__ int stage_table(const AttnParams& p, const int32_t* t
   const int b0 = block_of(p, s0);
   const int nb = block_of(p, s1 - 1) - b0 + 1;
   __syncthreads();  // the previous segment is done with s_tbl
-  for (int i = tid; i < nb; i += threads) {
-    const int b = tbl[b0 + i];
-    s_tbl[i] = ((unsigned)b < (unsigned)p.num_blocks) ? (uint32_t)b * (uint32_t)p.block_stride : 0u;
-  }
+  for (int i = tid; i < nb; i += threads) s_tbl[i] = table_entry(p, tbl[b0 + i]);
   __syncthreads();
   return b0;
 }
@@ -480,17 +469,6 @@ __device__ __forceinline__ u32x2 lds_read_transposed(const uint16_t* p) {
   typedef short v4i16 __attribute__((ext_vector_type(4)));
   return __builtin_bit_cast(
       u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p)));
-}
-
-// Element offset of position t in the cache, from the staged table segment that starts at
-// block b0: its block's offset plus (t mod block size) x token stride, the products on the
-// full-rate 24-bit multiplier (the block index is below the table width and the token
-// stride below 2^24: the host refuses wider tables and strides).
-__device__ __forceinline__ uint32_t kv_offset(const AttnParams& p, const uint32_t* s_tbl, int b0, int t,
-                                              uint32_t token_stride) {
-  const int b = block_of(p, t);
-  const uint32_t r = (uint32_t)t - __umul24((uint32_t)b, (uint32_t)p.block_size);
-  return s_tbl[b - b0] + __umul24(r, token_stride);
 }
 
 }  // namespace ayk

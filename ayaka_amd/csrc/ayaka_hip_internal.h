@@ -73,6 +73,13 @@ hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16,
                                    hipStream_t stream);
 hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipStream_t stream);
 
+// The host address walk (kv_reach.hip): while it is on for the calling thread, the attention
+// entry points enumerate the K/V loads of the launch they prepared instead of launching it.
+bool walking();
+void walk_decode(const AttnParams& p, int head_dim, bool mfma, bool kv8, bool split, bool window);
+void walk_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool kv8,
+                  int waves_per_group);
+
 hipError_t launch_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_cache,
                                     const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,
                                     int32_t head_dim, int32_t num_blocks, int32_t block_size,

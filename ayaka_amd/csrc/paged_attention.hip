@@ -37,8 +37,8 @@ namespace ayk {
 template <int D, int GC, int NLD, bool BF16, bool SPLIT>
 __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(const AttnParams p) {
   using E = Elem<BF16>;
-  constexpr int LPT = D / 8;         // lanes per token (8 elements = 16 bytes each)
-  constexpr int TPL = kWave / LPT;   // tokens per load instruction
+  constexpr int LPT = pieces_per_position(D);  // lanes per token (8 elements = 16 bytes each)
+  constexpr int TPL = positions_per_load(D);   // tokens per load instruction
   constexpr int CH = TPL * NLD;      // tokens per chunk
 
   __shared__ uint32_t s_tbl[kTableCap];
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
 
   const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
   // positions per staged table segment: at most kTableCap blocks, whatever s0's offset
-  const int seg_len = ((kTableCap - 1) * p.block_size / CH) * CH;
+  const int seg_len = segment_positions(p, CH);
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = p.k_cache + (int64_t)kvh * p.head_stride + c * 8;
@@ -117,8 +117,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
     auto offsets = [&](int ci, uint32_t(&dst)[NLD]) {
 #pragma unroll
       for (int j = 0; j < NLD; ++j) {
-        const int t = min(s0 + ci * CH + j * TPL + r, s1 - 1);
-        dst[j] = kv_offset(p, s_tbl, b0, t, token_stride);
+        dst[j] = kv_offset(p, s_tbl, b0, chunk_position(s0, s1, ci, CH, j, TPL, r), token_stride);
       }
     };
 
@@ -405,7 +404,7 @@ template <int D, int GC, bool BF16>
 static hipError_t launch_dpp_typed(const AttnParams& p, bool split, hipStream_t stream) {
   // Two loads per token slot per chunk: 8 tokens (D 128), 16 (D 64) or 4 (D 256) per
   // chunk keeps a group of 4 under 128 VGPRs, so two 8-wave workgroups share a CU.
-  constexpr int NLD = 2;
+  constexpr int NLD = dpp_loads_per_chunk();
   // One wave per virtual head, up to kMaxWaves per workgroup.
   const int waves = p.num_virtual_heads < kMaxWaves ? p.num_virtual_heads : kMaxWaves;
   const int groups = (p.num_virtual_heads + waves - 1) / waves;

@@ -63,17 +63,14 @@ __device__ __forceinline__ void wave_lds_sync() {
 // launches) are merged per row by row_reduce_kernel.
 template <int D, int GC, bool BF16, bool SPLIT, bool KV8, bool WIN = false>
 __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel(const AttnParams p) {
-  constexpr int MT = 16;            // tokens per MFMA tile
-  // Tiles per chunk, so that a wave keeps about as many bytes in flight as a
-  // 16-bit tile of head_dim 128: fp8 loads and head_dim 64 carry half of that per
-  // tile (two tiles), fp8 at head_dim 64 a quarter (four); at head_dim 256 two fp8
-  // tiles' loads do not fit the registers (they spilled), one does. Measured: C2
-  // (fp16, head_dim 64) 26.2 -> 25.2 us with two tiles.
-  constexpr int SUB = D == 64 ? (KV8 ? 4 : 2) : (KV8 && D <= 128 ? 2 : 1);
+  constexpr int MT = decode_tile_positions();  // tokens per MFMA tile
+  // Tiles per chunk (decode_tiles_per_chunk: about as many bytes in flight per wave as a
+  // 16-bit tile of head_dim 128). Measured: C2 (fp16, head_dim 64) 26.2 -> 25.2 us with two.
+  constexpr int SUB = decode_tiles_per_chunk(D, KV8);
   constexpr int CH = MT * SUB;      // tokens per chunk
   constexpr int KS = D / 32;        // MFMA k-steps over head_dim
-  constexpr int CPT = D / 8;        // 8-element pieces per token (= value lanes per token)
-  constexpr int TPL = kWave / CPT;  // tokens per load instruction
+  constexpr int CPT = pieces_per_position(D);  // 8-element pieces per token (= value lanes per token)
+  constexpr int TPL = positions_per_load(D);   // tokens per load instruction
   constexpr int NL1 = MT / TPL;     // load instructions per tile, for K and for V
   constexpr int NL = CH / TPL;      // load instructions per chunk
   constexpr int DT = D / 16;        // 16-element slices of head_dim for P.V
@@ -192,7 +189,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
 
   const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
   // positions per staged table segment: at most kTableCap blocks, whatever s0's offset
-  const int seg_len = ((kTableCap - 1) * p.block_size / CH) * CH;
+  const int seg_len = segment_positions(p, CH);
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride + c * 8);
@@ -204,13 +201,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     const int nch = (s1 - s0 + CH - 1) / CH;
     if (!active || slice >= nch) continue;
     // this wave's chunks: slice, slice + ws, ..., up to `last`
-    const int last = slice + (nch - 1 - slice) / ws * ws;
+    const int last = last_chunk_of_slice(nch, slice, ws);
 
     auto offsets = [&](int ci, uint32_t(&dst)[NL]) {
 #pragma unroll
       for (int j = 0; j < NL; ++j) {
-        const int t = min(s0 + ci * CH + j * TPL + r, s1 - 1);
-        dst[j] = kv_offset(p, s_tbl, b0, t, token_stride);
+        dst[j] = kv_offset(p, s_tbl, b0, chunk_position(s0, s1, ci, CH, j, TPL, r), token_stride);
       }
     };
 

@@ -87,12 +87,12 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
   // Positions per chunk: 64, or 32 at head_dim 256 with 1 or 2 waves per pair group, where a
   // 64-position stage (133 KB of LDS) and its load registers left one wave per SIMD; 32 fit
   // two workgroups per CU without spills (quarter tiles need 16 positions per wave: 64).
-  constexpr int CH = D == 256 && PS <= 2 ? 32 : 64;
+  constexpr int CH = prefill_chunk_positions(D, PS);
   constexpr int PTL = CH / 16;                  // 16-position tiles per chunk
   constexpr int PTL_W = PTL / PS;               // 16-position tiles per chunk of one wave
   constexpr int KS = D / 32;                    // q.k k-steps
   constexpr int DT = D / 16;                    // 16-element slices of head_dim for P.V
-  constexpr int CPT = D / 8;                    // 8-element pieces per position
+  constexpr int CPT = pieces_per_position(D);   // 8-element pieces per position
   constexpr int PIECES = CH * CPT;              // pieces per chunk of K (or V)
   constexpr int PER_THREAD = PIECES / THREADS;  // 2 (D 64), 4 (D 128), 4 or 8 (D 256)
   // Values in LDS token-major, rows VP elements apart: the transposing reads of the
@@ -196,7 +196,7 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
 
   const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
   // positions per staged table segment: at most kTableCap blocks, whatever s0's offset
-  const int seg_len = ((kTableCap - 1) * p.block_size / CH) * CH;
+  const int seg_len = segment_positions(p, CH);
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride);
@@ -225,27 +225,9 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
     // values). Block sizes that are a multiple of PER_THREAD (uniform across the launch)
     // take one table lookup per chunk for the thread's positions, the others one per
     // position.
-    const uint32_t bs = (uint32_t)p.block_size;
-    const bool one_block = bs % PER_THREAD == 0;
-    auto offset_of = [&](int t) {
-      const int b = block_of(p, t);
-      const uint32_t r = (uint32_t)t - __umul24((uint32_t)b, bs);
-      return s_tbl[b - b0] + __umul24(r, token_stride) + piece_c * 8;
-    };
     auto load_chunk = [&](int ci) {
-      const int t = s0 + ci * CH + first_pos;
       uint32_t off[PER_THREAD];
-      if (one_block) {
-        // t is a multiple of PER_THREAD (s0 and CH are), so t .. t + PER_THREAD - 1 share a
-        // block; a thread past the end reads the last position for all its pieces
-        const int last = s1 - 1;
-        const uint32_t o0 = offset_of(min(t, last));
-#pragma unroll
-        for (int u = 0; u < PER_THREAD; ++u) off[u] = o0 + (uint32_t)min(u, max(last - t, 0)) * token_stride;
-      } else {
-#pragma unroll
-        for (int u = 0; u < PER_THREAD; ++u) off[u] = offset_of(min(t + u, s1 - 1));
-      }
+      prefill_offsets<PER_THREAD>(p, s_tbl, b0, s0 + ci * CH + first_pos, s1, piece_c, token_stride, off);
 #pragma unroll
       for (int u = 0; u < PER_THREAD; ++u) {
         kr[u] = load_kv_raw<KV8, false>(kbase, off[u]);

@@ -340,6 +340,22 @@ int ayk_best_split(const int64_t* lengths, int32_t n_lengths, const int32_t* siz
                    int32_t cost, int32_t compute_units, int32_t xcds, int64_t max_items, int64_t round_items,
                    int32_t* best);
 
+/*
+ * Diagnostics, no counterpart in the reference: the host address walk. Between
+ * ayk_debug_kv_reach_begin and ayk_debug_kv_reach_end on one thread, the attention entry
+ * points (ayk_paged_attention_v1 / _v2 / _windows, ayk_paged_prefill) check and prepare each
+ * call as usual but launch nothing: they enumerate on the host every K/V load its workgroups
+ * would issue, with the kernels' own loops and address arithmetic. For the walk, the block
+ * table, lengths, request_of_row, positions, work list, staged split and tiles arguments are
+ * HOST pointers, and the q / out / cache / workspace pointers are never dereferenced.
+ * `table_entries` is the int32 entry count of the table allocation. ayk_debug_kv_reach_end
+ * writes reach[0..4]: the lowest byte and one past the highest byte any load touches, relative
+ * to a cache's base (K and V share their offsets), the number of loads, and the range
+ * [reach[3], reach[4]) of table entries read; then it turns the walk off. Needs no GPU.
+ */
+int ayk_debug_kv_reach_begin(int64_t table_entries);
+int ayk_debug_kv_reach_end(int64_t* reach);
+
 #ifdef __cplusplus
 }
 #endif
