@@ -71,6 +71,7 @@ struct AttnCall {
   int32_t n_rows, num_heads, num_kv_heads, head_dim, num_blocks, block_size, max_blocks, layout,
       dtype, kv_dtype;
   float scale;
+  float k_scale, v_scale;  // the cache holds keys / k_scale and values / v_scale (1, 1: as they are)
 };
 
 // Check a call and fill the launch record; returns AYK_OK or an error code.
@@ -148,7 +149,13 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
     return fail(AYK_ERR_UNSUPPORTED, "%s: a table of %d blocks of %d positions exceeds %lld positions per row", op,
                 c.max_blocks, c.block_size, (long long)max_table_len);
   p.max_len = (int32_t)table_len;
-  p.scale_log2 = c.scale * 1.4426950408889634f;
+  if (!(c.k_scale > 0.f) || !(c.v_scale > 0.f) || !std::isfinite(c.k_scale) || !std::isfinite(c.v_scale))
+    return fail(AYK_ERR_ARGUMENT, "%s: k_scale %g and v_scale %g must be positive and finite", op, c.k_scale,
+                c.v_scale);
+  // A key's score is scale * q.(k_scale * stored key): the key scale joins the score scale
+  // (exact at k_scale 1), and a value's scale multiplies each normalised output.
+  p.scale_log2 = c.scale * c.k_scale * 1.4426950408889634f;
+  p.v_scale = c.v_scale;
   p.partition_size = INT32_MAX;
   p.max_partitions = 1;
   p.wave_split = 1;
@@ -307,7 +314,7 @@ void* static_scratch(const char* op, void* stream) {
 
 extern "C" {
 
-int ayk_abi_version(void) { return 15; }
+int ayk_abi_version(void) { return 16; }
 
 int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 
@@ -339,8 +346,10 @@ int ayk_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_c
 int ayk_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void* v_cache,
                                const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads, int32_t head_dim,
                                int32_t num_blocks, int32_t block_size, int32_t layout, int32_t src_dtype,
-                               void* stream) {
+                               float k_scale, float v_scale, void* stream) {
   const char* op = "ayk_reshape_and_cache_e4m3";
+  if (!(k_scale > 0.f) || !(v_scale > 0.f) || !std::isfinite(k_scale) || !std::isfinite(v_scale))
+    return fail(AYK_ERR_ARGUMENT, "%s: k_scale %g and v_scale %g must be positive and finite", op, k_scale, v_scale);
   if (n_rows < 0) return fail(AYK_ERR_ARGUMENT, "%s: n_rows is negative", op);
   if (num_kv_heads <= 0 || head_dim <= 0 || num_blocks <= 0 || block_size <= 0)
     return fail(AYK_ERR_ARGUMENT, "%s: num_kv_heads %d, head_dim %d, num_blocks %d, block_size %d",
@@ -354,7 +363,8 @@ int ayk_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void
     return fail(AYK_ERR_ARGUMENT, "%s: a required pointer is null", op);
   return launched(ayk::launch_reshape_and_cache_e4m3(k, v, k_cache, v_cache, slot_mapping, n_rows, num_kv_heads,
                                                      head_dim, num_blocks, block_size, layout == AYK_LAYOUT_HND,
-                                                     src_dtype == AYK_DTYPE_BF16, static_cast<hipStream_t>(stream)),
+                                                     src_dtype == AYK_DTYPE_BF16, 1.0f / k_scale, 1.0f / v_scale,
+                                                     static_cast<hipStream_t>(stream)),
                   op);
 }
 
@@ -364,11 +374,11 @@ int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const 
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           int32_t kv_dtype, float scale, int32_t flags, void* stream) {
+                           int32_t kv_dtype, float scale, float k_scale, float v_scale, int32_t flags, void* stream) {
   const char* op = "ayk_paged_attention_v1";
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
-             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, kv_dtype, scale};
+             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, kv_dtype, scale, k_scale, v_scale};
   ayk::AttnParams p;
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
@@ -392,14 +402,14 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
+                           int32_t kv_dtype, float scale, float k_scale, float v_scale, int32_t partition_size, int32_t max_partitions,
                            const int32_t* work_items, int32_t n_work_items, const int32_t* staged,
                            void* workspace, size_t workspace_bytes, uint32_t* arrivals, int32_t flags,
                            void* stream) {
   const char* op = "ayk_paged_attention_v2";
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
-             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, kv_dtype, scale};
+             head_dim,  num_blocks, block_size, max_blocks, layout, dtype, kv_dtype, scale, k_scale, v_scale};
   ayk::AttnParams p;
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
@@ -444,7 +454,7 @@ int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache,
                                   const int32_t* request_of_row, const int32_t* positions, int32_t n_rows,
                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                                   int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                                  int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
+                                  int32_t kv_dtype, float scale, float k_scale, float v_scale, int32_t partition_size, int32_t max_partitions,
                                   const int32_t* work_items, int32_t n_work_items, const int32_t* staged,
                                   int32_t flags, void* stream) {
   const char* op = "ayk_paged_attention_v2_static";
@@ -459,7 +469,7 @@ int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache,
   if (n_rows <= 0 || num_heads <= 0) {  // nothing to launch: the checks of the allocating entry point apply
     return ayk_paged_attention_v2(out, q, k_cache, v_cache, block_table, table_stride, kv_lengths, request_of_row,
                                   positions, n_rows, num_heads, num_kv_heads, head_dim, num_blocks, block_size,
-                                  max_blocks, layout, dtype, kv_dtype, scale, partition_size, max_partitions,
+                                  max_blocks, layout, dtype, kv_dtype, scale, k_scale, v_scale, partition_size, max_partitions,
                                   work_items, n_work_items, staged, nullptr, 0, nullptr, flags, stream);
   }
   unsigned char* base = static_cast<unsigned char*>(static_scratch(op, stream));
@@ -470,7 +480,7 @@ int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache,
                            : nullptr;
   return ayk_paged_attention_v2(out, q, k_cache, v_cache, block_table, table_stride, kv_lengths, request_of_row,
                                 positions, n_rows, num_heads, num_kv_heads, head_dim, num_blocks, block_size,
-                                max_blocks, layout, dtype, kv_dtype, scale, partition_size, max_partitions, work_items,
+                                max_blocks, layout, dtype, kv_dtype, scale, k_scale, v_scale, partition_size, max_partitions, work_items,
                                 n_work_items, staged, base, kStaticPartialBytes, counters, flags, stream);
 }
 
@@ -489,14 +499,14 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
                       const int32_t* request_of_row, const int32_t* positions, const int32_t* tiles,
                       int32_t n_tiles, int32_t tile_pairs, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                       int32_t num_blocks, int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                      int32_t kv_dtype, float scale, int32_t partition_size, void* workspace,
+                      int32_t kv_dtype, float scale, float k_scale, float v_scale, int32_t partition_size, void* workspace,
                       size_t workspace_bytes, void* stream) {
   const char* op = "ayk_paged_prefill";
   if (!request_of_row || !positions)
     return fail(AYK_ERR_ARGUMENT, "%s: request_of_row and positions are required", op);
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
-             head_dim,  num_blocks, block_size, max_blocks, layout,      dtype,       kv_dtype, scale};
+             head_dim,  num_blocks, block_size, max_blocks, layout,      dtype,       kv_dtype, scale, k_scale, v_scale};
   ayk::AttnParams p;
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
@@ -559,14 +569,14 @@ int ayk_paged_attention_windows(void* out, const void* q, const void* k_cache, c
                                 const int32_t* request_of_row, const int32_t* positions, const int32_t* tiles,
                                 int32_t n_tiles, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads,
                                 int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t max_blocks,
-                                int32_t layout, int32_t dtype, int32_t kv_dtype, float scale, int32_t partition_size,
+                                int32_t layout, int32_t dtype, int32_t kv_dtype, float scale, float k_scale, float v_scale, int32_t partition_size,
                                 void* workspace, size_t workspace_bytes, void* stream) {
   const char* op = "ayk_paged_attention_windows";
   if (!request_of_row || !positions)
     return fail(AYK_ERR_ARGUMENT, "%s: request_of_row and positions are required", op);
   AttnCall c{out,       q,          k_cache,  v_cache,      block_table, table_stride,
              kv_lengths, request_of_row, positions, n_rows, num_heads, num_kv_heads,
-             head_dim,  num_blocks, block_size, max_blocks, layout,      dtype,       kv_dtype, scale};
+             head_dim,  num_blocks, block_size, max_blocks, layout,      dtype,       kv_dtype, scale, k_scale, v_scale};
   ayk::AttnParams p;
   int gc = 0;
   const int rc = prepare(op, c, p, gc);

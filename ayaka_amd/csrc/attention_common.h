@@ -232,12 +232,13 @@ __device__ __forceinline__ int64_t partial_index(const AttnParams& p, int row, i
 // Write one head's merged state from lane c (its 8 elements): the rounded
 // output (v1, or v2 for a row whose context is one partition: nothing to merge,
 // so it rounds exactly what v1 rounds) or the normalised partial and its (m, l)
-// (v2 partition `part` of `np`).
+// (v2 partition `part` of `np`). Both carry the value scale, so the merges of
+// partials need none.
 template <int D, bool BF16, bool SPLIT>
 __device__ __forceinline__ void store_head(const AttnParams& p, int row, int part, int np, int head, int c,
                                            const float (&o)[8], float m, float l) {
   using E = Elem<BF16>;
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  const float inv = (l > 0.f ? 1.0f / l : 0.f) * p.v_scale;  // exact at v_scale 1
   const int64_t head_row = (int64_t)row * p.num_heads + head;
   if (SPLIT && np > 1) {
     const int64_t slot = partial_index(p, row, head, np) + part;
@@ -266,7 +267,7 @@ template <int D, bool BF16, bool SPLIT>
 __device__ __forceinline__ void store_head_t(const AttnParams& p, int row, int part, int np, int head, int g,
                                              const f32x4 (&o)[D / 16], float m, float l) {
   using E = Elem<BF16>;
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  const float inv = (l > 0.f ? 1.0f / l : 0.f) * p.v_scale;  // exact at v_scale 1
   const int64_t head_row = (int64_t)row * p.num_heads + head;
   if (SPLIT && np > 1) {
     const int64_t slot = partial_index(p, row, head, np) + part;

@@ -50,7 +50,8 @@ struct AttnParams {
   int32_t n_work;
   int32_t wave_split;   // v1, matrix-core kernel: waves sharing one virtual head's context
                         // (1, 2, 4 or 8; a workgroup holds 8 / wave_split virtual heads)
-  float scale_log2;     // scale * log2(e): scores live in the log2 domain
+  float scale_log2;     // scale * k_scale * log2(e): scores live in the log2 domain
+  float v_scale;        // each normalised output (and partial) is multiplied by it
 };
 
 // The per-(row, head[, partition]) attention kernels; `waves` is the workgroup size in waves.
@@ -86,10 +87,11 @@ hipError_t launch_reshape_and_cache(const void* k, const void* v, void* k_cache,
                                     bool hnd, int32_t elem_bytes, hipStream_t stream);
 
 // KV write into fp8 e4m3 caches from fp16 (bf16 = false) or bf16 rows.
+// Each element is multiplied by its tensor's inverse scale (k_inv, v_inv) before it is encoded.
 hipError_t launch_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void* v_cache,
                                          const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,
                                          int32_t head_dim, int32_t num_blocks, int32_t block_size, bool hnd,
-                                         bool bf16, hipStream_t stream);
+                                         bool bf16, float k_inv, float v_inv, hipStream_t stream);
 
 // mode: 0 = gather (dst index i), 1 = copy (dst ids), 2 = zero (no source)
 hipError_t launch_block_op(int mode, const void* src_k, const void* src_v, void* dst_k, void* dst_v,

@@ -61,13 +61,14 @@ __device__ __forceinline__ float widen(uint32_t h) {
 }
 
 // KV write into fp8 caches: as reshape_and_cache, but each lane reads EPL
-// consecutive 16-bit elements of a row and writes their EPL codes.
+// consecutive 16-bit elements of a row and writes their EPL codes, each element
+// first multiplied by its tensor's inverse scale (one fp32 rounding; 1 leaves it as is).
 template <int EPL, bool BF16>
 __global__ __launch_bounds__(256) void reshape_and_cache_e4m3_kernel(
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint8_t* __restrict__ k_cache,
     uint8_t* __restrict__ v_cache, const int64_t* __restrict__ slot_mapping, int64_t total_groups,
     int32_t groups_per_row, int32_t groups_per_head, int64_t num_slots, int32_t block_size, int32_t num_kv_heads,
-    int32_t head_dim, int32_t hnd) {
+    int32_t head_dim, int32_t hnd, float k_inv, float v_inv) {
   typedef typename VecOf<2 * EPL>::T In;
   typedef typename VecOf<EPL>::T Out;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -90,6 +91,7 @@ __global__ __launch_bounds__(256) void reshape_and_cache_e4m3_kernel(
   }
   const uint16_t* srcs[2] = {k + src, v + src};
   uint8_t* dsts[2] = {k_cache + dst, v_cache + dst};
+  const float invs[2] = {k_inv, v_inv};
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const In in = *reinterpret_cast<const In*>(srcs[t]);
@@ -97,7 +99,7 @@ __global__ __launch_bounds__(256) void reshape_and_cache_e4m3_kernel(
     __builtin_memcpy(h, &in, sizeof(In));
     uint8_t c[EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) c[e] = (uint8_t)e4m3_code(widen<BF16>(h[e]));
+    for (int e = 0; e < EPL; ++e) c[e] = (uint8_t)e4m3_code(widen<BF16>(h[e]) * invs[t]);  // exact at 1
     Out out;
     __builtin_memcpy(&out, c, sizeof(Out));
     *reinterpret_cast<Out*>(dsts[t]) = out;
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(256) void reshape_and_cache_e4m3_kernel(
 hipError_t launch_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void* v_cache,
                                          const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads,
                                          int32_t head_dim, int32_t num_blocks, int32_t block_size, bool hnd,
-                                         bool bf16, hipStream_t stream) {
+                                         bool bf16, float k_inv, float v_inv, hipStream_t stream) {
   const int epl = (head_dim % 8 == 0) ? 8 : (head_dim % 4 == 0) ? 4 : (head_dim % 2 == 0) ? 2 : 1;
   const int32_t groups_per_head = head_dim / epl;
   const int32_t groups_per_row = groups_per_head * num_kv_heads;
@@ -124,11 +126,11 @@ hipError_t launch_reshape_and_cache_e4m3(const void* k, const void* v, void* k_c
     if (bf16)                                                                                           \
       hipLaunchKernelGGL((reshape_and_cache_e4m3_kernel<E, true>), grid, block, 0, stream, kb, vb, kc, vc, \
                          slot_mapping, total, groups_per_row, groups_per_head, num_slots, block_size,      \
-                         num_kv_heads, head_dim, (int32_t)hnd);                                         \
+                         num_kv_heads, head_dim, (int32_t)hnd, k_inv, v_inv);                           \
     else                                                                                                \
       hipLaunchKernelGGL((reshape_and_cache_e4m3_kernel<E, false>), grid, block, 0, stream, kb, vb, kc, vc, \
                          slot_mapping, total, groups_per_row, groups_per_head, num_slots, block_size,      \
-                         num_kv_heads, head_dim, (int32_t)hnd);                                         \
+                         num_kv_heads, head_dim, (int32_t)hnd, k_inv, v_inv);                           \
   } while (0)
   switch (epl) {
     case 8: AYK_E4M3_STORE(8); break;

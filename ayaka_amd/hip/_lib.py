@@ -17,7 +17,7 @@ from ayaka_amd.errors import BackendError, CapabilityError
 __all__ = ["ABI_VERSION", "EXPORTS", "LIB_PATH", "check", "lib"]
 
 LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libayaka_hip.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -35,24 +35,24 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
     ),
     "ayk_reshape_and_cache_e4m3": (
         ctypes.c_int,
-        [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _P],
+        [_P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32, _P],
     ),
     "ayk_paged_attention_v1": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _P, _P,
-         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P],
+         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32, _F32, _I32, _P],
     ),
     "ayk_paged_attention_v2_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
     "ayk_paged_attention_v2": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _P, _P,
-         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
+         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32, _F32,
          _I32, _I32, _P, _I32, _P, _P, _SZ, _P, _I32, _P],
     ),
     "ayk_paged_attention_v2_static": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _P, _P,
-         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
+         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32, _F32,
          _I32, _I32, _P, _I32, _P, _I32, _P],
     ),
     "ayk_paged_attention_v2_static_counters": (ctypes.c_int, [ctypes.POINTER(_P), ctypes.POINTER(_I64)]),
@@ -60,12 +60,12 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
     "ayk_paged_prefill": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I32, _I32, _I32,
-         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P, _SZ, _P],
+         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32, _F32, _I32, _P, _SZ, _P],
     ),
     "ayk_paged_attention_windows": (
         ctypes.c_int,
         [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P,
-         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _I32, _P, _SZ, _P],
+         _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _F32, _F32, _F32, _I32, _P, _SZ, _P],
     ),
     "ayk_split_model": (ctypes.c_int, [_P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _P, _P]),
     "ayk_work_list": (ctypes.c_int64, [_P, _I32, _I32, _P]),

@@ -52,7 +52,7 @@ from ayaka_amd.hip._checks import (
     require_like,
     stream_handle,
 )
-from ayaka_amd.kvcache import FP8_E4M3_CODEC, KVBuffers
+from ayaka_amd.kvcache import FP8_E4M3_CODEC, KVBuffers, codec_scales
 
 __all__ = [
     "PARTITION_SIZE",
@@ -1014,7 +1014,7 @@ def attend_with(
             meta.positions.data_ptr(), tiles.data_ptr(), tiles.numel() // 4, pairs, n_rows, heads, kv_heads,
             buffers.head_dim, buffers.num_blocks, block_size, table.shape[1],
             _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype], _kv_code(buffers, q.dtype),
-            float(scale), size, scratch.data_ptr() if scratch is not None else 0,
+            float(scale), *codec_scales(buffers.codec), size, scratch.data_ptr() if scratch is not None else 0,
             scratch.numel() if scratch is not None else 0,
         ), stream, device, scratch is not None, _record)
         return
@@ -1043,6 +1043,7 @@ def attend_with(
         _DTYPE_CODES[q.dtype],
         _kv_code(buffers, q.dtype),
         float(scale),
+        *codec_scales(buffers.codec),
     )
     staged = None
     if partitions is None:
@@ -1134,7 +1135,8 @@ def _attend_windows(op: str, q: torch.Tensor, buffers: KVBuffers, meta: Attentio
         table.stride(0), meta.kv_lengths.data_ptr(), meta.request_of_row.data_ptr(), meta.positions.data_ptr(),
         tiles.data_ptr(), tiles.numel() // 4, n_rows, heads, kv_heads, buffers.head_dim, buffers.num_blocks,
         buffers.block_size, table.shape[1], _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[q.dtype],
-        _kv_code(buffers, q.dtype), float(scale), size, scratch.data_ptr() if scratch is not None else 0,
+        _kv_code(buffers, q.dtype), float(scale), *codec_scales(buffers.codec), size,
+        scratch.data_ptr() if scratch is not None else 0,
         scratch.numel() if scratch is not None else 0,
     ), stream, device, scratch is not None, record)
 

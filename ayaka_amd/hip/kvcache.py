@@ -25,7 +25,7 @@ from ayaka_amd.hip._checks import (
     require_like,
     stream_handle,
 )
-from ayaka_amd.kvcache import FP8_E4M3_CODEC, KVBuffers
+from ayaka_amd.kvcache import FP8_E4M3_CODEC, KVBuffers, codec_scales
 
 __all__ = ["copy_blocks", "gather", "layout", "store", "zero_blocks"]
 
@@ -101,7 +101,7 @@ def _store(k: torch.Tensor, v: torch.Tensor, buffers: KVBuffers, meta: Attention
         fn = _lib.lib().ayk_reshape_and_cache_e4m3
         args = (k.data_ptr(), v.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), slots.data_ptr(), rows,
                 buffers.num_kv_heads, buffers.head_dim, buffers.num_blocks, buffers.block_size,
-                _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[dtype])
+                _LAYOUT_CODES[KVLayoutKind(buffers.layout)], _DTYPE_CODES[dtype], *codec_scales(buffers.codec))
     else:
         fn = _lib.lib().ayk_reshape_and_cache
         args = (k.data_ptr(), v.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), slots.data_ptr(), rows,

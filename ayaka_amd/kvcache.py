@@ -15,6 +15,8 @@ Restates the reference's layout definition (``python/ayaka/ops/kvcache.py:1-38``
   tensors are ``torch.float8_e4m3fn``, one byte per element, holding what
   torch's cast to that type gives (round to nearest even; a magnitude that
   rounds above 448 becomes NaN); readers decode it exactly to the compute dtype.
+  A layer may carry a key and a value scale (:func:`fp8_e4m3_codec`): the codes
+  are then those of ``x / scale`` and readers multiply by the scale.
 
 Importing this module does not import torch.
 """
@@ -30,11 +32,56 @@ if TYPE_CHECKING:
 
     from ayaka_amd.attention import AttentionMetadata
 
-__all__ = ["FP8_E4M3_CODEC", "RAW_CODEC", "KVBuffers", "KVCacheOps"]
+__all__ = ["FP8_E4M3_CODEC", "RAW_CODEC", "KVBuffers", "KVCacheOps", "ScaledFp8Codec", "codec_scales", "fp8_e4m3_codec"]
 
 RAW_CODEC = "raw"
 #: Keys and values as OCP fp8 e4m3 codes (``torch.float8_e4m3fn``), no scale.
 FP8_E4M3_CODEC = "fp8_e4m3"
+
+
+class ScaledFp8Codec(str):
+    """The ``"fp8_e4m3"`` codec of one layer with a key scale and a value scale.
+
+    It is the string ``"fp8_e4m3"`` (equal to :data:`FP8_E4M3_CODEC`, so code that compares
+    codecs keeps working) carrying ``k_scale`` and ``v_scale``: the cache holds the codes of
+    ``k * (1 / k_scale)`` and ``v * (1 / v_scale)`` (the inverse rounded once to float32, the
+    product once to float32, then encoded), and readers decode ``code * scale``. A layer whose
+    keys reach 4,000 stores them finite with ``k_scale = 4000 / 448``. Scales of 1 are the
+    unscaled codec, bit for bit. Make one with :func:`fp8_e4m3_codec`.
+    """
+
+    k_scale: float
+    v_scale: float
+
+    def __new__(cls, k_scale: float = 1.0, v_scale: float = 1.0) -> "ScaledFp8Codec":
+        import math
+        import struct
+
+        scales = []
+        for name, value in (("k_scale", k_scale), ("v_scale", v_scale)):
+            value = struct.unpack("f", struct.pack("f", float(value)))[0]  # as the library reads it
+            if not (math.isfinite(value) and value > 0.0):
+                raise ValueError(f"{name} must be a positive finite float32, got {value!r}")
+            scales.append(value)
+        codec = super().__new__(cls, FP8_E4M3_CODEC)
+        codec.k_scale, codec.v_scale = scales
+        return codec
+
+    def __repr__(self) -> str:
+        return f"fp8_e4m3_codec(k_scale={self.k_scale!r}, v_scale={self.v_scale!r})"
+
+    def __reduce__(self):
+        return (ScaledFp8Codec, (self.k_scale, self.v_scale))
+
+
+def fp8_e4m3_codec(k_scale: float = 1.0, v_scale: float = 1.0) -> ScaledFp8Codec:
+    """The ``"fp8_e4m3"`` codec with a layer's key and value scales (see :class:`ScaledFp8Codec`)."""
+    return ScaledFp8Codec(k_scale, v_scale)
+
+
+def codec_scales(codec: str) -> tuple[float, float]:
+    """``(k_scale, v_scale)`` of a codec: its own for a :class:`ScaledFp8Codec`, else (1, 1)."""
+    return (getattr(codec, "k_scale", 1.0), getattr(codec, "v_scale", 1.0))
 
 
 class _KVBuffers(NamedTuple):

@@ -90,10 +90,16 @@ int ayk_reshape_and_cache(const void* k, const void* v, void* k_cache, void* v_c
  * The reference defines the codec field and only the "raw" codec
  * (python/ayaka/ops/kvcache.py:35-36, :54-55); this is KVCacheOps.store
  * (python/ayaka/ops/backends/torch/kvcache.py:65-80) for a quantised one.
+ * k_scale and v_scale (positive, finite; 1 for none) are the layer's scales: an
+ * element x is stored as the code of x * (1 / scale), the inverse rounded once to
+ * fp32 and the product rounded once to fp32 before the encoding, so a cache of
+ * keys up to 448 * k_scale stays finite. The attention entry points take the same
+ * scales and read code * scale.
  */
 int ayk_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void* v_cache,
                                const int64_t* slot_mapping, int64_t n_rows, int32_t num_kv_heads, int32_t head_dim,
                                int32_t num_blocks, int32_t block_size, int32_t layout, int32_t src_dtype,
+                               float k_scale, float v_scale,
                                void* stream);
 
 /*
@@ -116,8 +122,13 @@ int ayk_reshape_and_cache_e4m3(const void* k, const void* v, void* k_cache, void
  * head_dim must be 64, 128 or 256 and block_size in [1, 65536]. `dtype` is
  * the type of q and out; `kv_dtype` that of the caches: the same, or
  * AYK_DTYPE_FP8_E4M3 (decoded exactly to `dtype` as it is read; matrix-core
- * kernel only). `flags` (AYK_FLAG_QK_*) forces one q.k implementation; 0 picks
- * by group size (matrix cores from 3 query heads per key/value head).
+ * kernel only). k_scale and v_scale (positive, finite; 1 for an unscaled cache,
+ * which leaves every result bit as without them) say the cache holds keys / k_scale
+ * and values / v_scale: a score is scale * k_scale * q.k over the stored keys (one
+ * fp32 product for the two scales) and each normalised output is multiplied by
+ * v_scale before rounding. The other attention entry points take them the same way.
+ * `flags` (AYK_FLAG_QK_*) forces one q.k implementation; 0 picks by group size
+ * (matrix cores from 3 query heads per key/value head).
  */
 int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const void* v_cache,
                            const int32_t* block_table, int64_t table_stride,
@@ -125,7 +136,8 @@ int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const 
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           int32_t kv_dtype, float scale, int32_t flags, void* stream);
+                           int32_t kv_dtype, float scale, float k_scale, float v_scale, int32_t flags,
+                           void* stream);
 
 /* Bytes of scratch ayk_paged_attention_v2 needs for these sizes. */
 size_t ayk_paged_attention_v2_workspace_bytes(int32_t n_rows, int32_t num_heads, int32_t head_dim,
@@ -177,7 +189,8 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
                            const int32_t* positions, int32_t n_rows, int32_t num_heads,
                            int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                            int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                           int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
+                           int32_t kv_dtype, float scale, float k_scale, float v_scale, int32_t partition_size,
+                           int32_t max_partitions,
                            const int32_t* work_items, int32_t n_work_items, const int32_t* staged,
                            void* workspace, size_t workspace_bytes, uint32_t* arrivals, int32_t flags,
                            void* stream);
@@ -207,7 +220,8 @@ int ayk_paged_attention_v2_static(void* out, const void* q, const void* k_cache,
                                   const int32_t* request_of_row, const int32_t* positions, int32_t n_rows,
                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t num_blocks,
                                   int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                                  int32_t kv_dtype, float scale, int32_t partition_size, int32_t max_partitions,
+                                  int32_t kv_dtype, float scale, float k_scale, float v_scale, int32_t partition_size,
+                           int32_t max_partitions,
                                   const int32_t* work_items, int32_t n_work_items, const int32_t* staged,
                                   int32_t flags, void* stream);
 
@@ -256,7 +270,7 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
                       const int32_t* request_of_row, const int32_t* positions, const int32_t* tiles,
                       int32_t n_tiles, int32_t tile_pairs, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                       int32_t num_blocks, int32_t block_size, int32_t max_blocks, int32_t layout, int32_t dtype,
-                      int32_t kv_dtype, float scale, int32_t partition_size, void* workspace,
+                      int32_t kv_dtype, float scale, float k_scale, float v_scale, int32_t partition_size, void* workspace,
                       size_t workspace_bytes, void* stream);
 
 /*
@@ -282,7 +296,8 @@ int ayk_paged_attention_windows(void* out, const void* q, const void* k_cache, c
                                 const int32_t* request_of_row, const int32_t* positions, const int32_t* tiles,
                                 int32_t n_tiles, int32_t n_rows, int32_t num_heads, int32_t num_kv_heads,
                                 int32_t head_dim, int32_t num_blocks, int32_t block_size, int32_t max_blocks,
-                                int32_t layout, int32_t dtype, int32_t kv_dtype, float scale, int32_t partition_size,
+                                int32_t layout, int32_t dtype, int32_t kv_dtype, float scale, float k_scale, float v_scale,
+                                int32_t partition_size,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*

@@ -84,6 +84,15 @@ def f32_to_e4m3(values: np.ndarray) -> np.ndarray:
     return (code.astype(np.uint32) | sign).astype(np.uint8)
 
 
+def f32_to_e4m3_scaled(values: np.ndarray, scale: float) -> np.ndarray:
+    """Encode ``values / scale`` as a scaled fp8 e4m3 cache stores it: the inverse scale
+    rounded once to float32, the product ``float32(x) * inverse`` rounded once to float32, then
+    :func:`f32_to_e4m3`. Scale 1 is :func:`f32_to_e4m3` itself. Follows the codec this build adds
+    beside the reference's only ``"raw"`` one (``python/ayaka/ops/kvcache.py:35-36``)."""
+    inverse = np.float32(1.0) / np.float32(scale)
+    return f32_to_e4m3(np.ascontiguousarray(values, dtype=np.float32) * inverse)
+
+
 def half_ulp(values: np.ndarray, dtype: str) -> np.ndarray:
     """Half a unit in the last place of ``dtype`` at each |value| (what one rounding can cost)."""
     mantissa = {"bf16": 7, "fp16": 10}[dtype]

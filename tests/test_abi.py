@@ -47,7 +47,8 @@ def test_workspace_size() -> None:
 def _v1(lib: ctypes.CDLL, **kw: object) -> int:
     args = dict(out=1, q=1, k=1, v=1, table=1, stride=4, lengths=1, ror=None, pos=None, n_rows=1,
                 heads=8, kv_heads=2, head_dim=128, num_blocks=10, block_size=16, max_blocks=4,
-                layout=0, dtype=1, kv_dtype=1, scale=ctypes.c_float(1.0), flags=0, stream=None)
+                layout=0, dtype=1, kv_dtype=1, scale=ctypes.c_float(1.0), k_scale=1.0, v_scale=1.0, flags=0,
+                stream=None)
     args.update(kw)
     return lib.ayk_paged_attention_v1(*args.values())
 
@@ -80,7 +81,7 @@ def test_bad_arguments_are_refused_without_a_launch(changes: dict, code: int, me
 
 def test_v2_and_store_refusals() -> None:
     lib = _lib.lib()
-    base = [1, 1, 1, 1, 1, 4, 1, None, None, 1, 8, 2, 128, 10, 16, 4, 0, 1, 1, ctypes.c_float(1.0)]
+    base = [1, 1, 1, 1, 1, 4, 1, None, None, 1, 8, 2, 128, 10, 16, 4, 0, 1, 1, ctypes.c_float(1.0), 1.0, 1.0]
     assert lib.ayk_paged_attention_v2(*base, 100, 4, None, 0, None, 1, 1 << 20, None, 0, None) == 1
     assert b"multiple of 64" in lib.ayk_last_error()
     assert lib.ayk_paged_attention_v2(*base, 512, 4, None, 0, None, 1, 16, None, 0, None) == 4
@@ -95,22 +96,26 @@ def test_v2_and_store_refusals() -> None:
     # quarter; a partition size that is not a multiple of 64; the partitions' workspace
     def prefill(tile_pairs: int, size: int = 0, workspace: int = 0) -> int:
         return lib.ayk_paged_prefill(1, 1, 1, 1, 1, 4, 1, 1, 1, 1, 2, tile_pairs, 3, 8, 2, 128, 10, 16, 4, 0, 1, 1,
-                                     ctypes.c_float(1.0), size, 1, workspace, None)
+                                     ctypes.c_float(1.0), 1.0, 1.0, size, 1, workspace, None)
     assert prefill(100) == 1 and b"tile_pairs 100 is not 128, 64 or 32" in lib.ayk_last_error()
     assert prefill(16) == 1
     # the window entry: positions required; more than 16 query heads per key/value head; a
     # partition size that is not a multiple of 64
     def windows(heads: int, positions: object = 1, size: int = 0) -> int:
         return lib.ayk_paged_attention_windows(1, 1, 1, 1, 1, 4, 1, 1, positions, 1, 2, 3, heads, 1, 128, 10, 16, 4,
-                                               0, 1, 1, ctypes.c_float(1.0), size, None, 0, None)
+                                               0, 1, 1, ctypes.c_float(1.0), 1.0, 1.0, size, None, 0, None)
     assert windows(8, positions=None) == 1 and b"positions are required" in lib.ayk_last_error()
     assert windows(32) == 2 and b"exceed a window's 16 columns" in lib.ayk_last_error()
     assert windows(8, size=96) == 1 and b"multiple of 64" in lib.ayk_last_error()
     assert prefill(32, size=96) == 1 and b"multiple of 64" in lib.ayk_last_error()
     assert prefill(64, size=64, workspace=16) == 4 and b"workspace" in lib.ayk_last_error()
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 3, None) == 2
-    assert lib.ayk_reshape_and_cache_e4m3(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 2, None) == 2
+    assert lib.ayk_reshape_and_cache_e4m3(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 2, 1.0, 1.0, None) == 2
     assert b"src_dtype 2" in lib.ayk_last_error()
-    assert lib.ayk_reshape_and_cache_e4m3(1, 1, 1, 1, 1, 0, 2, 64, 10, 16, 0, 1, None) == 0
+    assert lib.ayk_reshape_and_cache_e4m3(1, 1, 1, 1, 1, 0, 2, 64, 10, 16, 0, 1, 1.0, 1.0, None) == 0
+    for k_scale, v_scale in ((0.0, 1.0), (1.0, -2.0), (float("inf"), 1.0), (1.0, float("nan"))):
+        assert lib.ayk_reshape_and_cache_e4m3(1, 1, 1, 1, 1, 3, 2, 64, 10, 16, 0, 1, k_scale, v_scale, None) == 1
+        assert b"positive and finite" in lib.ayk_last_error()
+        assert _v1(lib, k_scale=k_scale, v_scale=v_scale) == 1 and b"positive and finite" in lib.ayk_last_error()
     assert lib.ayk_reshape_and_cache(1, 1, 1, 1, 1, 0, 2, 64, 10, 16, 0, 2, None) == 0
     assert lib.ayk_zero_blocks(1, 1, 1, 0, 2, 0, 64, None) == 1

@@ -523,6 +523,112 @@ def test_fp8_attention_matches_the_oracle_on_decoded_values(dtype: str, layout: 
     assert counters_are_clear()
 
 
+SCALED_STEPS = [(1, 16), (1, 0), (1, 1300), (7, 600), (2, 33), (3, 1100)]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(8, 2, 128), (32, 8, 64)])
+def test_scaled_fp8_cache_holds_large_keys(dtype: str, layout: str, heads: int, kv_heads: int,
+                                           head_dim: int) -> None:
+    # a layer whose keys reach 4,000 (and values 0.01): stored with k_scale = 4000 / 448 and
+    # v_scale = 0.01 / 448 they stay finite; the KV write is bit-exact against the oracle's
+    # scaled encoder, and every launch's output matches the float64 oracle on code * scale
+    from ayaka_amd.kvcache import fp8_e4m3_codec
+    from oracle.numerics import f32_to_e4m3_scaled
+
+    s = build_scenario(SCALED_STEPS, dtype=dtype, layout=layout, heads=heads, kv_heads=kv_heads,
+                       head_dim=head_dim, block_size=16, mode="mixed", seed=91)
+    k_scale, v_scale = 4000.0 / 448.0, 0.01 / 448.0
+    codec = fp8_e4m3_codec(k_scale, v_scale)
+    k_scale, v_scale = codec.k_scale, codec.v_scale
+    rng = np.random.default_rng(92)
+    big_k = np.clip(rng.standard_normal(s.k.shape) * 1500.0, -4000, 4000)
+    small_v = s.v * 0.003
+    kc = f32_to_e4m3_scaled(bits_to_f32(f32_to_bits(big_k.astype(np.float32), dtype), dtype), k_scale)
+    vc = f32_to_e4m3_scaled(bits_to_f32(f32_to_bits(small_v.astype(np.float32), dtype), dtype), v_scale)
+    kind = KVLayoutKind.NHD if layout == "nhd" else KVLayoutKind.HND
+    buffers = KVBuffers(torch.from_numpy(kc).view(torch.float8_e4m3fn).to(DEV),
+                        torch.from_numpy(vc).view(torch.float8_e4m3fn).to(DEV), kind, codec)
+    meta = plan_scenario(s)
+    # the step's own rows written through the library: large keys, small values
+    n = len(s.plan["slot_mapping"])
+    rows_k = np.clip(rng.standard_normal((n, kv_heads, head_dim)) * 1500.0, -4000, 4000).astype(np.float32)
+    rows_k.reshape(-1)[:4] = [4000.0, -4000.0, 3999.0, 0.5]
+    rows_v = (rng.standard_normal((n, kv_heads, head_dim)) * 0.003).astype(np.float32)
+    bits_k, bits_v = f32_to_bits(rows_k, dtype), f32_to_bits(rows_v, dtype)
+    hip_kvcache.store(to_device(bits_k, dtype), to_device(bits_v, dtype), buffers, meta)
+    torch.cuda.synchronize()
+    paged.store(kc, vc, f32_to_e4m3_scaled(bits_to_f32(bits_k, dtype), k_scale),
+                f32_to_e4m3_scaled(bits_to_f32(bits_v, dtype), v_scale), s.plan["slot_mapping"], layout)
+    assert np.array_equal(buffers.k.view(torch.uint8).cpu().numpy(), kc)
+    assert np.array_equal(buffers.v.view(torch.uint8).cpu().numpy(), vc)
+    real = s.plan["slot_mapping"] != 0
+    stored = e4m3_to_f32(paged.nhd(kc, layout).reshape(-1, kv_heads, head_dim)[s.plan["slot_mapping"][real]])
+    assert np.isfinite(stored).all() and np.abs(stored * k_scale).max() > 3000  # large keys kept finite
+    q = to_device(f32_to_bits((s.q * 0.01).astype(np.float32), dtype), dtype)  # scores of a sane range
+    expected = paged.attention(bits_to_f32(f32_to_bits((s.q * 0.01).astype(np.float32), dtype), dtype),
+                               e4m3_to_f32(kc).astype(np.float64) * k_scale,
+                               e4m3_to_f32(vc).astype(np.float64) * v_scale, s.table, np.asarray(s.lengths),
+                               scale=s.scale, layout=layout, request_of_row=s.plan["request_of_row"],
+                               positions=s.plan["positions"], precision=np.float64)
+    full = hip_attention.PREFILL_PAIRS[head_dim]
+    launches = [("multi-row", dict(partitions=None, prefill=True, window=False)),
+                ("multi-row/256/quarter", dict(partitions=None, partition_size=256, prefill=True, tile_pairs=full // 4)),
+                ("per-row v1", dict(partitions=0, prefill=False)),
+                ("per-row v2/in-kernel", dict(partitions=6, partition_size=256, merge="in-kernel", prefill=False)),
+                ("per-row v2/reduce-kernel", dict(partitions=6, partition_size=256, merge="reduce-kernel",
+                                                  prefill=False)),
+                ("auto", dict(partitions=None))]
+    for label, launch in launches:
+        out = torch.full_like(q, 7.0)
+        hip_attention.attend_with(q, buffers, meta, out, scale=s.scale, **launch)
+        torch.cuda.synchronize()
+        assert_parity(out, expected, dtype, f"scaled fp8 {label}")
+    # decode rows of the same caches: v1, v2 and the window launch
+    decode = build_scenario([(1, n) for n in s.lengths], dtype=dtype, layout=layout, heads=heads, kv_heads=kv_heads,
+                            head_dim=head_dim, block_size=16, mode="decode", seed=93)
+    decode.table = s.table
+    dmeta = plan_scenario(decode)
+    dq = to_device(f32_to_bits((decode.q * 0.01).astype(np.float32), dtype), dtype)
+    dexpected = paged.attention(bits_to_f32(f32_to_bits((decode.q * 0.01).astype(np.float32), dtype), dtype),
+                                e4m3_to_f32(kc).astype(np.float64) * k_scale,
+                                e4m3_to_f32(vc).astype(np.float64) * v_scale, s.table, np.asarray(s.lengths),
+                                scale=s.scale, layout=layout, precision=np.float64)
+    for label, launch in [("v1", dict(partitions=0)), ("v1/8 waves", dict(partitions=0, waves=8)),
+                          ("v2", dict(partitions=11, partition_size=128)), ("auto", dict(partitions=None))]:
+        out = torch.full_like(dq, 7.0)
+        hip_attention.attend_with(dq, buffers, dmeta, out, scale=s.scale, **launch)
+        torch.cuda.synchronize()
+        assert_parity(out, dexpected, dtype, f"scaled fp8 decode {label}")
+
+
+def test_unit_scales_are_the_unscaled_codec_bit_for_bit() -> None:
+    # fp8_e4m3_codec(1, 1) stores and reads exactly as the plain codec
+    from ayaka_amd.kvcache import fp8_e4m3_codec
+
+    s = build_scenario([(1, 700), (1, 33), (40, 300)], heads=8, kv_heads=2, head_dim=128, block_size=16,
+                       mode="mixed", seed=94)
+    plain, _, _ = fp8_buffers(s)
+    unit = KVBuffers(plain.k.clone(), plain.v.clone(), plain.layout, fp8_e4m3_codec(1.0, 1.0))
+    meta = plan_scenario(s)
+    rng = np.random.default_rng(95)
+    n = len(s.plan["slot_mapping"])
+    rows = to_device(f32_to_bits((rng.standard_normal((2, n, 2, 128)) * 50).astype(np.float32), "bf16"), "bf16")
+    for buffers in (plain, unit):
+        hip_kvcache.store(rows[0], rows[1], buffers, meta)
+    q = to_device(s.q_bits, "bf16")
+    outs = []
+    for buffers in (plain, unit):
+        out = torch.full_like(q, 7.0)
+        hip_attention.attend(q, buffers, meta, out, scale=s.scale)
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(plain.k.view(torch.uint8), unit.k.view(torch.uint8))
+    assert torch.equal(plain.v.view(torch.uint8), unit.v.view(torch.uint8))
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+
+
 def counters_are_clear() -> bool:
     return all(int(c.abs().max()) == 0 for c in hip_attention._counters.values())
 
@@ -999,13 +1105,13 @@ def test_c_abi_direct_call() -> None:
     stream = torch.cuda.current_stream().cuda_stream
     rc = lib.ayk_paged_attention_v1(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
                                     table.shape[1], lengths.data_ptr(), None, None, 3, 8, 2, 128,
-                                    k.shape[0], 16, table.shape[1], 0, 1, 1, ctypes.c_float(s.scale), 0, stream)
+                                    k.shape[0], 16, table.shape[1], 0, 1, 1, ctypes.c_float(s.scale), 1.0, 1.0, 0, stream)
     assert rc == 0, lib.ayk_last_error()
     torch.cuda.synchronize()
     assert_parity(out, s.expected(np.float64), "bf16", "abi")
     rc = lib.ayk_paged_attention_v1(out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
                                     table.shape[1], lengths.data_ptr(), None, None, 3, 8, 2, 96,
-                                    k.shape[0], 16, table.shape[1], 0, 1, 1, ctypes.c_float(1.0), 0, stream)
+                                    k.shape[0], 16, table.shape[1], 0, 1, 1, ctypes.c_float(1.0), 1.0, 1.0, 0, stream)
     assert rc == 2 and b"head_dim 96" in lib.ayk_last_error()
 
 
@@ -1031,7 +1137,7 @@ def test_c_abi_v2_follows_the_staged_split(merge_flag: int, heads: int) -> None:
     scratch = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
     arrivals = torch.zeros(1024, dtype=torch.int32, device=DEV)
     common = (q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), width, lengths.data_ptr(), None, None,
-              n_rows, heads, 2, 128, k.shape[0], 16, width, 0, 1, 1, ctypes.c_float(s.scale))
+              n_rows, heads, 2, 128, k.shape[0], 16, width, 0, 1, 1, ctypes.c_float(s.scale), 1.0, 1.0)
     staged = torch.zeros(2 + n_rows + 2 * capacity, dtype=torch.int32, device=DEV)
     work = 2 + n_rows
     for size in (256, 128, 704):

@@ -103,7 +103,7 @@ def _common(step: Step, heads: int, rows: int, request_of_row, positions) -> tup
     kv_dtype = 2 if step.kv8 else dtype
     return (FAKE, FAKE, FAKE, FAKE, _ptr(step.table), step.width, _ptr(step.lengths), _ptr(request_of_row),
             _ptr(positions), rows, heads, step.kv_heads, step.head_dim, step.num_blocks, step.block_size,
-            step.width, step.layout, dtype, kv_dtype, ctypes.c_float(0.125))
+            step.width, step.layout, dtype, kv_dtype, ctypes.c_float(0.125), 1.0, 1.0)
 
 
 def walk_v1(step: Step, heads: int, flags: int) -> np.ndarray:

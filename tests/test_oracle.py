@@ -86,6 +86,43 @@ def test_e4m3_encoding_matches_torch_on_float32_and_the_rounding_edges() -> None
     assert np.array_equal(e4m3_to_f32(f32_to_e4m3(finite)), finite)
 
 
+def test_scaled_e4m3_encoding_matches_torch() -> None:
+    # codes of float32(x) * float32(1 / scale), as torch's cast of that float32 product gives
+    # them; scale 1 is the unscaled encoder; a power-of-two scale shifts the code's exponent only
+    from oracle.numerics import f32_to_e4m3_scaled
+
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal(50_000) * np.exp2(rng.uniform(-12, 13, 50_000))).astype(np.float32)
+    for scale in (1.0, 8.928571, 0.37, 4096.0, 2.0 ** -5):
+        inverse = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(scale, dtype=torch.float32)
+        want = (torch.from_numpy(x) * inverse).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        got = f32_to_e4m3_scaled(x, scale)
+        assert np.array_equal(got, want), scale
+    assert np.array_equal(f32_to_e4m3_scaled(x, 1.0), f32_to_e4m3(x))
+    small = x[np.abs(x) < 100]
+    shifted = e4m3_to_f32(f32_to_e4m3_scaled(small, 4.0)) * 4.0
+    plain = e4m3_to_f32(f32_to_e4m3(small))
+    normal = np.abs(small) >= 4 * 2.0 ** -6  # away from the subnormal range of either encoding
+    assert np.array_equal(shifted[normal], plain[normal])
+
+
+def test_scaled_codec_is_the_fp8_codec_with_scales() -> None:
+    import pickle
+
+    from ayaka_amd.kvcache import FP8_E4M3_CODEC, codec_scales, fp8_e4m3_codec
+
+    codec = fp8_e4m3_codec(k_scale=4000 / 448, v_scale=0.1)
+    assert codec == FP8_E4M3_CODEC and hash(codec) == hash(FP8_E4M3_CODEC)
+    assert {FP8_E4M3_CODEC: 1}[codec] == 1
+    k_scale, v_scale = codec_scales(codec)
+    assert k_scale == float(np.float32(4000 / 448)) and v_scale == float(np.float32(0.1))  # float32, as read
+    assert codec_scales(FP8_E4M3_CODEC) == (1.0, 1.0) and codec_scales("raw") == (1.0, 1.0)
+    assert codec_scales(pickle.loads(pickle.dumps(codec))) == (k_scale, v_scale)
+    for bad in (0.0, -1.0, float("inf"), float("nan"), 1e39):
+        with pytest.raises(ValueError):
+            fp8_e4m3_codec(k_scale=bad)
+
+
 def test_half_ulp_and_metrics_on_hand_computed_values() -> None:
     assert half_ulp(np.array([1.0]), "bf16")[0] == 2**-8
     assert half_ulp(np.array([3.0]), "bf16")[0] == 2**-7

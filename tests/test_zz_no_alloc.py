@@ -36,7 +36,7 @@ def _call(lib, static: bool, out, s, tensors, size: int, parts: int, work, n_wor
     width = table.shape[1]
     common = (out.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(), width,
               lengths.data_ptr(), None, None, len(s.lengths), s.heads, s.kv_heads, s.head_dim, k.shape[0],
-              s.block_size, width, 0, 1, 1, ctypes.c_float(s.scale), size, parts, work, n_work, staged)
+              s.block_size, width, 0, 1, 1, ctypes.c_float(s.scale), 1.0, 1.0, size, parts, work, n_work, staged)
     stream = torch.cuda.current_stream().cuda_stream
     if static:
         return lib.ayk_paged_attention_v2_static(*common, flags, stream)
@@ -157,5 +157,5 @@ def test_calls_beyond_the_static_scratch_are_refused() -> None:
     # 512 rows x 32 heads x 8 partitions x (128 + 2) floats = 68 MB of partials: refused, no launch
     assert lib.ayk_paged_attention_v2_workspace_bytes(512, 32, 128, 8) > STATIC_PARTIAL_BYTES
     rc = lib.ayk_paged_attention_v2_static(1, 1, 1, 1, 1, 8, 1, None, None, 512, 32, 8, 128, 100, 16, 8, 0, 1, 1,
-                                           ctypes.c_float(1.0), 64, 8, None, 0, None, 0, None)
+                                           ctypes.c_float(1.0), 1.0, 1.0, 64, 8, None, 0, None, 0, None)
     assert rc == 4 and b"static scratch" in lib.ayk_last_error()
