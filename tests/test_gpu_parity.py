@@ -531,15 +531,15 @@ SCALED_STEPS = [(1, 16), (1, 0), (1, 1300), (7, 600), (2, 33), (3, 1100)]
 @pytest.mark.parametrize("heads,kv_heads,head_dim", [(8, 2, 128), (32, 8, 64)])
 def test_scaled_fp8_cache_holds_large_keys(dtype: str, layout: str, heads: int, kv_heads: int,
                                            head_dim: int) -> None:
-    # a layer whose keys reach 4,000 (and values 0.01): stored with k_scale = 4000 / 448 and
-    # v_scale = 0.01 / 448 they stay finite; the KV write is bit-exact against the oracle's
+    # a layer whose keys reach 4,000 (and values 0.015): stored with k_scale = 4000 / 448 and
+    # v_scale = 0.02 / 448 they stay finite; the KV write is bit-exact against the oracle's
     # scaled encoder, and every launch's output matches the float64 oracle on code * scale
     from ayaka_amd.kvcache import fp8_e4m3_codec
     from oracle.numerics import f32_to_e4m3_scaled
 
     s = build_scenario(SCALED_STEPS, dtype=dtype, layout=layout, heads=heads, kv_heads=kv_heads,
                        head_dim=head_dim, block_size=16, mode="mixed", seed=91)
-    k_scale, v_scale = 4000.0 / 448.0, 0.01 / 448.0
+    k_scale, v_scale = 4000.0 / 448.0, 0.02 / 448.0
     codec = fp8_e4m3_codec(k_scale, v_scale)
     k_scale, v_scale = codec.k_scale, codec.v_scale
     rng = np.random.default_rng(92)
@@ -563,6 +563,12 @@ def test_scaled_fp8_cache_holds_large_keys(dtype: str, layout: str, heads: int, 
                 f32_to_e4m3_scaled(bits_to_f32(bits_v, dtype), v_scale), s.plan["slot_mapping"], layout)
     assert np.array_equal(buffers.k.view(torch.uint8).cpu().numpy(), kc)
     assert np.array_equal(buffers.v.view(torch.uint8).cpu().numpy(), vc)
+    context = np.zeros(kc.shape, dtype=bool)  # every cache element some context reads
+    context_nhd = paged.nhd(context, layout)
+    for r, n in enumerate(s.lengths):
+        for t in range(n):
+            context_nhd[s.table[r, t // 16], t % 16] = True
+    assert np.isfinite(e4m3_to_f32(kc)[context]).all() and np.isfinite(e4m3_to_f32(vc)[context]).all()
     real = s.plan["slot_mapping"] != 0
     stored = e4m3_to_f32(paged.nhd(kc, layout).reshape(-1, kv_heads, head_dim)[s.plan["slot_mapping"][real]])
     assert np.isfinite(stored).all() and np.abs(stored * k_scale).max() > 3000  # large keys kept finite
