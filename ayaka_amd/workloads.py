@@ -16,7 +16,9 @@ Five configurations, numbered as in the benchmark definition:
 
 Every configuration ends its step with the KV write of each sequence's newest
 ``new_tokens`` positions (``store``) followed by decode attention over all
-sequences. Blocks come from a seeded permutation of the pool (never block 0).
+sequences. Those slots are free before the step (never written, NaN) and lie in
+blocks drawn from a random permutation of the pool, so C5's "256 new tokens into
+random free slots" is its 256 sequences' newest tokens, scattered over the pool. Blocks come from a seeded permutation of the pool (never block 0).
 Every slot that is not part of a context holds NaN, so a kernel that reads past
 a length, an unused table entry or block 0 shows it. Lengths are drawn on the
 host from ``numpy.random.default_rng(1000 + index)``; tensors from a
