@@ -18,7 +18,7 @@ __all__ = ["FLAGS", "LIB_PATH", "build_library", "hipcc_command"]
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_DIR = PACKAGE_DIR.parent
 SOURCES = ("api.hip", "paged_attention.hip", "paged_attention_mfma.hip", "paged_prefill.hip", "kv_cache.hip",
-           "split_model.cpp", "kv_reach.hip")
+           "paged_attention_f32.hip", "split_model.cpp", "kv_reach.hip")
 LIB_PATH = PACKAGE_DIR / "lib" / "libayaka_hip.so"
 ARCH = "gfx950"
 

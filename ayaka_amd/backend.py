@@ -218,7 +218,7 @@ register_backend(
         families=frozenset(FAMILIES),
         platforms=frozenset({"linux"}),
         devices=frozenset({"cuda"}),  # ROCm torch names HIP devices "cuda"
-        dtypes=frozenset({DType.FP16, DType.BF16}),
+        dtypes=frozenset({DType.FP16, DType.BF16, DType.FP32}),
         graph_safe=frozenset(FAMILIES),
         multi_row_attention=True,
     ),

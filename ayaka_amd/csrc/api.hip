@@ -79,11 +79,11 @@ int prepare(const char* op, const AttnCall& c, ayk::AttnParams& p, int& heads_pe
   if (c.n_rows < 0) return fail(AYK_ERR_ARGUMENT, "%s: n_rows is negative (%d)", op, c.n_rows);
   if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
     return fail(AYK_ERR_UNSUPPORTED, "%s: head_dim %d is not one of 64, 128, 256", op, c.head_dim);
-  if (c.dtype != AYK_DTYPE_FP16 && c.dtype != AYK_DTYPE_BF16)
-    return fail(AYK_ERR_UNSUPPORTED, "%s: dtype %d is not fp16 (0) or bf16 (1)", op, c.dtype);
-  if (c.kv_dtype != c.dtype && c.kv_dtype != AYK_DTYPE_FP8_E4M3)
-    return fail(AYK_ERR_UNSUPPORTED, "%s: kv_dtype %d is neither the dtype (%d) nor fp8 e4m3 (2)", op, c.kv_dtype,
-                c.dtype);
+  if (c.dtype != AYK_DTYPE_FP16 && c.dtype != AYK_DTYPE_BF16 && c.dtype != AYK_DTYPE_FP32)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: dtype %d is not fp16 (0), bf16 (1) or fp32 (3)", op, c.dtype);
+  if (c.kv_dtype != c.dtype && (c.kv_dtype != AYK_DTYPE_FP8_E4M3 || c.dtype == AYK_DTYPE_FP32))
+    return fail(AYK_ERR_UNSUPPORTED, "%s: kv_dtype %d is neither the dtype (%d) nor fp8 e4m3 (2) under fp16/bf16", op,
+                c.kv_dtype, c.dtype);
   if (c.layout != AYK_LAYOUT_NHD && c.layout != AYK_LAYOUT_HND)
     return fail(AYK_ERR_UNSUPPORTED, "%s: layout %d is not NHD (0) or HND (1)", op, c.layout);
   if (c.num_kv_heads <= 0 || c.num_heads <= 0 || c.num_heads % c.num_kv_heads != 0)
@@ -215,6 +215,27 @@ int wave_split_for(const ayk::AttnParams& p, bool split, int32_t flags) {
 }
 
 // The q.k path and workgroup shape for a launch, then the kernel(s).
+// fp32 models: the VALU decode kernel, one wave per virtual head, partitions merged by its own
+// reduce kernel (no wave split, no single launch, no q.k choice).
+int launch_f32(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool split, int32_t flags,
+               void* stream) {
+  if (flags & ~(AYK_FLAG_PARTIALS_ONLY | AYK_FLAG_SEPARATE_REDUCE | AYK_FLAG_WAVES_1))
+    return fail(AYK_ERR_UNSUPPORTED, "%s: flags 0x%x: fp32 runs one kernel shape (partials only, a separate "
+                "reduce and one wave per head are the flags it takes)", op, flags);
+  ayk::AttnParams q = p;
+  q.wave_split = 1;
+  q.arrivals = nullptr;
+  if (ayk::walking()) {  // the host address walk: the launch's loads, no launch
+    ayk::walk_f32(q, head_dim, split);
+    return ok();
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t err = ayk::launch_attention_f32(q, head_dim, gc, split, s);
+  if (err == hipSuccess && split && !(flags & AYK_FLAG_PARTIALS_ONLY))
+    err = ayk::launch_partition_reduce_f32(q, head_dim, s);
+  return launched(err, op);
+}
+
 int launch(const char* op, const ayk::AttnParams& p, int head_dim, int gc, bool bf16, bool kv8, bool split,
            int32_t flags, void* stream) {
   if (flags & ~(AYK_FLAG_QK_DPP | AYK_FLAG_QK_MFMA | AYK_FLAG_PARTIALS_ONLY | AYK_FLAG_SEPARATE_REDUCE |
@@ -314,7 +335,7 @@ void* static_scratch(const char* op, void* stream) {
 
 extern "C" {
 
-int ayk_abi_version(void) { return 16; }
+int ayk_abi_version(void) { return 17; }
 
 int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 
@@ -384,6 +405,7 @@ int ayk_paged_attention_v1(void* out, const void* q, const void* k_cache, const 
   const int rc = prepare(op, c, p, gc);
   if (rc != AYK_OK) return rc;
   if (n_rows == 0) return ok();
+  if (dtype == AYK_DTYPE_FP32) return launch_f32(op, p, head_dim, gc, false, flags, stream);
   return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, kv_dtype == AYK_DTYPE_FP8_E4M3, false, flags,
                 stream);
 }
@@ -445,6 +467,7 @@ int ayk_paged_attention_v2(void* out, const void* q, const void* k_cache, const 
   // asked, a reduce kernel does (and PARTIALS_ONLY runs neither merge).
   p.arrivals = (flags & (AYK_FLAG_SEPARATE_REDUCE | AYK_FLAG_PARTIALS_ONLY)) ? nullptr : arrivals;
   p.max_len = (int32_t)std::min<int64_t>(p.max_len, (int64_t)partition_size * max_partitions);
+  if (dtype == AYK_DTYPE_FP32) return launch_f32(op, p, head_dim, gc, true, flags, stream);
   return launch(op, p, head_dim, gc, dtype == AYK_DTYPE_BF16, kv_dtype == AYK_DTYPE_FP8_E4M3, true, flags,
                 stream);
 }
@@ -511,6 +534,8 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
   if (rc != AYK_OK) return rc;
+  if (dtype == AYK_DTYPE_FP32)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: fp32 runs on the decode entry points, row by row", op);
   // Tiles of the full capacity, or of a half or a quarter (2 or 4 waves then share
   // each group of pairs and split its chunks).
   const int full_pairs = ayk::prefill_tile_pairs_for(head_dim);
@@ -581,6 +606,8 @@ int ayk_paged_attention_windows(void* out, const void* q, const void* k_cache, c
   int gc = 0;
   const int rc = prepare(op, c, p, gc);
   if (rc != AYK_OK) return rc;
+  if (dtype == AYK_DTYPE_FP32)
+    return fail(AYK_ERR_UNSUPPORTED, "%s: fp32 runs on the decode entry points, row by row", op);
   if (p.group > 16)
     return fail(AYK_ERR_UNSUPPORTED, "%s: %d query heads per key/value head exceed a window's 16 columns", op,
                 p.group);

@@ -68,6 +68,10 @@ hipError_t launch_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles
 // Window launch of the decode kernel: p.work holds p.n_work tiles of the multi-row tile list
 // (first row, rows, request, partition) of at most 16 / group rows; p.head_chunks 1.
 hipError_t launch_window_mfma(const AttnParams& p, int head_dim, bool bf16, bool split, bool kv8, hipStream_t stream);
+// fp32 models: the VALU decode kernel (v1, or v2 partitions) and its partition merge.
+hipError_t launch_attention_f32(const AttnParams& p, int head_dim, int heads_per_chunk, bool split,
+                                hipStream_t stream);
+hipError_t launch_partition_reduce_f32(const AttnParams& p, int head_dim, hipStream_t stream);
 // The v2 log-sum-exp merge of the partitions of every (row, head); `compute_units` of the
 // device sets how many partition slots each pair gets.
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, int compute_units,
@@ -78,6 +82,7 @@ hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipSt
 // entry points enumerate the K/V loads of the launch they prepared instead of launching it.
 bool walking();
 void walk_decode(const AttnParams& p, int head_dim, bool mfma, bool kv8, bool split, bool window);
+void walk_f32(const AttnParams& p, int head_dim, bool split);
 void walk_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool kv8,
                   int waves_per_group);
 

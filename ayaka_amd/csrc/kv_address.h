@@ -104,6 +104,11 @@ constexpr int positions_per_load(int d) { return 64 / pieces_per_position(d); }
 // Decode (DPP kernel): two loads per lane per chunk.
 constexpr int dpp_loads_per_chunk() { return 2; }
 
+// Decode over fp32 caches: 4 floats (16 bytes) per lane, so D / 4 lanes per position, and four
+// loads per lane per chunk.
+constexpr int f32_lanes_per_position(int d) { return d / 4; }
+constexpr int f32_loads_per_chunk() { return 4; }
+
 // Multi-row kernel: 64-position chunks, or 32 at head_dim 256 with 1 or 2 waves per pair group
 // (a 64-position stage there took 133 KB of LDS and left one wave per SIMD).
 constexpr int prefill_chunk_positions(int d, int waves_per_group) { return d == 256 && waves_per_group <= 2 ? 32 : 64; }

@@ -85,9 +85,25 @@ std::vector<Item> decode_items(const AttnParams& p, bool split) {
   return items;
 }
 
-// The loads of one wave of a decode launch (the matrix-core kernel, its window launch, or the
-// DPP kernel): positions [t_begin, t_end) of request req, this wave's chunks of each segment.
+// Bytes of element `elem` of a cache and of one load: KV8 1-byte codes (8-byte loads), or
+// 16-bit elements (16-byte loads); the fp32 kernel's 4-byte elements (16-byte loads) use
+// F32Elems.
 template <bool KV8>
+struct KvElems {
+  static int64_t bytes(int64_t elem) { return kv_bytes_of<KV8>(elem); }
+  static constexpr int load = kv_load_bytes<KV8>();
+  static constexpr int per_lane = 8;  // elements a lane's piece covers
+};
+struct F32Elems {
+  static int64_t bytes(int64_t elem) { return 4 * elem; }
+  static constexpr int load = 16;
+  static constexpr int per_lane = 4;
+};
+
+// The loads of one wave of a decode launch (the matrix-core kernel, its window launch, the
+// DPP kernel or the fp32 kernel): positions [t_begin, t_end) of request req, this wave's chunks
+// of each segment.
+template <class E>
 void walk_wave(const AttnParams& p, int req, int t_begin, int t_end, int kvh, int slice, int ws, int ch, int tpl,
                int cpt, int loads_per_chunk, bool prefetch_clamped, std::vector<uint32_t>& buffer) {
   const int seg_len = segment_positions(p, ch);
@@ -104,7 +120,7 @@ void walk_wave(const AttnParams& p, int req, int t_begin, int t_end, int kvh, in
         for (int j = 0; j < loads_per_chunk; ++j) {
           const uint32_t off = kv_offset(p, buffer.data() + kTableCap, b0, chunk_position(s0, s1, ci, ch, j, tpl, r),
                                          token_stride);
-          record(kv_bytes_of<KV8>((int64_t)kvh * p.head_stride + c * 8 + (int64_t)off), kv_load_bytes<KV8>());
+          record(E::bytes((int64_t)kvh * p.head_stride + c * E::per_lane + (int64_t)off), E::load);
         }
       }
   }
@@ -131,8 +147,8 @@ void walk_mfma(const AttnParams& p, bool split) {
           t_begin = it.part * psize;
           t_end = imin(len, t_begin + psize);
         }
-        walk_wave<KV8>(p, req, t_begin, t_end, vh / p.head_chunks, wave % ws, ws, CH, TPL, pieces_per_position(D),
-                       CH / TPL, true, buffer);
+        walk_wave<KvElems<KV8>>(p, req, t_begin, t_end, vh / p.head_chunks, wave % ws, ws, CH, TPL,
+                                pieces_per_position(D), CH / TPL, true, buffer);
       }
 }
 
@@ -160,8 +176,8 @@ void walk_window(const AttnParams& p, bool split) {
       for (int wave = 0; wave < heads * ws; ++wave) {
         const int vh = g * heads + wave / ws;
         if (vh >= p.num_virtual_heads) continue;
-        walk_wave<KV8>(p, req, t_begin, t_end, vh, wave % ws, ws, CH, TPL, pieces_per_position(D), CH / TPL, true,
-                       buffer);
+        walk_wave<KvElems<KV8>>(p, req, t_begin, t_end, vh, wave % ws, ws, CH, TPL, pieces_per_position(D),
+                                CH / TPL, true, buffer);
       }
   }
 }
@@ -181,8 +197,29 @@ void walk_dpp(const AttnParams& p, bool split) {
         t_begin = it.part * psize;
         t_end = imin(len, t_begin + psize);
       }
-      walk_wave<false>(p, req, t_begin, t_end, vh / p.head_chunks, 0, 1, CH, TPL, pieces_per_position(D),
-                       dpp_loads_per_chunk(), false, buffer);
+      walk_wave<KvElems<false>>(p, req, t_begin, t_end, vh / p.head_chunks, 0, 1, CH, TPL, pieces_per_position(D),
+                                dpp_loads_per_chunk(), false, buffer);
+    }
+}
+
+template <int D>
+void walk_f32_d(const AttnParams& p, bool split) {
+  constexpr int LPT = f32_lanes_per_position(D);
+  constexpr int TPL = 64 / LPT;
+  constexpr int CH = TPL * f32_loads_per_chunk();
+  std::vector<uint32_t> buffer;
+  for (const Item& it : decode_items(p, split))
+    for (int vh = 0; vh < p.num_virtual_heads; ++vh) {
+      int req, len;
+      row_of(p, it.row, req, len);
+      int t_begin = 0, t_end = len;
+      if (split) {
+        const int psize = p.staged ? p.staged[0] : p.partition_size;
+        t_begin = it.part * psize;
+        t_end = imin(len, t_begin + psize);
+      }
+      walk_wave<F32Elems>(p, req, t_begin, t_end, vh / p.head_chunks, 0, 1, CH, TPL, LPT, f32_loads_per_chunk(),
+                          false, buffer);
     }
 }
 
@@ -256,6 +293,14 @@ void walk_decode(const AttnParams& p, int head_dim, bool mfma, bool kv8, bool sp
     case 64: walk_decode_d<64>(p, mfma, kv8, split, window); break;
     case 128: walk_decode_d<128>(p, mfma, kv8, split, window); break;
     default: walk_decode_d<256>(p, mfma, kv8, split, window); break;
+  }
+}
+
+void walk_f32(const AttnParams& p, int head_dim, bool split) {
+  switch (head_dim) {
+    case 64: walk_f32_d<64>(p, split); break;
+    case 128: walk_f32_d<128>(p, split); break;
+    default: walk_f32_d<256>(p, split); break;
   }
 }
 

@@ -1,0 +1,331 @@
+// Paged-attention decode for fp32 models (fp32 q, out and caches) on MI355X (gfx950).
+//
+// Semantics: the reference's decode rule (python/ayaka/ops/backends/torch/attention.py:237-271)
+// over fp32 caches, which its torch backend serves and flashinfer refuses
+// (python/ayaka/ops/backends/flashinfer/attention.py:298-301): row n attends to positions
+// [0, len_n) of its request, scores scale * q.k, softmax and the value sum in fp32, and the
+// output written in fp32. Rows with a position (multi-row steps run row by row here) see
+// [0, position].
+//
+// The path is bandwidth-bound like the 16-bit decode kernels, with twice the bytes per
+// position, so it keeps their shape on the VALU: one workgroup per (row[, partition]) and group
+// of up to 8 virtual heads, one wave per virtual head (a key/value head, or a chunk of up to 8 of
+// its query heads). A token's head_dim row (D fp32 = 4D bytes) is read by D/4 lanes with one
+// 16-byte nontemporal load each, so a load instruction covers 64 / (D/4) tokens; q.k is four FMAs
+// per lane and head, summed over the token's lanes by DPP and cross-lane shuffles; each lane group
+// keeps its own online softmax (log2 domain, lazily raised max) and the groups meet by shuffles at
+// the end. The next chunk's keys are in flight while the current chunk is folded. v2 writes each
+// partition's normalised partial and (m, l), merged by partition_reduce_f32_kernel.
+
+#include "attention_common.h"
+
+namespace ayk {
+
+template <int D, int GC, bool SPLIT>
+__global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(const AttnParams p) {
+  constexpr int LPT = f32_lanes_per_position(D);  // lanes per token, 4 floats each
+  constexpr int TPL = kWave / LPT;                 // tokens per load instruction
+  constexpr int NLD = f32_loads_per_chunk();
+  constexpr int CH = TPL * NLD;                    // tokens per chunk
+
+  __shared__ uint32_t s_tbl[kTableCap];
+
+  const int tid = threadIdx.x;
+  const int threads = blockDim.x;
+  const int waves = threads / kWave;
+  const int groups = (p.num_virtual_heads + waves - 1) / waves;
+  const WgCoord wg = wg_coord(p, groups, SPLIT);
+  if (wg.row < 0) return;  // past the staged work items (uniform per workgroup)
+  const int row = wg.row;
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
+  const int vh = wg.group * waves + wave;
+  const bool active = vh < p.num_virtual_heads;
+  const int kvh = vh / p.head_chunks;
+  const int h0 = kvh * p.group + (vh % p.head_chunks) * GC;
+  const int r = lane / LPT;
+  const int c = lane % LPT;
+  float* out = static_cast<float*>(p.out);
+
+  int req, len;
+  row_context(p, row, req, len);
+  int t_begin = 0, t_end = len;
+  const int psize = SPLIT ? partition_size_of(p) : 0;
+  const int np = SPLIT ? (len > 0 ? (len - 1) / psize + 1 : 0) : 1;  // partitions with tokens
+  if constexpr (SPLIT) {
+    t_begin = wg.part * psize;
+    t_end = imin(len, t_begin + psize);
+  }
+  if (t_begin >= t_end) {
+    // a padding row gets zeros (from partition 0); a partition past the row's context: nothing
+    if (len == 0 && wg.part == 0 && active && r == 0) {
+#pragma unroll
+      for (int g = 0; g < GC; ++g)
+        *reinterpret_cast<f32x4*>(out + ((int64_t)row * p.num_heads + h0 + g) * D + c * 4) = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    return;
+  }
+
+  f32x4 qv[GC];
+  float m[GC], l[GC];
+  f32x4 o[GC];
+#pragma unroll
+  for (int g = 0; g < GC; ++g) {
+    qv[g] = active ? *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p.q) +
+                                                     ((int64_t)row * p.num_heads + h0 + g) * D + c * 4)
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
+    m[g] = kNoScore;
+    l[g] = 0.f;
+    o[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
+  const int seg_len = segment_positions(p, CH);
+  const uint32_t token_stride = (uint32_t)p.token_stride;
+  const float scale_log2 = p.scale_log2;
+  const float* kbase = reinterpret_cast<const float*>(p.k_cache) + (int64_t)kvh * p.head_stride + c * 4;
+  const float* vbase = reinterpret_cast<const float*>(p.v_cache) + (int64_t)kvh * p.head_stride + c * 4;
+
+  for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
+    const int s1 = imin(t_end, s0 + seg_len);
+    const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, threads);
+    if (!active) continue;
+    const int nch = (s1 - s0 + CH - 1) / CH;
+
+    auto offsets = [&](int ci, uint32_t(&dst)[NLD]) {
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+        dst[j] = kv_offset(p, s_tbl, b0, chunk_position(s0, s1, ci, CH, j, TPL, r), token_stride);
+    };
+    auto load = [](const float* base, uint32_t off) {
+      return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base + off));
+    };
+
+    auto consume = [&](int ci, const f32x4(&kc)[NLD], const f32x4(&vc)[NLD]) {
+      const int tb = s0 + ci * CH;
+      const bool tail = tb + CH > s1;
+      float s[NLD][GC];
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+          float a = qv[g].x * kc[j].x;
+          a = fmaf(qv[g].y, kc[j].y, a);
+          a = fmaf(qv[g].z, kc[j].z, a);
+          s[j][g] = fmaf(qv[g].w, kc[j].w, a);
+        }
+      // Sum over the token's LPT lanes, one stage at a time across all the partial sums.
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[j][g] += dpp<0xB1>(s[j][g]);  // lane ^ 1
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[j][g] += dpp<0x4E>(s[j][g]);  // lane ^ 2
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[j][g] += dpp<0x141>(s[j][g]);  // the other quad of 8
+#pragma unroll
+      for (int j = 0; j < NLD; ++j)
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[j][g] += dpp<0x140>(s[j][g]);  // the other 8 of 16
+      if constexpr (LPT >= 32) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j)
+#pragma unroll
+          for (int g = 0; g < GC; ++g) s[j][g] += __shfl_xor(s[j][g], 16);
+      }
+      if constexpr (LPT >= 64) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j)
+#pragma unroll
+          for (int g = 0; g < GC; ++g) s[j][g] += __shfl_xor(s[j][g], 32);
+      }
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) {
+        const bool past = tail && tb + j * TPL + r >= s1;
+#pragma unroll
+        for (int g = 0; g < GC; ++g) s[j][g] = past ? -INFINITY : s[j][g] * scale_log2;
+      }
+      float mx[GC];
+      bool grow = false;
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        mx[g] = s[0][g];
+#pragma unroll
+        for (int j = 1; j < NLD; ++j) mx[g] = fmaxf(mx[g], s[j][g]);
+        grow |= mx[g] > m[g] + kRescaleSlack;
+      }
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+          const float mn = fmaxf(m[g], mx[g]);
+          const float alpha = fast_exp2(m[g] - mn);
+          l[g] *= alpha;
+          o[g] *= alpha;
+          m[g] = mn;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) {
+        // a slot past the context may hold anything, NaN included, and 0 * NaN is NaN
+        const f32x4 v = (tail && tb + j * TPL + r >= s1) ? f32x4{0.f, 0.f, 0.f, 0.f} : vc[j];
+#pragma unroll
+        for (int g = 0; g < GC; ++g) {
+          const float w = fast_exp2(s[j][g] - m[g]);
+          l[g] += w;
+          o[g].x = fmaf(w, v.x, o[g].x);
+          o[g].y = fmaf(w, v.y, o[g].y);
+          o[g].z = fmaf(w, v.z, o[g].z);
+          o[g].w = fmaf(w, v.w, o[g].w);
+        }
+      }
+    };
+
+    uint32_t offA[NLD], offB[NLD];
+    f32x4 kA[NLD], kB[NLD], vc[NLD];
+    int ci = 0;
+    offsets(0, offA);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) kA[j] = load(kbase, offA[j]);
+    while (ci < nch) {
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) vc[j] = load(vbase, offA[j]);
+      if (ci + 1 < nch) {
+        offsets(ci + 1, offB);
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) kB[j] = load(kbase, offB[j]);
+      }
+      consume(ci, kA, vc);
+      if (++ci >= nch) break;
+#pragma unroll
+      for (int j = 0; j < NLD; ++j) vc[j] = load(vbase, offB[j]);
+      if (ci + 1 < nch) {
+        offsets(ci + 1, offA);
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) kA[j] = load(kbase, offA[j]);
+      }
+      consume(ci, kB, vc);
+      ++ci;
+    }
+  }
+  if (!active) return;
+  // The TPL lane groups of the wave meet (butterfly: every group ends with the merged state).
+#pragma unroll
+  for (int st = LPT; st < kWave; st <<= 1) {
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      const float m2 = __shfl_xor(m[g], st);
+      const float l2 = __shfl_xor(l[g], st);
+      const float mn = fmaxf(m[g], m2);
+      const float a = fast_exp2(m[g] - mn);
+      const float b = fast_exp2(m2 - mn);
+      l[g] = l[g] * a + l2 * b;
+      m[g] = mn;
+      o[g].x = o[g].x * a + __shfl_xor(o[g].x, st) * b;
+      o[g].y = o[g].y * a + __shfl_xor(o[g].y, st) * b;
+      o[g].z = o[g].z * a + __shfl_xor(o[g].z, st) * b;
+      o[g].w = o[g].w * a + __shfl_xor(o[g].w, st) * b;
+    }
+  }
+  if (r != 0) return;
+#pragma unroll
+  for (int g = 0; g < GC; ++g) {
+    const int head = h0 + g;
+    const float inv = (l[g] > 0.f ? 1.0f / l[g] : 0.f) * p.v_scale;
+    if (SPLIT && np > 1) {
+      const int64_t slot = partial_index(p, row, head, np) + wg.part;
+      *reinterpret_cast<f32x4*>(p.part_o + slot * D + c * 4) = o[g] * inv;
+      if (c == 0) {
+        p.part_ml[slot * 2] = m[g];
+        p.part_ml[slot * 2 + 1] = l[g];
+      }
+    } else {
+      *reinterpret_cast<f32x4*>(out + ((int64_t)row * p.num_heads + head) * D + c * 4) = o[g] * inv;
+    }
+  }
+}
+
+// Merge the v2 partials of every (row, head): one thread per 4 output elements, folding the
+// row's partitions in order, o = sum_p w_p o_p / sum_p w_p with w_p = l_p 2^(m_p - max m). A row
+// of one partition (or none) was written by the partition kernel.
+template <int D>
+__global__ __launch_bounds__(256) void partition_reduce_f32_kernel(const AttnParams p) {
+  constexpr int QUADS = D / 4;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)p.n_rows * p.num_heads * QUADS) return;
+  const int quad = (int)(idx % QUADS);
+  const int head = (int)((idx / QUADS) % p.num_heads);
+  const int row = (int)(idx / ((int64_t)QUADS * p.num_heads));
+  int req, len;
+  row_context(p, row, req, len);
+  const int psize = partition_size_of(p);
+  const int np = len > 0 ? (len - 1) / psize + 1 : 0;
+  if (np <= 1) return;
+  const int64_t first = partial_index(p, row, head, np);
+  float m = kNoScore, l = 0.f;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < np; ++i) {
+    const float mi = p.part_ml[(first + i) * 2], wi = p.part_ml[(first + i) * 2 + 1];
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p.part_o + (first + i) * D + quad * 4);
+    const float mn = fmaxf(m, mi);
+    const float a = fast_exp2(m - mn), b = wi * fast_exp2(mi - mn);
+    l = l * a + b;
+    acc = acc * a + v * b;
+    m = mn;
+  }
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + ((int64_t)row * p.num_heads + head) * D + quad * 4) =
+      acc * inv;
+}
+
+template <int D, int GC>
+static hipError_t launch_f32_typed(const AttnParams& p, bool split, hipStream_t stream) {
+  const int waves = p.num_virtual_heads < kMaxWaves ? p.num_virtual_heads : kMaxWaves;
+  const int groups = (p.num_virtual_heads + waves - 1) / waves;
+  const int64_t items = (split && p.work) ? p.n_work : (int64_t)p.n_rows * (split ? p.max_partitions : 1);
+  const dim3 grid((unsigned)(items * groups)), block(waves * kWave);
+  if (split) hipLaunchKernelGGL((paged_attention_f32_kernel<D, GC, true>), grid, block, 0, stream, p);
+  else hipLaunchKernelGGL((paged_attention_f32_kernel<D, GC, false>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_f32_gc(const AttnParams& p, int gc, bool split, hipStream_t stream) {
+  switch (gc) {
+    case 1: return launch_f32_typed<D, 1>(p, split, stream);
+    case 2: return launch_f32_typed<D, 2>(p, split, stream);
+    case 3: return launch_f32_typed<D, 3>(p, split, stream);
+    case 4: return launch_f32_typed<D, 4>(p, split, stream);
+    case 5: return launch_f32_typed<D, 5>(p, split, stream);
+    case 6: return launch_f32_typed<D, 6>(p, split, stream);
+    case 7: return launch_f32_typed<D, 7>(p, split, stream);
+    case 8: return launch_f32_typed<D, 8>(p, split, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_attention_f32(const AttnParams& p, int head_dim, int gc, bool split, hipStream_t stream) {
+  switch (head_dim) {
+    case 64: return launch_f32_gc<64>(p, gc, split, stream);
+    case 128: return launch_f32_gc<128>(p, gc, split, stream);
+    case 256: return launch_f32_gc<256>(p, gc, split, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_partition_reduce_f32(const AttnParams& p, int head_dim, hipStream_t stream) {
+  const int64_t threads = (int64_t)p.n_rows * p.num_heads * (head_dim / 4);
+  const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+  switch (head_dim) {
+    case 64: hipLaunchKernelGGL((partition_reduce_f32_kernel<64>), grid, block, 0, stream, p); break;
+    case 128: hipLaunchKernelGGL((partition_reduce_f32_kernel<128>), grid, block, 0, stream, p); break;
+    case 256: hipLaunchKernelGGL((partition_reduce_f32_kernel<256>), grid, block, 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace ayk

@@ -2,9 +2,10 @@
 
 The messages follow the reference's (``python/ayaka/ops/backends/torch/_checks.py:21-59``,
 ``kvcache.py:39-62``) so that callers and tests read the same refusals. The
-hip backend computes in fp16 and bf16 only, on HIP devices, for head widths of
-64, 128 and 256 and block sizes of 1 to 65536 positions; it stores the ``"raw"`` codec
-(fp16/bf16 caches) and ``"fp8_e4m3"`` (``float8_e4m3fn`` caches).
+hip backend computes in fp16, bf16 and fp32 (fp32 on a decode kernel of its own, row by row),
+on HIP devices, for head widths of 64, 128 and 256 and block sizes of 1 to 65536 positions; it
+stores the ``"raw"`` codec (fp16/bf16/fp32 caches) and ``"fp8_e4m3"`` (``float8_e4m3fn`` caches,
+read by fp16/bf16 models).
 """
 
 from __future__ import annotations
@@ -30,7 +31,8 @@ __all__ = [
 ]
 
 HEAD_DIMS = frozenset({64, 128, 256})
-_DTYPES = (torch.float16, torch.bfloat16)
+_DTYPES = (torch.float16, torch.bfloat16)  # compute dtypes over a quantised codec
+_RAW_DTYPES = (torch.float16, torch.bfloat16, torch.float32)  # the raw codec's, fp32 on its own kernel
 _NAMES = {
     torch.float16: "float16",
     torch.bfloat16: "bfloat16",
@@ -41,7 +43,7 @@ _NAMES = {
     torch.float8_e4m3fn: "float8_e4m3fn",
 }
 # The cache element type of each codec this backend stores.
-_CODEC_DTYPES = {RAW_CODEC: _DTYPES, FP8_E4M3_CODEC: (torch.float8_e4m3fn,)}
+_CODEC_DTYPES = {RAW_CODEC: _RAW_DTYPES, FP8_E4M3_CODEC: (torch.float8_e4m3fn,)}
 
 
 def dtype_name(dtype: torch.dtype) -> str:

@@ -17,7 +17,7 @@ from ayaka_amd.errors import BackendError, CapabilityError
 __all__ = ["ABI_VERSION", "EXPORTS", "LIB_PATH", "check", "lib"]
 
 LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libayaka_hip.so"
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32

@@ -84,14 +84,14 @@ PARTITION_CANDIDATES = (64, 128, 192, 256, 320, 384, 448, 512, 576, 640, 704, 76
 #: time then tracks C5's ragged curve with correlation 0.87, against 0.11 at 80) and 160
 #: for fp8 caches (0.99); with them the model picks the fastest measured size of all
 #: three shapes for both.
-WORKGROUP_COSTS = {2: 320, 1: 160}
+WORKGROUP_COSTS = {2: 320, 1: 160, 4: 320}
 WORKGROUP_COST = WORKGROUP_COSTS[2]
 #: The same for a v1 workgroup, whose waves split each context among themselves and merge
 #: in LDS (no partials, no second launch): fitted so that the model prefers v1 where it
 #: measured faster than the best v2 launch (C3's 64 rows of 4096: 160.5 vs 162.8 us, with
 #: fp8 caches 90.7 vs 92.8; C1's four short rows: 12.1 vs 15.9 us, with fp8 caches 11.3 vs
 #: 15.7) and v2 where it is not (C2, C4, C5, both codecs).
-V1_WORKGROUP_COSTS = {2: 240, 1: 80}
+V1_WORKGROUP_COSTS = {2: 240, 1: 80, 4: 240}
 #: Waves a v1 workgroup may split each (row, key/value head)'s context among.
 V1_WAVE_SPLITS = (1, 2, 4, 8)
 #: XCDs of one MI355X; workgroups are dealt to them round-robin.
@@ -107,7 +107,7 @@ PREFILL_MIN_ROWS = 2
 COMPUTE_UNITS = 256
 
 _LAYOUT_CODES = {KVLayoutKind.NHD: 0, KVLayoutKind.HND: 1}
-_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+_DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 3}
 _KV_FP8_E4M3 = 2
 
 
@@ -660,7 +660,7 @@ def choose_split(
         if v1 and not min_size and not max_items and lengths.size:
             v2 = schedule_makespan(lengths, size, groups, WORKGROUP_COSTS[kv_bytes]) if size < max_length else None
             best = None
-            for ws in V1_WAVE_SPLITS:
+            for ws in (V1_WAVE_SPLITS if kv_bytes != 4 else (1,)):  # fp32: one wave per head
                 t = v1_makespan(lengths, ws, virtual_heads, V1_WORKGROUP_COSTS[kv_bytes])
                 if best is None or t < best[0]:
                     best = (t, ws)
@@ -974,6 +974,12 @@ def attend_with(
 
     lib = _lib.lib()
     stream = stream_handle(device)
+    if q.dtype == torch.float32:
+        # fp32 models run on the decode kernel for fp32, each row of a multi-row step on its own
+        if prefill or window or (qk is not None) or (waves not in (None, 1)) or merge == "in-kernel":
+            raise BackendError(f"{op}: fp32 runs one launch shape: the per-row decode kernel, one wave per "
+                               "head, partitions merged by the reduce kernel", context={"op": op})
+        prefill = False
     if prefill is None:
         prefill = not decode and _wants_prefill_kernel(step)
     if prefill and isinstance(step, HipAttentionPlan):
@@ -987,7 +993,7 @@ def attend_with(
         if not isinstance(step, HipAttentionPlan):
             raise BackendError(f"{op}: the multi-row kernel needs a planned step", context={"op": op})
         pairs = tile_pairs or step.prefill_launch(kv_heads, heads // kv_heads, buffers.head_dim,
-                                                  1 if buffers.codec == FP8_E4M3_CODEC else 2)[0]
+                                                  buffers.k.element_size())[0]
         if heads // kv_heads > pairs:
             raise BackendError(
                 f"{op}: {heads // kv_heads} query heads per key/value head exceed the multi-row "
@@ -995,7 +1001,7 @@ def attend_with(
                 context={"op": op, "argument": "q"},
             )
         group = heads // kv_heads
-        kv_bytes = 1 if buffers.codec == FP8_E4M3_CODEC else 2
+        kv_bytes = buffers.k.element_size()
         if partitions == 0:
             size = 0
         elif partition_size is not None:
@@ -1047,7 +1053,7 @@ def attend_with(
     )
     staged = None
     if partitions is None:
-        kv_bytes = 1 if buffers.codec == FP8_E4M3_CODEC else 2
+        kv_bytes = buffers.k.element_size()
         if isinstance(step, HipAttentionPlan):
             split = step.split_for(kv_heads, group, kv_bytes)
         else:
@@ -1113,7 +1119,7 @@ def _attend_windows(op: str, q: torch.Tensor, buffers: KVBuffers, meta: Attentio
             f"rows than {16 // group if group <= 16 else 0} at {group} query heads per key/value head",
             context={"op": op, "argument": "meta"},
         )
-    kv_bytes = 1 if buffers.codec == FP8_E4M3_CODEC else 2
+    kv_bytes = buffers.k.element_size()
     if partitions == 0:
         size = 0
     elif partition_size is not None:

@@ -41,8 +41,11 @@ enum {
 
 /* Element types. fp16/bf16 for q, out and 16-bit caches; AYK_DTYPE_FP8_E4M3 for
  * caches of the "fp8_e4m3" codec: OCP fp8 e4m3 codes (torch.float8_e4m3fn), 1
- * byte per element, decoded exactly to the compute dtype when read. */
-enum { AYK_DTYPE_FP16 = 0, AYK_DTYPE_BF16 = 1, AYK_DTYPE_FP8_E4M3 = 2 };
+ * byte per element, decoded exactly to the compute dtype when read; AYK_DTYPE_FP32
+ * for fp32 models (q, out and caches all fp32; decode entry points only, on the VALU:
+ * ayk_paged_attention_v1 / _v2 / _v2_static, whose rows may carry positions, so a
+ * multi-row step runs row by row; the window and multi-row entry points refuse it). */
+enum { AYK_DTYPE_FP16 = 0, AYK_DTYPE_BF16 = 1, AYK_DTYPE_FP8_E4M3 = 2, AYK_DTYPE_FP32 = 3 };
 
 /* flags of the attention calls: 0 lets the library pick the q.k path. */
 enum {

@@ -372,8 +372,11 @@ def test_ops_refuse_caches_they_cannot_serve() -> None:
         hip_attention.attend(q, _cpu_buffers(layout=KVLayoutKind.NLD), meta, q.clone(), scale=1.0)
     with pytest.raises(BackendError, match="stores the 'raw' and 'fp8_e4m3' codecs, not 'fp8'"):
         hip_kvcache.store(q[:, :2], q[:, :2], _cpu_buffers(codec="fp8"), meta)
-    fp32 = torch.zeros(4, 16, 2, 64)
-    with pytest.raises(BackendError, match="computes in float16, bfloat16"):
+    fp64 = torch.zeros(4, 16, 2, 64, dtype=torch.float64)
+    with pytest.raises(BackendError, match="computes in float16, bfloat16, float32"):
+        hip_attention.attend(q, KVBuffers(fp64, fp64, KVLayoutKind.NHD, RAW_CODEC), meta, q.clone(), scale=1.0)
+    fp32 = torch.zeros(4, 16, 2, 64)  # accepted as a cache (it fails on the device, as every CPU tensor does)
+    with pytest.raises(BackendError, match="runs on a HIP device"):
         hip_attention.attend(q, KVBuffers(fp32, fp32, KVLayoutKind.NHD, RAW_CODEC), meta, q.clone(), scale=1.0)
     with pytest.raises(BackendError, match="stores the 'fp8_e4m3' codec as float8_e4m3fn"):
         hip_attention.attend(q, _cpu_buffers(codec=FP8_E4M3_CODEC), meta, q.clone(), scale=1.0)

@@ -41,7 +41,8 @@ class Step:
     is the pool's last one."""
 
     def __init__(self, rng: np.random.Generator, lengths: list[int], block_size: int, kv_heads: int,
-                 head_dim: int, kv8: bool, layout: int, spare: int = 3) -> None:
+                 head_dim: int, kv8: bool, layout: int, spare: int = 3, fp32: bool = False) -> None:
+        self.fp32 = fp32
         self.lengths = np.asarray(lengths, dtype=np.int32)
         self.block_size, self.kv_heads, self.head_dim, self.kv8, self.layout = (block_size, kv_heads, head_dim,
                                                                                  kv8, layout)
@@ -56,14 +57,15 @@ class Step:
                 ids[-1] = self.num_blocks - 1  # the pool's last block holds this request's end
             self.table[r, :n] = ids
         self.width = width
-        elem = 1 if kv8 else 2
+        elem = 1 if kv8 else 4 if fp32 else 2
+        self.elem = elem
         self.block_bytes = block_size * kv_heads * head_dim * elem
         self.pool_bytes = self.num_blocks * self.block_bytes
 
     def expected_reach(self) -> tuple[int, int]:
         """(lowest byte, one past the highest byte) the step's contexts occupy."""
         lo, hi = None, 0
-        elem = 1 if self.kv8 else 2
+        elem = self.elem
         for r, n in enumerate(self.lengths):
             for b in range(-(-int(n) // self.block_size)):
                 block = int(self.table[r, b])
@@ -99,7 +101,7 @@ def _check(step: Step, reach: np.ndarray, label: str) -> None:
 
 
 def _common(step: Step, heads: int, rows: int, request_of_row, positions) -> tuple:
-    dtype = 1
+    dtype = 3 if step.fp32 else 1
     kv_dtype = 2 if step.kv8 else dtype
     return (FAKE, FAKE, FAKE, FAKE, _ptr(step.table), step.width, _ptr(step.lengths), _ptr(request_of_row),
             _ptr(positions), rows, heads, step.kv_heads, step.head_dim, step.num_blocks, step.block_size,
@@ -240,3 +242,21 @@ def test_the_walk_reports_out_of_range_tables() -> None:
     # a walk left on by a failed call is turned off by the next end, and nothing launches
     lib = _lib.lib()
     assert lib.ayk_debug_kv_reach_begin(-1) == 1
+
+
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_fp32_decode_loads_stay_in_the_cache(head_dim: int) -> None:
+    # the fp32 kernel: 16-byte loads of 4 floats, D / 4 lanes per position, v1 and v2 over every
+    # grid kind; multi-row steps of an fp32 model run row by row on it (rows carry positions)
+    rng = np.random.default_rng(300 + head_dim)
+    for case in range(20):
+        bs = BLOCK_SIZES[case % len(BLOCK_SIZES)]
+        kv_heads, group = [(2, 4), (3, 1), (1, 8), (4, 2)][case % 4]
+        step = Step(rng, _lengths(rng, bs, int(rng.integers(1, 6))), bs, kv_heads, head_dim, False, case % 2,
+                    fp32=True)
+        heads = kv_heads * group
+        _check(step, walk_v1(step, heads, FLAG_WAVES[1]), f"fp32 v1 case {case} bs {bs}")
+        for size in (64, 128, 320):
+            for grid in ("work list", "dense", "staged"):
+                _check(step, walk_v2(step, heads, size, grid, FLAG_SEPARATE_REDUCE),
+                       f"fp32 v2 case {case} bs {bs} size {size} {grid}")
