@@ -232,7 +232,7 @@ int launch_f32(const char* op, const ayk::AttnParams& p, int head_dim, int gc, b
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t err = ayk::launch_attention_f32(q, head_dim, gc, split, s);
   if (err == hipSuccess && split && !(flags & AYK_FLAG_PARTIALS_ONLY))
-    err = ayk::launch_partition_reduce_f32(q, head_dim, s);
+    err = ayk::launch_partition_reduce_f32(q, head_dim, compute_units(), s);
   return launched(err, op);
 }
 

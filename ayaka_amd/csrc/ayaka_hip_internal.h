@@ -71,7 +71,7 @@ hipError_t launch_window_mfma(const AttnParams& p, int head_dim, bool bf16, bool
 // fp32 models: the VALU decode kernel (v1, or v2 partitions) and its partition merge.
 hipError_t launch_attention_f32(const AttnParams& p, int head_dim, int heads_per_chunk, bool split,
                                 hipStream_t stream);
-hipError_t launch_partition_reduce_f32(const AttnParams& p, int head_dim, hipStream_t stream);
+hipError_t launch_partition_reduce_f32(const AttnParams& p, int head_dim, int compute_units, hipStream_t stream);
 // The v2 log-sum-exp merge of the partitions of every (row, head); `compute_units` of the
 // device sets how many partition slots each pair gets.
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, int compute_units,

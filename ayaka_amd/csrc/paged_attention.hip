@@ -299,7 +299,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_kernel(cons
 // partition rounds exactly the value v1 rounds; a row without context gets zeros.
 constexpr int kReduceThreads = 256;
 
-template <int D, bool BF16, int S>
+// F32: an fp32 model's merge, its output written in fp32 (BF16 then unused).
+template <int D, bool BF16, int S, bool F32 = false>
 __global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const AttnParams p) {
   using E = Elem<BF16>;
   constexpr int QUADS = D / 4;                // float4 groups of a row
@@ -324,7 +325,6 @@ __global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const 
   int req, len;
   row_context(p, row, req, len);
   const int np = valid ? (len > 0 ? (len - 1) / partition_size_of(p) + 1 : 0) : 1;
-  uint16_t* out = static_cast<uint16_t*>(p.out) + pair * D;
   // partial_index, with the staged slot read above
   const int64_t first = p.staged ? (int64_t)staged_first * p.num_heads + (int64_t)head * np
                                  : ((int64_t)row * p.num_heads + head) * p.max_partitions;
@@ -392,9 +392,13 @@ __global__ __launch_bounds__(kReduceThreads) void partition_reduce_kernel(const 
     }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;  // np == 0: zeros
-  uint32_t* o32 = reinterpret_cast<uint32_t*>(out) + quad * 2;
-  o32[0] = E::round(total.x * inv) | (E::round(total.y * inv) << 16);
-  o32[1] = E::round(total.z * inv) | (E::round(total.w * inv) << 16);
+  if constexpr (F32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + pair * D + quad * 4) = total * inv;
+  } else {
+    uint32_t* o32 = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.out) + pair * D) + quad * 2;
+    o32[0] = E::round(total.x * inv) | (E::round(total.y * inv) << 16);
+    o32[1] = E::round(total.z * inv) | (E::round(total.w * inv) << 16);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -485,7 +489,7 @@ hipError_t launch_row_reduce(const AttnParams& p, int head_dim, bool bf16, hipSt
   return hipGetLastError();
 }
 
-template <int D, bool BF16>
+template <int D, bool BF16, bool F32 = false>
 static hipError_t launch_reduce_typed(const AttnParams& p, int compute_units, hipStream_t stream) {
   // Partition slots per (row, head): one for up to 4 partitions per row, and up to 16 when
   // one slot still gives every compute unit a workgroup (many pairs, most of whose rows often
@@ -505,10 +509,20 @@ static hipError_t launch_reduce_typed(const AttnParams& p, int compute_units, hi
   const int s = one_slot ? 1 : (p.max_partitions <= 16 || groups4 >= compute_units) ? S4 : S_MAX;
   const dim3 block(kReduceThreads);
   auto grid = [&](int heads) { return dim3((unsigned)((pairs + heads - 1) / heads)); };
-  if (s == 1) hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, 1>), grid(S_MAX), block, 0, stream, p);
-  else if (s == S4) hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, S4>), grid(S_MAX / S4), block, 0, stream, p);
-  else hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, S_MAX>), grid(1), block, 0, stream, p);
+  if (s == 1) hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, 1, F32>), grid(S_MAX), block, 0, stream, p);
+  else if (s == S4)
+    hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, S4, F32>), grid(S_MAX / S4), block, 0, stream, p);
+  else hipLaunchKernelGGL((partition_reduce_kernel<D, BF16, S_MAX, F32>), grid(1), block, 0, stream, p);
   return hipGetLastError();
+}
+
+hipError_t launch_partition_reduce_f32(const AttnParams& p, int head_dim, int compute_units, hipStream_t stream) {
+  switch (head_dim) {
+    case 64: return launch_reduce_typed<64, false, true>(p, compute_units, stream);
+    case 128: return launch_reduce_typed<128, false, true>(p, compute_units, stream);
+    case 256: return launch_reduce_typed<256, false, true>(p, compute_units, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_partition_reduce(const AttnParams& p, int head_dim, bool bf16, int compute_units,

@@ -15,7 +15,7 @@
 // per lane and head, summed over the token's lanes by DPP and cross-lane shuffles; each lane group
 // keeps its own online softmax (log2 domain, lazily raised max) and the groups meet by shuffles at
 // the end. The next chunk's keys are in flight while the current chunk is folded. v2 writes each
-// partition's normalised partial and (m, l), merged by partition_reduce_f32_kernel.
+// partition's normalised partial and (m, l), merged by partition_reduce_kernel with fp32 output.
 
 #include "attention_common.h"
 
@@ -248,39 +248,6 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
   }
 }
 
-// Merge the v2 partials of every (row, head): one thread per 4 output elements, folding the
-// row's partitions in order, o = sum_p w_p o_p / sum_p w_p with w_p = l_p 2^(m_p - max m). A row
-// of one partition (or none) was written by the partition kernel.
-template <int D>
-__global__ __launch_bounds__(256) void partition_reduce_f32_kernel(const AttnParams p) {
-  constexpr int QUADS = D / 4;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)p.n_rows * p.num_heads * QUADS) return;
-  const int quad = (int)(idx % QUADS);
-  const int head = (int)((idx / QUADS) % p.num_heads);
-  const int row = (int)(idx / ((int64_t)QUADS * p.num_heads));
-  int req, len;
-  row_context(p, row, req, len);
-  const int psize = partition_size_of(p);
-  const int np = len > 0 ? (len - 1) / psize + 1 : 0;
-  if (np <= 1) return;
-  const int64_t first = partial_index(p, row, head, np);
-  float m = kNoScore, l = 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < np; ++i) {
-    const float mi = p.part_ml[(first + i) * 2], wi = p.part_ml[(first + i) * 2 + 1];
-    const f32x4 v = *reinterpret_cast<const f32x4*>(p.part_o + (first + i) * D + quad * 4);
-    const float mn = fmaxf(m, mi);
-    const float a = fast_exp2(m - mn), b = wi * fast_exp2(mi - mn);
-    l = l * a + b;
-    acc = acc * a + v * b;
-    m = mn;
-  }
-  const float inv = l > 0.f ? 1.0f / l : 0.f;
-  *reinterpret_cast<f32x4*>(static_cast<float*>(p.out) + ((int64_t)row * p.num_heads + head) * D + quad * 4) =
-      acc * inv;
-}
-
 template <int D, int GC>
 static hipError_t launch_f32_typed(const AttnParams& p, bool split, hipStream_t stream) {
   const int waves = p.num_virtual_heads < kMaxWaves ? p.num_virtual_heads : kMaxWaves;
@@ -314,18 +281,6 @@ hipError_t launch_attention_f32(const AttnParams& p, int head_dim, int gc, bool 
     case 256: return launch_f32_gc<256>(p, gc, split, stream);
     default: return hipErrorInvalidValue;
   }
-}
-
-hipError_t launch_partition_reduce_f32(const AttnParams& p, int head_dim, hipStream_t stream) {
-  const int64_t threads = (int64_t)p.n_rows * p.num_heads * (head_dim / 4);
-  const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
-  switch (head_dim) {
-    case 64: hipLaunchKernelGGL((partition_reduce_f32_kernel<64>), grid, block, 0, stream, p); break;
-    case 128: hipLaunchKernelGGL((partition_reduce_f32_kernel<128>), grid, block, 0, stream, p); break;
-    case 256: hipLaunchKernelGGL((partition_reduce_f32_kernel<256>), grid, block, 0, stream, p); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
 }
 
 }  // namespace ayk

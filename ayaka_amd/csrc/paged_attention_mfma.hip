@@ -211,41 +211,53 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     };
 
     typedef typename KvRaw<KV8>::T Raw;
+    // Fold chunk ci (keys kc, values vc) into the running state. The chunk's SUB tiles
+    // share one softmax step: their keys pass through the wave's LDS tile one after the
+    // other (each tile's q.k MFMAs read it before the next tile's stores, a wave's LDS
+    // accesses running in program order), the SUB independent score tiles then take one
+    // max, one rescale decision and one pass of exponentials, and the values follow tile
+    // by tile for P.V.
     auto consume = [&](int ci, const Raw(&kc)[NL], const Raw(&vc)[NL]) {
+      const int tc = s0 + ci * CH;
+      const bool tail = tc + CH > s1;
+      f32x4 acc[SUB];
 #pragma unroll
       for (int sub = 0; sub < SUB; ++sub) {
-        const int tb = s0 + ci * CH + sub * MT;
-        const bool tail = tb + MT > s1;
-        // The tile's keys to LDS (swizzled, read back as MFMA operands). A wave's LDS
-        // accesses run in program order, so these stores follow the previous tile's reads.
 #pragma unroll
         for (int j = 0; j < NL1; ++j) s_k[wave][key_slot(j * TPL + r, c)] = kv_pairs<KV8, BF16>(kc[sub * NL1 + j]);
         wave_lds_sync();
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc[sub] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) acc = mfma_qk<BF16>(s_k[wave][key_slot(mt, s * 4 + mq)], qb[s], acc);
-        float sc[4];
+        for (int s = 0; s < KS; ++s) acc[sub] = mfma_qk<BF16>(s_k[wave][key_slot(mt, s * 4 + mq)], qb[s], acc[sub]);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int sub = 0; sub < SUB; ++sub)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          sc[i] = acc[i] * scale_log2;
-          if (WIN ? (!win_col || tb + 4 * mq + i > win_lim) : mt >= GC) sc[i] = -INFINITY;
-          if (tail && tb + 4 * mq + i >= s1) sc[i] = -INFINITY;
+          const int t = tc + sub * MT + 4 * mq + i;
+          float v = acc[sub][i] * scale_log2;
+          if (WIN ? (!win_col || t > win_lim) : mt >= GC) v = -INFINITY;
+          if (tail && t >= s1) v = -INFINITY;
+          acc[sub][i] = v;
+          mx = fmaxf(mx, v);
         }
-        float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        if (__builtin_amdgcn_ballot_w64(mx > m_h + kRescaleSlack)) {
-          const float mn = fmaxf(m_h, mx);
-          const float alpha = fast_exp2(m_h - mn);  // head mt's, and o[] holds head mt
-          l_h *= alpha;
-          m_h = mn;
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      if (__builtin_amdgcn_ballot_w64(mx > m_h + kRescaleSlack)) {
+        const float mn = fmaxf(m_h, mx);
+        const float alpha = fast_exp2(m_h - mn);  // head mt's, and o[] holds head mt
+        l_h *= alpha;
+        m_h = mn;
 #pragma unroll
-          for (int t = 0; t < DT; ++t) o[t] *= alpha;
-        }
+        for (int t = 0; t < DT; ++t) o[t] *= alpha;
+      }
+#pragma unroll
+      for (int sub = 0; sub < SUB; ++sub) {
         float w[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          w[i] = fast_exp2(sc[i] - m_h);
+          w[i] = fast_exp2(acc[sub][i] - m_h);
           l_h += w[i];
         }
         // O^T += V^T P^T: P^T is the lane's own weights (tokens 4*mq + i of head mt, the

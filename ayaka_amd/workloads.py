@@ -63,7 +63,7 @@ class Config:
 
     @property
     def dtype_label(self) -> str:
-        return {torch.float16: "fp16", torch.bfloat16: "bf16"}[self.dtype]
+        return {torch.float16: "fp16", torch.bfloat16: "bf16", torch.float32: "fp32"}[self.dtype]
 
 
 def config(index: int) -> Config:
@@ -179,9 +179,9 @@ def build(cfg: Config, device: torch.device | str = "cpu", *, poison: bool = Tru
 
 def algorithmic_bytes(cfg: Config, kv_bytes: int = 2) -> int:
     """Bytes one decode-attention call must move: K and V of every context position (``kv_bytes``
-    per element: 2, or 1 for fp8 caches), q read, out written, the used table entries and the
-    lengths (v2 scratch not counted)."""
-    s = 2
+    per element: 2, 1 for fp8 caches, 4 for fp32 models), q read, out written, the used table entries and the
+    lengths (v2 scratch not counted). q and out have the model's element size."""
+    s = cfg.dtype.itemsize
     kv = sum(cfg.lengths) * cfg.kv_heads * cfg.head_dim * 2 * kv_bytes
     qo = 2 * cfg.batch * cfg.heads * cfg.head_dim * s
     table = 4 * sum(-(-n // cfg.block_size) for n in cfg.lengths)
@@ -189,10 +189,10 @@ def algorithmic_bytes(cfg: Config, kv_bytes: int = 2) -> int:
 
 
 def store_bytes(cfg: Config, kv_bytes: int = 2) -> int:
-    """Bytes of the step's KV write: read k and v rows (2 bytes per element), write them
+    """Bytes of the step's KV write: read k and v rows (the model's element size), write them
     (``kv_bytes`` per element), read the slots."""
     rows = sum(min(cfg.new_tokens, n) for n in cfg.lengths)
-    return 2 * rows * cfg.kv_heads * cfg.head_dim * (2 + kv_bytes) + 8 * rows
+    return 2 * rows * cfg.kv_heads * cfg.head_dim * (cfg.dtype.itemsize + kv_bytes) + 8 * rows
 
 
 def sample_rows(step: Step, rows: list[int]) -> dict[str, np.ndarray]:

@@ -17,6 +17,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3] [--no-cp
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import statistics
@@ -63,6 +64,11 @@ def parse() -> argparse.Namespace:
                     help="cache layout (default: the one the hip backend asks the pool for)")
     ap.add_argument("--codec", choices=["raw", "fp8_e4m3"], default="raw",
                     help="KV-cache codec: 16-bit values, or fp8 e4m3 codes decoded in the kernel")
+    ap.add_argument("--fp32", action="store_true",
+                    help="only time C1-C5 as fp32 models (fp32 q, out and caches, the fp32 decode kernel), "
+                         "one JSON record each")
+    ap.add_argument("--model-dtype", choices=["config", "fp32"], default="config",
+                    help="with --record: the configuration's own dtype, or fp32 throughout")
     ap.add_argument("--qk", choices=["dpp", "mfma"], default=None,
                     help="force the q.k implementation (default: the library's choice)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -607,6 +613,12 @@ def main() -> int:
         return host_trace(args)
     if args.reference_shapes:
         return reference_shapes(args)
+    if args.fp32:
+        for index in (1, 2, 3, 4, 5):
+            args.model_dtype = "fp32"
+            rec = child_record(index, "raw", args)
+            print(json.dumps({"config": f"C{index}", "model_dtype": "fp32", **rec}), flush=True)
+        return 0
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
@@ -653,6 +665,8 @@ def child_record(index: int, codec: str, args) -> dict:
         cmd += ["--qk", args.qk]
     if args.no_cpu_baseline:
         cmd += ["--no-cpu-baseline"]
+    if args.model_dtype != "config":
+        cmd += ["--model-dtype", args.model_dtype]
     done = subprocess.run(cmd, capture_output=True, text=True, timeout=300, check=False)
     sys.stderr.write(done.stderr)
     if done.returncode != 0:
@@ -668,6 +682,9 @@ ROTATION_BYTES = 1 << 30
 
 def kernel_label(mfma: bool, split, merge: str | None, kv_bytes: int) -> str:
     """The dominant kernel of a launch, as the bench line and the profiles name it."""
+    if kv_bytes == 4:
+        what = "v1" if not split.partitions else "v2, merge reduce-kernel"
+        return f"paged_attention_f32_kernel ({what})"
     name = "paged_attention_mfma_kernel" if mfma else "paged_attention_kernel"
     what = f"v1, {split.waves} waves per head" if not split.partitions else f"v2, merge {merge}"
     return f"{name} ({what}{', fp8 cache' if kv_bytes == 1 else ''})"
@@ -688,11 +705,15 @@ def measure(index: int, args, codec: str, layout_name: str | None, headline: boo
 
     dev = torch.device("cuda:0")
     cfg = workloads.config(index)
+    if args.model_dtype == "fp32":
+        if codec != "raw" or headline:
+            raise SystemExit("fp32 models are measured per configuration (--record or --fp32), raw caches only")
+        cfg = dataclasses.replace(cfg, dtype=torch.float32)
     group = cfg.heads // cfg.kv_heads
     layout = KVLayoutKind(layout_name) if layout_name else KVLayoutKind(hip_kvcache.layout())
     step = workloads.build(cfg, dev, poison=False, layout=str(layout.value), codec=codec)
     buffers = KVBuffers(step.k_cache, step.v_cache, layout, codec)
-    kv_bytes = 1 if codec == "fp8_e4m3" else 2
+    kv_bytes = 1 if codec == "fp8_e4m3" else cfg.dtype.itemsize
     write = hip_attention.plan(ForwardMode.MIXED, step.rows_per_request, step.lengths, step.table, cfg.block_size)
     hip_kvcache.store(step.k_new, step.v_new, buffers, write)
     meta = hip_attention.plan(ForwardMode.DECODE, torch.ones(cfg.batch, dtype=torch.int32, device=dev),
@@ -712,7 +733,7 @@ def measure(index: int, args, codec: str, layout_name: str | None, headline: boo
     auto = meta.plan.split_for(cfg.kv_heads, group, kv_bytes)  # what attend will launch
     mfma = args.qk == "mfma" or (args.qk is None and (hip_attention.uses_matrix_cores(group) or kv_bytes == 1
                                                       or (auto.partitions == 0 and auto.waves > 1)))
-    merge = None if not auto.partitions else \
+    merge = None if not auto.partitions else "reduce-kernel" if kv_bytes == 4 else \
         hip_attention.merge_site(cfg.kv_heads, group, meta.plan, auto.partition_size)
     kernel = kernel_label(mfma, auto, merge, kv_bytes)
 
