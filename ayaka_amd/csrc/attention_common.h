@@ -177,26 +177,51 @@ struct WgCoord {
   int row;
   int group;
   int part;
+  int psize;  // v2: the partition size (the launch's, or the one staged for this step)
 };
-
-// A workgroup's (row, head group, partition). With staged parameters the grid is an
-// upper bound: workgroups past the staged item count get row -1 and do nothing.
-__device__ __forceinline__ WgCoord wg_coord(const AttnParams& p, int groups, bool split) {
-  int id = blockIdx.x;
-  if (split && p.work) {
-    const int item = id / groups;
-    if (p.staged && item >= p.staged[1]) return WgCoord{-1, 0, 0};
-    return WgCoord{p.work[2 * item], id % groups, p.work[2 * item + 1]};
-  }
-  const int parts = split ? p.max_partitions : 1;
-  const int part = id % parts;
-  id /= parts;
-  return WgCoord{id / groups, id % groups, part};
-}
 
 // The v2 partition size: the launch's, or the one staged on the device for this step.
 __device__ __forceinline__ int partition_size_of(const AttnParams& p) {
   return p.staged ? p.staged[0] : p.partition_size;
+}
+
+// A workgroup's (row, head group, partition). With staged parameters the grid is an
+// upper bound: workgroups past the staged item count get row -1 and do nothing. The item's
+// entry (one exists for every workgroup of the grid: the list's capacity bounds it), the
+// staged count and the staged partition size are read unconditionally -- the last two from
+// a valid stand-in address when nothing is staged -- so they cost one round trip together.
+__device__ __forceinline__ WgCoord wg_coord(const AttnParams& p, int groups, bool split) {
+  int id = blockIdx.x;
+  if (split && p.work) {
+    const int item = id / groups;
+    const int32_t* st = p.staged ? p.staged : p.work;
+    const int row = p.work[2 * item], part = p.work[2 * item + 1];
+    const int size = st[0], count = st[1];
+    // a select, not an early return: the row and the count are then needed together
+    const bool past = p.staged && item >= count;
+    return WgCoord{past ? -1 : row, id % groups, part, p.staged ? size : p.partition_size};
+  }
+  const int parts = split ? p.max_partitions : 1;
+  const int part = id % parts;
+  id /= parts;
+  const int size = *(p.staged ? p.staged : p.kv_lengths);  // a valid stand-in address without staging
+  return WgCoord{id / groups, id % groups, part, split ? (p.staged ? size : p.partition_size) : 0};
+}
+
+// The request of row `row` (row n is request n without a request_of_row list).
+__device__ __forceinline__ int row_request(const AttnParams& p, int row) {
+  if (p.request_of_row) return p.request_of_row[row];  // uniform: decode launches load nothing
+  return row;
+}
+
+// Length of row `row`'s context (request `req`), clamped so no read leaves the table. The
+// row's position is read unconditionally (from a valid stand-in address when rows have none)
+// beside the request's length.
+__device__ __forceinline__ int row_length(const AttnParams& p, int row, int req) {
+  const int pos = *(p.positions ? p.positions + row : p.kv_lengths);
+  int len = p.kv_lengths[req];
+  if (len > 0 && p.positions) len = min(len, pos + 1);
+  return max(0, min(len, p.max_len));
 }
 
 // Length of row `row`'s context and its request, clamped so no read leaves the table.
@@ -417,6 +442,48 @@ __device__ __forceinline__ int stage_table(const AttnParams& p, const int32_t* t
   for (int i = tid; i < nb; i += threads) s_tbl[i] = table_entry(p, tbl[b0 + i]);
   __syncthreads();
   return b0;
+}
+
+// The first table segment of a context, read before the row's length is known: the blocks of
+// positions [t_begin, t_begin + span), cut at the table's last block (max_len), PF entries per
+// thread (entries past PF x threads are read by commit_table). Issued beside the length's load,
+// it takes the table's round trip off the chain that precedes the first K/V load.
+template <int PF>
+struct TableAhead {
+  int32_t e[PF];  // block ids as read (converted at commit_table, so nothing waits for them here)
+  int b0;
+  int n;
+};
+
+template <int PF>
+__device__ __forceinline__ void table_ahead(const AttnParams& p, const int32_t* tbl, int t_begin, int span, int tid,
+                                            int threads, TableAhead<PF>& a) {
+  const int tb = imin(t_begin, p.max_len);
+  const int64_t end = (int64_t)tb + span;
+  const int64_t last = (end < p.max_len ? end : (int64_t)p.max_len) - 1;
+  a.b0 = block_of(p, tb);
+  a.n = last >= tb ? block_of(p, (int)last) - a.b0 + 1 : 0;
+#pragma unroll
+  for (int k = 0; k < PF; ++k) {
+    const int i = tid + k * threads;
+    a.e[k] = i < a.n ? tbl[a.b0 + i] : 0;
+  }
+}
+
+// Stage the prefetched first segment [s0, s1) (s0 the prefetch's t_begin, s1 within its span)
+// in LDS, as stage_table does; returns its first block index.
+template <int PF>
+__device__ __forceinline__ int commit_table(const AttnParams& p, const int32_t* tbl, uint32_t* s_tbl,
+                                            const TableAhead<PF>& a, int s1, int tid, int threads) {
+  const int nb = block_of(p, s1 - 1) - a.b0 + 1;
+#pragma unroll
+  for (int k = 0; k < PF; ++k) {
+    const int i = tid + k * threads;
+    if (i < nb) s_tbl[i] = table_entry(p, a.e[k]);
+  }
+  for (int i = tid + PF * threads; i < nb; i += threads) s_tbl[i] = table_entry(p, tbl[a.b0 + i]);
+  __syncthreads();
+  return a.b0;
 }
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));

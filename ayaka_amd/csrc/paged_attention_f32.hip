@@ -47,10 +47,17 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
   const int c = lane % LPT;
   float* out = static_cast<float*>(p.out);
 
-  int req, len;
-  row_context(p, row, req, len);
+  const int psize = SPLIT ? wg.psize : 0;
+  // positions per staged table segment: at most kTableCap blocks, whatever s0's offset
+  const int seg_len = segment_positions(p, CH);
+  // the row's request, then its first table segment (known from the partition alone) and its
+  // length together
+  const int req = row_request(p, row);
+  const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
+  TableAhead<2> ahead;
+  table_ahead(p, tbl, SPLIT ? wg.part * psize : 0, SPLIT ? imin(psize, seg_len) : seg_len, tid, threads, ahead);
+  const int len = row_length(p, row, req);
   int t_begin = 0, t_end = len;
-  const int psize = SPLIT ? partition_size_of(p) : 0;
   const int np = SPLIT ? (len > 0 ? (len - 1) / psize + 1 : 0) : 1;  // partitions with tokens
   if constexpr (SPLIT) {
     t_begin = wg.part * psize;
@@ -79,8 +86,6 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
     o[g] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
-  const int seg_len = segment_positions(p, CH);
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const float* kbase = reinterpret_cast<const float*>(p.k_cache) + (int64_t)kvh * p.head_stride + c * 4;
@@ -88,7 +93,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
 
   for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
     const int s1 = imin(t_end, s0 + seg_len);
-    const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, threads);
+    const int b0 = s0 == t_begin ? commit_table(p, tbl, s_tbl, ahead, s1, tid, threads)
+                                 : stage_table(p, tbl, s_tbl, s0, s1, tid, threads);
     if (!active) continue;
     const int nch = (s1 - s0 + CH - 1) / CH;
 

@@ -102,7 +102,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     const int item = blockIdx.x / groups;
     win_first = p.work[4 * item];
     win_rows = p.work[4 * item + 1];
-    wg = WgCoord{p.work[4 * item + 2], (int)(blockIdx.x % groups), p.work[4 * item + 3]};
+    const int size = *(p.staged ? p.staged : p.work);  // a valid stand-in address without staging
+    wg = WgCoord{p.work[4 * item + 2], (int)(blockIdx.x % groups), p.work[4 * item + 3],
+                 SPLIT ? (p.staged ? size : p.partition_size) : 0};
   } else {
     wg = wg_coord(p, groups, SPLIT);
     if (wg.row < 0) return;  // past the staged work items (uniform per workgroup)
@@ -139,11 +141,20 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
     // the tile's last row sees the most; nothing past it is read (a negative position
     // leaves nothing to read: the tile's rows get zeros, as row_context gives them)
     if (len > 0) len = max(0, min(len, p.positions[win_first + win_rows - 1] + 1));
-  } else {
-    row_context(p, row, req, len);
+  }
+  const int psize = SPLIT ? wg.psize : 0;
+  // positions per staged table segment: at most kTableCap blocks, whatever s0's offset
+  const int seg_len = segment_positions(p, CH);
+  // Decode rows: the request, then its first table segment and its length together (the
+  // segment is known from the partition alone).
+  TableAhead<2> ahead;
+  if constexpr (!WIN) {
+    req = row_request(p, row);
+    table_ahead(p, p.block_table + (int64_t)req * p.table_stride, SPLIT ? wg.part * psize : 0,
+                SPLIT ? min(psize, seg_len) : seg_len, tid, threads, ahead);
+    len = row_length(p, row, req);
   }
   int t_begin = 0, t_end = len;
-  const int psize = SPLIT ? partition_size_of(p) : 0;
   const int np = SPLIT ? (len > 0 ? (len - 1) / psize + 1 : 0) : 1;  // partitions with tokens
   if constexpr (WIN) {
     if (len == 0 || (SPLIT && wg.part * psize >= len)) {
@@ -188,8 +199,6 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
   for (int t = 0; t < DT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int32_t* tbl = p.block_table + (int64_t)req * p.table_stride;
-  // positions per staged table segment: at most kTableCap blocks, whatever s0's offset
-  const int seg_len = segment_positions(p, CH);
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
   const uint16_t* kbase = kv_at<KV8>(p.k_cache, (int64_t)kvh * p.head_stride + c * 8);
@@ -197,7 +206,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
 
   for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
     const int s1 = min(t_end, s0 + seg_len);
-    const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, threads);
+    const int b0 = (!WIN && s0 == t_begin) ? commit_table(p, tbl, s_tbl, ahead, s1, tid, threads)
+                                           : stage_table(p, tbl, s_tbl, s0, s1, tid, threads);
     const int nch = (s1 - s0 + CH - 1) / CH;
     if (!active || slice >= nch) continue;
     // this wave's chunks: slice, slice + ws, ..., up to `last`
