@@ -6,7 +6,8 @@ backend's ops, and once directly with ctypes). Bars:
 * KV write and block ops: bit-exact.
 * Attention: against the float64 oracle, ``max_abs_excess`` (error beyond half
   an output ulp) <= 2e-3 and ``rel_l2`` (against the oracle rounded once to the
-  output dtype) <= 1e-3; plus the reference tests' own bound
+  output dtype) <= 1e-3 (or a raw relative L2 within 1e-4 of the once-rounded
+  oracle's own, for outputs whose excess is only rounding flips); plus the reference tests' own bound
   ``|out - exact| <= 4 eps max|y|`` (``tests/ops/test_parity.py:196-201``).
   The oracle's own rounded fp32 result is held to the same metrics and reported.
 """
@@ -57,7 +58,14 @@ def assert_parity(out: torch.Tensor, expected: np.ndarray, dtype: str, label: st
     bound = 4 * EPS[dtype] * float(np.abs(expected).max(initial=0.0))
     worst = float(np.abs(got - expected).max(initial=0.0))
     assert rep["max_abs_excess"] <= 2e-3, f"{label}: {rep} (reference rounding: {ref})"
-    assert rep["rel_l2"] <= 1e-3, f"{label}: {rep} (reference rounding: {ref})"
+    # rel_l2 counts every rounding flip at a full ulp. On an output of a few hundred elements, a
+    # handful of values within a hair of a rounding midpoint can flip and carry it past 1e-3
+    # while the output is as close to the exact result as the oracle rounded once (sweep case
+    # 29207: raw 1.74052e-3 against 1.74048e-3). Such an output passes when its raw distance from
+    # the exact result is within 1e-4 of the once-rounded oracle's; a real excess (one bf16
+    # weight per P.V product: raw ~2.3e-3 against ~1.6e-3) still fails.
+    assert rep["rel_l2"] <= 1e-3 or rep["rel_l2_raw"] <= ref["rel_l2_raw"] + 1e-4, \
+        f"{label}: {rep} (reference rounding: {ref})"
     assert worst <= max(bound, 1e-6), f"{label}: {worst} > 4 eps max|y| = {bound}"
     return rep
 

@@ -9,7 +9,8 @@ random ones. Every case runs the library's own launch and forced ones: v1 at a r
 v2 at a random partition size and merge site (decode), the multi-row kernel at a random tile size
 and partition size, and the window launch where the step allows it (multi-row). Each output is
 held to the parity suite's bar (``max_abs_excess`` <= 2e-3, ``rel_l2`` <= 1e-3 against the
-oracle, and the reference tests' 4 eps max|y|), padding rows must be zero, and a forced launch
+oracle or a raw error within 1e-4 of the once-rounded oracle's, and the reference tests' 4 eps
+max|y|), padding rows must be zero, and a forced launch
 the library refuses must be refused before any kernel runs (a ``BackendError``).
 """
 
@@ -87,7 +88,7 @@ def launches(d: dict, meta) -> list[tuple[str, dict]]:
     return out
 
 
-@pytest.mark.parametrize("case", range(CASES))
+@pytest.mark.parametrize("case", [*range(CASES), 29207])  # 29207: one row of 512 outputs, rounding flips
 def test_sweep(case: int) -> None:
     d = draw(case)
     s = build_scenario(d["steps"], dtype=d["dtype"], layout=d["layout"], heads=d["heads"], kv_heads=d["kv_heads"],
