@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0
 # the one profiled: (config, kernel, partition size) -> (read bytes, write bytes, summary).
 PROFILED_TRAFFIC = {
     (3, "paged_attention_mfma_kernel (v1, 4 waves per head)", 0):
-        (1_080_070_645, 524_288, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
+        (1_080_177_728, 524_288, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode.md"),
     (3, "paged_attention_mfma_kernel (v1, 4 waves per head, fp8 cache)", 0):
         (544_024_803, 524_288, "profiles/paged_attention_mfma_kernel_c3_llama3_8b_decode_fp8_cache.md"),
     (4, "paged_attention_mfma_kernel (v2, merge reduce-kernel)", 704):
