@@ -15,6 +15,9 @@
 namespace ayk {
 
 #define AYK_HD __host__ __device__ __forceinline__
+#ifndef AYK_F32_WIDE_GC
+#define AYK_F32_WIDE_GC 4
+#endif
 
 AYK_HD int imin(int a, int b) { return a < b ? a : b; }
 AYK_HD int imax(int a, int b) { return a > b ? a : b; }
@@ -105,9 +108,13 @@ constexpr int positions_per_load(int d) { return 64 / pieces_per_position(d); }
 constexpr int dpp_loads_per_chunk() { return 2; }
 
 // Decode over fp32 caches: 4 floats (16 bytes) per lane, so D / 4 lanes per position, and four
-// loads per lane per chunk.
-constexpr int f32_lanes_per_position(int d) { return d / 4; }
-constexpr int f32_loads_per_chunk() { return 4; }
+// token slots per lane and chunk; with more than AYK_F32_WIDE_GC query heads per wave 8 floats
+// (two adjacent 16-byte loads) per lane, D / 8 lanes per position and two token slots, which
+// halves the lane reductions per byte (measured: 8 heads per wave 1060 -> 987 us at C5's shape,
+// 4 heads 321 -> 351 us at C3's, so 4 heads keep the narrow rows).
+constexpr int f32_floats_per_lane(int gc) { return AYK_F32_WIDE_GC < gc ? 8 : 4; }
+constexpr int f32_lanes_per_position(int d, int gc) { return d / f32_floats_per_lane(gc); }
+constexpr int f32_loads_per_chunk(int gc) { return f32_floats_per_lane(gc) == 8 ? 2 : 4; }
 
 // Multi-row kernel: 64-position chunks, or 32 at head_dim 256 with 1 or 2 waves per pair group
 // (a 64-position stage there took 133 KB of LDS and left one wave per SIMD).

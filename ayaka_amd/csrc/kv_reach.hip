@@ -94,10 +94,11 @@ struct KvElems {
   static constexpr int load = kv_load_bytes<KV8>();
   static constexpr int per_lane = 8;  // elements a lane's piece covers
 };
-struct F32Elems {
+template <int F>
+struct F32Elems {  // F floats per lane, read as F / 4 adjacent 16-byte loads: one 4F-byte range
   static int64_t bytes(int64_t elem) { return 4 * elem; }
-  static constexpr int load = 16;
-  static constexpr int per_lane = 4;
+  static constexpr int load = 4 * F;
+  static constexpr int per_lane = F;
 };
 
 // The loads of one wave of a decode launch (the matrix-core kernel, its window launch, the
@@ -202,11 +203,12 @@ void walk_dpp(const AttnParams& p, bool split) {
     }
 }
 
-template <int D>
+template <int D, int GC>
 void walk_f32_d(const AttnParams& p, bool split) {
-  constexpr int LPT = f32_lanes_per_position(D);
+  constexpr int F = f32_floats_per_lane(GC);
+  constexpr int LPT = f32_lanes_per_position(D, GC);
   constexpr int TPL = 64 / LPT;
-  constexpr int CH = TPL * f32_loads_per_chunk();
+  constexpr int CH = TPL * f32_loads_per_chunk(GC);
   std::vector<uint32_t> buffer;
   for (const Item& it : decode_items(p, split))
     for (int vh = 0; vh < p.num_virtual_heads; ++vh) {
@@ -218,7 +220,7 @@ void walk_f32_d(const AttnParams& p, bool split) {
         t_begin = it.part * psize;
         t_end = imin(len, t_begin + psize);
       }
-      walk_wave<F32Elems>(p, req, t_begin, t_end, vh / p.head_chunks, 0, 1, CH, TPL, LPT, f32_loads_per_chunk(),
+      walk_wave<F32Elems<F>>(p, req, t_begin, t_end, vh / p.head_chunks, 0, 1, CH, TPL, LPT, f32_loads_per_chunk(GC),
                           false, buffer);
     }
 }
@@ -296,12 +298,19 @@ void walk_decode(const AttnParams& p, int head_dim, bool mfma, bool kv8, bool sp
   }
 }
 
-void walk_f32(const AttnParams& p, int head_dim, bool split) {
+template <int GC>
+void walk_f32_gc(const AttnParams& p, int head_dim, bool split) {
   switch (head_dim) {
-    case 64: walk_f32_d<64>(p, split); break;
-    case 128: walk_f32_d<128>(p, split); break;
-    default: walk_f32_d<256>(p, split); break;
+    case 64: walk_f32_d<64, GC>(p, split); break;
+    case 128: walk_f32_d<128, GC>(p, split); break;
+    default: walk_f32_d<256, GC>(p, split); break;
   }
+}
+
+void walk_f32(const AttnParams& p, int head_dim, bool split) {
+  // the kernel's lane geometry depends only on whether its heads per wave take the wide rows
+  if (f32_floats_per_lane(p.group / p.head_chunks) == 8) walk_f32_gc<8>(p, head_dim, split);
+  else walk_f32_gc<1>(p, head_dim, split);
 }
 
 void walk_prefill(const AttnParams& p, const int32_t* tiles, int n_tiles, int head_dim, bool kv8,

@@ -23,10 +23,13 @@ namespace ayk {
 
 template <int D, int GC, bool SPLIT>
 __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(const AttnParams p) {
-  constexpr int LPT = f32_lanes_per_position(D);  // lanes per token, 4 floats each
+  constexpr int F = f32_floats_per_lane(GC);       // floats of a token a lane reads (4 or 8)
+  constexpr int FQ = F / 4;                        // its 16-byte loads
+  constexpr int LPT = f32_lanes_per_position(D, GC);  // lanes per token
   constexpr int TPL = kWave / LPT;                 // tokens per load instruction
-  constexpr int NLD = f32_loads_per_chunk();
+  constexpr int NLD = f32_loads_per_chunk(GC);     // token slots per lane and chunk
   constexpr int CH = TPL * NLD;                    // tokens per chunk
+  typedef f32x4 Row[FQ];
 
   __shared__ uint32_t s_tbl[kTableCap];
 
@@ -68,28 +71,33 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
     if (len == 0 && wg.part == 0 && active && r == 0) {
 #pragma unroll
       for (int g = 0; g < GC; ++g)
-        *reinterpret_cast<f32x4*>(out + ((int64_t)row * p.num_heads + h0 + g) * D + c * 4) = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < FQ; ++u)
+          *reinterpret_cast<f32x4*>(out + ((int64_t)row * p.num_heads + h0 + g) * D + c * F + 4 * u) =
+              f32x4{0.f, 0.f, 0.f, 0.f};
     }
     return;
   }
 
-  f32x4 qv[GC];
+  Row qv[GC], o[GC];
   float m[GC], l[GC];
-  f32x4 o[GC];
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
-    qv[g] = active ? *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p.q) +
-                                                     ((int64_t)row * p.num_heads + h0 + g) * D + c * 4)
-                   : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < FQ; ++u) {
+      qv[g][u] = active ? *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(p.q) +
+                                                          ((int64_t)row * p.num_heads + h0 + g) * D + c * F + 4 * u)
+                        : f32x4{0.f, 0.f, 0.f, 0.f};
+      o[g][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     m[g] = kNoScore;
     l[g] = 0.f;
-    o[g] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
   const uint32_t token_stride = (uint32_t)p.token_stride;
   const float scale_log2 = p.scale_log2;
-  const float* kbase = reinterpret_cast<const float*>(p.k_cache) + (int64_t)kvh * p.head_stride + c * 4;
-  const float* vbase = reinterpret_cast<const float*>(p.v_cache) + (int64_t)kvh * p.head_stride + c * 4;
+  const float* kbase = reinterpret_cast<const float*>(p.k_cache) + (int64_t)kvh * p.head_stride + c * F;
+  const float* vbase = reinterpret_cast<const float*>(p.v_cache) + (int64_t)kvh * p.head_stride + c * F;
 
   for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
     const int s1 = imin(t_end, s0 + seg_len);
@@ -103,11 +111,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
       for (int j = 0; j < NLD; ++j)
         dst[j] = kv_offset(p, s_tbl, b0, chunk_position(s0, s1, ci, CH, j, TPL, r), token_stride);
     };
-    auto load = [](const float* base, uint32_t off) {
-      return __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base + off));
+    auto load = [](const float* base, uint32_t off, Row& dst) {
+#pragma unroll
+      for (int u = 0; u < FQ; ++u) dst[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base + off) + u);
     };
 
-    auto consume = [&](int ci, const f32x4(&kc)[NLD], const f32x4(&vc)[NLD]) {
+    auto consume = [&](int ci, const Row(&kc)[NLD], const Row(&vc)[NLD]) {
       const int tb = s0 + ci * CH;
       const bool tail = tb + CH > s1;
       float s[NLD][GC];
@@ -115,10 +124,18 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
       for (int j = 0; j < NLD; ++j)
 #pragma unroll
         for (int g = 0; g < GC; ++g) {
-          float a = qv[g].x * kc[j].x;
-          a = fmaf(qv[g].y, kc[j].y, a);
-          a = fmaf(qv[g].z, kc[j].z, a);
-          s[j][g] = fmaf(qv[g].w, kc[j].w, a);
+          float a = qv[g][0].x * kc[j][0].x;
+          a = fmaf(qv[g][0].y, kc[j][0].y, a);
+          a = fmaf(qv[g][0].z, kc[j][0].z, a);
+          a = fmaf(qv[g][0].w, kc[j][0].w, a);
+#pragma unroll
+          for (int u = 1; u < FQ; ++u) {
+            a = fmaf(qv[g][u].x, kc[j][u].x, a);
+            a = fmaf(qv[g][u].y, kc[j][u].y, a);
+            a = fmaf(qv[g][u].z, kc[j][u].z, a);
+            a = fmaf(qv[g][u].w, kc[j][u].w, a);
+          }
+          s[j][g] = a;
         }
       // Sum over the token's LPT lanes, one stage at a time across all the partial sums.
 #pragma unroll
@@ -133,10 +150,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
       for (int j = 0; j < NLD; ++j)
 #pragma unroll
         for (int g = 0; g < GC; ++g) s[j][g] += dpp<0x141>(s[j][g]);  // the other quad of 8
+      if constexpr (LPT >= 16) {
 #pragma unroll
-      for (int j = 0; j < NLD; ++j)
+        for (int j = 0; j < NLD; ++j)
 #pragma unroll
-        for (int g = 0; g < GC; ++g) s[j][g] += dpp<0x140>(s[j][g]);  // the other 8 of 16
+          for (int g = 0; g < GC; ++g) s[j][g] += dpp<0x140>(s[j][g]);  // the other 8 of 16
+      }
       if constexpr (LPT >= 32) {
 #pragma unroll
         for (int j = 0; j < NLD; ++j)
@@ -170,48 +189,53 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
           const float mn = fmaxf(m[g], mx[g]);
           const float alpha = fast_exp2(m[g] - mn);
           l[g] *= alpha;
-          o[g] *= alpha;
+#pragma unroll
+          for (int u = 0; u < FQ; ++u) o[g][u] *= alpha;
           m[g] = mn;
         }
       }
 #pragma unroll
       for (int j = 0; j < NLD; ++j) {
         // a slot past the context may hold anything, NaN included, and 0 * NaN is NaN
-        const f32x4 v = (tail && tb + j * TPL + r >= s1) ? f32x4{0.f, 0.f, 0.f, 0.f} : vc[j];
+        const bool past = tail && tb + j * TPL + r >= s1;
 #pragma unroll
         for (int g = 0; g < GC; ++g) {
           const float w = fast_exp2(s[j][g] - m[g]);
           l[g] += w;
-          o[g].x = fmaf(w, v.x, o[g].x);
-          o[g].y = fmaf(w, v.y, o[g].y);
-          o[g].z = fmaf(w, v.z, o[g].z);
-          o[g].w = fmaf(w, v.w, o[g].w);
+#pragma unroll
+          for (int u = 0; u < FQ; ++u) {
+            const f32x4 v = past ? f32x4{0.f, 0.f, 0.f, 0.f} : vc[j][u];
+            o[g][u].x = fmaf(w, v.x, o[g][u].x);
+            o[g][u].y = fmaf(w, v.y, o[g][u].y);
+            o[g][u].z = fmaf(w, v.z, o[g][u].z);
+            o[g][u].w = fmaf(w, v.w, o[g][u].w);
+          }
         }
       }
     };
 
     uint32_t offA[NLD], offB[NLD];
-    f32x4 kA[NLD], kB[NLD], vc[NLD];
+    Row kA[NLD], kB[NLD], vc[NLD];
     int ci = 0;
     offsets(0, offA);
 #pragma unroll
-    for (int j = 0; j < NLD; ++j) kA[j] = load(kbase, offA[j]);
+    for (int j = 0; j < NLD; ++j) load(kbase, offA[j], kA[j]);
     while (ci < nch) {
 #pragma unroll
-      for (int j = 0; j < NLD; ++j) vc[j] = load(vbase, offA[j]);
+      for (int j = 0; j < NLD; ++j) load(vbase, offA[j], vc[j]);
       if (ci + 1 < nch) {
         offsets(ci + 1, offB);
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) kB[j] = load(kbase, offB[j]);
+        for (int j = 0; j < NLD; ++j) load(kbase, offB[j], kB[j]);
       }
       consume(ci, kA, vc);
       if (++ci >= nch) break;
 #pragma unroll
-      for (int j = 0; j < NLD; ++j) vc[j] = load(vbase, offB[j]);
+      for (int j = 0; j < NLD; ++j) load(vbase, offB[j], vc[j]);
       if (ci + 1 < nch) {
         offsets(ci + 1, offA);
 #pragma unroll
-        for (int j = 0; j < NLD; ++j) kA[j] = load(kbase, offA[j]);
+        for (int j = 0; j < NLD; ++j) load(kbase, offA[j], kA[j]);
       }
       consume(ci, kB, vc);
       ++ci;
@@ -230,10 +254,13 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
       const float b = fast_exp2(m2 - mn);
       l[g] = l[g] * a + l2 * b;
       m[g] = mn;
-      o[g].x = o[g].x * a + __shfl_xor(o[g].x, st) * b;
-      o[g].y = o[g].y * a + __shfl_xor(o[g].y, st) * b;
-      o[g].z = o[g].z * a + __shfl_xor(o[g].z, st) * b;
-      o[g].w = o[g].w * a + __shfl_xor(o[g].w, st) * b;
+#pragma unroll
+      for (int u = 0; u < FQ; ++u) {
+        o[g][u].x = o[g][u].x * a + __shfl_xor(o[g][u].x, st) * b;
+        o[g][u].y = o[g][u].y * a + __shfl_xor(o[g][u].y, st) * b;
+        o[g][u].z = o[g][u].z * a + __shfl_xor(o[g][u].z, st) * b;
+        o[g][u].w = o[g][u].w * a + __shfl_xor(o[g][u].w, st) * b;
+      }
     }
   }
   if (r != 0) return;
@@ -243,13 +270,16 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_f32_kernel(
     const float inv = (l[g] > 0.f ? 1.0f / l[g] : 0.f) * p.v_scale;
     if (SPLIT && np > 1) {
       const int64_t slot = partial_index(p, row, head, np) + wg.part;
-      *reinterpret_cast<f32x4*>(p.part_o + slot * D + c * 4) = o[g] * inv;
+#pragma unroll
+      for (int u = 0; u < FQ; ++u) *reinterpret_cast<f32x4*>(p.part_o + slot * D + c * F + 4 * u) = o[g][u] * inv;
       if (c == 0) {
         p.part_ml[slot * 2] = m[g];
         p.part_ml[slot * 2 + 1] = l[g];
       }
     } else {
-      *reinterpret_cast<f32x4*>(out + ((int64_t)row * p.num_heads + head) * D + c * 4) = o[g] * inv;
+#pragma unroll
+      for (int u = 0; u < FQ; ++u)
+        *reinterpret_cast<f32x4*>(out + ((int64_t)row * p.num_heads + head) * D + c * F + 4 * u) = o[g][u] * inv;
     }
   }
 }
