@@ -398,6 +398,18 @@ def test_table_segments(block_size: int) -> None:
                       f"bs{block_size}/windows/{launch}")
 
 
+@pytest.mark.parametrize("heads,qk", [(1, "dpp"), (4, "mfma")])
+def test_first_table_segment_wider_than_its_prefetch(heads: int, qk: str) -> None:
+    # One key/value head makes one-wave (64-thread) workgroups, whose read-ahead of the first
+    # table segment covers 128 entries; with blocks of one position that segment holds 511, so
+    # the rest are read when it is staged. v1 over whole contexts, v2 over partitions of 1024.
+    s = build_scenario([(1, 1300), (1, 700), (1, 129), (1, 0), (1, 1024)], block_size=1, head_dim=128, heads=heads,
+                       kv_heads=1, mode="decode", seed=46)
+    expected = s.expected(np.float64)
+    for launch in (dict(partitions=0, waves=1), dict(partitions=2, partition_size=1024)):
+        assert_parity(run_attention(s, qk=qk, **launch), expected, "bf16", f"{qk}/{launch}")
+
+
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("head_dim", [64, 128, 256])
 @pytest.mark.parametrize("qk", QK)
