@@ -537,12 +537,14 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   if (dtype == AYK_DTYPE_FP32)
     return fail(AYK_ERR_UNSUPPORTED, "%s: fp32 runs on the decode entry points, row by row", op);
   // Tiles of the full capacity, or of a half or a quarter (2 or 4 waves then share
-  // each group of pairs and split its chunks).
+  // each group of pairs and split its chunks), or at head_dim 128 and 256 of twice it (an
+  // 8-wave workgroup; waves_per_group 0 below).
   const int full_pairs = ayk::prefill_tile_pairs_for(head_dim);
-  const int waves_per_group = tile_pairs > 0 && full_pairs % tile_pairs == 0 ? full_pairs / tile_pairs : 0;
-  if (waves_per_group != 1 && waves_per_group != 2 && waves_per_group != 4)
-    return fail(AYK_ERR_ARGUMENT, "%s: tile_pairs %d is not %d, %d or %d", op, tile_pairs, full_pairs,
-                full_pairs / 2, full_pairs / 4);
+  const bool twice = head_dim != 64 && tile_pairs == 2 * full_pairs;
+  const int waves_per_group = twice ? 0 : tile_pairs > 0 && full_pairs % tile_pairs == 0 ? full_pairs / tile_pairs : -1;
+  if (waves_per_group != 0 && waves_per_group != 1 && waves_per_group != 2 && waves_per_group != 4)
+    return fail(AYK_ERR_ARGUMENT, "%s: tile_pairs %d is not %d, %d or %d%s", op, tile_pairs, full_pairs,
+                full_pairs / 2, full_pairs / 4, head_dim != 64 ? " (or twice the first)" : "");
   if (p.group > tile_pairs)
     return fail(AYK_ERR_UNSUPPORTED, "%s: %d query heads per key/value head exceed a tile of %d", op, p.group,
                 tile_pairs);

@@ -225,13 +225,12 @@ void walk_f32_d(const AttnParams& p, bool split) {
     }
 }
 
-template <int D, bool KV8, int PS, int N>
+template <int D, bool KV8, int PS, int N, int THREADS>
 void walk_prefill_typed(const AttnParams& p, const int32_t* tiles, int n_tiles) {
   constexpr int CH = prefill_chunk_positions(D, PS);
   constexpr int CPT = pieces_per_position(D);
-  constexpr int THREADS = 256;
   static_assert(CH * CPT == N * THREADS, "a chunk's pieces, N per thread");
-  const int tile_pairs = prefill_tile_pairs_for(D) / PS;
+  const int tile_pairs = prefill_tile_pairs_for(D) * (THREADS / 256) / PS;
   const int kv_heads = p.num_heads / p.group;
   const uint32_t token_stride = (uint32_t)p.token_stride;
   std::vector<uint32_t> buffer;
@@ -264,15 +263,18 @@ void walk_prefill_typed(const AttnParams& p, const int32_t* tiles, int n_tiles) 
   }
 }
 
-template <int D, bool KV8, int PS>
+template <int D, bool KV8, int PS, int THREADS = 256>
 void walk_prefill_ps(const AttnParams& p, const int32_t* tiles, int n_tiles) {
-  constexpr int N = prefill_chunk_positions(D, PS) * pieces_per_position(D) / 256;
-  walk_prefill_typed<D, KV8, PS, N>(p, tiles, n_tiles);
+  constexpr int N = prefill_chunk_positions(D, PS) * pieces_per_position(D) / THREADS;
+  walk_prefill_typed<D, KV8, PS, N, THREADS>(p, tiles, n_tiles);
 }
 
 template <int D, bool KV8>
 void walk_prefill_d(const AttnParams& p, const int32_t* tiles, int n_tiles, int waves_per_group) {
   switch (waves_per_group) {
+    case 0:  // the double tile: 8-wave workgroups (head_dim 128 and 256)
+      if constexpr (D != 64) walk_prefill_ps<D, KV8, 1, 512>(p, tiles, n_tiles);
+      break;
     case 1: walk_prefill_ps<D, KV8, 1>(p, tiles, n_tiles); break;
     case 2: walk_prefill_ps<D, KV8, 2>(p, tiles, n_tiles); break;
     default: walk_prefill_ps<D, KV8, 4>(p, tiles, n_tiles); break;

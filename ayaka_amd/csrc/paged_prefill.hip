@@ -42,7 +42,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kPrefillWaves = 4;
-constexpr int kPrefillThreads = kPrefillWaves * kWave;
 
 // (row, head) pairs one workgroup serves: 2 groups of 16 per wave, 1 at head_dim 256
 // (the accumulators of 2 groups would not fit the register file there).
@@ -77,13 +76,18 @@ __host__ __device__ constexpr int prefill_workgroups_per_cu(int head_dim, int wa
   return head_dim == 256 && waves_per_group == 4 ? 1 : 2;
 }
 
-template <int D, bool BF16, bool KV8, int PS>
-__global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) void paged_prefill_kernel(
+// W: waves per workgroup, kPrefillWaves, or 8 for the double tile (head_dim 128 and 256, one
+// workgroup per CU): one stage of each chunk then serves 8 waves' pairs, which halves the
+// staging loads, LDS writes and barrier per pair (4 x 512 rows over 4K, settled: 174.5 -> 171.5
+// us; GQA 8 335 -> 322; fp16 140 -> 135; head_dim 256 208 -> 193).
+template <int D, bool BF16, bool KV8, int PS, int W = kPrefillWaves>
+__global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D, PS)) void paged_prefill_kernel(
     const AttnParams p, const int32_t* tiles) {
-  constexpr int THREADS = kPrefillThreads;
+  static_assert(W == kPrefillWaves || (W == 8 && PS == 1 && D != 64), "the double tile: 8 waves, one per pair group");
+  constexpr int THREADS = W * kWave;
   constexpr int PT = D == 256 ? 1 : 2;          // 16-pair groups per wave
-  constexpr int PGROUPS = kPrefillWaves / PS;   // waves with distinct pairs
-  constexpr int TILE_PAIRS = prefill_tile_pairs(D) / PS;
+  constexpr int PGROUPS = W / PS;               // waves with distinct pairs
+  constexpr int TILE_PAIRS = prefill_tile_pairs(D) * (W / kPrefillWaves) / PS;
   // Positions per chunk: 64, or 32 at head_dim 256 with 1 or 2 waves per pair group, where a
   // 64-position stage (133 KB of LDS) and its load registers left one wave per SIMD; 32 fit
   // two workgroups per CU without spills (quarter tiles need 16 positions per wave: 64).
@@ -94,7 +98,7 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
   constexpr int DT = D / 16;                    // 16-element slices of head_dim for P.V
   constexpr int CPT = pieces_per_position(D);   // 8-element pieces per position
   constexpr int PIECES = CH * CPT;              // pieces per chunk of K (or V)
-  constexpr int PER_THREAD = PIECES / THREADS;  // 2 (D 64), 4 (D 128), 4 or 8 (D 256)
+  constexpr int PER_THREAD = PIECES / THREADS;  // 2 (D 64), 4 (D 128), 4 or 8 (D 256); half with 8 waves
   // Values in LDS token-major, rows VP elements apart: the transposing reads of the
   // P.V operand (16 rows of one 16-lane group, 8 bytes each) then cover the banks evenly.
   constexpr int VP = D + 16;
@@ -457,24 +461,29 @@ __global__ __launch_bounds__(kPrefillThreads, prefill_workgroups_per_cu(D, PS)) 
   }
 }
 
-template <int D, int PS>
+template <int D, int PS, int W = kPrefillWaves>
 static hipError_t launch_prefill_ps(const AttnParams& p, const int32_t* tiles, dim3 grid, bool bf16, bool kv8,
                                     hipStream_t stream) {
-  const dim3 block(kPrefillThreads);
+  const dim3 block(W * kWave);
   if (kv8) {
-    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, true, PS>), grid, block, 0, stream, p, tiles);
-    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, true, PS>), grid, block, 0, stream, p, tiles);
+    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, true, PS, W>), grid, block, 0, stream, p, tiles);
+    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, true, PS, W>), grid, block, 0, stream, p, tiles);
   } else {
-    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, false, PS>), grid, block, 0, stream, p, tiles);
-    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, false, PS>), grid, block, 0, stream, p, tiles);
+    if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, false, PS, W>), grid, block, 0, stream, p, tiles);
+    else hipLaunchKernelGGL((paged_prefill_kernel<D, false, false, PS, W>), grid, block, 0, stream, p, tiles);
   }
   return hipGetLastError();
 }
 
+// waves_per_group 1, 2, 4: tiles of the full capacity, a half, a quarter (4-wave workgroups);
+// 0: the double tile (8-wave workgroups, head_dim 128 and 256).
 template <int D>
 static hipError_t launch_prefill_d(const AttnParams& p, const int32_t* tiles, dim3 grid, bool bf16, bool kv8,
                                    int waves_per_group, hipStream_t stream) {
   switch (waves_per_group) {
+    case 0:
+      if constexpr (D != 64) return launch_prefill_ps<D, 1, 8>(p, tiles, grid, bf16, kv8, stream);
+      return hipErrorInvalidValue;
     case 1: return launch_prefill_ps<D, 1>(p, tiles, grid, bf16, kv8, stream);
     case 2: return launch_prefill_ps<D, 2>(p, tiles, grid, bf16, kv8, stream);
     case 4: return launch_prefill_ps<D, 4>(p, tiles, grid, bf16, kv8, stream);

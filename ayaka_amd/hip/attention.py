@@ -101,6 +101,16 @@ MFMA_MIN_HEADS = 3
 #: (row, query head) pairs one workgroup of the multi-row kernel serves, by head width
 #: (the C library's ``ayk_paged_prefill_tile_pairs``; a test checks they agree).
 PREFILL_PAIRS = {64: 128, 128: 128, 256: 64}
+#: Head widths whose multi-row kernel also runs the double tile: twice the pairs in an 8-wave
+#: workgroup, one per compute unit, which stages each chunk once for all of them.
+PREFILL_DOUBLE_TILE_DIMS = (128, 256)
+
+
+def prefill_waves_per_group(head_dim: int, pairs: int) -> int:
+    """How a tile of ``pairs`` runs: 1, 2 or 4 waves per group of 16 pairs in a 4-wave workgroup
+    (the full tile, a half, a quarter), or 0 for the double tile (an 8-wave workgroup)."""
+    full = PREFILL_PAIRS[head_dim]
+    return 0 if pairs == 2 * full and head_dim in PREFILL_DOUBLE_TILE_DIMS else full // pairs
 #: Rows per request (on average) from which a multi-row step runs the multi-row kernel.
 PREFILL_MIN_ROWS = 2
 #: Compute units of one MI355X; the split heuristic aims to keep all of them busy.
@@ -179,7 +189,7 @@ class HipAttentionPlan:
         if found is None:
             lengths = [g[0] for g in self.prefill_groups(group, pairs)]
             found = choose_prefill_partition(lengths, self.row_lengths, num_kv_heads, num_kv_heads * group,
-                                             head_dim, PREFILL_PAIRS[head_dim] // pairs,
+                                             head_dim, prefill_waves_per_group(head_dim, pairs),
                                              self.context_bytes(num_kv_heads, head_dim, kv_bytes))
             self.splits[key] = found
         return found
@@ -190,17 +200,17 @@ class HipAttentionPlan:
         return positions * num_kv_heads * head_dim * 2 * kv_bytes
 
     def prefill_launch(self, num_kv_heads: int, group: int, head_dim: int, kv_bytes: int = 2) -> tuple[int, int]:
-        """(tile pairs, partition size) of the step's multi-row launch: of the full tile, a
-        half and a quarter (each at its best partition size), the one with the smallest
-        :func:`prefill_model_us`; chosen once for every layer."""
+        """(tile pairs, partition size) of the step's multi-row launch: of the double tile (head
+        widths 128 and 256), the full tile, a half and a quarter (each at its best partition
+        size), the one with the smallest :func:`prefill_model_us`; chosen once for every layer."""
         key = ("prefill-launch", num_kv_heads, group, head_dim, kv_bytes)
         found = self.splits.get(key)
         if found is None:
             full = PREFILL_PAIRS[head_dim]
             context = self.context_bytes(num_kv_heads, head_dim, kv_bytes)
             best = None
-            for waves in (1, 2, 4):
-                pairs = full // waves
+            for waves in ((0, 1, 2, 4) if head_dim in PREFILL_DOUBLE_TILE_DIMS else (1, 2, 4)):
+                pairs = 2 * full if waves == 0 else full // waves
                 if pairs < group:
                     break
                 size = self.prefill_split(num_kv_heads, group, pairs, head_dim, kv_bytes)
@@ -685,9 +695,10 @@ PREFILL_WORKGROUPS_PER_CU = 2
 #: pair group (tiles of the full capacity, a half, a quarter); with the streaming rate, the
 #: partials' rate and the reduce launch below, fitted to a sweep of 13 step shapes x 3 tile
 #: sizes x 5 partition sizes on MI355X (the model's choice averaged 2% and at worst 8%
-#: above the fastest measured launch).
+#: above the fastest measured launch). Key 0 is the double tile, one workgroup per compute
+#: unit: a step of its 8 waves measured 2% under two full tiles' steps side by side.
 PREFILL_CHUNK = 64
-PREFILL_CHUNK_US_BY_WAVES = {1: 2.5, 2: 1.75, 4: 1.5}
+PREFILL_CHUNK_US_BY_WAVES = {0: 2.45, 1: 2.5, 2: 1.75, 4: 1.5}
 #: Rate (bytes per us) at which a launch streams K and V it reads once (about 7 TB/s).
 PREFILL_STREAM_BYTES_PER_US = 7.0e6
 #: Rate (bytes per us) at which partials are written and read back, and the reduce launch.
@@ -727,7 +738,7 @@ def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | li
     With partitions, writing and reading back the partials of rows that span several and
     the reduce launch are added.
     """
-    slots = COMPUTE_UNITS * PREFILL_WORKGROUPS_PER_CU
+    slots = COMPUTE_UNITS * (PREFILL_WORKGROUPS_PER_CU if waves_per_group else 1)
     steps = []
     for length in group_lengths:
         if partition_size:
@@ -751,7 +762,7 @@ def choose_prefill_partition(group_lengths: list[int], row_lengths: tuple[int, .
     lengths: the candidate with the smallest :func:`prefill_model_us`, considered only when
     the unsplit grid fills at most two rounds of the GPU (beyond that the partials' traffic
     outweighs any balance gained)."""
-    slots = COMPUTE_UNITS * PREFILL_WORKGROUPS_PER_CU
+    slots = COMPUTE_UNITS * (PREFILL_WORKGROUPS_PER_CU if waves_per_group else 1)
     if not group_lengths or len(group_lengths) * num_kv_heads >= 2 * slots:
         return 0
     longest = max(group_lengths)
@@ -911,7 +922,8 @@ def attend_with(
     covers each tile's context in one workgroup, ``partition_size`` splits it into
     partitions of that size (a multiple of 64) merged by the reduce kernel, and ``None``
     for both lets :func:`choose_prefill_partition` decide; ``tile_pairs`` forces the tile
-    capacity (:data:`PREFILL_PAIRS`, or a half or a quarter of it; ``None``:
+    capacity (:data:`PREFILL_PAIRS`, a half or a quarter of it, or twice it at head widths 128 and
+    256, an 8-wave workgroup; ``None``:
     :meth:`HipAttentionPlan.prefill_launch`). ``waves`` (1, 2, 4 or 8) forces how many
     waves share each (row, key/value head)'s context (v1) or partition (v2) (``None``: the
     split model's choice, else the library's).

@@ -246,7 +246,9 @@ int ayk_paged_attention_v2_static_counters(void** counters, int64_t* words);
  * that many pairs are not computed). tile_pairs is
  * ayk_paged_prefill_tile_pairs(head_dim), or a half or a quarter of it: smaller
  * tiles (few rows per request, verify windows) share each tile's chunks among 2
- * or 4 waves instead of spending them on empty pairs. One workgroup per
+ * or 4 waves instead of spending them on empty pairs. At head_dim 128 and 256 it
+ * may also be twice that capacity: the tile then runs in an 8-wave workgroup,
+ * one per compute unit, which stages each chunk once for all its pairs. One workgroup per
  * (tile, key/value head) loads each chunk of the context once into LDS for all
  * its rows and query heads; q.k and P.V run on the matrix cores with fp32
  * accumulation. With partition_size 0 a tile covers its whole context and its

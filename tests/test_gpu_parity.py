@@ -229,7 +229,7 @@ def test_window_kernel(size: int | None, dtype: str, heads: int, kv_heads: int, 
     assert torch.count_nonzero(out[padding_rows]) == 0
 
 
-@pytest.mark.parametrize("waves", [1, 2, 4])
+@pytest.mark.parametrize("waves", [0, 1, 2, 4])
 @pytest.mark.parametrize("size", [0, 64, 192, 512])
 @pytest.mark.parametrize("heads,kv_heads,head_dim,dtype", [(8, 2, 64, "fp16"), (32, 8, 128, "bf16"),
                                                            (4, 4, 256, "bf16")])
@@ -239,11 +239,15 @@ def test_multi_row_partitions(size: int, waves: int, heads: int, kv_heads: int, 
     # size 0: each tile's whole context in one workgroup; otherwise partitions of `size`
     # positions merged by the reduce kernel, each row over the partitions it sees. waves:
     # tiles of the full pair capacity, or of a half or a quarter whose 2 or 4 waves per
-    # pair group split every chunk and merge their states at the end
+    # pair group split every chunk and merge their states at the end; waves 0: the double tile
+    # (twice the pairs in an 8-wave workgroup, head widths 128 and 256)
+    if waves == 0 and head_dim not in hip_attention.PREFILL_DOUBLE_TILE_DIMS:
+        pytest.skip("no double tile at this head width")
     s = build_scenario(steps, dtype=dtype, heads=heads, kv_heads=kv_heads, head_dim=head_dim, block_size=16,
                        mode="mixed", seed=68, spare_blocks=2)
     launch = dict(partitions=0) if size == 0 else dict(partition_size=size)
-    pairs = hip_attention.PREFILL_PAIRS[head_dim] // waves
+    full = hip_attention.PREFILL_PAIRS[head_dim]
+    pairs = 2 * full if waves == 0 else full // waves
     out = run_attention(s, prefill=True, tile_pairs=pairs, **launch)
     assert_parity(out, s.expected(np.float64), dtype, f"prefill/{name}/{size}/{pairs}")
     padding_rows = [i for i, r in enumerate(s.plan["request_of_row"]) if s.lengths[r] == 0]

@@ -81,6 +81,9 @@ def launches(d: dict, meta) -> list[tuple[str, dict]]:
         size = int([0, 64, 256, 512][rng.integers(4)])
         launch = dict(partitions=0) if size == 0 else dict(partitions=None, partition_size=size)
         out.append((f"multi-row/{pairs} pairs/{size}", dict(prefill=True, window=False, tile_pairs=pairs, **launch)))
+        if d["head_dim"] in hip_attention.PREFILL_DOUBLE_TILE_DIMS:  # the 8-wave double tile, same split
+            out.append((f"multi-row/{2 * full} pairs/{size}",
+                        dict(prefill=True, window=False, tile_pairs=2 * full, **launch)))
         if meta.plan.window_pairs(group):
             wsize = int([0, 64, 256][rng.integers(3)])
             wlaunch = dict(partitions=0) if wsize == 0 else dict(partitions=None, partition_size=wsize)

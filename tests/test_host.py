@@ -320,8 +320,11 @@ def test_multi_row_launch_choice() -> None:
         table = torch.ones(len(rows), max(lengths) // 16 + 1, dtype=torch.int32)
         step = hip_attention.plan(ForwardMode.MIXED, _ints(*rows), _ints(*lengths), table, 16).plan
         return step.prefill_launch(8, 4, 128)
-    # long chunks that fill the GPU: full tiles, no partitions
-    assert launch([512] * 4, [4096] * 4) == (128, 0)
+    # long chunks that fill the GPU: double tiles (8-wave workgroups), no partitions
+    assert launch([512] * 4, [4096] * 4) == (256, 0)
+    # one 2048-row prompt and 128-row chunks: a double tile per compute unit would leave the
+    # causal triangle's short tiles unbalanced; quarter tiles measured fastest
+    assert launch([2048], [2048])[0] < 128 and launch([128] * 8, [2048] * 8)[0] < 128
     # short verify windows: small tiles; few of them: partitions as well
     assert launch([2] * 64, [2048] * 64)[0] < 128
     pairs, size = launch([8] * 16, [1024] * 16)

@@ -218,7 +218,7 @@ def test_multi_row_and_window_loads_stay_in_the_cache(head_dim: int, kv8: bool) 
         step = Step(rng, _lengths(rng, bs, int(rng.integers(1, 5))), bs, kv_heads, head_dim, kv8, case % 2)
         heads = kv_heads * group
         rows = [int(rng.integers(1, min(n, 40) + 1)) if n else 1 for n in step.lengths]
-        for tile_pairs in (full, full // 2, full // 4):
+        for tile_pairs in ((2 * full,) if head_dim != 64 else ()) + (full, full // 2, full // 4):
             if group > tile_pairs:
                 continue
             for size in (0, 64, 192):
