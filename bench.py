@@ -654,6 +654,12 @@ def main() -> int:
                     line[key][f"C{index}"] = head
                     continue
                 line[key][f"C{index}"] = child_record(index, codec, args)
+        # the same configurations as fp32 models (fp32 q, out and caches: the fp32 decode kernel)
+        line["configs_fp32"] = {}
+        dtype_arg, args.model_dtype = args.model_dtype, "fp32"
+        for index in (1, 2, 3, 4, 5):
+            line["configs_fp32"][f"C{index}"] = child_record(index, "raw", args)
+        args.model_dtype = dtype_arg
     print(json.dumps(line), flush=True)
     return 0
 
