@@ -298,8 +298,9 @@ def test_multi_row_full_size_against_the_oracle(requests: int, rows: int, contex
     assert_parity(out, expected, dtype, f"{requests} x {rows} over {context}")
 
 
-@pytest.mark.parametrize("launch", [dict(partitions=0), dict(partitions=None, partition_size=128)],
-                         ids=["whole", "partitions"])
+@pytest.mark.parametrize("launch", [dict(partitions=0), dict(partitions=None, partition_size=128),
+                                    dict(partitions=None, partition_size=128, tile_pairs=256, window=False)],
+                         ids=["whole", "partitions", "double-tile"])
 @pytest.mark.parametrize("steps", [[(40, 600), (3, 3), (7, 300)], [(4, 600), (3, 3), (1, 300), (2, 0)]],
                          ids=["multi-row-kernel", "window-launch"])
 def test_multi_row_step_in_a_captured_graph(launch: dict, steps: list) -> None:
