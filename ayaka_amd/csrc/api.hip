@@ -559,6 +559,19 @@ int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void*
   if (n_tiles == 0 || n_rows == 0) return ok();
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool walk = ayk::walking();  // the host address walk: the launch's loads, no launch
+  // bf16 models over bf16 caches: a workspace with room for one int32 per workgroup (after the
+  // partials, 16-byte aligned) lets the kernel run P.V in fp16 where the values allow and hand
+  // the other workgroups to a bf16 pass (the slots need no initial contents)
+  size_t partial_bytes = 0;
+  if (partition_size > 0) {
+    const int64_t parts = ((int64_t)p.max_len + partition_size - 1) / partition_size;
+    if (parts >= 1 && parts <= 65535)
+      partial_bytes = (ayk_paged_attention_v2_workspace_bytes(n_rows, num_heads, head_dim, (int32_t)parts) + 15) & ~size_t(15);
+  }
+  const size_t flag_bytes = (size_t)n_tiles * num_kv_heads * sizeof(uint32_t);
+  if (dtype == AYK_DTYPE_BF16 && kv_dtype == AYK_DTYPE_BF16 && workspace && workspace_bytes >= partial_bytes + flag_bytes &&
+      reinterpret_cast<uintptr_t>(workspace) % 16 == 0)
+    p.arrivals = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + partial_bytes);
   if (partition_size == 0 && walk) {
     ayk::walk_prefill(p, tiles, n_tiles, head_dim, kv_dtype == AYK_DTYPE_FP8_E4M3, waves_per_group);
     return ok();

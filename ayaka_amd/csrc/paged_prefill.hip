@@ -80,10 +80,31 @@ __host__ __device__ constexpr int prefill_workgroups_per_cu(int head_dim, int wa
 // workgroup per CU): one stage of each chunk then serves 8 waves' pairs, which halves the
 // staging loads, LDS writes and barrier per pair (4 x 512 rows over 4K, settled: 174.5 -> 171.5
 // us; GQA 8 335 -> 322; fp16 140 -> 135; head_dim 256 208 -> 193).
-template <int D, bool BF16, bool KV8, int PS, int W = kPrefillWaves>
+//
+// MODE (bf16 models over bf16 caches; 0 otherwise): P.V costs two MFMAs per step for a bf16 P
+// (its split) but one for an fp16 P rounded to nearest, which needs the values in fp16. Every
+// bf16 value with 2^-17 <= |v| < 65536 is an fp16 value (fp16's normal range, and the
+// subnormals that still hold bf16's 8 significant bits); smaller ones round to within 2^-25.
+// MODE 1 stages each chunk's values as fp16 and votes: a chunk holding a value of 65536 or more
+// (or not finite), or none of 2^-10 or more (where the small values' rounding could matter),
+// does not convert. A workgroup that met such a chunk stores nothing and marks its slot of
+// p.arrivals, which MODE 1 otherwise clears at its start. MODE 2, launched after it on the
+// same grid, runs only the marked workgroups, with the split bf16 P. fp8 caches decode
+// straight to fp16 (every e4m3 value is one), so bf16 models over them always take one MFMA.
+template <int D, bool BF16, bool KV8, int PS, int W = kPrefillWaves, int MODE = 0>
 __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D, PS)) void paged_prefill_kernel(
     const AttnParams p, const int32_t* tiles) {
   static_assert(W == kPrefillWaves || (W == 8 && PS == 1 && D != 64), "the double tile: 8 waves, one per pair group");
+  static_assert(MODE == 0 || (BF16 && !KV8), "the fp16 values pass: bf16 models over bf16 caches");
+  constexpr bool V16_ALWAYS = KV8 && BF16;  // fp8 codes decode to fp16 values
+  constexpr bool V16_FAST = MODE == 1;      // bf16 values, staged as fp16 when they all convert
+  constexpr bool V16 = V16_ALWAYS || V16_FAST;
+  if constexpr (MODE == 2) {
+    if (p.arrivals[blockIdx.x] == 0) return;  // the fast pass finished this workgroup (uniform)
+  }
+  if constexpr (MODE == 1) {
+    if (threadIdx.x == 0) p.arrivals[blockIdx.x] = 0;
+  }
   constexpr int THREADS = W * kWave;
   constexpr int PT = D == 256 ? 1 : 2;          // 16-pair groups per wave
   constexpr int PGROUPS = W / PS;               // waves with distinct pairs
@@ -120,6 +141,7 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
   __shared__ uint32_t s_tbl[kTableCap];
   __shared__ Lds lds;
   __shared__ float s_ml[MERGE_WAVES][PT][2][16];
+  __shared__ int s_vbad[2][W];  // V16_FAST: per buffer, each wave's vote (a value that does not convert)
   auto& s_k = lds.st.k;
   auto& s_v = lds.st.v;
 
@@ -217,6 +239,10 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
   // This workgroup's positions: the tile's whole context, or one partition of it.
   const int t_begin = split ? part * p.partition_size : 0;
   const int t_end = split ? min(last_pos + 1, t_begin + p.partition_size) : last_pos + 1;
+  // V16_FAST: a chunk whose values did not all convert (uniform); its results are then not
+  // stored, and the fallback pass computes the workgroup (the rest of the chunks still run:
+  // leaving the loop early costs the common case registers)
+  bool stop = false;
   for (int s0 = t_begin; s0 < t_end; s0 += seg_len) {
     const int s1 = min(t_end, s0 + seg_len);
     const int b0 = stage_table(p, tbl, s_tbl, s0, s1, tid, THREADS);
@@ -243,9 +269,31 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
       for (int u = 0; u < PER_THREAD; ++u) s_k[buf][key_slot(first_pos + u, piece_c)] = kv_pairs<KV8, BF16>(kr[u]);
     };
     auto stage_values = [&](int buf) {
+      typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+      u16x2 hi_bits = {0, 0};  // V16_FAST: the largest |bits| of the thread's values
 #pragma unroll
-      for (int u = 0; u < PER_THREAD; ++u)
-        *reinterpret_cast<u32x4*>(&s_v[buf][(first_pos + u) * VP + piece_c * 8]) = kv_pairs<KV8, BF16>(vr[u]);
+      for (int u = 0; u < PER_THREAD; ++u) {
+        u32x4 w = kv_pairs<KV8, V16_ALWAYS ? false : BF16>(vr[u]);
+        if constexpr (V16_FAST) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const u16x2 a = __builtin_bit_cast(u16x2, w[e] & 0x7fff7fffu);
+            hi_bits = __builtin_elementwise_max(hi_bits, a);
+            // bf16 -> fp32 -> fp16, to nearest: exact from 2^-17 up, within 2^-25 below
+            w[e] = __builtin_bit_cast(uint32_t, f16x2{(_Float16)__uint_as_float(w[e] << 16),
+                                                      (_Float16)__uint_as_float(w[e] & 0xffff0000u)});
+          }
+        }
+        *reinterpret_cast<u32x4*>(&s_v[buf][(first_pos + u) * VP + piece_c * 8]) = w;
+      }
+      if constexpr (V16_FAST) {
+        // 2: a value fp16 cannot hold (|v| >= 65536, or not finite); 1: none of the wave's
+        // values reaches 2^-10 (a chunk all of whose waves say so does not convert either)
+        const unsigned top = max(hi_bits.x, hi_bits.y);
+        const uint64_t no = __builtin_amdgcn_ballot_w64(top > 0x477f);
+        const uint64_t sized = __builtin_amdgcn_ballot_w64(top >= 0x3a80);
+        if (lane == 0) s_vbad[buf][wave] = no != 0 ? 2 : sized == 0 ? 1 : 0;
+      }
     };
 
     typedef f32x4 Scores[PTL_W][PT];
@@ -267,6 +315,8 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
     };
     // Fold chunk ci's scores acc (its values in LDS buffer vb) into every pair's running
     // state; mid() runs between the rescale and the weights.
+    // P.V's operand type: fp16 when the values in LDS are fp16 values, else the model's
+    constexpr bool PB = V16 ? false : BF16;
     auto fold = [&](int ci, int vb, Scores& acc, auto&& mid) {
       const int buf = vb;
       const int tb = s0 + ci * CH;
@@ -332,7 +382,7 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
             const float w[8] = {acc[2 * kw][j][0],     acc[2 * kw][j][1],     acc[2 * kw][j][2],
                                 acc[2 * kw][j][3],     acc[2 * kw + 1][j][0], acc[2 * kw + 1][j][1],
                                 acc[2 * kw + 1][j][2], acc[2 * kw + 1][j][3]};
-            split_weights<BF16>(w, phi[j], plo[j]);
+            split_weights<PB>(w, phi[j], plo[j]);
           }
 #pragma unroll
           for (int t = 0; t < DT; ++t) {
@@ -344,8 +394,8 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
             const u32x4 va = u32x4{lo4.x, lo4.y, hi4.x, hi4.y};
 #pragma unroll
             for (int j = 0; j < PT; ++j) {
-              o[j][t] = mfma32<BF16>(va, phi[j], o[j][t]);
-              if constexpr (split_p(BF16)) o[j][t] = mfma32<BF16>(va, plo[j], o[j][t]);
+              o[j][t] = mfma32<PB>(va, phi[j], o[j][t]);
+              if constexpr (split_p(PB)) o[j][t] = mfma32<PB>(va, plo[j], o[j][t]);
             }
           }
         }
@@ -356,15 +406,15 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
 #pragma unroll
         for (int j = 0; j < PT; ++j) {
           const float w[4] = {acc[0][j][0], acc[0][j][1], acc[0][j][2], acc[0][j][3]};
-          split_weights4<BF16>(w, phi[j], plo[j]);
+          split_weights4<PB>(w, phi[j], plo[j]);
         }
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
           const u32x2 va = lds_read_transposed(&s_v[buf][(ps * 16 + 4 * mq + (mt >> 2)) * VP + t * 16 + 4 * (mt & 3)]);
 #pragma unroll
           for (int j = 0; j < PT; ++j) {
-            o[j][t] = mfma_pv<BF16>(va, phi[j], o[j][t]);
-            if constexpr (split_p(BF16)) o[j][t] = mfma_pv<BF16>(va, plo[j], o[j][t]);
+            o[j][t] = mfma_pv<PB>(va, phi[j], o[j][t]);
+            if constexpr (split_p(PB)) o[j][t] = mfma_pv<PB>(va, plo[j], o[j][t]);
           }
         }
       }
@@ -376,6 +426,16 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
     lds_barrier();
     // Two chunks per iteration, so that each body's LDS buffer is a constant (immediate
     // address offsets instead of per-access arithmetic).
+    // V16_FAST: whether a chunk's values all converted (every wave's vote, uniform)
+    auto values_convert = [&](int buf) {
+      int no = 0, small = 1;
+#pragma unroll
+      for (int v = 0; v < W; ++v) {
+        no |= s_vbad[buf][v] & 2;
+        small &= s_vbad[buf][v];
+      }
+      return no == 0 && small == 0;
+    };
     auto chunk_step = [&](int ci, int buf) {
       if (ci + 1 < nch) load_chunk(ci + 1);
       // The two waves a SIMD holds (one per workgroup) take turns: a wave raises its
@@ -395,11 +455,19 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
       lds_barrier();
     };
     for (int ci = 0; ci < nch; ci += 2) {
+      if constexpr (V16_FAST) stop |= !values_convert(0);
       chunk_step(ci, 0);
-      if (ci + 1 < nch) chunk_step(ci + 1, 1);
+      if (ci + 1 < nch) {
+        if constexpr (V16_FAST) stop |= !values_convert(1);
+        chunk_step(ci + 1, 1);
+      }
     }
   }
 
+  if (stop) {
+    if (tid == 0) p.arrivals[blockIdx.x] = 1;
+    return;
+  }
   // Each pair's weight sum over the 4 position groups; lane (mq, mt) holds
   // elements 16*t + 4*mq + i of pair mt of each group.
   float lsum[PT];
@@ -468,6 +536,10 @@ static hipError_t launch_prefill_ps(const AttnParams& p, const int32_t* tiles, d
   if (kv8) {
     if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, true, PS, W>), grid, block, 0, stream, p, tiles);
     else hipLaunchKernelGGL((paged_prefill_kernel<D, false, true, PS, W>), grid, block, 0, stream, p, tiles);
+  } else if (bf16 && p.arrivals && PS == 1) {  // (for split tiles the second launch cost more than it saved)
+    // the fp16 values pass, then the bf16 pass over the workgroups it handed back
+    hipLaunchKernelGGL((paged_prefill_kernel<D, true, false, PS, W, 1>), grid, block, 0, stream, p, tiles);
+    hipLaunchKernelGGL((paged_prefill_kernel<D, true, false, PS, W, 2>), grid, block, 0, stream, p, tiles);
   } else {
     if (bf16) hipLaunchKernelGGL((paged_prefill_kernel<D, true, false, PS, W>), grid, block, 0, stream, p, tiles);
     else hipLaunchKernelGGL((paged_prefill_kernel<D, false, false, PS, W>), grid, block, 0, stream, p, tiles);

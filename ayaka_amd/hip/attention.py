@@ -1025,6 +1025,11 @@ def attend_with(
         if size:
             max_partitions = -(-table.shape[1] * block_size // size)
             nbytes = lib.ayk_paged_attention_v2_workspace_bytes(n_rows, heads, buffers.head_dim, max_partitions)
+        if q.dtype == torch.bfloat16 and _kv_code(buffers, q.dtype) == _DTYPE_CODES[torch.bfloat16]:
+            # one int32 per workgroup after the partials: the fp16 values pass hands a workgroup
+            # whose values fp16 cannot hold to the bf16 pass through it
+            nbytes = -(-nbytes // 16) * 16 + 4 * (tiles.numel() // 4) * kv_heads
+        if nbytes:
             scratch = _workspace(op, device, nbytes, capturing(q), stream)
         _call(op, lib.ayk_paged_prefill, (
             out.data_ptr(), q.data_ptr(), buffers.k.data_ptr(), buffers.v.data_ptr(), table.data_ptr(),

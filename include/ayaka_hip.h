@@ -264,10 +264,17 @@ int ayk_paged_attention_v2_static_counters(void** counters, int64_t* words);
  * windows) fill the GPU this way. Replaces the reference's per-request SDPA loop,
  * python/ayaka/ops/backends/torch/attention.py:209-234, and flashinfer's batch
  * prefill (python/ayaka/ops/backends/flashinfer/attention.py:150-152, :253-266).
+ * bf16 models over bf16 caches: a workspace with room, after the partials (16-byte
+ * aligned), for one int32 per workgroup (n_tiles * num_kv_heads) lets the kernel stage
+ * each chunk's values as fp16 and run P.V in one fp16 MFMA where all of a chunk's values
+ * are fp16 values (|v| < 65536, at least one of them 2^-10 or more; values below 2^-17 round
+ * to within 2^-25), and hand every other workgroup to a second, bf16 pass; the slots need no
+ * initial contents. Without that room every workgroup runs the bf16 P.V.
  */
 /* (row, query head) pairs one tile of ayk_paged_prefill may hold: 128 for head_dim
  * 64 and 128, 64 for 256, 0 for a width with no kernel. No reference counterpart: it
- * sizes the tiles the caller builds. */
+ * sizes the tiles the caller builds.
+ */
 int ayk_paged_prefill_tile_pairs(int32_t head_dim);
 
 int ayk_paged_prefill(void* out, const void* q, const void* k_cache, const void* v_cache,

@@ -255,6 +255,47 @@ def test_multi_row_partitions(size: int, waves: int, heads: int, kv_heads: int, 
         assert torch.count_nonzero(out[padding_rows]) == 0
 
 
+@pytest.mark.parametrize("size", [0, 256])
+@pytest.mark.parametrize("tile", ["double", "full", "half"])
+@pytest.mark.parametrize("kind", ["a-huge-value", "all-small", "one-request-small", "normal"])
+def test_multi_row_values_fp16_cannot_hold(kind: str, tile: str, size: int) -> None:
+    # bf16 caches: the kernel runs P.V in fp16 where a chunk's values allow it and hands the
+    # workgroups that met any other chunk to a bf16 pass. A value of 65536 or more, or a context
+    # whose values all lie below 2^-10, sends its tiles there; the rest stay on the fp16 pass
+    s = build_scenario([(40, 600), (3, 300), (20, 200)], dtype="bf16", heads=8, kv_heads=2, head_dim=128,
+                       block_size=16, mode="mixed", seed=70)
+    v = s.v.copy()
+    if kind == "a-huge-value":
+        pos = 100  # request 0, a position every one of its rows sees
+        v[s.table[0][pos // 16], pos % 16, 1, 5] = 99840.0
+    elif kind == "all-small":
+        v *= 1e-4
+    elif kind == "one-request-small":
+        for b in s.table[1][: -(-300 // 16)]:
+            v[b] *= 1e-4
+    s.v_bits = f32_to_bits(v, "bf16")
+    full = hip_attention.PREFILL_PAIRS[128]
+    pairs = {"double": 2 * full, "full": full, "half": full // 2}[tile]
+    launch = dict(partitions=0) if size == 0 else dict(partition_size=size)
+    out = run_attention(s, prefill=True, window=False, tile_pairs=pairs, **launch)
+    assert_parity(out, s.expected(np.float64), "bf16", f"{kind}/{tile}/{size}")
+    # the hand-off slots (one int32 per workgroup, after the partials in the shared workspace)
+    meta = plan_scenario(s)
+    n_slots = meta.plan.prefill_tiles(4, pairs, size, DEV, False).numel() // 4 * 2
+    offset = 0
+    if size:
+        parts = -(-meta.block_table.shape[1] * 16 // size)
+        offset = -(-_lib.lib().ayk_paged_attention_v2_workspace_bytes(sum(s.rows), 8, 128, parts) // 16) * 16
+    slots = hip_attention._workspaces[DEV][offset:offset + 4 * n_slots].view(torch.int32).cpu()
+    handed = int(slots.sum())
+    if kind == "normal":
+        assert handed == 0, "every workgroup stays on the fp16 pass"
+    elif kind == "all-small":
+        assert handed == n_slots
+    else:
+        assert 0 < handed < n_slots, (handed, n_slots)
+
+
 @pytest.mark.parametrize("block_size", [1, 2])
 def test_multi_row_partitions_across_table_segments(block_size: int) -> None:
     # partitions of 512 positions of one- and two-position blocks each span several staged
