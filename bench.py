@@ -500,6 +500,22 @@ def reference_shapes(args) -> int:
             if kind == "prefill":
                 visible = sum(n - rows[0] + j + 1 for j in range(rows[0]) for n in lengths)
                 record["tflops"] = round(4 * heads * dim * visible / us / 1e6, 1)
+            else:
+                # as the engine's decode runs: replays of one captured graph of up to 128 calls,
+                # each over its own copy of the blocks
+                calls = min(copies, 128)
+                graph = torch.cuda.CUDAGraph()
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    hip_attention.attend(q, buffers, metas[0], out, scale=scale)
+                torch.cuda.current_stream().wait_stream(side)
+                torch.cuda.synchronize()
+                with torch.cuda.graph(graph):
+                    for c in range(calls):
+                        hip_attention.attend(q, buffers, metas[c], out, scale=scale)
+                record["us_graph"] = round(time_calls(graph.replay, 10, 3)["median_us"] / calls, 2)
+                del graph
             print(json.dumps(record), flush=True)
             del metas, k, v, buffers
             torch.cuda.empty_cache()
