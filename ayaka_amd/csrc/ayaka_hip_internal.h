@@ -30,7 +30,9 @@ struct AttnParams {
                                   // staged parameters the rows packed (partial_index)
   float* part_ml;                 // v2 only: the same slots' (m, l)
   uint32_t* arrivals;             // v2 single launch: [n_rows, head groups] counters, zero between calls;
-                                  // nullptr: a separate reduce kernel merges the partitions
+                                  // nullptr: a separate reduce kernel merges the partitions. Multi-row
+                                  // kernel: one hand-off slot per workgroup for the fp16 values pass
+                                  // (nullptr: one bf16 pass)
   int64_t table_stride;
   int64_t block_stride;
   int64_t token_stride;
