@@ -258,10 +258,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void paged_attention_mfma_kernel
           acc[sub][i] = v;
           mx = fmaxf(mx, v);
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      // m_h is the same in the 4 lanes of a column, so some lane's own maximum passes it by
+      // more than the slack iff some column's does: the cross-lane maximum only on a rescale
       if (__builtin_amdgcn_ballot_w64(mx > m_h + kRescaleSlack)) {
-        const float mn = fmaxf(m_h, mx);
+        const float mn = fmaxf(m_h, column_max(mx));
         const float alpha = fast_exp2(m_h - mn);  // head mt's, and o[] holds head mt
         l_h *= alpha;
         m_h = mn;

@@ -355,10 +355,11 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
               mx = fmaxf(mx, acc[w][j][i]);
             }
         }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // m[j] is the same in the 4 lanes of a column, so some lane's own maximum passes it
+        // by more than the slack iff some column's does: the cross-lane maximum only on a
+        // rescale
         if (__builtin_amdgcn_ballot_w64(mx > m[j] + kRescaleSlack)) {
-          const float mn = fmaxf(m[j], mx);
+          const float mn = fmaxf(m[j], column_max(mx));
           const float alpha = fast_exp2(m[j] - mn);
           l[j] *= alpha;
           if constexpr (LSUM_MFMA) lo1[j] *= alpha;
