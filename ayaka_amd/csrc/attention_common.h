@@ -76,20 +76,11 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-// The other lane of each pair (l, l ^ 16), and of each pair (l, l ^ 32), through gfx950's
-// lane-swap instructions (no LDS round trip, unlike a bpermute): v_permlane16_swap exchanges
-// the odd 16-lane rows of its first operand with the even rows of its second, so with x in
-// both, one result holds x[l] and the other x[l ^ 16]; v_permlane32_swap does the same with
-// the wave's halves.
-__device__ __forceinline__ float lane_xor16(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(((threadIdx.x >> 4) & 1) ? r[0] : r[1]);
-}
-__device__ __forceinline__ float lane_xor32(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(((threadIdx.x >> 5) & 1) ? r[0] : r[1]);
-}
-// The maximum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (one value per 16-lane column).
+// The maximum over lanes l, l ^ 16, l ^ 32 and l ^ 48 (one value per 16-lane column), through
+// gfx950's lane-swap instructions (no LDS round trip, unlike a bpermute): v_permlane16_swap
+// exchanges the odd 16-lane rows of its first operand with the even rows of its second, so
+// with x in both, the two results hold x[l] and x[l ^ 16] in some order; v_permlane32_swap
+// does the same with the wave's halves.
 __device__ __forceinline__ float column_max(float x) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
