@@ -217,7 +217,10 @@ class HipAttentionPlan:
                 lengths = [g[0] for g in self.prefill_groups(group, pairs)]
                 t = prefill_model_us(lengths, self.row_lengths, num_kv_heads, num_kv_heads * group, head_dim, size,
                                      waves, context)
-                if best is None or t < best[0]:
+                # a smaller tile (they come in decreasing size) must win by a margin: at a tie
+                # the model under-prices the quarter tile's short steps (a 1024-row prompt:
+                # modelled equal, measured 38.6 against 31.4 us on the half tile)
+                if best is None or t < best[0] * (1 - PREFILL_SMALLER_TILE_MARGIN):
                     best = (t, pairs, size)
             found = (best[1], best[2])
             self.splits[key] = found
@@ -691,19 +694,29 @@ def choose_partitions(n_rows: int, num_kv_heads: int, group: int, max_length: in
 
 #: Multi-row workgroups one compute unit runs at a time (the kernel's launch bounds).
 PREFILL_WORKGROUPS_PER_CU = 2
-#: Positions one multi-row workgroup folds per step, and the time of a step by waves per
-#: pair group (tiles of the full capacity, a half, a quarter); with the streaming rate, the
-#: partials' rate and the reduce launch below, fitted to a sweep of 13 step shapes x 3 tile
-#: sizes x 5 partition sizes on MI355X (the model's choice averaged 2% and at worst 8%
-#: above the fastest measured launch). Key 0 is the double tile, one workgroup per compute
-#: unit: a step of its 8 waves measured 2% under two full tiles' steps side by side.
+#: Positions one multi-row workgroup folds per step, the time of a step by head width and waves
+#: per pair group (0: the double tile, an 8-wave workgroup, one per compute unit; 1, 2, 4: the
+#: full tile, a half and a quarter), and each workgroup's fixed time by tile (its prologue,
+#: and the fold of a group's waves at the end); with the streaming rate, the partials' rate and
+#: the reduce launch below, fitted to a sweep of 40 step shapes (head widths 64, 128 and 256,
+#: GQA 4 and 8, 1 to 4096 rows per request over 512 to 8192 positions, decode rows beside a
+#: chunk) x every tile x 5 partition sizes on MI355X: the library's choice averaged 1.1% and at
+#: worst 9.5% above the fastest measured launch, against 4.6% and 28% with the constants fitted
+#: before to head width 128 alone.
 PREFILL_CHUNK = 64
-PREFILL_CHUNK_US_BY_WAVES = {0: 2.45, 1: 2.5, 2: 1.75, 4: 1.5}
+PREFILL_CHUNK_US = {
+    (64, 1): 1.02, (64, 2): 0.86, (64, 4): 0.57,
+    (128, 0): 2.08, (128, 1): 2.42, (128, 2): 1.76, (128, 4): 1.42,
+    (256, 0): 2.84, (256, 1): 2.90, (256, 2): 2.60, (256, 4): 3.79,
+}
+PREFILL_WORKGROUP_US = {0: 3.84, 1: 3.52, 2: 1.13, 4: 2.63}
+#: How much faster a smaller tile must model to be chosen over a larger one.
+PREFILL_SMALLER_TILE_MARGIN = 0.03
 #: Rate (bytes per us) at which a launch streams K and V it reads once (about 7 TB/s).
 PREFILL_STREAM_BYTES_PER_US = 7.0e6
 #: Rate (bytes per us) at which partials are written and read back, and the reduce launch.
-PREFILL_PARTIALS_BYTES_PER_US = 3.0e6
-PREFILL_REDUCE_US = 2.0
+PREFILL_PARTIALS_BYTES_PER_US = 5.0e6
+PREFILL_REDUCE_US = 11.2
 #: Whether steps whose requests' rows all fit one window tile run on the decode kernel's window
 #: launch (``ayk_paged_attention_windows``) rather than the multi-row kernel.
 WINDOWS = True
@@ -711,9 +724,9 @@ WINDOWS = True
 PREFILL_PARTITION_CANDIDATES = (128, 256, 512, 1024, 2048, 4096)
 
 
-def _dispatch_makespan(steps: list[int], slots: int) -> int:
-    """Finish time (in chunk steps) of workgroups of these lengths started longest first, each
-    in the first of ``slots`` identical slots to free up."""
+def _dispatch_makespan(steps: list[float], slots: int) -> float:
+    """Finish time of workgroups of these durations started longest first, each in the first of
+    ``slots`` identical slots to free up."""
     if len(steps) <= slots:
         return max(steps, default=0)
     steps = sorted(steps, reverse=True)
@@ -732,13 +745,15 @@ def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | li
     """Modelled time (us) of a multi-row launch.
 
     Its workgroups (one per tile, partition and key/value head) start longest first, each
-    in the first of the GPU's workgroup slots to free up (:func:`_dispatch_makespan`), at
-    :data:`PREFILL_CHUNK_US_BY_WAVES` per 64-position chunk, but the launch takes no less
-    than streaming the requests' K and V once (``context_bytes``).
+    in the first of the GPU's workgroup slots to free up (:func:`_dispatch_makespan`), taking
+    :data:`PREFILL_CHUNK_US` per 64-position chunk plus :data:`PREFILL_WORKGROUP_US`, but the
+    launch takes no less than streaming the requests' K and V once (``context_bytes``).
     With partitions, writing and reading back the partials of rows that span several and
     the reduce launch are added.
     """
     slots = COMPUTE_UNITS * (PREFILL_WORKGROUPS_PER_CU if waves_per_group else 1)
+    chunk_us = PREFILL_CHUNK_US[(head_dim, waves_per_group)]
+    fixed_us = PREFILL_WORKGROUP_US[waves_per_group]
     steps = []
     for length in group_lengths:
         if partition_size:
@@ -746,8 +761,8 @@ def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | li
             pieces = [partition_size] * full + ([rest] if rest else [])
         else:
             pieces = [length]
-        steps.extend([-(-piece // PREFILL_CHUNK) for piece in pieces or [0]] * num_kv_heads)
-    t = _dispatch_makespan(steps, slots) * PREFILL_CHUNK_US_BY_WAVES[waves_per_group]
+        steps.extend([-(-piece // PREFILL_CHUNK) * chunk_us + fixed_us for piece in pieces or [0]] * num_kv_heads)
+    t = _dispatch_makespan(steps, slots)
     t = max(t, context_bytes / PREFILL_STREAM_BYTES_PER_US)
     if partition_size:
         parts = sum(-(-n // partition_size) for n in row_lengths if n > partition_size)

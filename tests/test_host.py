@@ -323,8 +323,10 @@ def test_multi_row_launch_choice() -> None:
     # long chunks that fill the GPU: double tiles (8-wave workgroups), no partitions
     assert launch([512] * 4, [4096] * 4) == (256, 0)
     # one 2048-row prompt and 128-row chunks: a double tile per compute unit would leave the
-    # causal triangle's short tiles unbalanced; quarter tiles measured fastest
-    assert launch([2048], [2048])[0] < 128 and launch([128] * 8, [2048] * 8)[0] < 128
+    # causal triangle's short tiles unbalanced; half tiles measured within 1% and 8% of the best
+    assert launch([2048], [2048]) == (64, 0) and launch([128] * 8, [2048] * 8) == (64, 0)
+    # a 1024-row prompt: half tiles (31.4 us), not quarter tiles (38.6), which model about equal
+    assert launch([1024], [1024]) == (64, 0)
     # short verify windows: small tiles; few of them: partitions as well
     assert launch([2] * 64, [2048] * 64)[0] < 128
     pairs, size = launch([8] * 16, [1024] * 16)
@@ -332,6 +334,23 @@ def test_multi_row_launch_choice() -> None:
     # decode rows beside one chunk: small tiles, split (they would stream alone otherwise)
     pairs, size = launch([1] * 64 + [64], [4096] * 65)
     assert pairs < 128 and size > 0
+
+
+def test_multi_row_launch_choice_by_head_width() -> None:
+    def launch(rows: list[int], lengths: list[int], heads: int, head_dim: int) -> tuple[int, int]:
+        table = torch.ones(len(rows), max(lengths) // 16 + 1, dtype=torch.int32)
+        step = hip_attention.plan(ForwardMode.MIXED, _ints(*rows), _ints(*lengths), table, 16).plan
+        return step.prefill_launch(8, heads // 8, head_dim)
+    # the measured fastest launches of a sweep on MI355X (us, chosen against the runner-up)
+    # head_dim 64: a 2048-row prompt on unsplit half tiles (34.6), not full tiles in partitions
+    # of 1024 (41.0)
+    assert launch([2048], [2048], 32, 64) == (64, 0)
+    # head_dim 256: 128-row chunks on double tiles in partitions of 1024 (66.6, against
+    # 85.8 on unsplit quarter tiles), and long chunks on unsplit double tiles
+    assert launch([128] * 8, [2048] * 8, 16, 256) == (128, 1024)
+    assert launch([512] * 4, [4096] * 4, 16, 256) == (128, 0)
+    # GQA 8: long chunks on unsplit double tiles
+    assert launch([512] * 4, [4096] * 4, 64, 128) == (256, 0)
 
 
 def test_window_tiles_and_split() -> None:
