@@ -698,25 +698,26 @@ PREFILL_WORKGROUPS_PER_CU = 2
 #: per pair group (0: the double tile, an 8-wave workgroup, one per compute unit; 1, 2, 4: the
 #: full tile, a half and a quarter), and each workgroup's fixed time by tile (its prologue,
 #: and the fold of a group's waves at the end); with the streaming rate, the partials' rate and
-#: the reduce launch below, fitted to a sweep of 40 step shapes (head widths 64, 128 and 256,
-#: GQA 4 and 8, 1 to 4096 rows per request over 512 to 8192 positions, decode rows beside a
-#: chunk) x every tile x 5 partition sizes on MI355X: the library's choice averaged 1.1% and at
-#: worst 9.5% above the fastest measured launch, against 4.6% and 28% with the constants fitted
-#: before to head width 128 alone.
+#: the reduce launch below, fitted to a sweep of 52 step shapes (head widths 64, 128 and 256,
+#: 3 to 8 key/value heads, GQA 3, 4 and 8, 1 to 4096 rows per request over 512 to 8192
+#: positions, decode rows beside a chunk) x every tile x 5 partition sizes on MI355X: the
+#: library's choice averaged 1.2% and at worst 14% above the fastest measured launch (over fp8
+#: caches, 8 shapes: 1.0% and 5.8%), against 4.2% and 28% with the constants fitted before to
+#: head width 128 alone.
 PREFILL_CHUNK = 64
 PREFILL_CHUNK_US = {
-    (64, 1): 1.02, (64, 2): 0.86, (64, 4): 0.57,
-    (128, 0): 2.08, (128, 1): 2.42, (128, 2): 1.76, (128, 4): 1.42,
-    (256, 0): 2.84, (256, 1): 2.90, (256, 2): 2.60, (256, 4): 3.79,
+    (64, 1): 0.99, (64, 2): 0.81, (64, 4): 0.60,
+    (128, 0): 2.05, (128, 1): 2.38, (128, 2): 1.68, (128, 4): 1.40,
+    (256, 0): 2.84, (256, 1): 2.93, (256, 2): 2.56, (256, 4): 3.81,
 }
-PREFILL_WORKGROUP_US = {0: 3.84, 1: 3.52, 2: 1.13, 4: 2.63}
+PREFILL_WORKGROUP_US = {0: 4.56, 1: 3.98, 2: 2.09, 4: 2.70}
 #: How much faster a smaller tile must model to be chosen over a larger one.
 PREFILL_SMALLER_TILE_MARGIN = 0.03
 #: Rate (bytes per us) at which a launch streams K and V it reads once (about 7 TB/s).
 PREFILL_STREAM_BYTES_PER_US = 7.0e6
 #: Rate (bytes per us) at which partials are written and read back, and the reduce launch.
-PREFILL_PARTIALS_BYTES_PER_US = 5.0e6
-PREFILL_REDUCE_US = 11.2
+PREFILL_PARTIALS_BYTES_PER_US = 5.4e6
+PREFILL_REDUCE_US = 9.9
 #: Whether steps whose requests' rows all fit one window tile run on the decode kernel's window
 #: launch (``ayk_paged_attention_windows``) rather than the multi-row kernel.
 WINDOWS = True

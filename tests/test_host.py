@@ -337,10 +337,10 @@ def test_multi_row_launch_choice() -> None:
 
 
 def test_multi_row_launch_choice_by_head_width() -> None:
-    def launch(rows: list[int], lengths: list[int], heads: int, head_dim: int) -> tuple[int, int]:
+    def launch(rows: list[int], lengths: list[int], heads: int, head_dim: int, kv_heads: int = 8) -> tuple[int, int]:
         table = torch.ones(len(rows), max(lengths) // 16 + 1, dtype=torch.int32)
         step = hip_attention.plan(ForwardMode.MIXED, _ints(*rows), _ints(*lengths), table, 16).plan
-        return step.prefill_launch(8, heads // 8, head_dim)
+        return step.prefill_launch(kv_heads, heads // kv_heads, head_dim)
     # the measured fastest launches of a sweep on MI355X (us, chosen against the runner-up)
     # head_dim 64: a 2048-row prompt on unsplit half tiles (34.6), not full tiles in partitions
     # of 1024 (41.0)
@@ -351,6 +351,9 @@ def test_multi_row_launch_choice_by_head_width() -> None:
     assert launch([512] * 4, [4096] * 4, 16, 256) == (128, 0)
     # GQA 8: long chunks on unsplit double tiles
     assert launch([512] * 4, [4096] * 4, 64, 128) == (256, 0)
+    # TinyLlama (32/4/64): 256 rows over 2048 on half tiles in partitions of 512 (21.3, against
+    # 24.7 on unsplit quarter tiles)
+    assert launch([256], [2048], 32, 64, kv_heads=4) == (64, 512)
 
 
 def test_window_tiles_and_split() -> None:
