@@ -215,9 +215,11 @@ __global__ __launch_bounds__(W * kWave, W == 8 ? 1 : prefill_workgroups_per_cu(D
   // of O^T whose A operand is a row of ones (row 0; the other rows zero): the sum of exactly
   // the weights the P.V products use, for one MFMA per k-step and group instead of a VALU add
   // per weight. Measured on 4 x 512 rows over 4K (settled, us): head_dim 64 fp16 91.9 -> 87.5,
-  // head_dim 256 187 -> 183; at head_dim 128 within 1% either way (bf16 and GQA 8 1% faster,
-  // fp8 caches and 128-row chunks 2% slower) with more registers, so it stays off there.
-  constexpr bool LSUM_MFMA = PTL_W >= 2 && D != 128;
+  // head_dim 256 187 -> 183; at head_dim 128 in the double tile over 16-bit caches bf16
+  // 138.0 -> 137.0, GQA 8 260.4 -> 257.4, fp16 130.6 -> 130.2, but over fp8 caches 120.1 ->
+  // 122.9 and on half tiles (the 2048-row prompt) 68.1 -> 68.9, and the full tile's fp16
+  // values pass would spill, so it stays off for those.
+  constexpr bool LSUM_MFMA = PTL_W >= 2 && (D != 128 || (W == 8 && !KV8));
   f32x4 lo1[PT];
   f32x4 o[PT][DT];
 #pragma unroll
