@@ -47,8 +47,8 @@ PROFILED_TRAFFIC = {
         (148_332_170, 2_128_368, "profiles/paged_attention_mfma_kernel_c2_llama32_1b_decode.md"),
     (1, "paged_attention_mfma_kernel (v1, 8 waves per head)", 0):
         (1_634_780, 4_608, "profiles/paged_attention_mfma_kernel_c1_smollm2_decode.md"),
-    (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 1280):
-        (1_316_632_688, 20_077_328, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
+    (5, "paged_attention_mfma_kernel (v2, merge reduce-kernel, fp8 cache)", 2560):
+        (1_307_048_278, 11_526_016, "profiles/paged_attention_mfma_kernel_c5_ragged_gqa8_fp8_cache.md"),
 }
 
 

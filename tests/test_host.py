@@ -250,11 +250,11 @@ def test_the_native_launch_model_is_the_python_statement() -> None:
 
 @pytest.mark.parametrize("index,kv_bytes,expected", [
     (1, 2, (0, 8)), (1, 1, (0, 8)), (2, 2, (320, 0)), (2, 1, (320, 0)), (3, 2, (0, 4)), (3, 1, (0, 4)),
-    (4, 2, (704, 0)), (4, 1, (704, 0)), (5, 2, (3072, 0)), (5, 1, (1280, 0))])
+    (4, 2, (704, 0)), (4, 1, (704, 0)), (5, 2, (3072, 0)), (5, 1, (2560, 0))])
 def test_the_launches_chosen_for_the_benchmark_steps(index: int, kv_bytes: int, expected: tuple) -> None:
     # the library's launch for each benchmark configuration: (partition size, v1 waves per head),
     # (0, n) being v1 with each context split among n waves (measured choices: C3 v1 at 4 waves,
-    # C1 v1 at 8, C2 v2 at 320, C4 v2 at 704, C5 v2 at 3072, or 1280 over fp8 caches)
+    # C1 v1 at 8, C2 v2 at 320, C4 v2 at 704, C5 v2 at 3072, or 2560 over fp8 caches)
     cfg = workloads.config(index)
     hip_attention._split_cache.clear()
     split = hip_attention.choose_split(cfg.batch, cfg.kv_heads, cfg.heads // cfg.kv_heads, max(cfg.lengths),
@@ -538,7 +538,6 @@ def test_the_pruned_best_split_is_the_exhaustive_one() -> None:
     from tests._support import python_schedule_makespan
 
     rng = np.random.default_rng(23)
-    sizes = list(hip_attention.PARTITION_CANDIDATES)
     for trial in range(150):
         n = int(rng.integers(1, 300))
         lengths = [int(x) for x in np.exp(rng.uniform(0, np.log(40000), n)).astype(int)]
@@ -548,6 +547,7 @@ def test_the_pruned_best_split_is_the_exhaustive_one() -> None:
         kv_bytes = int(rng.choice([1, 2]))
         max_items = int(rng.choice([0, 0, 64, 2048]))
         cost = hip_attention.WORKGROUP_COSTS[kv_bytes]
+        sizes = list(hip_attention.FP8_PARTITION_CANDIDATES if kv_bytes == 1 else hip_attention.PARTITION_CANDIDATES)
         got = hip_attention._best_size(lengths, max(lengths), groups, kv_bytes, 0, max_items)
         cands = sizes
         for i, size in enumerate(sizes):
