@@ -166,24 +166,36 @@ class HipAttentionPlan:
             self.splits[key] = found
         return found
 
-    def prefill_groups(self, group: int, pairs: int) -> list[tuple[int, int, int, int]]:
+    def prefill_group_arrays(self, group: int, pairs: int) -> tuple[np.ndarray, ...]:
         """(context length, first row, row count, request) of each group of rows the multi-row
-        kernel serves together, heaviest first.
+        kernel serves together, as four int64 arrays, heaviest first (ties: the first row);
+        built once per step and tile size.
 
         Each group holds consecutive rows of one request, at most ``pairs`` (row, query head)
         pairs; its context length is that of its last row (0 for a padding request).
         """
-        per_tile = max(1, pairs // group)
-        groups = []
-        first = 0
-        for request, (count, length) in enumerate(zip(self.rows, self.kv_lengths)):
-            for start in range(0, count, per_tile):
-                n = min(per_tile, count - start)
-                last = self.row_lengths[first + start + n - 1] if length else 0
-                groups.append((last, first + start, n, request))
-            first += count
-        groups.sort(key=lambda g: (-g[0], g[1]))
-        return groups
+        key = ("groups", group, pairs)
+        found = self.splits.get(key)
+        if found is None:
+            per_tile = max(1, pairs // group)
+            rows = np.asarray(self.rows, dtype=np.int64)
+            lengths = np.asarray(self.kv_lengths, dtype=np.int64)
+            row_lengths = np.asarray(self.row_lengths, dtype=np.int64)
+            first = np.cumsum(rows) - rows
+            tiles = -(-rows // per_tile)
+            request = np.repeat(np.arange(rows.size, dtype=np.int64), tiles)
+            start = (np.arange(request.size, dtype=np.int64) - np.repeat(np.cumsum(tiles) - tiles, tiles)) * per_tile
+            count = np.minimum(per_tile, rows[request] - start)
+            row = first[request] + start
+            last = np.where(lengths[request] > 0, row_lengths[row + count - 1], 0) if request.size else row
+            order = np.lexsort((row, -last))
+            found = (last[order], row[order], count[order], request[order])
+            self.splits[key] = found
+        return found
+
+    def prefill_groups(self, group: int, pairs: int) -> list[tuple[int, int, int, int]]:
+        """:meth:`prefill_group_arrays` as (context length, first row, row count, request) tuples."""
+        return list(zip(*(a.tolist() for a in self.prefill_group_arrays(group, pairs))))
 
     def prefill_split(self, num_kv_heads: int, group: int, pairs: int, head_dim: int, kv_bytes: int = 2) -> int:
         """The partition size of the step's multi-row launch with tiles of ``pairs`` (0: none),
@@ -191,7 +203,7 @@ class HipAttentionPlan:
         key = ("prefill", num_kv_heads, group, pairs, head_dim, kv_bytes)
         found = self.splits.get(key)
         if found is None:
-            lengths = [g[0] for g in self.prefill_groups(group, pairs)]
+            lengths = self.prefill_group_arrays(group, pairs)[0]
             found = choose_prefill_partition(lengths, self.row_lengths, num_kv_heads, num_kv_heads * group,
                                              head_dim, prefill_waves_per_group(head_dim, pairs),
                                              self.context_bytes(num_kv_heads, head_dim, kv_bytes))
@@ -218,7 +230,7 @@ class HipAttentionPlan:
                 if pairs < group:
                     break
                 size = self.prefill_split(num_kv_heads, group, pairs, head_dim, kv_bytes)
-                lengths = [g[0] for g in self.prefill_groups(group, pairs)]
+                lengths = self.prefill_group_arrays(group, pairs)[0]
                 t = prefill_model_us(lengths, self.row_lengths, num_kv_heads, num_kv_heads * group, head_dim, size,
                                      waves, context)
                 # a smaller tile (they come in decreasing size) must win by a margin: at a tie
@@ -248,7 +260,7 @@ class HipAttentionPlan:
         key = ("window", num_kv_heads, group, kv_bytes)
         found = self.splits.get(key)
         if found is None:
-            lengths = tuple(g[0] for g in self.prefill_groups(group, self.window_pairs(group)))
+            lengths = self.prefill_group_arrays(group, self.window_pairs(group))[0].tolist()
             found = window_partition_size([n for n in lengths if n > 0], num_kv_heads, kv_bytes)
             self.splits[key] = found
         return found
@@ -271,16 +283,19 @@ class HipAttentionPlan:
                 context={"op": "attention.attend"},
             )
         if found is None:
-            tiles = []
-            for length, row, n, request in self.prefill_groups(group, pairs):
-                if not partition_size:
-                    tiles.append((-length, row, n, request, 0))
-                    continue
-                for part in range(max(1, -(-length // partition_size))):
-                    tiles.append((-min(partition_size, length - part * partition_size), row, n, request, part))
-            tiles.sort()
-            flat = [v for _, row, n, request, part in tiles for v in (row, n, request, part)]
-            found = torch.tensor(flat, dtype=torch.int32).to(device)
+            length, row, count, request = self.prefill_group_arrays(group, pairs)
+            if partition_size:
+                parts = np.maximum(1, -(-length // partition_size))
+                index = np.repeat(np.arange(length.size), parts)
+                part = np.arange(index.size, dtype=np.int64) - np.repeat(np.cumsum(parts) - parts, parts)
+                piece = np.minimum(partition_size, length[index] - part * partition_size)
+                row, count, request = row[index], count[index], request[index]
+                order = np.lexsort((part, request, count, row, -piece))  # longest piece first
+                row, count, request, part = row[order], count[order], request[order], part[order]
+            else:
+                part = np.zeros_like(row)
+            flat = np.stack((row, count, request, part), axis=1).reshape(-1).astype(np.int32)
+            found = torch.from_numpy(flat).to(device)
             self.work[key] = found
         return found
 
@@ -730,17 +745,17 @@ WINDOWS = True
 PREFILL_PARTITION_CANDIDATES = (128, 256, 512, 1024, 2048, 4096)
 
 
-def _dispatch_makespan(steps: list[float], slots: int) -> float:
+def _dispatch_makespan(steps: "list[float] | np.ndarray", slots: int) -> float:
     """Finish time of workgroups of these durations started longest first, each in the first of
     ``slots`` identical slots to free up."""
-    if len(steps) <= slots:
-        return max(steps, default=0)
-    steps = sorted(steps, reverse=True)
+    steps = np.sort(np.asarray(steps, dtype=np.float64))[::-1]
+    if steps.size <= slots:
+        return float(steps[0]) if steps.size else 0
     if steps[0] == steps[-1]:
-        return -(-len(steps) // slots) * steps[0]
-    loads = steps[:slots]
+        return -(-steps.size // slots) * float(steps[0])
+    loads = steps[:slots].tolist()
     heapq.heapify(loads)
-    for s in steps[slots:]:
+    for s in steps[slots:].tolist():
         heapq.heapreplace(loads, loads[0] + s)
     return max(loads)
 
@@ -760,18 +775,20 @@ def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | li
     slots = COMPUTE_UNITS * (PREFILL_WORKGROUPS_PER_CU if waves_per_group else 1)
     chunk_us = PREFILL_CHUNK_US[(head_dim, waves_per_group)]
     fixed_us = PREFILL_WORKGROUP_US[waves_per_group]
-    steps = []
-    for length in group_lengths:
-        if partition_size:
-            full, rest = divmod(length, partition_size)
-            pieces = [partition_size] * full + ([rest] if rest else [])
-        else:
-            pieces = [length]
-        steps.extend([-(-piece // PREFILL_CHUNK) * chunk_us + fixed_us for piece in pieces or [0]] * num_kv_heads)
+    lengths = np.asarray(group_lengths, dtype=np.int64)
+    if partition_size:
+        # each length's full partitions, its remainder, and one empty piece for a length of 0
+        full, rest = np.divmod(lengths, partition_size)
+        chunks = np.concatenate((np.full(int(full.sum()), -(-partition_size // PREFILL_CHUNK), dtype=np.int64),
+                                 -(-rest[rest > 0] // PREFILL_CHUNK), np.zeros(int((lengths == 0).sum()), np.int64)))
+    else:
+        chunks = -(-lengths // PREFILL_CHUNK)
+    steps = np.repeat(chunks * chunk_us + fixed_us, num_kv_heads)
     t = _dispatch_makespan(steps, slots)
     t = max(t, context_bytes / PREFILL_STREAM_BYTES_PER_US)
     if partition_size:
-        parts = sum(-(-n // partition_size) for n in row_lengths if n > partition_size)
+        rows = np.asarray(row_lengths, dtype=np.int64)
+        parts = int((-(-rows[rows > partition_size] // partition_size)).sum())
         t += 2 * parts * num_heads * (head_dim + 2) * 4 / PREFILL_PARTIALS_BYTES_PER_US + PREFILL_REDUCE_US
     return t
 
@@ -784,16 +801,17 @@ def choose_prefill_partition(group_lengths: list[int], row_lengths: tuple[int, .
     the unsplit grid fills at most two rounds of the GPU (beyond that the partials' traffic
     outweighs any balance gained)."""
     slots = COMPUTE_UNITS * (PREFILL_WORKGROUPS_PER_CU if waves_per_group else 1)
-    if not group_lengths or len(group_lengths) * num_kv_heads >= 2 * slots:
+    group_lengths = np.asarray(group_lengths, dtype=np.int64)
+    if not group_lengths.size or group_lengths.size * num_kv_heads >= 2 * slots:
         return 0
-    longest = max(group_lengths)
+    longest = int(group_lengths.max())
     model = functools.partial(prefill_model_us, group_lengths, row_lengths, num_kv_heads, num_heads, head_dim,
                               waves_per_group=waves_per_group, context_bytes=context_bytes)
     best = (model(0), 0)
     for size in PREFILL_PARTITION_CANDIDATES:
         if size >= longest:
             break
-        if sum(-(-n // size) for n in group_lengths) * num_kv_heads > 8 * slots:
+        if int((-(-group_lengths // size)).sum()) * num_kv_heads > 8 * slots:
             continue  # more than 8 rounds of partitions: their partials outweigh any balance
         t = model(size)
         if t < best[0]:

@@ -281,6 +281,38 @@ def test_multi_row_tiles_list_every_partition_a_group_sees_once() -> None:
         assert work == sorted(work, reverse=True)
 
 
+def test_multi_row_groups_and_tiles_match_a_loop_restatement() -> None:
+    # the array builders against the definition written as loops: groups of at most
+    # pairs // group consecutive rows of one request, each with its last row's context (0 for
+    # a padding request), heaviest first then by first row; tiles of one group per partition
+    # its context reaches (one for an empty context), longest piece first
+    rng = np.random.default_rng(41)
+    for _ in range(60):
+        count = int(rng.integers(1, 30))
+        rows = [int(x) for x in rng.integers(0, 70, count)]
+        lengths = [r + int(rng.integers(0, 3000)) if r else int(rng.integers(0, 2)) * 40 for r in rows]
+        if not any(rows):
+            rows[0], lengths[0] = 1, max(lengths[0], 1)
+        table = torch.ones(count, max(lengths) // 16 + 2, dtype=torch.int32)
+        step = hip_attention.plan(ForwardMode.MIXED, _ints(*rows), _ints(*lengths), table, 16).plan
+        group, pairs = int(rng.choice([1, 4, 8])), int(rng.choice([16, 32, 64, 128]))
+        per_tile, want, first = max(1, pairs // group), [], 0
+        for request, (n_rows, length) in enumerate(zip(rows, lengths)):
+            for start in range(0, n_rows, per_tile):
+                n = min(per_tile, n_rows - start)
+                want.append((step.row_lengths[first + start + n - 1] if length else 0, first + start, n, request))
+            first += n_rows
+        want.sort(key=lambda g: (-g[0], g[1]))
+        assert step.prefill_groups(group, pairs) == want
+        for size in (0, 64, 448, 1024):
+            tiles = []
+            for length, row, n, request in want:
+                for part in range(max(1, -(-length // size)) if size else 1):
+                    tiles.append((-min(size, length - part * size) if size else -length, row, n, request, part))
+            flat = [v for _, row, n, request, part in sorted(tiles) for v in (row, n, request, part)]
+            assert step.prefill_tiles(group, pairs, size, torch.device("cpu")).tolist() == flat
+
+
 def test_multi_row_partition_choice() -> None:
     choose = hip_attention.choose_prefill_partition
     # 16 verify windows of 8 rows over 1K fill 128 of 512 workgroup slots: split
