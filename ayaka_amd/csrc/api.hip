@@ -335,7 +335,7 @@ void* static_scratch(const char* op, void* stream) {
 
 extern "C" {
 
-int ayk_abi_version(void) { return 17; }
+int ayk_abi_version(void) { return 18; }
 
 int ayk_paged_prefill_tile_pairs(int32_t head_dim) { return ayk::prefill_tile_pairs_for(head_dim); }
 

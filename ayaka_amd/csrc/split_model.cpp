@@ -8,6 +8,7 @@
 #include <climits>
 #include <cstdint>
 #include <functional>
+#include <queue>
 #include <vector>
 
 #include "ayaka_hip.h"
@@ -208,6 +209,35 @@ int64_t ayk_work_list(const int64_t* lengths, int32_t n_lengths, int32_t partiti
       *w++ = 0;
     }
   return n;
+}
+
+// The multi-row launch model's schedule: durations sorted longest first, each started in the
+// slot that frees up first (a min-heap of slot loads); equal durations fill whole rounds.
+int ayk_dispatch_makespan(const double* durations, int64_t n, int32_t slots, double* makespan) {
+  if (n < 0 || slots < 1 || !makespan || (n > 0 && !durations)) return AYK_ERR_ARGUMENT;
+  std::vector<double> d(durations, durations + n);
+  std::sort(d.begin(), d.end(), std::greater<double>());
+  if (n <= slots) {
+    *makespan = n ? d[0] : 0.0;
+    return AYK_OK;
+  }
+  if (d[0] == d[n - 1]) {
+    *makespan = (double)((n + slots - 1) / slots) * d[0];
+    return AYK_OK;
+  }
+  std::priority_queue<double, std::vector<double>, std::greater<double>> loads(d.begin(), d.begin() + slots);
+  for (int64_t i = slots; i < n; ++i) {
+    const double least = loads.top();
+    loads.pop();
+    loads.push(least + d[i]);
+  }
+  double last = 0.0;
+  while (!loads.empty()) {
+    last = std::max(last, loads.top());
+    loads.pop();
+  }
+  *makespan = last;
+  return AYK_OK;
 }
 
 }  // extern "C"

@@ -17,7 +17,7 @@ from ayaka_amd.errors import BackendError, CapabilityError
 __all__ = ["ABI_VERSION", "EXPORTS", "LIB_PATH", "check", "lib"]
 
 LIB_PATH = Path(__file__).resolve().parent.parent / "lib" / "libayaka_hip.so"
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
@@ -70,6 +70,7 @@ EXPORTS: dict[str, tuple[object, list[object]]] = {
     "ayk_split_model": (ctypes.c_int, [_P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _P, _P]),
     "ayk_work_list": (ctypes.c_int64, [_P, _I32, _I32, _P]),
     "ayk_best_split": (ctypes.c_int, [_P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I64, _I64, _P]),
+    "ayk_dispatch_makespan": (ctypes.c_int, [_P, _I64, _I32, _P]),
     "ayk_debug_kv_reach_begin": (ctypes.c_int, [_I64]),
     "ayk_debug_kv_reach_end": (ctypes.c_int, [_P]),
     "ayk_gather_blocks": (ctypes.c_int, [_P, _P, _P, _P, _P, _I32, _I64, _I32, _I64, _P]),

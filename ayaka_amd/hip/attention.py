@@ -747,17 +747,14 @@ PREFILL_PARTITION_CANDIDATES = (128, 256, 512, 1024, 2048, 4096)
 
 def _dispatch_makespan(steps: "list[float] | np.ndarray", slots: int) -> float:
     """Finish time of workgroups of these durations started longest first, each in the first of
-    ``slots`` identical slots to free up."""
-    steps = np.sort(np.asarray(steps, dtype=np.float64))[::-1]
-    if steps.size <= slots:
-        return float(steps[0]) if steps.size else 0
-    if steps[0] == steps[-1]:
-        return -(-steps.size // slots) * float(steps[0])
-    loads = steps[:slots].tolist()
-    heapq.heapify(loads)
-    for s in steps[slots:].tolist():
-        heapq.heapreplace(loads, loads[0] + s)
-    return max(loads)
+    ``slots`` identical slots to free up (the library's host code, ``ayk_dispatch_makespan``)."""
+    steps = np.ascontiguousarray(steps, dtype=np.float64).reshape(-1)
+    out = ctypes.c_double()
+    rc = _lib.lib().ayk_dispatch_makespan(steps.ctypes.data, steps.size, slots, ctypes.byref(out))
+    if rc != 0:
+        raise BackendError(f"attention._dispatch_makespan: {steps.size} durations over {slots} slots",
+                           context={"op": "attention._dispatch_makespan"})
+    return out.value
 
 
 def prefill_model_us(group_lengths: list[int], row_lengths: tuple[int, ...] | list[int], num_kv_heads: int,

@@ -366,6 +366,13 @@ int64_t ayk_work_list(const int64_t* lengths, int32_t n_lengths, int32_t partiti
 int ayk_best_split(const int64_t* lengths, int32_t n_lengths, const int32_t* sizes, int32_t n_sizes, int32_t groups,
                    int32_t cost, int32_t compute_units, int32_t xcds, int64_t max_items, int64_t round_items,
                    int32_t* best);
+/*
+ * ayk_dispatch_makespan: the finish time (`*makespan`) of `n` workgroups of these durations
+ * started longest first, each in the first of `slots` identical slots to free up (the
+ * multi-row launch model: a slot per workgroup a compute unit holds). Returns AYK_OK, or
+ * AYK_ERR_ARGUMENT for a negative count, no slot or a null pointer.
+ */
+int ayk_dispatch_makespan(const double* durations, int64_t n, int32_t slots, double* makespan);
 
 /*
  * Diagnostics, no counterpart in the reference: the host address walk. Between

@@ -21,7 +21,7 @@ def declared() -> list[str]:
 
 def test_every_declared_function_is_exported_and_bound() -> None:
     names = declared()
-    assert len(names) == 20
+    assert len(names) == 21
     lib = _lib.lib()
     for name in names:
         assert hasattr(lib, name), name
