@@ -151,7 +151,9 @@ class HipAttentionPlan:
     row_lengths: tuple[int, ...] = ()
     # v2 work lists built by the step's first attend, keyed by partition size, for the later layers
     work: dict[int, torch.Tensor] = field(default_factory=dict, compare=False, repr=False)
-    splits: dict[tuple[int, int, int], Split] = field(default_factory=dict, compare=False, repr=False)
+    # per-step choices shared by every layer: decode splits, multi-row partition sizes and launches,
+    # window splits, and the multi-row row groups they are scored on
+    splits: dict[tuple, object] = field(default_factory=dict, compare=False, repr=False)
     # library calls recorded by attend / store, replayed for the same objects (_fastpath)
     launches: dict = field(default_factory=dict, compare=False, repr=False)
 
